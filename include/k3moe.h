@@ -1,0 +1,122 @@
+/* k3moe: MXFP4 mixture-of-experts step for AMD Instinct MI355X (gfx950).
+ *
+ * C ABI of the native library libk3moe.so. Plain pointers and sizes only;
+ * every pointer argument except `stream` is a device pointer. The library
+ * never allocates device memory, never frees caller memory and never writes
+ * an input buffer. All work is enqueued asynchronously on `stream` (a
+ * hipStream_t passed as void*); no entry point synchronises the host.
+ *
+ * Return value: 0 on success, a negative K3MOE_E* code on failure, with a
+ * thread-local message available from k3moe_last_error().
+ *
+ * Reference counterpart: the reference has no native code. Its MoE step is
+ * inline Python in megabench/tasks/kimi.py:307-324, reached through the
+ * candidate plug-in `build(case) -> run(inputs)`
+ * (megabench/harness/runner.py:53-69). Each entry point below names the
+ * reference lines it replaces.
+ */
+#ifndef K3MOE_H
+#define K3MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define K3MOE_OK 0
+#define K3MOE_EINVAL -1      /* bad geometry, dtype code or null pointer */
+#define K3MOE_EWORKSPACE -2  /* workspace too small or misaligned */
+#define K3MOE_EHIP -3        /* a HIP runtime call failed */
+
+/* Gating rule. */
+#define K3MOE_GATING_SIGMOID_BIAS 0 /* kimi.py:308-315: sigmoid, +bias, top-k, renorm */
+#define K3MOE_GATING_SOFTMAX 1      /* tasks/distributed.py:174-176: top-k logits, softmax */
+
+/* Gated activation between the gate/up and down projections. */
+#define K3MOE_ACT_SITU 0 /* kimi.py:194-196: 4 tanh(g/4) sigmoid(g) 25 tanh(u/25) */
+#define K3MOE_ACT_SILU 1 /* tasks/distributed.py:184: silu(g) u */
+
+/* Element type codes. */
+#define K3MOE_DTYPE_BF16 0
+#define K3MOE_DTYPE_F32 1
+
+/* Geometry and options of one MoE step.
+ *   tokens   B: rows of x (and of latent)
+ *   experts  E: router rows; leading dim of every expert tensor
+ *   topk     k: experts per token, 1 <= k <= 32, k <= E
+ *   hidden   h: width of x and of the router rows (the router's K)
+ *   latent   K: width of the expert input and of expert_sum (== hidden
+ *               unless a separate latent input is given); multiple of 32
+ *   inter    I: expert intermediate width; multiple of 32
+ * Expert tensor layouts are the reference's (kimi.py:116-119), all u8:
+ *   gate_blocks, up_blocks [E, I, K/32, 16]   gate_scales, up_scales [E, I, K/32]
+ *   down_blocks            [E, K, I/32, 16]   down_scales            [E, K, I/32]
+ * Byte j of a 16-byte block holds element 2j (low nibble) and 2j+1 (high). */
+typedef struct k3moe_dims {
+    int32_t tokens;
+    int32_t experts;
+    int32_t topk;
+    int32_t hidden;
+    int32_t latent;
+    int32_t inter;
+    int32_t gating;     /* K3MOE_GATING_* */
+    int32_t activation; /* K3MOE_ACT_* */
+    int32_t x_dtype;    /* K3MOE_DTYPE_BF16 (x, latent and router are bf16) */
+    int32_t reserved;   /* must be 0 */
+} k3moe_dims;
+
+/* Device workspace bytes the step needs for `dims` (256-byte aligned base).
+ * Replaces the temporaries of kimi.py:308-323 (logits, index lists, the
+ * per-expert decoded weights, which this library never materialises). */
+int k3moe_workspace_bytes(const k3moe_dims *dims, size_t *bytes);
+
+/* One MoE step (kimi.py:307-324 without the TP all-reduce of line 324):
+ *   x            [B, h]  bf16   router input (`normalized`, kimi.py:308)
+ *   latent       [B, K]  bf16   expert input, or NULL to use x (kimi.py:317,322)
+ *   router       [E, h]  bf16   (kimi.py:114)
+ *   router_bias  [E]     fp32   or NULL for zero bias (kimi.py:115, 309)
+ *   expert tensors as in k3moe_dims
+ *   routes       [B, k]  int64  forced expert sets (kimi.py:311-313), or NULL;
+ *                               ids must be in range and distinct per row
+ * Outputs (written, never read):
+ *   expert_sum   [B, K]  fp32   routing-weighted sum of expert outputs (kimi.py:318, 323)
+ *   expert_ids   [B, k]  int64  chosen experts, ascending per row (kimi.py:316)
+ *   route_weights[B, k]  fp32   gating weights aligned with expert_ids (kimi.py:314-315)
+ *   shortfall    [B]     fp32   k-th best biased score minus the weakest chosen
+ *                               one, clamped at 0 (kimi.py:313); NULL allowed,
+ *                               written only when routes != NULL
+ * Numerics follow the BF16 serving oracle: FP32 router logits and gating,
+ * FP32 accumulation, gate/up outputs, the activation and the down output
+ * rounded to bf16 where kimi.py:322 casts, FP32 weighted combine in ascending
+ * expert order. */
+int k3moe_moe_step(const k3moe_dims *dims,
+                   const void *x, const void *latent,
+                   const void *router, const float *router_bias,
+                   const uint8_t *gate_blocks, const uint8_t *gate_scales,
+                   const uint8_t *up_blocks, const uint8_t *up_scales,
+                   const uint8_t *down_blocks, const uint8_t *down_scales,
+                   const int64_t *routes,
+                   float *expert_sum, int64_t *expert_ids, float *route_weights,
+                   float *shortfall,
+                   void *workspace, size_t workspace_bytes, void *stream);
+
+/* MXFP4 decode, unpack_mxfp4 (megabench/tasks/quantization.py:40-51) plus the
+ * `.to(act)` cast of kimi.py:321: n_blocks blocks of 16 bytes and n_blocks
+ * scales -> n_blocks*32 values of out_dtype (K3MOE_DTYPE_F32 or _BF16),
+ * bit-exact including -0.0, subnormal results and NaN for scale 255. */
+int k3moe_mxfp4_decode(const uint8_t *blocks, const uint8_t *scales, int64_t n_blocks,
+                       int32_t out_dtype, void *out, void *stream);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *k3moe_last_error(void);
+
+/* Library version string. */
+const char *k3moe_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* K3MOE_H */

@@ -1,0 +1,158 @@
+// Device-side building blocks shared by the k3moe kernels (gfx950 only).
+//
+// MFMA tile convention (v_mfma_f32_16x16x32_bf16, one wave of 64 lanes):
+//   A (16 weight rows x 32 k):  lane l holds row (l % 16), k = 8*(l / 16) + e, e = 0..7
+//   B (32 k x 16 token cols):   lane l holds col (l % 16), k = 8*(l / 16) + e
+//   D (16 x 16 fp32):           lane l holds col (l % 16), rows 4*(l / 16) + v, v = 0..3
+// A and B use the same (lane group, element) -> k assignment, so any
+// consistent k permutation gives the same dot products.
+//
+// One "k-step" covers 128 consecutive k (four 32-wide MXFP4 blocks): lane
+// group q = l / 16 owns block 4*step + q of its row and feeds its 32 values
+// to four MFMAs (kk = 0..3, elements 8*kk .. 8*kk+7 of the block).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace k3moe {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+
+constexpr int kWave = 64;
+constexpr int kBlockK = 32;  // MXFP4 block (quantization.py:10)
+constexpr int kStepK = 128;  // k covered by one k-step of a wave
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// ---------------------------------------------------------------- bf16 bits --
+
+// FP32 -> BF16 with round-to-nearest-even; NaN -> quiet NaN with the sign kept.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  uint32_t rounding = 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)((u + rounding) >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Round an FP32 value to the nearest BF16 and return it as FP32.
+__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// ------------------------------------------------------------ MXFP4 decode --
+
+// Exact FP32 bits of one E2M1 code scaled by 2^(s-127) (OCP MX v1.0):
+// sign bit 3, exponent bits 2..1 (bias 1), mantissa bit 0; E8M0 255 is NaN.
+__device__ __forceinline__ uint32_t mxfp4_bits(uint32_t code, uint32_t s) {
+  if (s == 255u) return 0x7FC00000u;
+  uint32_t sign = (code & 8u) << 28;
+  uint32_t e = (code >> 1) & 3u, m = code & 1u;
+  if (e == 0u && m == 0u) return sign;
+  // unscaled value as (biased exponent, 1-bit mantissa): 0.5 = 2^-1, else 2^(e-1)(1+m/2)
+  int32_t be = (e == 0u) ? 126 : (int32_t)(e + 126u);
+  uint32_t mant = (e == 0u) ? 0u : (m << 22);
+  int32_t ne = be + (int32_t)s - 127;
+  if (ne >= 255) return sign | 0x7F800000u;
+  if (ne >= 1) return sign | ((uint32_t)ne << 23) | mant;
+  uint32_t sig = (1u << 23) | mant;  // subnormal result: exact right shift
+  return sign | (sig >> (1 - ne));
+}
+
+// E8M0 byte placed in the exponent field of an FP32 scale operand.
+__device__ __forceinline__ float e8m0_to_f32(uint32_t s) { return __uint_as_float(s << 23); }
+
+// v_cvt_scalef32_pk_{bf16,f32}_fp4 reads only the exponent field of its FP32
+// scale operand and reproduces the exact decode (subnormal and overflowing
+// products included) for every E8M0 byte except 255, where it returns a
+// negative NaN instead of the canonical quiet NaN; measured over all 256 x 256
+// (byte, scale) pairs on MI355X. Byte 255 therefore takes the bit construction.
+__device__ __forceinline__ bool scale_is_plain(uint32_t s) { return s != 255u; }
+
+// Eight E2M1 codes (one 32-bit word, element order = nibble order, low nibble
+// first) scaled by `scale` -> bf16x8 via v_cvt_scalef32_pk_bf16_fp4.
+__device__ __forceinline__ bf16x8 fp4x8_to_bf16(uint32_t w, float scale) {
+  bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
+  bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
+  bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);
+  bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3);
+  bf16x8 r;
+  r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+  r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+  return r;
+}
+
+// Exact decode of eight codes to bf16 by bit construction (any scale byte).
+__device__ __forceinline__ bf16x8 fp4x8_to_bf16_exact(uint32_t w, uint32_t s) {
+  uint32_t packed[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t lo = mxfp4_bits((w >> (8 * i)) & 15u, s) >> 16;
+    uint32_t hi = mxfp4_bits((w >> (8 * i + 4)) & 15u, s) >> 16;
+    packed[i] = lo | (hi << 16);
+  }
+  u32x4 v = {packed[0], packed[1], packed[2], packed[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// The 32 values of one MXFP4 block (16 bytes) as four bf16x8 MFMA operands:
+// hardware conversion for scale bytes 0..254, bit construction for 255.
+__device__ __forceinline__ void convert_block(const u32x4 &w, uint32_t s, bf16x8 out[4]) {
+  if (scale_is_plain(s)) {
+    float sc = e8m0_to_f32(s);
+    out[0] = fp4x8_to_bf16(w[0], sc);
+    out[1] = fp4x8_to_bf16(w[1], sc);
+    out[2] = fp4x8_to_bf16(w[2], sc);
+    out[3] = fp4x8_to_bf16(w[3], sc);
+  } else {
+    out[0] = fp4x8_to_bf16_exact(w[0], s);
+    out[1] = fp4x8_to_bf16_exact(w[1], s);
+    out[2] = fp4x8_to_bf16_exact(w[2], s);
+    out[3] = fp4x8_to_bf16_exact(w[3], s);
+  }
+}
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8 &a, const bf16x8 &b, const f32x4 &c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 load16(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
+
+__device__ __forceinline__ u32x4 load16_nt(const void *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
+
+// ------------------------------------------------------------- activations --
+
+// SiTU (kimi.py:194-196) on bf16-rounded gate/up values, in FP32 with the
+// reference's operation order: ((4 tanh(g/4)) sigmoid(g)) (25 tanh(u/25)).
+__device__ __forceinline__ float act_situ(float g, float u) {
+  float sig = 1.0f / (1.0f + expf(-g));
+  float a = __fmul_rn(4.0f, tanhf(g / 4.0f));
+  a = __fmul_rn(a, sig);
+  float b = __fmul_rn(25.0f, tanhf(u / 25.0f));
+  return __fmul_rn(a, b);
+}
+
+// silu(g) u (distributed.py:184) in FP32.
+__device__ __forceinline__ float act_silu(float g, float u) {
+  float sig = 1.0f / (1.0f + expf(-g));
+  return __fmul_rn(__fmul_rn(g, sig), u);
+}
+
+__device__ __forceinline__ float apply_act(int act, float g, float u) {
+  return act == 0 ? act_situ(g, u) : act_silu(g, u);
+}
+
+// ----------------------------------------------------------- wave helpers --
+
+template <typename T>
+__device__ __forceinline__ T shfl_xor(T v, int mask) {
+  return __shfl_xor(v, mask, kWave);
+}
+
+}  // namespace k3moe

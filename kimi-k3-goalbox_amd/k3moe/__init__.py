@@ -1,0 +1,17 @@
+"""k3moe: the MXFP4 mixture-of-experts step of the Kimi K3 decode oracle on MI355X.
+
+Public API
+  moe_step(x, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales,
+           down_blocks, down_scales, *, topk, gating, activation, fp32, routes, latent)
+  moe_layer(values, layer, x, *, topk, ...)     reads the reference's weight-dict keys
+  mxfp4_decode(blocks, scales, dtype)           bit-exact unpack_mxfp4 on the GPU
+  submission.build(case) -> run(inputs)         the reference's plug-in interface
+
+The kernels live in libk3moe.so (hand-written HIP for gfx950, C ABI in
+include/k3moe.h). There is no CPU fallback.
+"""
+
+from .moe import moe_layer, moe_step, mxfp4_decode, workspace_bytes  # noqa: F401
+from .configs import ALL as CONFIGS, MoEConfig  # noqa: F401
+
+__all__ = ['moe_step', 'moe_layer', 'mxfp4_decode', 'workspace_bytes', 'CONFIGS', 'MoEConfig']

@@ -1,0 +1,85 @@
+"""The C-ABI library loads and exports what include/k3moe.h declares (no GPU calls)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from k3moe import _native, moe
+from k3moe.configs import ALL as CONFIGS
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), 'include', 'k3moe.h')
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r'^\s*(?:int|const char \*)\s*(k3moe_\w+)\s*\(', text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    names = declared_functions()
+    assert set(names) == set(_native.EXPORTS)
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.k3moe_version().decode().startswith('k3moe')
+
+
+def test_dims_struct_matches_header():
+    text = open(HEADER).read()
+    body = re.search(r'typedef struct k3moe_dims \{(.*?)\} k3moe_dims;', text, flags=re.S).group(1)
+    fields = re.findall(r'int32_t\s+(\w+);', body)
+    assert fields == [f for f, _ in _native.Dims._fields_]
+
+
+@pytest.mark.parametrize('name', sorted(CONFIGS))
+def test_workspace_bytes_for_every_config(name):
+    c = CONFIGS[name]
+    d = _native.Dims(tokens=c.tokens, experts=c.experts, topk=c.topk, hidden=c.hidden, latent=c.width,
+                     inter=c.inter, gating=_native.GATING[c.gating], activation=_native.ACTIVATION[c.activation],
+                     x_dtype=0, reserved=0)
+    n = moe.workspace_bytes(d)
+    assert n > 0 and n % 256 == 0
+    # the expert intermediates alone need at least B k (I + K) bf16 values
+    assert n >= c.tokens * c.topk * (c.inter + c.width) * 2
+
+
+@pytest.mark.parametrize('field,value,msg', [
+    ('experts', 0, 'experts'), ('experts', 2000, 'experts'), ('topk', 0, 'topk'), ('topk', 33, 'topk'),
+    ('hidden', 100, 'hidden'), ('latent', 48, 'latent'), ('inter', 40, 'inter'), ('gating', 7, 'gating'),
+    ('activation', 9, 'activation'), ('x_dtype', 1, 'x_dtype'), ('reserved', 1, 'reserved'),
+    ('tokens', 0, 'tokens')])
+def test_invalid_dims_are_rejected_with_a_message(field, value, msg):
+    d = _native.Dims(tokens=2, experts=16, topk=4, hidden=64, latent=64, inter=64, gating=0, activation=0,
+                     x_dtype=0, reserved=0)
+    setattr(d, field, value)
+    with pytest.raises(ValueError, match=msg):
+        moe.workspace_bytes(d)
+
+
+def test_moe_step_rejects_host_tensors_and_bad_dtypes():
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    r = torch.zeros(8, 64, dtype=torch.bfloat16)
+    gb = torch.zeros(8, 64, 2, 16, dtype=torch.uint8)
+    gs = torch.zeros(8, 64, 2, dtype=torch.uint8)
+    db = torch.zeros(8, 64, 2, 16, dtype=torch.uint8)
+    with pytest.raises(ValueError, match='ROCm GPU'):
+        moe.moe_step(x, r, None, gb, gs, gb, gs, db, gs, topk=2)
+    with pytest.raises(NotImplementedError):
+        moe.moe_step(x, r, None, gb, gs, gb, gs, db, gs, topk=2, fp32=True)
+    with pytest.raises(ValueError, match='uint8'):
+        moe.mxfp4_decode(torch.zeros(2, 16, dtype=torch.int8), torch.zeros(2, dtype=torch.uint8))
+    with pytest.raises(ValueError, match='geometry'):
+        moe.mxfp4_decode(torch.zeros(2, 8, dtype=torch.uint8), torch.zeros(2, dtype=torch.uint8))
+
+
+def test_product_package_does_not_import_the_oracle():
+    pkg = os.path.dirname(os.path.abspath(moe.__file__))
+    for root, _, files in os.walk(os.path.dirname(pkg)):
+        for f in files:
+            if f.endswith(('.py', '.hip', '.hpp', '.cpp', '.h')):
+                text = open(os.path.join(root, f)).read()
+                assert not re.search(r'^\s*(from|import)\s+oracle\b', text, flags=re.M), f
+                assert 'liborc' not in text, f

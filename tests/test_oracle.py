@@ -1,0 +1,249 @@
+"""CPU pins of the oracle (no GPU).
+
+The oracle is trusted only after these checks:
+  * decode: torch restatement == C bit construction == float64 closed form on
+    every (byte, scale) pair, plus hand-computed special values and the
+    committed code x scale table;
+  * top-k / grouping: torch restatement == C restatement == brute force;
+  * the FP32 expert chain == an independent float64 brute force (per token,
+    closed-form decode) to FP32 rounding, on several seeds and both
+    activations / gatings; a planted mistake fails it;
+  * band grader, shortfall and no-mutation rules behave as the reference's
+    own unit tests require (megabench/tests/test_kimi.py:67-109).
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cdecode, grading, moe_ref
+
+GOLDEN = os.path.join(os.path.dirname(__file__), 'golden')
+
+
+def tiny_inputs(seed=0, E=8, k=2, h=64, I=64, B=3, gating='sigmoid_bias'):
+    from k3moe import synthetic
+    from k3moe.configs import MoEConfig
+    cfg = MoEConfig('tiny', E, k, h, I, B, gating=gating)
+    return cfg, synthetic.moe_layer_inputs(cfg, seed, scale_mode='kimi')
+
+
+# ----------------------------------------------------------------- decode --
+
+def all_pairs():
+    blocks = np.tile(np.arange(256, dtype=np.uint8).reshape(1, 16, 16), (256, 1, 1))
+    scales = np.repeat(np.arange(256, dtype=np.uint8)[:, None], 16, axis=1)
+    return blocks, scales
+
+
+def test_decode_three_restatements_agree_bitwise():
+    blocks, scales = all_pairs()
+    c = cdecode.mxfp4_decode_bits(blocks, scales)
+    t = moe_ref.unpack_mxfp4(torch.from_numpy(blocks), torch.from_numpy(scales)).numpy().view(np.uint32)
+    with np.errstate(over='ignore'):
+        f = moe_ref._decode_f64(blocks, scales).astype(np.float32).view(np.uint32)
+    assert c.shape == (256, 512)
+    assert np.array_equal(c, t)
+    assert np.array_equal(c, f)
+
+
+def test_decode_special_values():
+    def dec(byte, scale):
+        return cdecode.mxfp4_decode_bits(np.full((1, 16), byte, np.uint8), np.array([scale], np.uint8))[:2]
+    assert list(dec(0x21, 127).view(np.float32)) == [0.5, 1.0]           # low nibble is the even element
+    assert list(dec(0x7F, 127).view(np.float32)) == [-6.0, 6.0]
+    assert list(dec(0x88, 127)) == [0x80000000, 0x80000000]            # code 8 = -0.0
+    assert list(dec(0x11, 0)) == [0x00200000, 0x00200000]              # 0.5 * 2^-127 = 2^-128, subnormal
+    assert list(dec(0x33, 0)) == [0x00600000, 0x00600000]              # 1.5 * 2^-127
+    assert list(dec(0x00, 255)) == [0x7FC00000, 0x7FC00000]            # scale 255 -> NaN, even for zero codes
+    assert list(dec(0x37, 254)) == [0x7F800000, 0x7F400000]            # 6*2^127 = inf, 1.5*2^127 finite
+    assert list(dec(0x44, 130).view(np.float32)) == [16.0, 16.0]       # 2 * 2^3
+
+
+def test_decode_matches_committed_table():
+    table = np.load(os.path.join(GOLDEN, 'mxfp4_code_scale_table.npy'))   # [scale][code] uint32
+    assert table.shape == (256, 16) and table.dtype == np.uint32
+    blocks = np.tile((np.arange(16, dtype=np.uint8) * 17).reshape(1, 1, 16), (256, 1, 1))  # byte = code | code<<4
+    scales = np.arange(256, dtype=np.uint8).reshape(256, 1)
+    bits = cdecode.mxfp4_decode_bits(blocks, scales)[:, 0:32:2]
+    assert np.array_equal(bits, table)
+    # closed form for every finite entry
+    for s in range(255):
+        for code in range(16):
+            sign = -1.0 if code & 8 else 1.0
+            e, m = (code >> 1) & 3, code & 1
+            mag = m * 0.5 if e == 0 else 2.0 ** (e - 1) * (1 + m / 2)
+            with np.errstate(over='ignore'):
+                want = np.float32(sign * mag * 2.0 ** (s - 127))
+            assert table[s, code] == want.view(np.uint32), (s, code)
+
+
+def test_decode_rejects_bad_inputs():
+    with pytest.raises(ValueError):
+        moe_ref.unpack_mxfp4(torch.zeros(2, 16, dtype=torch.int8), torch.zeros(2, dtype=torch.uint8))
+    with pytest.raises(ValueError):
+        moe_ref.unpack_mxfp4(torch.zeros(2, 8, dtype=torch.uint8), torch.zeros(2, dtype=torch.uint8))
+
+
+# ------------------------------------------------------- top-k / grouping --
+
+def test_topk_restatements_agree():
+    g = torch.Generator().manual_seed(7)
+    v = torch.rand(50, 40, generator=g)
+    v[3, 5] = v[3, 9] = v[3].max() + 1        # exact tie: lower index first
+    v[4, 2] = float('nan')                     # NaN ranks first
+    k = 6
+    c = cdecode.topk_sorted(v.numpy(), k)
+    t = moe_ref._stable_topk_desc(v, k).sort(-1).values.numpy()
+    assert np.array_equal(c, t)
+    assert 5 in c[3] and 9 in c[3]
+    assert 2 in c[4]
+    # brute force on tiny rows: enumerate all k-subsets
+    import itertools
+    small = torch.rand(5, 7, generator=g)
+    for r in range(5):
+        best = max(itertools.combinations(range(7), 3), key=lambda s: (sorted(small[r, list(s)].tolist())[0]))
+        assert sorted(best) == list(cdecode.topk_sorted(small[r:r+1].numpy(), 3)[0])
+
+
+def test_group_matches_nonzero_order():
+    g = torch.Generator().manual_seed(3)
+    B, E, k = 37, 20, 4
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(B)])
+    counts, offsets, prow, pslot = cdecode.group(ids.numpy(), E)
+    for e in range(E):
+        rows, slots = (ids == e).nonzero(as_tuple=True)          # kimi.py:320
+        lo, hi = offsets[e], offsets[e + 1]
+        assert counts[e] == len(rows)
+        assert list(prow[lo:hi]) == rows.tolist()
+        assert list(pslot[lo:hi]) == slots.tolist()
+
+
+# ------------------------------------------------------------ float chain --
+
+@pytest.mark.parametrize('seed', [0, 1, 2])
+@pytest.mark.parametrize('activation', ['situ', 'silu'])
+def test_fp32_chain_matches_float64_brute_force(seed, activation):
+    cfg, inp = tiny_inputs(seed)
+    args = tuple(inp[k] for k in ('x', 'router', 'router_bias', 'gate_blocks', 'gate_scales', 'up_blocks',
+                                  'up_scales', 'down_blocks', 'down_scales'))
+    r = moe_ref.moe_step(*args, topk=cfg.topk, activation=activation, fp32=True)
+    ref = moe_ref.moe_step_f64(*args, routes=r['expert_ids'], weights=r['route_weights'], activation=activation)
+    assert moe_ref.rel_l2(r['expert_sum'], ref) < 2e-6
+    bf = moe_ref.moe_step(*args, topk=cfg.topk, activation=activation)
+    err = moe_ref.rel_l2(bf['expert_sum'], ref)
+    assert 1e-4 < err < 2e-2          # the BF16 oracle is visibly coarser than FP32, but close
+
+
+def test_planted_mistake_fails_brute_force():
+    cfg, inp = tiny_inputs(0)
+    args = [inp[k] for k in ('x', 'router', 'router_bias', 'gate_blocks', 'gate_scales', 'up_blocks',
+                             'up_scales', 'down_blocks', 'down_scales')]
+    r = moe_ref.moe_step(*args, topk=cfg.topk, fp32=True)
+    ref = moe_ref.moe_step_f64(*args, routes=r['expert_ids'], weights=r['route_weights'])
+    # swap the gate and up operands: a plausible transposition mistake
+    swapped = list(args)
+    swapped[3], swapped[5] = args[5], args[3]
+    swapped[4], swapped[6] = args[6], args[4]
+    bad = moe_ref.moe_step(*swapped, topk=cfg.topk, fp32=True, routes=r['expert_ids'])
+    assert moe_ref.rel_l2(bad['expert_sum'], ref) > 0.05
+
+
+def test_routing_closed_form():
+    cfg, inp = tiny_inputs(1, E=16, k=4, B=5)
+    r = moe_ref.route(inp['x'], inp['router'], inp['router_bias'], 4)
+    logits = inp['x'].double() @ inp['router'].double().T
+    s = 1/(1 + torch.exp(-logits))
+    biased = s + inp['router_bias'].double()
+    for b in range(5):
+        want = sorted(torch.argsort(biased[b], descending=True)[:4].tolist())
+        assert r['expert_ids'][b].tolist() == want
+        w = s[b, want] / s[b, want].sum()
+        assert torch.allclose(r['route_weights'][b].double(), w, rtol=1e-6, atol=0)
+    soft = moe_ref.route(inp['x'], inp['router'], None, 4, gating='softmax')
+    for b in range(5):
+        want = sorted(torch.argsort(logits[b], descending=True)[:4].tolist())
+        assert soft['expert_ids'][b].tolist() == want
+        p = torch.softmax(logits[b, want], 0)
+        assert torch.allclose(soft['route_weights'][b].double(), p, rtol=1e-6, atol=0)
+
+
+# ---------------------------------------------------------- grading rules --
+
+def test_band_accepts_oracle_and_fp32_rejects_noise():
+    cfg, inp = tiny_inputs(5)
+    args = tuple(inp[k] for k in ('x', 'router', 'router_bias', 'gate_blocks', 'gate_scales', 'up_blocks',
+                                  'up_scales', 'down_blocks', 'down_scales'))
+    bf = moe_ref.moe_step(*args, topk=cfg.topk)
+    tr = moe_ref.moe_step(*args, topk=cfg.topk, fp32=True, routes=bf['expert_ids'])
+    grading.band_check(bf['expert_sum'], bf['expert_sum'], tr['expert_sum'], tr['expert_sum'])
+    grading.band_check(tr['expert_sum'], bf['expert_sum'], tr['expert_sum'], tr['expert_sum'])
+    g = torch.Generator().manual_seed(0)
+    noisy = bf['expert_sum'] + 0.2*bf['expert_sum'].std()*torch.randn(bf['expert_sum'].shape, generator=g)
+    with pytest.raises(AssertionError):
+        grading.band_check(noisy, bf['expert_sum'], tr['expert_sum'], tr['expert_sum'])
+    nan = bf['expert_sum'].clone()
+    nan[0, 0] = float('nan')
+    with pytest.raises(AssertionError):
+        grading.band_check(nan, bf['expert_sum'], tr['expert_sum'], tr['expert_sum'])
+
+
+def test_forced_routes_and_shortfall():
+    cfg, inp = tiny_inputs(9)
+    args = tuple(inp[k] for k in ('x', 'router', 'router_bias', 'gate_blocks', 'gate_scales', 'up_blocks',
+                                  'up_scales', 'down_blocks', 'down_scales'))
+    own = moe_ref.moe_step(*args, topk=cfg.topk, fp32=True)
+    forced = moe_ref.moe_step(*args, topk=cfg.topk, fp32=True, routes=own['expert_ids'])
+    assert torch.equal(own['expert_sum'], forced['expert_sum'])
+    assert float(forced['route_shortfall'].max()) == 0.0
+    worst = torch.arange(cfg.experts - cfg.topk, cfg.experts).expand(cfg.tokens, -1)
+    bad = moe_ref.moe_step(*args, topk=cfg.topk, fp32=True, routes=worst)
+    assert float(bad['route_shortfall'].max()) > grading.ROUTE_FLOOR
+    assert grading.valid_routes(own['expert_ids'], cfg.experts)
+    assert grading.valid_routes(own['expert_ids'].flip(-1), cfg.experts)
+    rep = own['expert_ids'].clone()
+    rep[:, 1] = rep[:, 0]
+    assert not grading.valid_routes(rep, cfg.experts)
+
+
+def test_oracle_does_not_mutate_inputs():
+    cfg, inp = tiny_inputs(17)
+    before = grading.snapshot(inp)
+    moe_ref.moe_step(*(inp[k] for k in ('x', 'router', 'router_bias', 'gate_blocks', 'gate_scales', 'up_blocks',
+                                        'up_scales', 'down_blocks', 'down_scales')), topk=cfg.topk)
+    grading.check_unchanged(inp, before)
+    inp['x'][0, 0] += 1
+    with pytest.raises(AssertionError):
+        grading.check_unchanged(inp, before)
+
+
+def test_route_set_certification():
+    cfg, inp = tiny_inputs(2, E=16, k=4, B=4)
+    r = moe_ref.route(inp['x'], inp['router'], inp['router_bias'], 4)
+    ok = grading.route_sets(r['expert_ids'], r['expert_ids'], inp['x'], inp['router'], inp['router_bias'], 4)
+    assert ok['exact'] and ok['ok']
+    other = r['expert_ids'].clone()
+    b = r['biased'][0]
+    order = torch.argsort(b, descending=True)
+    other[0] = torch.cat([order[:3], order[4:5]]).sort().values     # swap the 4th and 5th best
+    det = grading.route_sets(other, r['expert_ids'], inp['x'], inp['router'], inp['router_bias'], 4)
+    assert det['differing'] == 1 and not det['ok']                   # gap is far above the tie threshold
+
+
+def test_golden_tiny_case_regression():
+    data = np.load(os.path.join(GOLDEN, 'tiny_moe_seed0.npz'))
+    cfg, inp = tiny_inputs(0)
+    for key in ('x', 'router', 'gate_blocks', 'down_scales'):
+        t = inp[key]
+        arr = t.view(torch.int16).numpy() if t.dtype == torch.bfloat16 else t.numpy()
+        assert np.array_equal(arr, data['in_' + key]), key
+    args = tuple(inp[k] for k in ('x', 'router', 'router_bias', 'gate_blocks', 'gate_scales', 'up_blocks',
+                                  'up_scales', 'down_blocks', 'down_scales'))
+    bf = moe_ref.moe_step(*args, topk=cfg.topk)
+    fp = moe_ref.moe_step(*args, topk=cfg.topk, fp32=True)
+    assert np.array_equal(bf['expert_ids'].numpy(), data['expert_ids'])
+    assert np.allclose(bf['route_weights'].numpy(), data['route_weights'], rtol=1e-6, atol=0)
+    assert moe_ref.rel_l2(bf['expert_sum'], torch.from_numpy(data['expert_sum_bf16'])) < 1e-6
+    assert moe_ref.rel_l2(fp['expert_sum'], torch.from_numpy(data['expert_sum_fp32'])) < 1e-6
