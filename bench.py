@@ -1,0 +1,301 @@
+#!/usr/bin/env python3
+"""µs per MXFP4 MoE layer and achieved HBM bandwidth on one MI355X.
+
+A step is one MoE layer (router top-k, MXFP4 gate/up, activation, down,
+weighted combine) over one batch of seeded synthetic inputs resident in HBM.
+Default workload: one TP8 rank's expert shard (E=384, top-8, h=7168, I=256)
+at batch 1 (the headline line), with batches 8 and 64 reported beside it.
+
+Timing: the step is captured once in a HIP graph (torch.cuda.CUDAGraph) and
+replayed. Before every timed replay a 1 GiB buffer is read (summed) so that
+L2 and the 256 MB MALL hold none of the step's weights (cold cache); a read
+leaves no dirty lines whose write-back would land inside the timed region.
+HIP events on the replay stream bracket each replay. W untimed replays come
+first.
+
+Roofline: algorithmic bytes of the step (router + bias + x + the distinct
+experts' MXFP4 gate/up/down + outputs, k3moe.traffic.step_bytes) over the
+measured duration, against the 8 TB/s HBM peak.
+
+CPU baseline: the CPU oracle's BF16 MoE step (oracle/moe_ref.py, the
+restatement of megabench/tasks/kimi.py:307-323) on the same inputs on the host
+cores, warmup 1, median of 3.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--workload tp8|tp8-l8|prefill]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(REPO, 'kimi-k3-goalbox_amd'), REPO]
+
+METRIC = 'µs per MoE layer + achieved HBM GB/s (% of peak), b=1/8/64 on 1 MI355X'
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def percentile(vals, q):
+    s = sorted(vals)
+    at = (len(s) - 1)*q
+    lo = int(at)
+    return s[lo] + (s[min(lo + 1, len(s) - 1)] - s[lo])*(at - lo)
+
+
+PHASES = ('router', 'barrier1', 'topk', 'barrier2', 'group', 'gate_up', 'barrier3', 'down_combine')
+
+
+def read_trace(cfg, device):
+    """Per-phase timing of the last persistent step from its workspace trace area (K3MOE_TRACE=1)."""
+    import torch
+    import k3moe
+    from k3moe import moe
+    ws = moe._WORKSPACES.get((device.type, device.index))
+    x = torch.empty(cfg.tokens, cfg.hidden, dtype=torch.bfloat16, device=device)
+    g = torch.empty(cfg.experts, cfg.inter, cfg.width//32, 16, dtype=torch.uint8, device=device)
+    d = torch.empty(cfg.experts, cfg.width, cfg.inter//32, 16, dtype=torch.uint8, device=device)
+    r = torch.empty(cfg.experts, cfg.hidden, dtype=torch.bfloat16, device=device)
+    total = k3moe.workspace_bytes(moe.dims_for(x, r, g, d, cfg.topk, cfg.gating, cfg.activation))
+    full = ws[total - 262144: total].cpu().view(torch.int64).view(1024, 32).double()
+    G = int((full[:, 8] > 0).sum())
+    full = full[:G]
+    raw = full[:, :9]
+    dump = os.environ.get('K3MOE_TRACE_DUMP')
+    if dump:
+        import numpy as np
+        np.save(f'{dump}_{cfg.name}.npy', full.numpy())
+    t0 = raw[:, 0].min()
+    out = {'workgroups': G}
+    for n, name in enumerate(PHASES):
+        dur = (raw[:, n + 1] - raw[:, n])*0.01   # 100 MHz ticks -> us
+        out[name] = {'median_us': round(float(dur.median()), 2), 'max_us': round(float(dur.max()), 2),
+                     'grid_done_at_us': round(float((raw[:, n + 1].max() - t0)*0.01), 2)}
+    out['total_us'] = round(float((raw[:, 8].max() - t0)*0.01), 2)
+    gu = (raw[:, 6] - raw[:, 5])*0.01
+    out['gate_up_by_wg_mod8'] = [round(float(gu[j::8].mean()), 1) for j in range(8)]
+    out['gate_up_pct'] = [round(float(gu.quantile(q)), 1) for q in (0.0, 0.1, 0.5, 0.9, 1.0)]
+    out['gate_up_slowest_wgs'] = [int(x) for x in gu.argsort(descending=True)[:8]]
+    out['start_spread_us'] = round(float((raw[:, 0].max() - t0)*0.01), 2)
+    if float(full[:, 9].max()) > 0:   # expert-major down: stream end, then barrier 4 and the combine
+        out['down_stream_done_at_us'] = round(float((full[:, 9].max() - t0)*0.01), 2)
+    for n in range(4):   # inside each grid barrier: release+add, spin, acquire
+        if float(full[:, 13 + 4*n].max()) <= 0:
+            continue
+        b = full[:, 12 + 4*n: 16 + 4*n]
+        out[f'barrier{n + 1}_parts'] = {
+            'release_add_med_us': round(float(((b[:, 1] - b[:, 0])*0.01).median()), 2),
+            'release_add_max_us': round(float(((b[:, 1] - b[:, 0])*0.01).max()), 2),
+            'last_arrival_at_us': round(float((b[:, 1].max() - t0)*0.01), 2),
+            'first_release_seen_at_us': round(float((b[:, 2].min() - t0)*0.01), 2),
+            'last_release_seen_at_us': round(float((b[:, 2].max() - t0)*0.01), 2),
+            'acquire_max_us': round(float(((b[:, 3] - b[:, 2])*0.01).max()), 2)}
+    return out
+
+
+def gpu_inputs(cfg, seed, layers, device, host_gen):
+    from k3moe import synthetic
+    import torch
+    out = []
+    for layer in range(layers):
+        if host_gen:
+            inp = synthetic.moe_layer_inputs(cfg, seed, layer=layer)
+            host = inp
+            inp = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+        else:
+            host = None
+            inp = synthetic.moe_layer_inputs(cfg, seed, layer=layer, device=device)
+        out.append((inp, host))
+    return out
+
+
+def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True):
+    """Replay a captured graph of `layers` MoE layers; returns per-replay ms and the routing stats."""
+    import torch
+    import k3moe
+    from k3moe import synthetic, traffic
+
+    data = gpu_inputs(cfg, seed, layers, device, host_gen)
+    kw = dict(topk=cfg.topk, gating=cfg.gating, activation=cfg.activation)
+    distinct = []
+    for inp, _ in data:
+        o = k3moe.moe_step(*synthetic.step_args(inp), **kw, latent=inp.get('latent'))
+        distinct.append(int(o['expert_ids'].unique().numel()))
+    torch.cuda.synchronize(device)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        for inp, _ in data:   # warm the allocator outside the capture
+            k3moe.moe_step(*synthetic.step_args(inp), **kw, latent=inp.get('latent'))
+    torch.cuda.current_stream(device).wait_stream(stream)
+    torch.cuda.synchronize(device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [k3moe.moe_step(*synthetic.step_args(inp), **kw, latent=inp.get('latent')) for inp, _ in data]
+    flush = torch.ones(1 << 28, dtype=torch.float32, device=device) if cold else None
+    sink = torch.zeros((), dtype=torch.float32, device=device)
+    for i in range(warmup):
+        if cold:
+            torch.sum(flush, 0, out=sink)
+        graph.replay()
+    torch.cuda.synchronize(device)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        if cold:
+            torch.sum(flush, 0, out=sink)
+        starts[i].record()
+        graph.replay()
+        ends[i].record()
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - t0
+    ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    # the graph's outputs equal an eager step on the same inputs (bitwise)
+    inp0 = data[0][0]
+    eager = k3moe.moe_step(*synthetic.step_args(inp0), **kw, latent=inp0.get('latent'))
+    torch.cuda.synchronize(device)
+    same = all(torch.equal(outs[0][k], eager[k]) for k in eager)
+    nbytes = sum(traffic.step_bytes(B=cfg.tokens, E=cfg.experts, k=cfg.topk, h=cfg.hidden, I=cfg.inter,
+                                    distinct=d, K=cfg.width) for d in distinct)
+    flops = layers*traffic.step_flops(B=cfg.tokens, E=cfg.experts, k=cfg.topk, h=cfg.hidden, I=cfg.inter,
+                                      K=cfg.width)
+    trace = read_trace(cfg, device) if os.environ.get('K3MOE_TRACE') == '1' and layers == 1 else None
+    del graph, outs, flush
+    return {'ms': ms, 'wall_s': wall, 'distinct': distinct, 'bytes': nbytes, 'flops': flops,
+            'graph_matches_eager': same, 'host_inputs': [h for _, h in data], 'trace': trace}
+
+
+def summarize(cfg, m, layers):
+    ms_mean = statistics.fmean(m['ms'])
+    ms_p50 = statistics.median(m['ms'])
+    us_layer = ms_mean*1000/layers
+    gbps = m['bytes']/(ms_mean*1e-3)/1e9
+    return {'tokens': cfg.tokens, 'layers': layers, 'us_per_layer': round(us_layer, 3),
+            'us_per_layer_p50': round(ms_p50*1000/layers, 3),
+            'us_per_layer_p95': round(percentile(m['ms'], 0.95)*1000/layers, 3),
+            'distinct_experts': m['distinct'] if layers > 1 else m['distinct'][0],
+            'algorithmic_bytes': m['bytes'], 'hbm_GBps': round(gbps, 1),
+            'hbm_frac': round(gbps/8000.0, 4), 'tflops': round(m['flops']/(ms_mean*1e-3)/1e12, 3),
+            'graph_matches_eager': m['graph_matches_eager'], **({'trace': m['trace']} if m['trace'] else {})}
+
+
+def cpu_baseline(cfg, host_inputs, reps=3):
+    """The CPU oracle's BF16 step on the same inputs (warmup 1, median of reps)."""
+    import torch
+    from oracle import moe_ref
+    from k3moe import synthetic
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    args = synthetic.step_args(host_inputs)
+    kw = dict(topk=cfg.topk, gating=cfg.gating, activation=cfg.activation, latent=host_inputs.get('latent'))
+    moe_ref.moe_step(*args, **kw)
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        moe_ref.moe_step(*args, **kw)
+        ts.append(time.perf_counter() - t)
+    return {'us_per_layer': round(statistics.median(ts)*1e6, 1), 'cores': torch.get_num_threads(), 'reps': reps}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=20)
+    ap.add_argument('--warmup', type=int, default=2)
+    ap.add_argument('--workload', default='tp8', choices=['tp8', 'tp8-l8', 'prefill'])
+    ap.add_argument('--batches', default='1,8,64', help='batches of the tp8 workload; the first is the headline')
+    ap.add_argument('--seed', type=int, default=0)
+    ap.add_argument('--warm-cache', action='store_true', help='skip the L2/MALL flush before each replay')
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--trace', action='store_true', help='record per-phase timestamps of the persistent kernel '
+                    '(sets K3MOE_TRACE=1; adds a few stores per phase)')
+    args = ap.parse_args()
+    if args.trace:
+        os.environ['K3MOE_TRACE'] = '1'
+    if args.gpus != 1:
+        print(f'bench.py measures one GPU (a TP rank\'s expert shard on one MI355X); --gpus {args.gpus} is not '
+              'supported: the multi-GPU path (TP all-reduce of expert_sum) is not part of this build',
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from k3moe import configs
+    device = torch.device('cuda:0')
+    cold = not args.warm_cache
+
+    if args.workload == 'tp8':
+        batches = [int(b) for b in args.batches.split(',')]
+        runs = [(configs.TP8_B1.with_tokens(b), 1, True) for b in batches]
+        workload = f'tp8-rank-b{batches[0]}'
+    elif args.workload == 'tp8-l8':
+        runs = [(configs.TP8_B64_L8, 8, False)]
+        workload = 'tp8-rank-b64-8-stacked-layers'
+    else:
+        runs = [(configs.PREFILL, 1, False)]
+        workload = 'unsharded-prefill-b4096'
+
+    results, host = {}, {}
+    for cfg, layers, host_gen in runs:
+        log(f'bench: {cfg.name} layers={layers} steps={args.steps} warmup={args.warmup} cold={cold}')
+        m = measure(cfg, seed=args.seed, steps=args.steps, warmup=args.warmup, cold=cold, device=device,
+                    layers=layers, host_gen=host_gen)
+        results[cfg.name] = summarize(cfg, m, layers)
+        host[cfg.name] = m['host_inputs'][0]
+        log(f'bench: {cfg.name} {results[cfg.name]}')
+        torch.cuda.empty_cache()
+
+    head_cfg, head_layers, _ = runs[0]
+    head = results[head_cfg.name]
+    cpu = None
+    if not args.no_cpu_baseline and args.workload == 'tp8':
+        per = {}
+        for cfg, _, _ in runs:
+            log(f'cpu baseline: {cfg.name}')
+            per[cfg.name] = cpu_baseline(cfg, host[cfg.name])
+            results[cfg.name]['cpu_us_per_layer'] = per[cfg.name]['us_per_layer']
+        c0 = per[head_cfg.name]
+        cpu = {'value': c0['us_per_layer'], 'unit': 'us/layer', 'cores': c0['cores'], 'kind': 'port',
+               'sample': f'{head_cfg.name} seed {args.seed}: one full MoE layer of the CPU oracle '
+                         f'(BF16 mode), median of 3 after 1 warmup; batches '
+                         + ', '.join(f'{k}: {v["us_per_layer"]} us' for k, v in per.items()),
+               'cpu': platform.processor() or platform.machine()}
+
+    ms_step = head['us_per_layer']*head_layers/1000.0
+    line = {
+        'metric': METRIC,
+        'value': head['us_per_layer'],
+        'unit': 'us/layer',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(ms_step, 6),
+        'higher_is_better': False,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'bf16',
+        'data': 'synthetic',
+        'config': {'workload': workload, 'experts': head_cfg.experts, 'topk': head_cfg.topk,
+                   'hidden': head_cfg.hidden, 'inter': head_cfg.inter, 'tokens': head_cfg.tokens,
+                   'layers': head_layers, 'weights': 'mxfp4 (e2m1 + e8m0/32), dequantized to bf16 in registers',
+                   'accumulate': 'fp32', 'cache': 'cold (1 GiB read before each replay)' if cold else 'warm',
+                   'timing': 'HIP events around HIP-graph replays'},
+        'hbm_GBps': head['hbm_GBps'],
+        'hbm_frac': head['hbm_frac'],
+        'per_batch': results,
+        'roofline': {'bound': 'hbm', 'kernel': 'k3moe_moe_step (whole step)', 'achieved': head['hbm_GBps'],
+                     'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac'], 'traffic': None},
+        'cpu_baseline': cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()

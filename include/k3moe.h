@@ -38,6 +38,14 @@ extern "C" {
 #define K3MOE_ACT_SITU 0 /* kimi.py:194-196: 4 tanh(g/4) sigmoid(g) 25 tanh(u/25) */
 #define K3MOE_ACT_SILU 1 /* tasks/distributed.py:184: silu(g) u */
 
+/* Execution path. AUTO runs the single persistent kernel for decode-sized
+ * batches (tokens <= 64, tokens*topk <= 1024) and the multi-kernel path
+ * otherwise; the other values force one (DECODE fails with K3MOE_EINVAL when
+ * the shape does not fit it). Both give the same expert sets. */
+#define K3MOE_PATH_AUTO 0
+#define K3MOE_PATH_GENERAL 1
+#define K3MOE_PATH_DECODE 2
+
 /* Element type codes. */
 #define K3MOE_DTYPE_BF16 0
 #define K3MOE_DTYPE_F32 1
@@ -64,10 +72,11 @@ typedef struct k3moe_dims {
     int32_t gating;     /* K3MOE_GATING_* */
     int32_t activation; /* K3MOE_ACT_* */
     int32_t x_dtype;    /* K3MOE_DTYPE_BF16 (x, latent and router are bf16) */
-    int32_t reserved;   /* must be 0 */
+    int32_t path;       /* K3MOE_PATH_*: execution path, normally AUTO */
 } k3moe_dims;
 
-/* Device workspace bytes the step needs for `dims` (256-byte aligned base).
+/* Device workspace bytes the step needs for `dims` (256-byte aligned base,
+ * zero-initialised control block, see k3moe_workspace_init).
  * Replaces the temporaries of kimi.py:308-323 (logits, index lists, the
  * per-expert decoded weights, which this library never materialises). */
 int k3moe_workspace_bytes(const k3moe_dims *dims, size_t *bytes);
@@ -101,6 +110,20 @@ int k3moe_moe_step(const k3moe_dims *dims,
                    float *expert_sum, int64_t *expert_ids, float *route_weights,
                    float *shortfall,
                    void *workspace, size_t workspace_bytes, void *stream);
+
+/* Zero the workspace's first 69632 bytes (the control block with the barrier
+ * counters and the sticky status word, and a zero area the kernels read in
+ * place of inactive data) with a small kernel on `stream`. A workspace must be
+ * initialised once before its first step; each step leaves the counters at
+ * zero, so one workspace serves any number of consecutive steps on one
+ * stream (steps that overlap on one workspace race). No reference
+ * counterpart: the reference allocates its temporaries per call. */
+int k3moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
+
+/* Copy the workspace's sticky status word to *status (0 = every step so far
+ * completed normally; 1 = a persistent step's grid barrier timed out, its
+ * outputs are invalid). Synchronises `stream`. No reference counterpart. */
+int k3moe_workspace_status(const void *workspace, int32_t *status, void *stream);
 
 /* MXFP4 decode, unpack_mxfp4 (megabench/tasks/quantization.py:40-51) plus the
  * `.to(act)` cast of kimi.py:321: n_blocks blocks of 16 bytes and n_blocks

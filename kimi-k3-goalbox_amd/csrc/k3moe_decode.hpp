@@ -1,0 +1,831 @@
+// Decode path: the whole MoE step in one persistent kernel (B <= 64 tokens).
+//
+// One 512-thread workgroup (8 waves) per CU. Phases, separated by grid
+// barriers where a phase needs every workgroup's results:
+//   R   router logits on MFMA. Workgroup unit = (16 router rows, 16 tokens,
+//       k-range); the 8 waves split the k-range and meet in LDS, so at most
+//       Srw (<= 8) partials per logit reach memory.             (kimi.py:308)
+//   --- barrier 1
+//   T   gating and top-k, one workgroup per token: partials summed in a fixed
+//       order, sigmoid + bias (or softmax), k wave arg-max rounds, weights
+//       renormalised, ids sorted.                               (kimi.py:308-316)
+//   --- barrier 2
+//   G   every workgroup rebuilds the expert grouping in its own LDS (active
+//       experts ascending, token pairs ascending inside an expert), so no
+//       barrier is needed after it.                             (kimi.py:319-320)
+//   GU  gate/up: workgroup unit = (active expert, 8 gate + 8 up rows); one
+//       16-row MFMA tile, the 8 waves split K and meet in LDS; SiTU/SiLU
+//       epilogue; bf16 h to memory.                             (kimi.py:321-322)
+//   --- barrier 3
+//   DN  down + combine: workgroup unit = 16 output rows for every active
+//       expert, experts split over the waves; each wave accumulates
+//       w * bf16(y) per token in LDS in ascending expert order, the waves are
+//       summed in a fixed order and expert_sum is written once. (kimi.py:318-323)
+// The barrier spin is bounded: a workgroup that waits too long sets the
+// error word and every workgroup runs to the end.
+#pragma once
+
+#include "k3moe_device.hpp"
+#include "k3moe_general.hpp"
+#include "k3moe_plan.hpp"
+
+namespace k3moe {
+
+constexpr unsigned kSpinLimit = 1u << 21;  // bounded barrier wait (about 0.1-1 s)
+constexpr int kGuDepth = 8;                // gate/up k-steps loaded per batch per wave
+constexpr int kDnDepth = 2;                // down k-steps per pipelined item
+constexpr int kDnExpertMajorMin = 32;      // more active experts: expert-major down + combine
+
+struct DecodeArgs {
+  const uint16_t *x;     // [B, h] router input
+  const uint16_t *xin;   // [B, K] expert input (x or latent)
+  const uint16_t *router;
+  const float *bias;
+  const uint8_t *gblk, *gscl, *ublk, *uscl, *dblk, *dscl;
+  const int64_t *routes;
+  float *out;
+  int64_t *out_ids;
+  float *out_w;
+  float *out_short;
+  char *ws;
+};
+
+// Grid barrier number `n` (1-based) over gridDim.x workgroups. Arrival is
+// two-level so that no counter sees more than kBarGroups arrivals per
+// barrier: workgroup b counts in on group counter b mod kBarGroups; the last
+// arrival of a group counts the group in on the top counter. Release before
+// arriving, acquire after the top counter shows every group.
+__device__ __forceinline__ void grid_barrier(unsigned *ctl, unsigned n, uint64_t *trace = nullptr) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned G = gridDim.x;
+    const unsigned groups = G < kBarGroups ? G : kBarGroups;
+    const unsigned g = blockIdx.x % groups;
+    const unsigned members = (G - g + groups - 1) / groups;  // workgroups b < G with b mod groups == g
+    if (trace) trace[0] = __builtin_amdgcn_s_memrealtime();
+    const unsigned old = __hip_atomic_fetch_add(ctl + kCtlGroup + g * kCtlStride, 1u, __ATOMIC_RELEASE,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    if (old == n * members - 1u)
+      __hip_atomic_fetch_add(ctl + kCtlBar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (trace) trace[1] = __builtin_amdgcn_s_memrealtime();
+    const unsigned target = n * groups;
+    unsigned spins = 0;
+    while (__hip_atomic_load(ctl + kCtlBar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      if ((++spins & 63u) == 0u) {
+        if (__hip_atomic_load(ctl + kCtlErr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+        if (spins > kSpinLimit) {
+          __hip_atomic_store(ctl + kCtlErr, (unsigned)kErrBarrierTimeout, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+      }
+    }
+    if (trace) trace[2] = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (trace) trace[3] = __builtin_amdgcn_s_memrealtime();
+  }
+  __syncthreads();
+}
+
+// Trace slots of workgroup blockIdx.x starting at `slot`, or null when not tracing.
+__device__ __forceinline__ uint64_t *trace_slots(const Plan &pl, char *ws, int slot) {
+  return pl.o_trace ? reinterpret_cast<uint64_t *>(ws + pl.o_trace) + blockIdx.x * kTraceSlots + slot : nullptr;
+}
+
+// Phase timestamps (100 MHz real-time counter) of workgroup blockIdx.x, when
+// the plan carries a trace area; slot n of kTraceSlots.
+__device__ __forceinline__ void trace_mark(const Plan &pl, char *ws, int n) {
+  if (pl.o_trace && threadIdx.x == 0)
+    reinterpret_cast<uint64_t *>(ws + pl.o_trace)[blockIdx.x * kTraceSlots + n] = __builtin_amdgcn_s_memrealtime();
+}
+
+__device__ __forceinline__ void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Sum of the 8 per-wave tiles at element `idx` of the LDS reduction area, in wave order.
+__device__ __forceinline__ float red_sum(const float *red, int idx) {
+  float s = red[idx];
+#pragma unroll
+  for (int w = 1; w < kDecWaves; ++w) s += red[w * 256 + idx];
+  return s;
+}
+
+// Position of element (row, col) of a 16x16 MFMA result in a wave's 256-float tile.
+__device__ __forceinline__ int tile_index(int row, int col) { return (col + 16 * (row >> 2)) * 4 + (row & 3); }
+
+
+// ------------------------------------------------------ gate/up streaming --
+// A wave streams W units (8 gate + 8 up rows each, one MFMA tile per unit) of
+// one expert over a range of super-steps. A super-step is 16 MXFP4 blocks (512
+// k) of every row; in it lane group q owns the 4 consecutive blocks 4q..4q+3,
+// one per k-step t (any k permutation shared by A and B gives the same dot
+// products), so its 4 E8M0 scales are one aligned dword. Per k-step a lane
+// loads 16 bytes of each unit's A row and 64 bytes of its token's activations,
+// shared by the W units; loads come in batches of two k-steps, two batches in
+// flight. Every pointer is a per-lane row base fixed for the whole stream:
+// absent units read the workspace's zero area, inactive token lanes use a
+// buffer offset past the activations (a zero load that touches no memory).
+constexpr int kGuW = 4;  // units per stream, many-unit path
+
+template <int W>
+struct GuCtx {
+  const uint8_t *wrow[W];   // this lane's A row + 64 q bytes, per unit
+  const uint8_t *srow[W];   // this lane's scale row + 4 q bytes, per unit
+  __amdgpu_buffer_rsrc_t xr;  // activations [B, K] bf16
+  uint32_t xoff;            // this lane's row + 128 q elements, in bytes (kOffNone: inactive lane)
+};
+
+// one k-step of A (per unit) and B
+template <int W>
+struct GuStep {
+  u32x4 a[W];
+  u32x4 b[4];
+};
+
+template <int W>
+__device__ __forceinline__ void gu_issue(GuStep<W> &st, const GuCtx<W> &cx, int ss, int t) {
+#pragma unroll
+  for (int u = 0; u < W; ++u) st.a[u] = load16(cx.wrow[u] + ss * 256 + t * 16);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) st.b[kk] = bload16(cx.xr, cx.xoff + ss * 1024 + t * 64 + kk * 16);
+}
+
+template <int W>
+__device__ __forceinline__ void gu_scales(uint32_t (&sv)[W], const GuCtx<W> &cx, int ss) {
+#pragma unroll
+  for (int u = 0; u < W; ++u) sv[u] = *reinterpret_cast<const uint32_t *>(cx.srow[u] + ss * 16);
+}
+
+template <int W>
+__device__ __forceinline__ void gu_compute(const GuStep<W> &st, const uint32_t (&sv)[W], int t, f32x4 *acc) {
+#pragma unroll
+  for (int u = 0; u < W; ++u) {
+    bf16x8 av[4];
+    convert_block_fast(st.a[u], (sv[u] >> (8 * t)) & 0xFFu, av);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) acc[u] = mfma16(av[kk], as_bf16x8(st.b[kk]), acc[u]);
+  }
+}
+
+// acc[u] += the unit tiles over super-steps [ss0, ss1): one k-step per
+// buffer, two buffers in flight, the super-step's scales loaded once.
+template <int W>
+__device__ __forceinline__ void gu_stream(const GuCtx<W> &cx, int ss0, int ss1, f32x4 *acc) {
+  if (ss0 >= ss1) return;
+  GuStep<W> b0, b1;
+  uint32_t sc[W], sn[W];
+  gu_scales(sc, cx, ss0);
+  gu_issue(b0, cx, ss0, 0);
+  for (int ss = ss0; ss < ss1; ++ss) {
+    gu_issue(b1, cx, ss, 1);
+    gu_compute(b0, sc, 0, acc);
+    gu_issue(b0, cx, ss, 2);
+    gu_compute(b1, sc, 1, acc);
+    gu_issue(b1, cx, ss, 3);
+    gu_compute(b0, sc, 2, acc);
+    const bool more = ss + 1 < ss1;
+    if (more) {
+      gu_scales(sn, cx, ss + 1);
+      gu_issue(b0, cx, ss + 1, 0);
+    }
+    gu_compute(b1, sc, 3, acc);
+    if (more) {
+#pragma unroll
+      for (int u = 0; u < W; ++u) sc[u] = sn[u];
+    }
+  }
+}
+
+// Blocks past the last full super-step (K not a multiple of 512), one block
+// per lane group and k-step as blocks 16 nss + 4 kt + q, with per-lane checks.
+template <int W>
+__device__ __forceinline__ void gu_tail(const GuCtx<W> &cx, int nss, int KB, const uint8_t *zero, f32x4 *acc) {
+  const int q = (threadIdx.x & 63) >> 4;
+  for (int kt = 0; 16 * nss + 4 * kt < KB; ++kt) {
+    const int kb = 16 * nss + 4 * kt + q;  // absolute block of this lane
+    const bool ok = kb < KB;
+#pragma unroll
+    for (int u = 0; u < W; ++u) {
+      // wrow/srow carry the super-step lane offset (64 q / 4 q): undo it
+      const u32x4 wv = load16(ok ? cx.wrow[u] - 64 * q + kb * 16 : zero);
+      const uint32_t sv = ok ? cx.srow[u][kb - 4 * q] : 0u;
+      u32x4 bv[4];
+      const uint32_t xo = ok ? cx.xoff - 256 * q + kb * 64 : kOffNone;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) bv[kk] = bload16(cx.xr, xo + kk * 16);
+      bf16x8 av[4];
+      convert_block_fast(wv, sv, av);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc[u] = mfma16(av[kk], as_bf16x8(bv[kk]), acc[u]);
+    }
+  }
+}
+
+// Unit (expert e, rows r8*8 ..) A row pointers of this lane: rows 0-7 of the
+// tile are gate rows, rows 8-15 the same up rows.
+__device__ __forceinline__ void gu_rows(const Plan &pl, const DecodeArgs &a, int e, int r8, int i, int q, int KB,
+                                        const uint8_t *&wrow, const uint8_t *&srow) {
+  const size_t row = (size_t)e * pl.I + r8 * 8 + (i & 7);
+  wrow = (i >= 8 ? a.ublk : a.gblk) + row * KB * 16 + q * 64;
+  srow = (i >= 8 ? a.uscl : a.gscl) + row * KB + q * 4;
+}
+
+// Activation epilogue of a full-K unit tile held by one wave: lanes 0-31 hold
+// the gate rows, lanes 32-63 the up rows of the same (row, token); lanes 0-31
+// write h[p][row0 .. row0+7] for their token column.
+__device__ __forceinline__ void gu_finish_wave(const Plan &pl, uint16_t *hbuf, const f32x4 &acc, int p,
+                                               bool tok_ok, int row0) {
+  const int l = threadIdx.x & 63;
+  float up[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) up[v] = __shfl_xor(acc[v], 32, 64);
+  if (l < 32 && tok_ok) {
+    uint16_t hb[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) hb[v] = f32_to_bf16_bits(apply_act(pl.act, round_bf16(acc[v]), round_bf16(up[v])));
+    u32x2 packed = {(uint32_t)hb[0] | ((uint32_t)hb[1] << 16), (uint32_t)hb[2] | ((uint32_t)hb[3] << 16)};
+    *reinterpret_cast<u32x2 *>(hbuf + (size_t)p * pl.I + row0 + 4 * (l >> 4)) = packed;
+  }
+}
+
+// ---------------------------------------------------- down, expert-major --
+// For many active experts: a wave streams a contiguous run of (expert, 16-row
+// tile) items; the B operand (the expert's h rows, at most two k-steps) is
+// loaded once per expert and token chunk; bf16 y goes to the pair buffer and
+// a combine phase sums it. Tiles come in batches of kDnTiles, two in flight.
+constexpr int kDnTiles = 4;
+
+struct DnTileBatch {
+  u32x4 a[kDnTiles][2];
+  uint32_t s[kDnTiles][2];
+};
+
+// wrow/srow: this lane's row (tile rt0) + 32 q / + 2 q bytes: lane group q
+// owns blocks 2q and 2q+1 of the row (k-steps 0 and 1), so both scales are one
+// 16-bit load. Rows of later tiles are 16 rows further each; tiles at or past
+// rt1 read the zero area. Requires I == 256 (8 blocks per row).
+__device__ __forceinline__ void dnc_issue(DnTileBatch &bt, const Plan &pl, const uint8_t *wrow,
+                                          const uint8_t *srow, const uint8_t *zero, int rt0, int rt1) {
+  constexpr size_t tstride = (size_t)16 * 8 * 16, sstride = (size_t)16 * 8;
+#pragma unroll
+  for (int t = 0; t < kDnTiles; ++t) {
+    const bool ok = rt0 + t < rt1;  // wave-uniform
+    const uint32_t sc = ok ? *reinterpret_cast<const uint16_t *>(srow + t * sstride) : 0u;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bt.a[t][ks] = load16(ok ? wrow + t * tstride + ks * 16 : zero);
+      bt.s[t][ks] = (sc >> (8 * ks)) & 0xFFu;
+    }
+  }
+}
+
+__device__ __forceinline__ void dnc_compute(const DnTileBatch &bt, const Plan &pl, const u32x4 (&hb)[2][4],
+                                            uint16_t *ybuf, int rt0, int rt1, int p, bool tok_ok) {
+  const int l = threadIdx.x & 63, q = l >> 4;
+#pragma unroll
+  for (int t = 0; t < kDnTiles; ++t) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 av[4];
+      convert_block_fast(bt.a[t][ks], bt.s[t][ks], av);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc = mfma16(av[kk], as_bf16x8(hb[ks][kk]), acc);
+    }
+    if (tok_ok && rt0 + t < rt1) {
+      u32x2 packed = {(uint32_t)f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16),
+                      (uint32_t)f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16)};
+      *reinterpret_cast<u32x2 *>(ybuf + (size_t)p * pl.K + (rt0 + t) * 16 + 4 * q) = packed;
+    }
+  }
+}
+
+// Loads of one down-projection item: up to kDnDepth k-steps of A (weights and
+// scales) and B (the activated h of the item's 16-token chunk).
+struct DnLoad {
+  u32x4 w[kDnDepth];
+  uint32_t s[kDnDepth];
+  u32x4 b[kDnDepth][4];
+};
+
+__device__ __forceinline__ void dn_issue(const Plan &pl, const DecodeArgs &a, const uint16_t *hbuf,
+                                         const int *g_act, const int *g_aoff, const int *g_acnt, int rt, int d,
+                                         int c, int kc, int KB, DnLoad &L) {
+  const int l = threadIdx.x & 63, i = l & 15, q = l >> 4;
+  const int e = g_act[d], p0 = g_aoff[d], n = g_acnt[d];
+  const int pj = c * 16 + i;
+  const bool tok_ok = pj < n;
+  const size_t row = (size_t)e * pl.K + rt * 16 + i;
+  const uint16_t *hr = hbuf + (size_t)(p0 + (tok_ok ? pj : 0)) * pl.I;
+#pragma unroll
+  for (int j = 0; j < kDnDepth; ++j) {
+    const int kb = (kc + j) * 4 + q;
+    const bool ok = kc + j < pl.KSd && kb < KB;
+    L.w[j] = ok ? load16(a.dblk + (row * KB + kb) * 16) : u32x4{0, 0, 0, 0};
+    L.s[j] = ok ? a.dscl[row * KB + kb] : 127u;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      L.b[j][kk] = (ok && tok_ok) ? load16(hr + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
+  }
+}
+
+__global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  float *red = reinterpret_cast<float *>(lds);
+  int *g_act = reinterpret_cast<int *>(lds + pl.lds_red);
+  int *g_aoff = g_act + pl.Dmax;
+  int *g_acnt = g_aoff + pl.Dmax;
+  int *g_ptok = g_acnt + pl.Dmax;
+  float *g_pw = reinterpret_cast<float *>(g_ptok + pl.P);
+  int *g_pof = reinterpret_cast<int *>(g_pw + pl.P);  // pair index of (token, slot)
+  char *scr = lds + pl.lds_red + pl.lds_grp;
+  __shared__ int s_nact;
+
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int i = l & 15, q = l >> 4;
+  unsigned *ctl = reinterpret_cast<unsigned *>(a.ws + pl.o_ctl);
+  float *part = reinterpret_cast<float *>(a.ws + pl.o_logit);
+  int *ws_ids = reinterpret_cast<int *>(a.ws + pl.o_ids);
+  float *ws_w = reinterpret_cast<float *>(a.ws + pl.o_w);
+  uint16_t *hbuf = reinterpret_cast<uint16_t *>(a.ws + pl.o_h);
+  const uint8_t *zero = reinterpret_cast<const uint8_t *>(a.ws + pl.o_zero);  // kZeroBytes of zeros
+  const int B = pl.B, E = pl.E, k = pl.k;
+  trace_mark(pl, a.ws, 0);
+
+  // ------------------------------------------------------------ R: router --
+  {
+    const int NU = pl.RTr * pl.TTr * pl.Srw;
+    const int KB = pl.h / kBlockK;
+    for (int u = blockIdx.x; u < NU; u += gridDim.x) {
+      const int s = u % pl.Srw, rest = u / pl.Srw;
+      const int rt = rest % pl.RTr, tt = rest / pl.RTr;
+      const int k0 = (int)((long)s * pl.KSr / pl.Srw), k1 = (int)((long)(s + 1) * pl.KSr / pl.Srw);
+      const int ka = k0 + (k1 - k0) * w / kDecWaves, kb1 = k0 + (k1 - k0) * (w + 1) / kDecWaves;
+      const int row = rt * 16 + i, tok = tt * 16 + i;
+      const bool row_ok = row < E, tok_ok = tok < B;
+      const uint16_t *arow = a.router + (size_t)(row_ok ? row : 0) * pl.h;
+      const uint16_t *brow = a.x + (size_t)(tok_ok ? tok : 0) * pl.h;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int ks = ka; ks < kb1; ++ks) {
+        const int kb = ks * 4 + q;
+        const bool ok = kb < KB;
+        u32x4 va[4], vb[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          va[kk] = (ok && row_ok) ? load16(arow + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
+          vb[kk] = (ok && tok_ok) ? load16(brow + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) acc = mfma16(as_bf16x8(va[kk]), as_bf16x8(vb[kk]), acc);
+      }
+      *reinterpret_cast<f32x4 *>(red + w * 256 + l * 4) = acc;
+      __syncthreads();
+      if (tid < 256) {
+        const int ln = tid >> 2, v = tid & 3;
+        const int r = 4 * (ln >> 4) + v, c = ln & 15;
+        const int t = tt * 16 + c, e = rt * 16 + r;
+        if (t < B) part[((size_t)s * B + t) * pl.Epad + e] = red_sum(red, tid);
+      }
+      __syncthreads();
+    }
+  }
+  trace_mark(pl, a.ws, 1);
+  unsigned nbar = 0;  // barriers passed so far (barrier n waits for n * G arrivals)
+  grid_barrier(ctl, ++nbar, trace_slots(pl, a.ws, 12));
+  trace_mark(pl, a.ws, 2);
+
+  // -------------------------------------------------------- T: top-k/gating --
+  // Small batches: every workgroup routes every token itself (no barrier, the
+  // grouping reads its own LDS). Larger batches: token t is routed by
+  // workgroup t mod G and the results meet in the workspace after barrier 2.
+  const bool redundant = pl.redundant;
+  int *rid = reinterpret_cast<int *>(scr);     // [P] expert ids, ascending per token
+  float *rw = reinterpret_cast<float *>(rid + pl.P);  // [P] weights aligned with rid
+  char *scr2 = scr + 8 * pl.P;
+  {
+    const int nt = redundant ? B : 1;  // tokens routed per pass of this workgroup
+    uint32_t *kyl = reinterpret_cast<uint32_t *>(scr2);  // [nt][E] ordered keys
+    float *kyf = reinterpret_cast<float *>(kyl + nt * E);  // [nt][E] keys as float
+    float *scl = kyf + nt * E;                           // [nt][E] scores (sigmoid or logits)
+    int *sel = reinterpret_cast<int *>(scl + nt * E);    // [8 waves][kMaxTopk]
+    for (int t0 = redundant ? 0 : blockIdx.x; t0 < B; t0 += redundant ? B : gridDim.x) {
+      // logits of (t0 + f / E, f % E): partials summed in split order, four
+      // flat items per thread with every load in flight together
+      for (int f0 = tid; f0 < nt * E; f0 += 4 * kDecThreads) {
+        float ps[4][kDecMaxSplits];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int f = f0 + j * kDecThreads;
+          const int t = t0 + f / E, e = f % E;
+#pragma unroll
+          for (int sp = 0; sp < kDecMaxSplits; ++sp)
+            ps[j][sp] = (f < nt * E && sp < pl.Srw) ? part[((size_t)sp * B + t) * pl.Epad + e] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int f = f0 + j * kDecThreads;
+          if (f >= nt * E) break;
+          float logit = ps[j][0];
+#pragma unroll
+          for (int sp = 1; sp < kDecMaxSplits; ++sp)
+            if (sp < pl.Srw) logit += ps[j][sp];
+          const int e = f % E;
+          float score, key;
+          if (pl.gating == K3MOE_GATING_SIGMOID_BIAS) {
+            score = 1.0f / (1.0f + expf(-logit));
+            key = a.bias ? __fadd_rn(score, a.bias[e]) : score;
+          } else {
+            score = logit;
+            key = logit;
+          }
+          scl[f] = score;
+          kyf[f] = key;
+          kyl[f] = ordered_key(key);
+        }
+      }
+      __syncthreads();
+      for (int tl = w; tl < nt; tl += kDecWaves) {
+        const int t = t0 + tl;
+        int *mysel = sel + w * kMaxTopk;
+        wave_topk(kyl + tl * E, E, k, mysel);
+        wave_lds_order();
+        int my_e = -1;
+        float my_score = 0.f, my_key = 0.f;
+        if (l < k) {
+          my_e = a.routes ? (int)a.routes[(size_t)t * k + l] : mysel[l];
+          my_score = scl[tl * E + my_e];
+          my_key = kyf[tl * E + my_e];
+        }
+        float wt = 0.f;
+        if (pl.gating == K3MOE_GATING_SIGMOID_BIAS) {
+          float sum = 0.f;
+          for (int r = 0; r < k; ++r) sum = __fadd_rn(sum, __shfl(my_score, r, 64));
+          wt = my_score / __fadd_rn(sum, 1e-20f);
+        } else {
+          float mx = -INFINITY;
+          for (int r = 0; r < k; ++r) mx = fmaxf(mx, __shfl(my_score, r, 64));
+          const float ex = (l < k) ? expf(my_score - mx) : 0.f;
+          float sum = 0.f;
+          for (int r = 0; r < k; ++r) sum = __fadd_rn(sum, __shfl(ex, r, 64));
+          wt = ex / sum;
+        }
+        const bool writer = redundant ? blockIdx.x == 0 : true;
+        if (a.routes && a.out_short) {
+          float mn = INFINITY;
+          for (int r = 0; r < k; ++r) mn = fminf(mn, __shfl(my_key, r, 64));
+          if (l == 0 && writer) a.out_short[t] = fmaxf(kyf[tl * E + mysel[k - 1]] - mn, 0.f);
+        }
+        int rank = 0;
+        for (int r = 0; r < k; ++r) rank += (__shfl(my_e, r, 64) < my_e) ? 1 : 0;
+        if (l < k) {
+          const size_t o = (size_t)t * k + rank;
+          if (writer) {
+            a.out_ids[o] = my_e;
+            a.out_w[o] = wt;
+          }
+          if (redundant) {
+            rid[o] = my_e;
+            rw[o] = wt;
+          } else {
+            ws_ids[o] = my_e;
+            ws_w[o] = wt;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  trace_mark(pl, a.ws, 3);
+  if (!redundant) {
+    grid_barrier(ctl, ++nbar, trace_slots(pl, a.ws, 16));
+    for (int p0 = tid; p0 < pl.P; p0 += 4 * kDecThreads) {
+      int iv[4];
+      float wv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int p = p0 + j * kDecThreads;
+        iv[j] = p < pl.P ? ws_ids[p] : 0;
+        wv[j] = p < pl.P ? ws_w[p] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int p = p0 + j * kDecThreads;
+        if (p < pl.P) {
+          rid[p] = iv[j];
+          rw[p] = wv[j];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  trace_mark(pl, a.ws, 4);
+
+  // ------------------------------------------------- G: grouping (in LDS) --
+  {
+    int *cnt = reinterpret_cast<int *>(scr2);  // [E]
+    int *off = cnt + E;                        // [E]
+    uint32_t *bits = reinterpret_cast<uint32_t *>(off + E);  // [E][2] token bitmaps (B <= 64)
+    for (int e = tid; e < E; e += kDecThreads) {
+      cnt[e] = 0;
+      bits[2 * e] = 0;
+      bits[2 * e + 1] = 0;
+    }
+    __syncthreads();
+    for (int p = tid; p < pl.P; p += kDecThreads) {
+      const int e = rid[p];
+      const int t = p / k;
+      atomicAdd(&cnt[e], 1);
+      atomicOr(&bits[2 * e + (t >> 5)], 1u << (t & 31));
+    }
+    __syncthreads();
+    if (w == 0) {
+      // lane l owns experts [16 l, 16 l + 16): local sums, then a wave scan
+      int tot = 0, nac = 0;
+      for (int j = 0; j < 16; ++j) {
+        const int e = 16 * l + j;
+        const int c = e < E ? cnt[e] : 0;
+        tot += c;
+        nac += c > 0;
+      }
+      int it = tot, ia = nac;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int ot = __shfl_up(it, d, 64), oa = __shfl_up(ia, d, 64);
+        if (l >= d) {
+          it += ot;
+          ia += oa;
+        }
+      }
+      int base = it - tot, abase = ia - nac;
+      for (int j = 0; j < 16; ++j) {
+        const int e = 16 * l + j;
+        if (e >= E) break;
+        const int c = cnt[e];
+        off[e] = base;
+        if (c > 0) {
+          g_act[abase] = e;
+          g_aoff[abase] = base;
+          g_acnt[abase] = c;
+          ++abase;
+        }
+        base += c;
+      }
+      if (l == 63) s_nact = ia;
+    }
+    __syncthreads();
+    for (int p = tid; p < pl.P; p += kDecThreads) {
+      const int e = rid[p], t = p / k;
+      const uint32_t lo = bits[2 * e], hi = bits[2 * e + 1];
+      const int rank = t < 32 ? __popc(lo & ((1u << t) - 1u)) : __popc(lo) + __popc(hi & ((1u << (t - 32)) - 1u));
+      const int pos = off[e] + rank;
+      g_ptok[pos] = t;
+      g_pw[pos] = rw[p];
+      g_pof[p] = pos;
+    }
+    __syncthreads();
+  }
+  const int D = s_nact;
+  trace_mark(pl, a.ws, 5);
+
+  // ------------------------------------------------------------ GU: gate/up --
+  {
+    const int KB = pl.K / kBlockK;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.xin, (uint32_t)B * pl.K * 2);
+    const int NU = D * pl.U8;  // units (expert, 8 gate + 8 up rows), expert-major
+    const int GW = gridDim.x * kDecWaves;
+    const int gw = blockIdx.x * kDecWaves + w;
+    if (NU <= GW) {
+      // few units: KS waves split each unit's K and meet in LDS
+      int KS = 1;
+      while (KS < kDecWaves && NU * KS * 2 <= GW) KS *= 2;
+      const int upw = kDecWaves / KS;  // units per workgroup
+      const int u = gw / KS, sl = gw % KS;
+      const int nss = KB % 4 ? 0 : KB / 16;  // full super-steps (aligned scale dwords need K % 128 == 0)
+      const int ss0 = nss * sl / KS, ss1 = nss * (sl + 1) / KS;
+      const bool tail = sl == KS - 1 && 16 * nss < KB;
+      // token chunks: the largest expert count among this workgroup's units
+      int nmax = 0;
+      for (int j = 0; j < upw; ++j) {
+        const int uu = blockIdx.x * upw + j;
+        if (uu < NU) nmax = max(nmax, g_acnt[uu / pl.U8]);
+      }
+      const bool live = u < NU;
+      const int d = live ? u / pl.U8 : 0, r8 = live ? u % pl.U8 : 0;
+      const int e = g_act[d], p0 = g_aoff[d], n = live ? g_acnt[d] : 0;
+      GuCtx<1> cx;
+      gu_rows(pl, a, e, r8, i, q, KB, cx.wrow[0], cx.srow[0]);
+      cx.xr = xrs;
+      for (int c = 0; c * 16 < nmax; ++c) {
+        const int pj = c * 16 + i;
+        const bool tok_ok = live && pj < n;
+        cx.xoff = tok_ok ? ((uint32_t)g_ptok[p0 + pj] * pl.K + q * 128) * 2 : kOffNone;
+        f32x4 acc[1] = {{0.f, 0.f, 0.f, 0.f}};
+        if (live) {
+          gu_stream<1>(cx, ss0, ss1, acc);
+          if (tail) gu_tail<1>(cx, nss, KB, zero, acc);
+        }
+        if (KS == 1) {
+          if (live) gu_finish_wave(pl, hbuf, acc[0], p0 + pj, tok_ok, r8 * 8);
+        } else {
+          *reinterpret_cast<f32x4 *>(red + w * 256 + l * 4) = acc[0];
+          __syncthreads();
+          for (int t = tid; t < upw * 128; t += kDecThreads) {
+            const int ul = t >> 7, r = (t >> 4) & 7, j = t & 15;
+            const int uu = blockIdx.x * upw + ul;
+            if (uu >= NU) continue;
+            const int dd = uu / pl.U8, nn = g_acnt[dd];
+            if (c * 16 + j >= nn) continue;
+            float g = 0.f, uv = 0.f;
+            for (int sp = 0; sp < KS; ++sp) {
+              g += red[(ul * KS + sp) * 256 + tile_index(r, j)];
+              uv += red[(ul * KS + sp) * 256 + tile_index(r + 8, j)];
+            }
+            const float hv = apply_act(pl.act, round_bf16(g), round_bf16(uv));
+            hbuf[(size_t)(g_aoff[dd] + c * 16 + j) * pl.I + (uu % pl.U8) * 8 + r] = f32_to_bf16_bits(hv);
+          }
+          __syncthreads();
+        }
+      }
+    } else {
+      // many units: each wave streams a contiguous run over full K, up to kGuW
+      // same-expert units at a time sharing the activation loads
+      const int ua = (int)((long)NU * gw / GW), ub = (int)((long)NU * (gw + 1) / GW);
+      const int nss = KB % 4 ? 0 : KB / 16;
+      for (int u = ua; u < ub;) {
+        const int d = u / pl.U8;
+        int cnt = min(kGuW, ub - u);
+        cnt = min(cnt, (d + 1) * pl.U8 - u);
+        const int e = g_act[d], p0 = g_aoff[d], n = g_acnt[d];
+        GuCtx<kGuW> cx;
+#pragma unroll
+        for (int j = 0; j < kGuW; ++j) {
+          gu_rows(pl, a, e, (u + min(j, cnt - 1)) % pl.U8, i, q, KB, cx.wrow[j], cx.srow[j]);
+          if (j >= cnt) {  // absent unit: zero rows (the lane offsets stay inside the zero area)
+            cx.wrow[j] = zero + q * 64;
+            cx.srow[j] = zero + q * 4;
+          }
+        }
+        cx.xr = xrs;
+        for (int c = 0; c * 16 < n; ++c) {
+          const int pj = c * 16 + i;
+          const bool tok_ok = pj < n;
+          cx.xoff = tok_ok ? ((uint32_t)g_ptok[p0 + pj] * pl.K + q * 128) * 2 : kOffNone;
+          f32x4 acc[kGuW];
+#pragma unroll
+          for (int j = 0; j < kGuW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+          gu_stream<kGuW>(cx, 0, nss, acc);
+          if (16 * nss < KB) gu_tail<kGuW>(cx, nss, KB, zero, acc);
+#pragma unroll
+          for (int j = 0; j < kGuW; ++j)
+            if (j < cnt) gu_finish_wave(pl, hbuf, acc[j], p0 + pj, tok_ok, ((u + j) % pl.U8) * 8);
+        }
+        u += cnt;
+      }
+    }
+  }
+  trace_mark(pl, a.ws, 6);
+  grid_barrier(ctl, ++nbar, trace_slots(pl, a.ws, 20));
+  trace_mark(pl, a.ws, 7);
+
+  // ------------------------------------------------------- DN: down+combine --
+  const bool expert_major = D > kDnExpertMajorMin && pl.I == 256 && pl.o_y;
+  if (expert_major) {
+    uint16_t *ybuf = reinterpret_cast<uint16_t *>(a.ws + pl.o_y);
+    const __amdgpu_buffer_rsrc_t hrs = make_rsrc(hbuf, (uint32_t)pl.P * pl.I * 2);
+    const int NT = D * pl.RTd;  // (expert, 16-row tile) items, expert-major
+    const int GW = gridDim.x * kDecWaves;
+    const int gw = blockIdx.x * kDecWaves + w;
+    const int ta = (int)((long)NT * gw / GW), tb = (int)((long)NT * (gw + 1) / GW);
+    const int KB = pl.I / kBlockK;
+    for (int t = ta; t < tb;) {
+      const int d = t / pl.RTd;
+      const int rt0 = t % pl.RTd, rt1 = min(pl.RTd, rt0 + (tb - t));
+      const int e = g_act[d], p0 = g_aoff[d], n = g_acnt[d];
+      const size_t row0 = (size_t)e * pl.K + rt0 * 16 + i;
+      const uint8_t *wrow = a.dblk + row0 * KB * 16 + q * 32, *srow = a.dscl + row0 * KB + q * 2;
+      const size_t tstride = (size_t)16 * KB * 16, sstride = (size_t)16 * KB;
+      for (int c = 0; c * 16 < n; ++c) {
+        const int pj = c * 16 + i;
+        const bool tok_ok = pj < n;
+        // lane group q feeds blocks 2q (k-step 0) and 2q+1 (k-step 1) of the h row
+        const uint32_t hoff = tok_ok ? (uint32_t)(p0 + pj) * pl.I * 2 + q * 128 : kOffNone;
+        u32x4 hb[2][4];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const uint32_t ho = hoff + ks * 64;
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) hb[ks][kk] = bload16(hrs, ho + kk * 16);
+        }
+        DnTileBatch b0, b1;
+        dnc_issue(b0, pl, wrow, srow, zero, rt0, rt1);
+        for (int rt = rt0; rt < rt1; rt += 2 * kDnTiles) {
+          const int o1 = rt + kDnTiles - rt0, o2 = rt + 2 * kDnTiles - rt0;
+          if (rt + kDnTiles < rt1) dnc_issue(b1, pl, wrow + o1 * tstride, srow + o1 * sstride, zero, rt + kDnTiles, rt1);
+          dnc_compute(b0, pl, hb, ybuf, rt, rt1, p0 + pj, tok_ok);
+          if (rt + kDnTiles < rt1) {
+            if (rt + 2 * kDnTiles < rt1)
+              dnc_issue(b0, pl, wrow + o2 * tstride, srow + o2 * sstride, zero, rt + 2 * kDnTiles, rt1);
+            dnc_compute(b1, pl, hb, ybuf, rt + kDnTiles, rt1, p0 + pj, tok_ok);
+          }
+        }
+      }
+      t += rt1 - rt0;
+    }
+    trace_mark(pl, a.ws, 9);
+    grid_barrier(ctl, ++nbar, trace_slots(pl, a.ws, 24));
+    // combine (kimi.py:318,323): expert_sum[t][col] = sum over the token's
+    // experts in ascending id order of w * bf16(y), from zero, FP32 adds
+    const int K4 = pl.K / 4;
+    for (long idx = (long)blockIdx.x * kDecThreads + tid; idx < (long)B * K4; idx += (long)gridDim.x * kDecThreads) {
+      const int t = (int)(idx / K4), c4 = (int)(idx % K4) * 4;
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int sl = 0; sl < k; ++sl) {
+        const int p = g_pof[t * k + sl];
+        const float wt = g_pw[p];
+        const u32x2 yv = *reinterpret_cast<const u32x2 *>(ybuf + (size_t)p * pl.K + c4);
+        acc[0] = __fadd_rn(acc[0], __fmul_rn(bf16_bits_to_f32(yv[0] & 0xFFFFu), wt));
+        acc[1] = __fadd_rn(acc[1], __fmul_rn(bf16_bits_to_f32(yv[0] >> 16), wt));
+        acc[2] = __fadd_rn(acc[2], __fmul_rn(bf16_bits_to_f32(yv[1] & 0xFFFFu), wt));
+        acc[3] = __fadd_rn(acc[3], __fmul_rn(bf16_bits_to_f32(yv[1] >> 16), wt));
+      }
+      *reinterpret_cast<f32x4 *>(a.out + (size_t)t * pl.K + c4) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+    }
+  } else
+  {
+    const int KB = pl.I / kBlockK;
+    float *acc_lds = reinterpret_cast<float *>(scr);  // [8 waves][B][16]
+    float *mine = acc_lds + w * B * 16;
+    const int da = D * w / kDecWaves, db = D * (w + 1) / kDecWaves;
+    for (int rt = blockIdx.x; rt < pl.RTd; rt += gridDim.x) {
+      for (int j = l; j < B * 16; j += 64) mine[j] = 0.f;
+      wave_lds_order();
+      // The wave walks items (expert d, 16-token chunk c, k-steps kc..kc+1) in
+      // order with the next item's loads in flight while the current one runs.
+      DnLoad cur, nxt;
+      int d = da, c = 0, kc = 0;
+      if (d < db) dn_issue(pl, a, hbuf, g_act, g_aoff, g_acnt, rt, d, c, kc, KB, cur);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      while (d < db) {
+        int nd = d, nc = c, nkc = kc + kDnDepth;
+        if (nkc >= pl.KSd) {
+          nkc = 0;
+          if (++nc * 16 >= g_acnt[d]) {
+            nc = 0;
+            ++nd;
+          }
+        }
+        if (nd < db) dn_issue(pl, a, hbuf, g_act, g_aoff, g_acnt, rt, nd, nc, nkc, KB, nxt);
+#pragma unroll
+        for (int j = 0; j < kDnDepth; ++j) {
+          if (kc + j >= pl.KSd) break;
+          bf16x8 av[4];
+          convert_block_fast(cur.w[j], cur.s[j], av);
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) acc = mfma16(av[kk], as_bf16x8(cur.b[j][kk]), acc);
+        }
+        if (nkc == 0) {  // (d, c) complete: fold w * bf16(y) into the wave's accumulators
+          const int p0 = g_aoff[d], pj = c * 16 + i;
+          if (pj < g_acnt[d]) {
+            const int t = g_ptok[p0 + pj];
+            const float wt = g_pw[p0 + pj];
+            float *dst = mine + t * 16 + 4 * q;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) dst[v] = __fadd_rn(dst[v], __fmul_rn(round_bf16(acc[v]), wt));
+          }
+          wave_lds_order();
+          acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        cur = nxt;
+        d = nd;
+        c = nc;
+        kc = nkc;
+      }
+      __syncthreads();
+      for (int j = tid; j < B * 16; j += kDecThreads) {
+        float sum = acc_lds[j];
+#pragma unroll
+        for (int ww = 1; ww < kDecWaves; ++ww) sum = __fadd_rn(sum, acc_lds[ww * B * 16 + j]);
+        a.out[(size_t)(j >> 4) * pl.K + rt * 16 + (j & 15)] = sum;
+      }
+      __syncthreads();
+    }
+  }
+
+  // ------------------------------------------------ exit: reset the counters --
+  __syncthreads();
+  trace_mark(pl, a.ws, 8);
+  if (tid == 0) {
+    const unsigned old = __hip_atomic_fetch_add(ctl + kCtlExit, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == gridDim.x - 1) {
+      __hip_atomic_store(ctl + kCtlBar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (unsigned g = 0; g < kBarGroups; ++g)
+        __hip_atomic_store(ctl + kCtlGroup + g * kCtlStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctl + kCtlExit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+}  // namespace k3moe

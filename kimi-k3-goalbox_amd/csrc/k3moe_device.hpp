@@ -116,15 +116,40 @@ __device__ __forceinline__ void convert_block(const u32x4 &w, uint32_t s, bf16x8
   }
 }
 
+// Same conversion with the hardware path for every scale byte, for the GEMMs:
+// scale 255 then yields NaN of the other sign, which propagates to the same
+// NaN outputs.
+__device__ __forceinline__ void convert_block_fast(const u32x4 &w, uint32_t s, bf16x8 out[4]) {
+  const float sc = e8m0_to_f32(s);
+  out[0] = fp4x8_to_bf16(w[0], sc);
+  out[1] = fp4x8_to_bf16(w[1], sc);
+  out[2] = fp4x8_to_bf16(w[2], sc);
+  out[3] = fp4x8_to_bf16(w[3], sc);
+}
+
 __device__ __forceinline__ f32x4 mfma16(const bf16x8 &a, const bf16x8 &b, const f32x4 &c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ u32x4 load16(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
-__device__ __forceinline__ u32x4 load16_nt(const void *p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+// Raw buffer resource over [base, base + bytes) (gfx9 descriptor word 3): a
+// load at an offset past the end returns zero and touches no memory, which is
+// how inactive lanes skip their operand loads without branching.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
 }
+
+constexpr uint32_t kOffNone = 0x80000000u;  // a buffer offset past every resource used here
+
+__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+// Streaming weight load. A wave's 16-byte loads cover half of each 128-byte
+// line (4 blocks of 16 rows); the other half is loaded one k-step later, so
+// the line must stay in L2 in between: plain loads, not non-temporal ones.
+__device__ __forceinline__ u32x4 load16_nt(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
 // ------------------------------------------------------------- activations --
 
@@ -153,6 +178,78 @@ __device__ __forceinline__ float apply_act(int act, float g, float u) {
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask) {
   return __shfl_xor(v, mask, kWave);
+}
+
+// DPP controls (GFX9): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror,
+// row_mirror, row_bcast:15, row_bcast:31.
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140,
+              kDppBcast15 = 0x142, kDppBcast31 = 0x143;
+
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, Ctrl, RowMask, 0xF, false);
+}
+
+// Wave-wide maximum / minimum of an unsigned value, returned to every lane:
+// pairs inside quads, then half-rows and rows, then the row broadcasts fold
+// rows 0..3 into lane 63.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp<kDppQuadXor1, 0xF>(v));
+  v = max(v, dpp<kDppQuadXor2, 0xF>(v));
+  v = max(v, dpp<kDppHalfMirror, 0xF>(v));
+  v = max(v, dpp<kDppMirror, 0xF>(v));
+  v = max(v, dpp<kDppBcast15, 0xA>(v));
+  v = max(v, dpp<kDppBcast31, 0xC>(v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, dpp<kDppQuadXor1, 0xF>(v));
+  v = min(v, dpp<kDppQuadXor2, 0xF>(v));
+  v = min(v, dpp<kDppHalfMirror, 0xF>(v));
+  v = min(v, dpp<kDppMirror, 0xF>(v));
+  v = min(v, dpp<kDppBcast15, 0xA>(v));
+  v = min(v, dpp<kDppBcast31, 0xC>(v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Order-preserving map of an FP32 value to uint32: larger float -> larger
+// key; -0.0 and +0.0 share a key; every NaN maps above +inf (top-k treats NaN
+// as the largest value).
+__device__ __forceinline__ uint32_t ordered_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0xFFFFFFFFu;
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// k rounds of wave arg-max over the keys of experts e = lane + 64 m (m < 16,
+// e < E): selected experts in rank order go to sel[0..k) (lowest index first
+// among equal keys). Every lane must call it.
+__device__ __forceinline__ void wave_topk(const uint32_t *keys_lds, int E, int k, int *sel) {
+  const int l = __lane_id();
+  uint32_t kv[16];
+  uint32_t live = 0;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int e = l + 64 * m;
+    kv[m] = e < E ? keys_lds[e] : 0u;
+    if (e < E) live |= 1u << m;
+  }
+  for (int r = 0; r < k; ++r) {
+    uint32_t best = 0u;
+    int bm = -1;
+#pragma unroll
+    for (int m = 0; m < 16; ++m)
+      if (((live >> m) & 1u) && (bm < 0 || kv[m] > best)) {  // ascending m = ascending index
+        best = kv[m];
+        bm = m;
+      }
+    const uint32_t top = wave_max_u32(bm >= 0 ? best : 0u);
+    const uint32_t idx = wave_min_u32((bm >= 0 && best == top) ? (uint32_t)(l + 64 * bm) : 0xFFFFFFFFu);
+    if ((int)(idx & 63u) == l) live &= ~(1u << (idx >> 6));
+    if (l == 0) sel[r] = (int)idx;
+  }
 }
 
 }  // namespace k3moe

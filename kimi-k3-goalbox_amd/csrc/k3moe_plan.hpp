@@ -1,0 +1,170 @@
+// Launch plan and workspace layout of one MoE step (host and device).
+//
+// Two execution paths share the workspace conventions:
+//   decode   B <= 64 tokens: one persistent kernel, one 512-thread workgroup
+//            per CU, phases separated by grid barriers (k3moe_decode.hpp)
+//   general  any B: a chain of six kernels (k3moe_general.hpp)
+// The workspace starts with a control block (kCtlBytes): barrier and exit
+// counters of the persistent kernel and a sticky error word. It must be zero
+// before the first step; every step leaves the counters at zero on exit.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "k3moe.h"
+
+namespace k3moe {
+
+constexpr int kWavesPerBlock = 4;  // general path: 4 independent waves per block
+constexpr int kThreads = kWavesPerBlock * 64;
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxTopk = 32;
+constexpr int kGroupChunk = 128;   // tokens per placement chunk in k_group
+
+constexpr int kDecWaves = 8;       // decode path: waves per workgroup
+constexpr int kDecThreads = kDecWaves * 64;
+constexpr int kDecMaxTokens = 64;
+constexpr int kDecMaxPairs = 1024;
+constexpr int kDecMaxSplits = 8;   // router k-splits across workgroups
+constexpr int kDecMaxLds = 160 * 1024;   // gfx950: 160 KiB of LDS per workgroup
+
+constexpr int kRedundantTokens = 16;   // decode: route every token in every workgroup up to this batch
+constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert) keys
+
+// Control block (uint32 words): top barrier counter, exit counter, sticky
+// error word, then kBarGroups group counters kCtlStride words (128 B) apart.
+constexpr int kCtlBar = 0, kCtlExit = 1, kCtlErr = 2;
+constexpr int kBarGroups = 16, kCtlGroup = 32, kCtlStride = 32;
+constexpr int kCtlBytes = 4 * (kCtlGroup + kBarGroups * kCtlStride);  // 2176
+// A zero area follows the control block: loads of inactive lanes and of k-steps
+// past a range read it instead of branching. Zeroed with the control block by
+// the workspace init and never written by a step. Holds any row offset used
+// (K <= 16384 activations: 32 KiB + lane offsets).
+constexpr int kZeroBytes = 64 * 1024;
+constexpr int kInitBytes = 4096 + kZeroBytes;  // control block (page-padded) + zero area
+constexpr int kTraceSlots = 32;    // phase timestamps per workgroup when tracing
+constexpr int kErrBarrierTimeout = 1;
+
+enum Path { kPathGeneral = 0, kPathDecode = 1 };
+
+struct Plan {
+  int B, E, k, h, K, I, gating, act;
+  int P;     // token-expert pairs, B*k
+  int Dmax;  // upper bound of distinct experts, min(E, P)
+  int Epad;  // E rounded up to 16
+  int path;
+  // general path
+  int RTr, TTr, KSr, Sr;
+  int RTg, KSg, Sg;
+  int RTd, KSd, RPWd, RGd;
+  // decode path
+  int G;    // persistent workgroups
+  int Srw;  // router k-splits across workgroups
+  int U8;   // gate/up units per expert: 8 gate + 8 up rows each
+  int lds_red, lds_grp, lds_scr, lds_total;  // dynamic LDS layout, bytes
+  int trace;      // 1: the decode kernel records phase timestamps at o_trace
+  int redundant;  // 1: every workgroup routes every token (no barrier before grouping)
+  // workspace byte offsets
+  size_t o_ctl, o_zero, o_logit, o_ids, o_w, o_nact, o_active, o_aoff, o_acnt, o_ptok, o_pw, o_pof, o_gpart, o_gcnt,
+      o_h, o_y, o_trace, total;
+};
+
+__host__ __device__ inline int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
+
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+inline int align16(int v) { return (v + 15) & ~15; }
+
+// Decode-path LDS layout for plan p; returns the total bytes.
+inline int decode_lds(Plan &p) {
+  p.lds_red = kDecWaves * 256 * 4;                                  // per-wave 16x16 fp32 tiles
+  p.lds_grp = align16(4 * (3 * p.Dmax + 3 * p.P));                  // active list + pairs + pair index
+  p.redundant = p.B * p.E <= kRedundantKeys && p.B <= kRedundantTokens;
+  const int nt = p.redundant ? p.B : 1;
+  const int routed = 8 * p.P;                                       // ids + weights per pair
+  const int topk = routed + 4 * (3 * nt * p.E + kDecWaves * kMaxTopk);  // keys (u32, f32), scores, picks
+  const int group = routed + 4 * (4 * p.E);                         // counts, offsets, bitmaps
+  const int down = kDecWaves * p.B * 16 * 4;                        // per-wave combine accumulators
+  int scr = topk;
+  if (group > scr) scr = group;
+  if (down > scr) scr = down;
+  p.lds_scr = align16(scr);
+  p.lds_total = p.lds_red + p.lds_grp + p.lds_scr;
+  return p.lds_total;
+}
+
+// n_cus: compute units of the device (the persistent grid size); trace: reserve
+// a timestamp area (kTraceSlots x 8 bytes per workgroup, up to 1024 groups).
+inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
+  p.B = d.tokens; p.E = d.experts; p.k = d.topk; p.h = d.hidden; p.K = d.latent; p.I = d.inter;
+  p.gating = d.gating; p.act = d.activation;
+  p.P = p.B * p.k;
+  p.Dmax = p.E < p.P ? p.E : p.P;
+  p.Epad = cdiv(p.E, 16) * 16;
+  p.RTr = cdiv(p.E, 16);
+  p.TTr = cdiv(p.B, 16);
+  p.KSr = cdiv(p.h, 128);
+  p.RTg = p.I / 16;
+  p.KSg = cdiv(p.K, 128);
+  p.RTd = p.K / 16;
+  p.KSd = cdiv(p.I, 128);
+  p.RPWd = 4;
+  p.RGd = cdiv(p.RTd, p.RPWd);
+  p.U8 = p.I / 8;
+
+  // decode path when the token count, pair count and LDS layout fit. The
+  // choice and the workspace size use the largest router split (srw_cap), so
+  // they do not depend on the device's CU count; the split used is smaller
+  // when the grid is small.
+  p.G = n_cus > 0 ? (n_cus < 1024 ? n_cus : 1024) : 1;
+  long base = (long)p.RTr * p.TTr;
+  int srw_cap = p.KSr / kDecWaves;
+  if (srw_cap > kDecMaxSplits) srw_cap = kDecMaxSplits;
+  if (srw_cap < 1) srw_cap = 1;
+  p.Srw = srw_cap;
+  p.path = kPathGeneral;
+  if (d.path != K3MOE_PATH_GENERAL && p.B <= kDecMaxTokens && p.P <= kDecMaxPairs && decode_lds(p) <= kDecMaxLds)
+    p.path = kPathDecode;
+  p.Srw = (int)(p.G / base);
+  if (p.Srw > srw_cap) p.Srw = srw_cap;
+  if (p.Srw < 1) p.Srw = 1;
+  decode_lds(p);
+
+  // general path splits: router about 1024 waves (at most 4 splits), gate/up about 2048 waves
+  p.Sr = cdiv(1024, base);
+  if (p.Sr > 4) p.Sr = 4;
+  if (p.Sr > p.KSr) p.Sr = p.KSr;
+  if (p.Sr < 1) p.Sr = 1;
+  base = (long)p.Dmax * p.RTg;
+  p.Sg = cdiv(2048, base);
+  if (p.Sg > p.KSg) p.Sg = p.KSg;
+  if (p.Sg < 1) p.Sg = 1;
+  const int logit_splits = p.path == kPathDecode ? srw_cap : p.Sr;
+  if (p.path == kPathDecode) p.Sr = p.Srw;
+
+  size_t o = 0;
+  auto take = [&](size_t bytes) { size_t at = o; o = align256(o + bytes); return at; };
+  p.o_ctl = take(4096);
+  p.o_zero = take(kZeroBytes);
+  p.o_logit = take((size_t)logit_splits * p.B * p.Epad * 4);
+  p.o_ids = take((size_t)p.P * 4);
+  p.o_w = take((size_t)p.P * 4);
+  p.o_nact = take(4);
+  p.o_active = take((size_t)p.E * 4);
+  p.o_aoff = take((size_t)p.E * 4);
+  p.o_acnt = take((size_t)p.E * 4);
+  p.o_ptok = take((size_t)p.P * 4);
+  p.o_pw = take((size_t)p.P * 4);
+  p.o_pof = take((size_t)p.P * 4);
+  const bool general = p.path == kPathGeneral;
+  p.o_gpart = take(general && p.Sg > 1 ? (size_t)p.Sg * p.P * 2 * p.I * 4 : 0);
+  p.o_gcnt = take(general ? (size_t)p.Dmax * p.RTg * 4 : 0);
+  p.o_h = take((size_t)p.P * p.I * 2);
+  // pair outputs: the general path, and the decode path's expert-major down (I == 256)
+  p.o_y = take((general || p.I == 256) ? (size_t)p.P * p.K * 2 : 0);
+  p.trace = trace && p.path == kPathDecode;
+  p.o_trace = p.trace ? take((size_t)1024 * kTraceSlots * 8) : 0;  // last area of the workspace
+  p.total = o;
+}
+
+}  // namespace k3moe

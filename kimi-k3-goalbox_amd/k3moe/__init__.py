@@ -11,7 +11,8 @@ The kernels live in libk3moe.so (hand-written HIP for gfx950, C ABI in
 include/k3moe.h). There is no CPU fallback.
 """
 
-from .moe import moe_layer, moe_step, mxfp4_decode, workspace_bytes  # noqa: F401
+from .moe import (moe_layer, moe_step, mxfp4_decode, new_workspace, workspace_bytes,  # noqa: F401
+                  workspace_status)
 from .configs import ALL as CONFIGS, MoEConfig  # noqa: F401
 
 __all__ = ['moe_step', 'moe_layer', 'mxfp4_decode', 'workspace_bytes', 'CONFIGS', 'MoEConfig']

@@ -20,6 +20,7 @@ K3MOE_OK = 0
 GATING = {'sigmoid_bias': 0, 'softmax': 1}
 ACTIVATION = {'situ': 0, 'silu': 1}
 DTYPE_BF16, DTYPE_F32 = 0, 1
+PATH = {'auto': 0, 'general': 1, 'decode': 2}
 
 
 class Dims(ctypes.Structure):
@@ -27,11 +28,11 @@ class Dims(ctypes.Structure):
     _fields_ = [('tokens', ctypes.c_int32), ('experts', ctypes.c_int32), ('topk', ctypes.c_int32),
                 ('hidden', ctypes.c_int32), ('latent', ctypes.c_int32), ('inter', ctypes.c_int32),
                 ('gating', ctypes.c_int32), ('activation', ctypes.c_int32), ('x_dtype', ctypes.c_int32),
-                ('reserved', ctypes.c_int32)]
+                ('path', ctypes.c_int32)]
 
 
-EXPORTS = ('k3moe_workspace_bytes', 'k3moe_moe_step', 'k3moe_mxfp4_decode', 'k3moe_last_error',
-           'k3moe_version')
+EXPORTS = ('k3moe_workspace_bytes', 'k3moe_workspace_init', 'k3moe_workspace_status', 'k3moe_moe_step',
+           'k3moe_mxfp4_decode', 'k3moe_last_error', 'k3moe_version')
 
 _lib = None
 
@@ -53,6 +54,10 @@ def load(path: str | None = None):
     p, i32, i64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
     lib.k3moe_workspace_bytes.argtypes = [ctypes.POINTER(Dims), ctypes.POINTER(sz)]
     lib.k3moe_workspace_bytes.restype = ctypes.c_int
+    lib.k3moe_workspace_init.argtypes = [p, sz, p]
+    lib.k3moe_workspace_init.restype = ctypes.c_int
+    lib.k3moe_workspace_status.argtypes = [p, ctypes.POINTER(i32), p]
+    lib.k3moe_workspace_status.restype = ctypes.c_int
     lib.k3moe_moe_step.argtypes = [ctypes.POINTER(Dims)] + [p]*15 + [p, sz, p]
     lib.k3moe_moe_step.restype = ctypes.c_int
     lib.k3moe_mxfp4_decode.argtypes = [p, p, i64, i32, p, p]

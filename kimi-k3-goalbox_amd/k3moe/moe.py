@@ -19,6 +19,7 @@ from . import _native
 from ._native import ACTIVATION, GATING, Dims, check
 
 MX_BLOCK = 32
+INIT_BYTES = 4096 + 65536  # control block + zero area zeroed by k3moe_workspace_init
 
 
 def _dev_ptr(t: torch.Tensor | None):
@@ -39,11 +40,14 @@ def _expect(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple, device
 
 
 def dims_for(x: torch.Tensor, router: torch.Tensor, gate_blocks: torch.Tensor, down_blocks: torch.Tensor,
-             topk: int, gating: str, activation: str, latent: torch.Tensor | None = None) -> Dims:
+             topk: int, gating: str, activation: str, latent: torch.Tensor | None = None,
+             path: str = 'auto') -> Dims:
     if gating not in GATING:
         raise ValueError(f'gating must be one of {sorted(GATING)}, got {gating!r}')
     if activation not in ACTIVATION:
         raise ValueError(f'activation must be one of {sorted(ACTIVATION)}, got {activation!r}')
+    if path not in _native.PATH:
+        raise ValueError(f'path must be one of {sorted(_native.PATH)}, got {path!r}')
     if x.dim() != 2 or router.dim() != 2 or gate_blocks.dim() != 4 or down_blocks.dim() != 4:
         raise ValueError('invalid MXFP4 block/scale geometry')
     B, h = x.shape
@@ -51,7 +55,7 @@ def dims_for(x: torch.Tensor, router: torch.Tensor, gate_blocks: torch.Tensor, d
     K = latent.shape[1] if latent is not None else h
     return Dims(tokens=B, experts=E, topk=int(topk), hidden=h, latent=K, inter=I,
                 gating=GATING[gating], activation=ACTIVATION[activation], x_dtype=_native.DTYPE_BF16,
-                reserved=0)
+                path=_native.PATH[path])
 
 
 def workspace_bytes(dims: Dims) -> int:
@@ -59,6 +63,46 @@ def workspace_bytes(dims: Dims) -> int:
     n = ctypes.c_size_t(0)
     check(lib.k3moe_workspace_bytes(ctypes.byref(dims), ctypes.byref(n)), 'k3moe_workspace_bytes')
     return int(n.value)
+
+
+_WORKSPACES: dict = {}
+
+
+def get_workspace(dims: Dims, device: torch.device) -> torch.Tensor:
+    """The cached step workspace of `device`, grown to fit `dims`.
+
+    A new workspace is zero-initialised by k3moe_workspace_init (a kernel on
+    the current stream, never a memset). Steps leave its control words at
+    zero, so one workspace serves consecutive steps in stream order; steps
+    that may run concurrently on other streams must pass their own workspace.
+    """
+    need = max(workspace_bytes(dims), INIT_BYTES)
+    key = (device.type, device.index)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = new_workspace(need, device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def new_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """A fresh, initialised workspace of at least `nbytes` bytes."""
+    ws = torch.empty(max(int(nbytes), INIT_BYTES), dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        check(_native.load().k3moe_workspace_init(_dev_ptr(ws), ctypes.c_size_t(ws.numel()),
+                                                   ctypes.c_void_p(stream)), 'k3moe_workspace_init')
+    return ws
+
+
+def workspace_status(ws: torch.Tensor) -> int:
+    """Sticky status word of a workspace (0 = every step completed normally). Synchronises."""
+    st = ctypes.c_int32(-1)
+    with torch.cuda.device(ws.device):
+        stream = torch.cuda.current_stream(ws.device).cuda_stream
+        check(_native.load().k3moe_workspace_status(_dev_ptr(ws), ctypes.byref(st), ctypes.c_void_p(stream)),
+              'k3moe_workspace_status')
+    return int(st.value)
 
 
 def _validate_routes(routes: torch.Tensor, B: int, k: int, E: int, device) -> torch.Tensor:
@@ -81,7 +125,8 @@ def moe_step(x: torch.Tensor, router: torch.Tensor, router_bias: torch.Tensor | 
              down_blocks: torch.Tensor, down_scales: torch.Tensor, *,
              topk: int, gating: str = 'sigmoid_bias', activation: str = 'situ',
              fp32: bool = False, routes: torch.Tensor | None = None,
-             latent: torch.Tensor | None = None, out: dict | None = None) -> dict:
+             latent: torch.Tensor | None = None, out: dict | None = None,
+             workspace: torch.Tensor | None = None, path: str = 'auto') -> dict:
     """One MXFP4 MoE step (kimi.py:307-324 without the TP all-reduce) on the GPU.
 
     x [B, h] bf16 (the router input, kimi.py:308); router [E, h] bf16;
@@ -94,7 +139,10 @@ def moe_step(x: torch.Tensor, router: torch.Tensor, router_bias: torch.Tensor | 
     Returns {'expert_sum': fp32 [B, K], 'expert_ids': int64 [B, k] ascending,
     'route_weights': fp32 [B, k] aligned with expert_ids,
     ['route_shortfall': fp32 [B]]}, all on x's device. Inputs are never
-    written. `out` may supply preallocated output tensors by the same keys.
+    written. `out` may supply preallocated output tensors by the same keys;
+    `workspace` an initialised workspace (new_workspace), else the device's
+    cached one is used. `path` forces an execution path ('auto', 'general',
+    'decode'); the default picks the persistent kernel for decode batches.
     """
     if fp32:
         raise NotImplementedError('fp32=True is the FP32 truth mode of the CPU oracle; '
@@ -104,7 +152,7 @@ def moe_step(x: torch.Tensor, router: torch.Tensor, router_bias: torch.Tensor | 
     device = x.device
     if device.type != 'cuda':
         raise ValueError(f'x is on {device}; the k3moe step runs on a ROCm GPU')
-    dims = dims_for(x, router, gate_blocks, down_blocks, topk, gating, activation, latent)
+    dims = dims_for(x, router, gate_blocks, down_blocks, topk, gating, activation, latent, path)
     B, h, E, k, K, I = dims.tokens, dims.hidden, dims.experts, dims.topk, dims.latent, dims.inter
     if not 1 <= k <= min(E, 32):
         raise ValueError(f'topk must be in [1, min(32, experts)], got {k}')
@@ -146,7 +194,10 @@ def moe_step(x: torch.Tensor, router: torch.Tensor, router_bias: torch.Tensor | 
         _expect(expert_sum, 'expert_sum', torch.float32, (B, K), device)
         _expect(ids, 'expert_ids', torch.int64, (B, k), device)
         _expect(weights, 'route_weights', torch.float32, (B, k), device)
-        workspace = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=device)
+        if workspace is None:
+            workspace = get_workspace(dims, device)
+        elif workspace.dtype != torch.uint8 or workspace.device != device or workspace.numel() < ws_bytes:
+            raise ValueError(f'workspace must be a uint8 tensor of at least {ws_bytes} bytes on {device}')
         stream = torch.cuda.current_stream(device).cuda_stream
         rc = lib.k3moe_moe_step(ctypes.byref(dims), _dev_ptr(x), _dev_ptr(latent), _dev_ptr(router),
                                 _dev_ptr(router_bias), _dev_ptr(gate_blocks), _dev_ptr(gate_scales),

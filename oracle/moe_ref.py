@@ -228,34 +228,6 @@ def router_f64(x, router, bias, gating='sigmoid_bias') -> np.ndarray:
     return scores + (bias.double().numpy() if bias is not None else 0.0)
 
 
-def expected_distinct(E: int, k: int, B: int) -> float:
-    """Expected distinct experts under uniform routing, E (1 - (1 - k/E)**B) (sol.py:42-43)."""
-    return E*(1.0 - (1.0 - k/E)**B)
-
-
-def mxfp4_bytes(rows: int, cols: int) -> int:
-    """Packed MXFP4 bytes of a rows x cols matrix, r c / 2 + r c / 32 (sol.py:23-24)."""
-    return rows*cols//2 + rows*cols//32
-
-
-def algorithmic_bytes(*, B: int, E: int, k: int, h: int, I: int, distinct: int, K: int | None = None) -> int:
-    """Bytes the MoE step must move at least once.
-
-    router E h 2 + bias E 4 + tokens B h 2 + distinct experts x (gate + up + down
-    MXFP4) + expert_sum B K 4 + ids and weights B k (8 + 4). K is the expert
-    width (h unless a separate latent input is used).
-    """
-    K = h if K is None else K
-    return (E*h*2 + E*4 + B*h*2 + distinct*(2*mxfp4_bytes(I, K) + mxfp4_bytes(K, I))
-            + B*K*4 + B*k*(8 + 4))
-
-
-def algorithmic_flops(*, B: int, E: int, k: int, h: int, I: int, K: int | None = None) -> int:
-    """2 B E h (router) + 2 B k 3 I K (gate, up, down)."""
-    K = h if K is None else K
-    return 2*B*E*h + 2*B*k*3*I*K
-
-
 def rel_l2(a, b) -> float:
     """||a - b|| / ||b|| in float64 (the band's distance, kimi.py:420-424)."""
     a = torch.as_tensor(a).double()

@@ -26,14 +26,27 @@ def to_dev(inputs, dev):
     return {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in inputs.items()}
 
 
-def run_and_check(cfg, inputs, dev, *, routes=None, rows=None, check_close_to_oracle=True):
+def decode_ok(cfg):
+    return cfg.tokens <= 64 and cfg.tokens*cfg.topk <= 1024
+
+
+def run_and_check(cfg, inputs, dev, *, routes=None, rows=None, check_close_to_oracle=True, path='auto'):
     """GPU step vs oracle on `inputs` (CPU tensors). rows: optional subset of token rows for the oracle."""
     kw = dict(topk=cfg.topk, gating=cfg.gating, activation=cfg.activation)
     g = to_dev(inputs, dev)
     before = grading.snapshot({k: v for k, v in g.items() if v is not None})
+    ws = k3moe.new_workspace(1 << 20, dev) if path != 'auto' else None
+    if ws is not None:
+        from k3moe.moe import dims_for, workspace_bytes
+        need = workspace_bytes(dims_for(g['x'], g['router'], g['gate_blocks'], g['down_blocks'], cfg.topk,
+                                        cfg.gating, cfg.activation, g.get('latent'), path))
+        if need > ws.numel():
+            ws = k3moe.new_workspace(need, dev)
     got = k3moe.moe_step(*synthetic.step_args(g), **kw, routes=None if routes is None else routes.to(dev),
-                         latent=g.get('latent'))
+                         latent=g.get('latent'), path=path, workspace=ws)
     torch.cuda.synchronize(dev)
+    if ws is not None:
+        assert k3moe.workspace_status(ws) == 0
     grading.check_unchanged({k: v for k, v in g.items() if v is not None}, before)
     got = {k: v.cpu() for k, v in got.items()}
     ref_in = dict(inputs)
@@ -113,9 +126,12 @@ TINY = [
 
 @pytest.mark.parametrize('cfg', TINY, ids=lambda c: c.name)
 @pytest.mark.parametrize('seed', [0, 1])
-def test_moe_small_geometries(gpu, cfg, seed):
-    say(f'case: {cfg.name} seed={seed}')
-    run_and_check(cfg, synthetic.moe_layer_inputs(cfg, seed, scale_mode='kimi'), gpu)
+@pytest.mark.parametrize('path', ['general', 'decode'])
+def test_moe_small_geometries(gpu, cfg, seed, path):
+    if path == 'decode' and not decode_ok(cfg):
+        pytest.skip('shape is outside the persistent decode path')
+    say(f'case: {cfg.name} seed={seed} path={path}')
+    run_and_check(cfg, synthetic.moe_layer_inputs(cfg, seed, scale_mode='kimi'), gpu, path=path)
 
 
 @pytest.mark.parametrize('seed', [0, 1, 2])
@@ -126,16 +142,34 @@ def test_moe_cpu_plumbing(gpu, seed):
 
 
 @pytest.mark.parametrize('cfg', [configs.TP8_B1, configs.TP8_B8], ids=lambda c: c.name)
-def test_moe_tp8_rank(gpu, cfg):
-    say(f'case: {cfg.name} seed=0')
-    run_and_check(cfg, synthetic.moe_layer_inputs(cfg, 0), gpu)
+@pytest.mark.parametrize('path', ['general', 'decode'])
+def test_moe_tp8_rank(gpu, cfg, path):
+    say(f'case: {cfg.name} seed=0 path={path}')
+    run_and_check(cfg, synthetic.moe_layer_inputs(cfg, 0), gpu, path=path)
 
 
-def test_moe_tp8_b64_sampled_rows(gpu):
+def test_paths_agree_tp8_b8(gpu):
+    cfg = configs.TP8_B8
+    say(f'case: {cfg.name} seed=3, general vs persistent decode path')
+    g = to_dev(synthetic.moe_layer_inputs(cfg, 3), gpu)
+    outs = {}
+    for path in ('general', 'decode'):
+        ws = k3moe.new_workspace(64 << 20, gpu)
+        outs[path] = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, path=path, workspace=ws)
+        torch.cuda.synchronize(gpu)
+        assert k3moe.workspace_status(ws) == 0
+    a, b = outs['general'], outs['decode']
+    assert torch.equal(a['expert_ids'], b['expert_ids'])
+    assert (a['route_weights'] - b['route_weights']).abs().max().item() <= 2e-7
+    assert moe_ref.rel_l2(b['expert_sum'].cpu(), a['expert_sum'].cpu()) < 5e-3
+
+
+@pytest.mark.parametrize('path', ['general', 'decode'])
+def test_moe_tp8_b64_sampled_rows(gpu, path):
     cfg = configs.TP8_B64
-    say(f'case: {cfg.name} seed=1 (oracle on 8 sampled rows)')
+    say(f'case: {cfg.name} seed=1 path={path} (oracle on 8 sampled rows)')
     rows = torch.tensor([0, 5, 17, 31, 32, 47, 58, 63])
-    run_and_check(cfg, synthetic.moe_layer_inputs(cfg, 1), gpu, rows=rows)
+    run_and_check(cfg, synthetic.moe_layer_inputs(cfg, 1), gpu, rows=rows, path=path)
 
 
 def test_moe_latent_input(gpu):

@@ -39,21 +39,21 @@ def test_workspace_bytes_for_every_config(name):
     c = CONFIGS[name]
     d = _native.Dims(tokens=c.tokens, experts=c.experts, topk=c.topk, hidden=c.hidden, latent=c.width,
                      inter=c.inter, gating=_native.GATING[c.gating], activation=_native.ACTIVATION[c.activation],
-                     x_dtype=0, reserved=0)
+                     x_dtype=0, path=0)
     n = moe.workspace_bytes(d)
     assert n > 0 and n % 256 == 0
-    # the expert intermediates alone need at least B k (I + K) bf16 values
-    assert n >= c.tokens * c.topk * (c.inter + c.width) * 2
+    # the activated intermediates alone need B k I bf16 values
+    assert n >= c.tokens * c.topk * c.inter * 2
 
 
 @pytest.mark.parametrize('field,value,msg', [
     ('experts', 0, 'experts'), ('experts', 2000, 'experts'), ('topk', 0, 'topk'), ('topk', 33, 'topk'),
     ('hidden', 100, 'hidden'), ('latent', 48, 'latent'), ('inter', 40, 'inter'), ('gating', 7, 'gating'),
-    ('activation', 9, 'activation'), ('x_dtype', 1, 'x_dtype'), ('reserved', 1, 'reserved'),
+    ('activation', 9, 'activation'), ('x_dtype', 1, 'x_dtype'), ('path', 7, 'path'),
     ('tokens', 0, 'tokens')])
 def test_invalid_dims_are_rejected_with_a_message(field, value, msg):
     d = _native.Dims(tokens=2, experts=16, topk=4, hidden=64, latent=64, inter=64, gating=0, activation=0,
-                     x_dtype=0, reserved=0)
+                     x_dtype=0, path=0)
     setattr(d, field, value)
     with pytest.raises(ValueError, match=msg):
         moe.workspace_bytes(d)
