@@ -105,10 +105,12 @@ int launch_check(const char *what) {
 int allow_lds(int bytes) {
   static int granted = 0;
   if (bytes <= 65536 || bytes <= granted) return K3MOE_OK;
+  // dynamic + static LDS must fit the 160 KiB of a workgroup
+  const int limit = kDecMaxLds - kDecStaticLds;
   if (hipFuncSetAttribute(reinterpret_cast<const void *>(&k_moe_decode), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          kDecMaxLds) != hipSuccess)
+                          limit) != hipSuccess)
     return fail(K3MOE_EHIP, "setting the decode kernel's LDS limit failed: %s", hipGetErrorString(hipGetLastError()));
-  granted = kDecMaxLds;
+  granted = limit;
   return K3MOE_OK;
 }
 

@@ -32,7 +32,6 @@
 namespace k3moe {
 
 constexpr unsigned kSpinLimit = 1u << 21;  // bounded barrier wait (about 0.1-1 s)
-constexpr int kGuDepth = 8;                // gate/up k-steps loaded per batch per wave
 constexpr int kDnDepth = 2;                // down k-steps per pipelined item
 constexpr int kDnExpertMajorMin = 32;      // more active experts: expert-major down + combine
 
@@ -117,120 +116,79 @@ __device__ __forceinline__ float red_sum(const float *red, int idx) {
 __device__ __forceinline__ int tile_index(int row, int col) { return (col + 16 * (row >> 2)) * 4 + (row & 3); }
 
 
-// ------------------------------------------------------ gate/up streaming --
-// A wave streams W units (8 gate + 8 up rows each, one MFMA tile per unit) of
-// one expert over a range of super-steps. A super-step is 16 MXFP4 blocks (512
-// k) of every row; in it lane group q owns the 4 consecutive blocks 4q..4q+3,
-// one per k-step t (any k permutation shared by A and B gives the same dot
-// products), so its 4 E8M0 scales are one aligned dword. Per k-step a lane
-// loads 16 bytes of each unit's A row and 64 bytes of its token's activations,
-// shared by the W units; loads come in batches of two k-steps, two batches in
-// flight. Every pointer is a per-lane row base fixed for the whole stream:
-// absent units read the workspace's zero area, inactive token lanes use a
-// buffer offset past the activations (a zero load that touches no memory).
-constexpr int kGuW = 4;  // units per stream, many-unit path
-
+// ---------------------------------------------------------------- gate/up --
+// A unit is 8 gate + 8 up rows of one (active expert, chunk of up to NX
+// tokens): one 16x16 MFMA tile. Units form groups of W (W = 2 when the grid
+// has at least two units per workgroup, else 1), ordered expert-major, chunk,
+// unit. Workgroup b takes groups [NG b / G, NG (b + 1) / G) in rounds; a round
+// is a run of whole chunks whose token rows fit the LDS staging area (NX
+// rows), copied there once, so the MFMA B operand comes from LDS. Inside a
+// round the (group, super-step) pairs -- a super-step is 16 MXFP4 blocks, 512
+// k -- are cut into 8 equal contiguous ranges, one per wave: a wave streams its
+// range with the next super-step's loads in flight, finishes every group it
+// covers whole and leaves partial tiles of the groups cut by its range ends in
+// LDS; after a barrier, the wave holding a cut group's first part adds the
+// other parts in ascending k order and finishes it.
+// Lane (i, q) covers row i of a tile and, at k-step t of super-step ss, block
+// 16 ss + 4 t + q: a load instruction reads 64 contiguous bytes of 16 rows,
+// and the lane's 4 scales of a super-step are byte q of the dwords of one
+// 16-byte load (K a multiple of 512; otherwise per-lane byte loads).
 template <int W>
-struct GuCtx {
-  const uint8_t *wrow[W];   // this lane's A row + 64 q bytes, per unit
-  const uint8_t *srow[W];   // this lane's scale row + 4 q bytes, per unit
-  __amdgpu_buffer_rsrc_t xr;  // activations [B, K] bf16
-  uint32_t xoff;            // this lane's row + 128 q elements, in bytes (kOffNone: inactive lane)
+struct GuSS {
+  u32x4 a[W][4];  // per unit, k-steps t = 0..3
+  u32x4 s[W];     // per unit, dword t holds the scale of this lane's block in byte q
 };
 
-// one k-step of A (per unit) and B
-template <int W>
-struct GuStep {
-  u32x4 a[W];
-  u32x4 b[4];
+struct GuChunk {  // one chunk of the current round (LDS)
+  int e;          // expert id
+  int pbase;      // pair index of the chunk's first token
+  int n;          // tokens in the chunk
+  int xrow;       // first staged row
 };
 
-template <int W>
-__device__ __forceinline__ void gu_issue(GuStep<W> &st, const GuCtx<W> &cx, int ss, int t) {
-#pragma unroll
-  for (int u = 0; u < W; ++u) st.a[u] = load16(cx.wrow[u] + ss * 256 + t * 16);
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) st.b[kk] = bload16(cx.xr, cx.xoff + ss * 1024 + t * 64 + kk * 16);
-}
-
-template <int W>
-__device__ __forceinline__ void gu_scales(uint32_t (&sv)[W], const GuCtx<W> &cx, int ss) {
-#pragma unroll
-  for (int u = 0; u < W; ++u) sv[u] = *reinterpret_cast<const uint32_t *>(cx.srow[u] + ss * 16);
-}
-
-template <int W>
-__device__ __forceinline__ void gu_compute(const GuStep<W> &st, const uint32_t (&sv)[W], int t, f32x4 *acc) {
+template <int W, bool AL>
+__device__ __forceinline__ void gu_issue(GuSS<W> &B, const uint8_t *const (&wr)[W], const uint8_t *const (&sr)[W],
+                                         int ss, int KB) {
+  const int q = (threadIdx.x & 63) >> 4;
 #pragma unroll
   for (int u = 0; u < W; ++u) {
-    bf16x8 av[4];
-    convert_block_fast(st.a[u], (sv[u] >> (8 * t)) & 0xFFu, av);
+    if (AL) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) acc[u] = mfma16(av[kk], as_bf16x8(st.b[kk]), acc[u]);
-  }
-}
-
-// acc[u] += the unit tiles over super-steps [ss0, ss1): one k-step per
-// buffer, two buffers in flight, the super-step's scales loaded once.
-template <int W>
-__device__ __forceinline__ void gu_stream(const GuCtx<W> &cx, int ss0, int ss1, f32x4 *acc) {
-  if (ss0 >= ss1) return;
-  GuStep<W> b0, b1;
-  uint32_t sc[W], sn[W];
-  gu_scales(sc, cx, ss0);
-  gu_issue(b0, cx, ss0, 0);
-  for (int ss = ss0; ss < ss1; ++ss) {
-    gu_issue(b1, cx, ss, 1);
-    gu_compute(b0, sc, 0, acc);
-    gu_issue(b0, cx, ss, 2);
-    gu_compute(b1, sc, 1, acc);
-    gu_issue(b1, cx, ss, 3);
-    gu_compute(b0, sc, 2, acc);
-    const bool more = ss + 1 < ss1;
-    if (more) {
-      gu_scales(sn, cx, ss + 1);
-      gu_issue(b0, cx, ss + 1, 0);
-    }
-    gu_compute(b1, sc, 3, acc);
-    if (more) {
+      for (int t = 0; t < 4; ++t) B.a[u][t] = load16(wr[u] + (16 * ss + 4 * t + q) * 16);
+      B.s[u] = load16(sr[u] + 16 * ss);
+    } else {
 #pragma unroll
-      for (int u = 0; u < W; ++u) sc[u] = sn[u];
+      for (int t = 0; t < 4; ++t) {
+        const int kb = 16 * ss + 4 * t + q;
+        const bool ok = kb < KB;
+        B.a[u][t] = ok ? load16(wr[u] + kb * 16) : u32x4{0, 0, 0, 0};
+        B.s[u][t] = ok ? (uint32_t)sr[u][kb] << (8 * q) : 0u;
+      }
     }
   }
 }
 
-// Blocks past the last full super-step (K not a multiple of 512), one block
-// per lane group and k-step as blocks 16 nss + 4 kt + q, with per-lane checks.
-template <int W>
-__device__ __forceinline__ void gu_tail(const GuCtx<W> &cx, int nss, int KB, const uint8_t *zero, f32x4 *acc) {
+// acc[u] += tile u over super-step ss; xrow: this lane's staged token row (LDS)
+template <int W, bool AL>
+__device__ __forceinline__ void gu_compute(const GuSS<W> &B, const uint16_t *xrow, int ss, int KB, f32x4 (&acc)[W]) {
   const int q = (threadIdx.x & 63) >> 4;
-  for (int kt = 0; 16 * nss + 4 * kt < KB; ++kt) {
-    const int kb = 16 * nss + 4 * kt + q;  // absolute block of this lane
-    const bool ok = kb < KB;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (!AL && 16 * ss + 4 * t >= KB) break;  // wave-uniform: nothing left in this super-step
+    const int kb = 16 * ss + 4 * t + q;
+    const bool ok = AL || kb < KB;
+    u32x4 b[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      b[kk] = ok ? *reinterpret_cast<const u32x4 *>(xrow + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int u = 0; u < W; ++u) {
-      // wrow/srow carry the super-step lane offset (64 q / 4 q): undo it
-      const u32x4 wv = load16(ok ? cx.wrow[u] - 64 * q + kb * 16 : zero);
-      const uint32_t sv = ok ? cx.srow[u][kb - 4 * q] : 0u;
-      u32x4 bv[4];
-      const uint32_t xo = ok ? cx.xoff - 256 * q + kb * 64 : kOffNone;
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) bv[kk] = bload16(cx.xr, xo + kk * 16);
       bf16x8 av[4];
-      convert_block_fast(wv, sv, av);
+      convert_block_fast(B.a[u][t], (B.s[u][t] >> (8 * q)) & 0xFFu, av);
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) acc[u] = mfma16(av[kk], as_bf16x8(bv[kk]), acc[u]);
+      for (int kk = 0; kk < 4; ++kk) acc[u] = mfma16(av[kk], as_bf16x8(b[kk]), acc[u]);
     }
   }
-}
-
-// Unit (expert e, rows r8*8 ..) A row pointers of this lane: rows 0-7 of the
-// tile are gate rows, rows 8-15 the same up rows.
-__device__ __forceinline__ void gu_rows(const Plan &pl, const DecodeArgs &a, int e, int r8, int i, int q, int KB,
-                                        const uint8_t *&wrow, const uint8_t *&srow) {
-  const size_t row = (size_t)e * pl.I + r8 * 8 + (i & 7);
-  wrow = (i >= 8 ? a.ublk : a.gblk) + row * KB * 16 + q * 64;
-  srow = (i >= 8 ? a.uscl : a.gscl) + row * KB + q * 4;
 }
 
 // Activation epilogue of a full-K unit tile held by one wave: lanes 0-31 hold
@@ -248,6 +206,177 @@ __device__ __forceinline__ void gu_finish_wave(const Plan &pl, uint16_t *hbuf, c
     for (int v = 0; v < 4; ++v) hb[v] = f32_to_bf16_bits(apply_act(pl.act, round_bf16(acc[v]), round_bf16(up[v])));
     u32x2 packed = {(uint32_t)hb[0] | ((uint32_t)hb[1] << 16), (uint32_t)hb[2] | ((uint32_t)hb[3] << 16)};
     *reinterpret_cast<u32x2 *>(hbuf + (size_t)p * pl.I + row0 + 4 * (l >> 4)) = packed;
+  }
+}
+
+// The gate/up phase of one workgroup (see the comment above GuSS).
+template <int W, bool AL>
+__device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, float *red, const int *g_act,
+                                      const int *g_aoff, const int *g_acnt, const int *g_coff, const int *g_ptok,
+                                      uint16_t *xs, GuChunk *tab, int *s_round, int *s_rowtok, int D, uint16_t *hbuf) {
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i = l & 15;
+  const int KB = pl.K / kBlockK, NSS = (KB + 15) / 16, K8 = pl.K / 8;
+  const int GPC = pl.U8 / W;  // groups per chunk
+  const int NG = g_coff[D] * GPC;
+  const int ga = (int)((long)NG * blockIdx.x / gridDim.x), gb = (int)((long)NG * (blockIdx.x + 1) / gridDim.x);
+  auto slot = [&](int wv, int which, int u) { return red + ((wv * 2 + which) * 2 + u) * 256 + l * 4; };
+  for (int g0 = ga; g0 < gb;) {
+    const int ci0 = g0 / GPC;
+    __syncthreads();  // the previous round is done with the table, the staged rows and the partial tiles
+    if (w == 0) {
+      // lane j < 16 takes chunk ci0 + j; the round is the prefix of chunks whose rows fit
+      const int ci = ci0 + l;
+      const bool in = l < 16 && ci * GPC < gb;
+      int n = 0, e = 0, pbase = 0;
+      if (in) {
+        int lo = 0, hi = D - 1;  // active expert of chunk ci: largest lo with g_coff[lo] <= ci
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (g_coff[mid] <= ci) lo = mid; else hi = mid - 1;
+        }
+        const int c = ci - g_coff[lo];
+        e = g_act[lo];
+        pbase = g_aoff[lo] + c * pl.NX;
+        n = min(pl.NX, g_acnt[lo] - c * pl.NX);
+      }
+      int pre = n;  // inclusive prefix of the token counts
+#pragma unroll
+      for (int dd = 1; dd < 16; dd <<= 1) {
+        const int o = __shfl_up(pre, dd, 64);
+        if (l >= dd) pre += o;
+      }
+      const bool fits = in && pre <= pl.NX;
+      const int nch = __popcll(__ballot(fits));  // >= 1: one chunk never exceeds NX rows
+      const int rows = __shfl(pre, nch - 1, 64);
+      if (fits) tab[l] = GuChunk{e, pbase, n, pre - n};
+      wave_lds_order();
+      if (l < rows) {  // staged row l: token of its chunk
+        int j = 0;
+        while (j + 1 < nch && tab[j + 1].xrow <= l) ++j;
+        s_rowtok[l] = g_ptok[tab[j].pbase + l - tab[j].xrow];
+      }
+      if (l == 0) {
+        s_round[0] = nch;
+        s_round[1] = rows;
+      }
+    }
+    __syncthreads();
+    const int nch = s_round[0], rows = s_round[1];
+    const int g1 = min(gb, (ci0 + nch) * GPC);
+    const int work = (g1 - g0) * NSS;
+    const int s = (int)((long)work * w / kDecWaves), e = (int)((long)work * (w + 1) / kDecWaves);
+    // unit rows of group gg of the round (relative to g0)
+    auto rows_of = [&](int gg, const uint8_t *(&wr)[W], const uint8_t *(&sr)[W]) {
+      const int G = g0 + gg, j = G / GPC - ci0, pg = G % GPC;
+      const int ex = tab[j].e;
+#pragma unroll
+      for (int u = 0; u < W; ++u) {
+        const size_t row = (size_t)ex * pl.I + (pg * W + u) * 8 + (i & 7);
+        wr[u] = (i >= 8 ? a.ublk : a.gblk) + row * KB * 16;
+        sr[u] = (i >= 8 ? a.uscl : a.gscl) + row * KB;
+      }
+    };
+    auto xrow_of = [&](int gg) {
+      const GuChunk ch = tab[(g0 + gg) / GPC - ci0];
+      return (const uint16_t *)(xs + (size_t)(ch.xrow + min(i, ch.n - 1)) * pl.xpitch);
+    };
+    auto finish = [&](int gg, const f32x4 (&acc)[W]) {
+      const int G = g0 + gg, pg = G % GPC;
+      const GuChunk ch = tab[G / GPC - ci0];
+#pragma unroll
+      for (int u = 0; u < W; ++u) gu_finish_wave(pl, hbuf, acc[u], ch.pbase + i, i < ch.n, (pg * W + u) * 8);
+    };
+    GuSS<W> B0, B1;
+    const uint8_t *iwr[W], *isr[W];
+    int ig = s / NSS, iss = s % NSS;  // issue cursor
+    if (s < e) {
+      rows_of(ig, iwr, isr);
+      gu_issue<W, AL>(B0, iwr, isr, iss, KB);
+    }
+    // stage the round's activation rows (four rows per pass, every load in flight)
+    for (int r0 = 0; r0 < rows; r0 += 4) {
+      for (int c0 = 0; c0 < K8; c0 += 2 * kDecThreads) {
+        u32x4 v[4][2];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int c = c0 + hh * kDecThreads + tid;
+            const bool ok = r0 + rr < rows && c < K8;
+            v[rr][hh] = ok ? load16(a.xin + (size_t)s_rowtok[r0 + rr] * pl.K + c * 8) : u32x4{0, 0, 0, 0};
+          }
+        }
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int c = c0 + hh * kDecThreads + tid;
+            if (r0 + rr < rows && c < K8) *reinterpret_cast<u32x4 *>(xs + (size_t)(r0 + rr) * pl.xpitch + c * 8) = v[rr][hh];
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (s < e) {
+      int cg = ig, css = iss;  // compute cursor
+      const uint16_t *xrow = xrow_of(cg);
+      f32x4 acc[W];
+#pragma unroll
+      for (int u = 0; u < W; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      auto step = [&](GuSS<W> &cur, GuSS<W> &nxt, int pos) {
+        if (pos + 1 < e) {
+          if (++iss == NSS) {
+            iss = 0;
+            rows_of(++ig, iwr, isr);
+          }
+          gu_issue<W, AL>(nxt, iwr, isr, iss, KB);
+        }
+        gu_compute<W, AL>(cur, xrow, css, KB, acc);
+        if (++css == NSS || pos + 1 == e) {
+          const bool started_here = cg * NSS >= s;
+          if (started_here && css == NSS) {
+            finish(cg, acc);
+          } else {
+#pragma unroll
+            for (int u = 0; u < W; ++u) *reinterpret_cast<f32x4 *>(slot(w, started_here ? 1 : 0, u)) = acc[u];
+          }
+#pragma unroll
+          for (int u = 0; u < W; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (css == NSS && pos + 1 < e) {
+            css = 0;
+            xrow = xrow_of(++cg);
+          }
+        }
+      };
+      for (int pos = s; pos < e; pos += 2) {
+        step(B0, B1, pos);
+        if (pos + 1 < e) step(B1, B0, pos + 1);
+      }
+    }
+    __syncthreads();
+    // a group cut by wave ranges: the wave holding its first part adds the rest in wave (= k) order
+    if (s < e) {
+      const int gl = (e - 1) / NSS;
+      if (gl * NSS >= s && e < (gl + 1) * NSS) {
+        f32x4 sum[W];
+#pragma unroll
+        for (int u = 0; u < W; ++u) sum[u] = *reinterpret_cast<const f32x4 *>(slot(w, 1, u));
+        for (int w2 = w + 1; w2 < kDecWaves; ++w2) {
+          const int s2 = (int)((long)work * w2 / kDecWaves), e2 = (int)((long)work * (w2 + 1) / kDecWaves);
+          if (s2 >= (gl + 1) * NSS) break;
+          if (e2 > s2) {
+#pragma unroll
+            for (int u = 0; u < W; ++u) {
+              const f32x4 v = *reinterpret_cast<const f32x4 *>(slot(w2, 0, u));
+#pragma unroll
+              for (int vv = 0; vv < 4; ++vv) sum[u][vv] += v[vv];
+            }
+          }
+        }
+        finish(gl, sum);
+      }
+    }
+    g0 = g1;
   }
 }
 
@@ -338,11 +467,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
   int *g_act = reinterpret_cast<int *>(lds + pl.lds_red);
   int *g_aoff = g_act + pl.Dmax;
   int *g_acnt = g_aoff + pl.Dmax;
-  int *g_ptok = g_acnt + pl.Dmax;
+  int *g_coff = g_acnt + pl.Dmax;  // [Dmax + 1] gate/up chunks (NX tokens) before each active expert
+  int *g_ptok = g_coff + pl.Dmax + 1;
   float *g_pw = reinterpret_cast<float *>(g_ptok + pl.P);
   int *g_pof = reinterpret_cast<int *>(g_pw + pl.P);  // pair index of (token, slot)
   char *scr = lds + pl.lds_red + pl.lds_grp;
   __shared__ int s_nact;
+  __shared__ GuChunk s_tab[16];
+  __shared__ int s_round[2], s_rowtok[16];
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int i = l & 15, q = l >> 4;
@@ -543,23 +675,25 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
     __syncthreads();
     if (w == 0) {
       // lane l owns experts [16 l, 16 l + 16): local sums, then a wave scan
-      int tot = 0, nac = 0;
+      int tot = 0, nac = 0, nch = 0;
       for (int j = 0; j < 16; ++j) {
         const int e = 16 * l + j;
         const int c = e < E ? cnt[e] : 0;
         tot += c;
         nac += c > 0;
+        nch += (c + pl.NX - 1) / pl.NX;
       }
-      int it = tot, ia = nac;
+      int it = tot, ia = nac, ic = nch;
 #pragma unroll
       for (int d = 1; d < 64; d <<= 1) {
-        const int ot = __shfl_up(it, d, 64), oa = __shfl_up(ia, d, 64);
+        const int ot = __shfl_up(it, d, 64), oa = __shfl_up(ia, d, 64), oc = __shfl_up(ic, d, 64);
         if (l >= d) {
           it += ot;
           ia += oa;
+          ic += oc;
         }
       }
-      int base = it - tot, abase = ia - nac;
+      int base = it - tot, abase = ia - nac, cbase = ic - nch;
       for (int j = 0; j < 16; ++j) {
         const int e = 16 * l + j;
         if (e >= E) break;
@@ -569,11 +703,16 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
           g_act[abase] = e;
           g_aoff[abase] = base;
           g_acnt[abase] = c;
+          g_coff[abase] = cbase;
           ++abase;
+          cbase += (c + pl.NX - 1) / pl.NX;
         }
         base += c;
       }
-      if (l == 63) s_nact = ia;
+      if (l == 63) {
+        s_nact = ia;
+        g_coff[ia] = ic;
+      }
     }
     __syncthreads();
     for (int p = tid; p < pl.P; p += kDecThreads) {
@@ -592,98 +731,15 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
 
   // ------------------------------------------------------------ GU: gate/up --
   {
-    const int KB = pl.K / kBlockK;
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.xin, (uint32_t)B * pl.K * 2);
-    const int NU = D * pl.U8;  // units (expert, 8 gate + 8 up rows), expert-major
-    const int GW = gridDim.x * kDecWaves;
-    const int gw = blockIdx.x * kDecWaves + w;
-    if (NU <= GW) {
-      // few units: KS waves split each unit's K and meet in LDS
-      int KS = 1;
-      while (KS < kDecWaves && NU * KS * 2 <= GW) KS *= 2;
-      const int upw = kDecWaves / KS;  // units per workgroup
-      const int u = gw / KS, sl = gw % KS;
-      const int nss = KB % 4 ? 0 : KB / 16;  // full super-steps (aligned scale dwords need K % 128 == 0)
-      const int ss0 = nss * sl / KS, ss1 = nss * (sl + 1) / KS;
-      const bool tail = sl == KS - 1 && 16 * nss < KB;
-      // token chunks: the largest expert count among this workgroup's units
-      int nmax = 0;
-      for (int j = 0; j < upw; ++j) {
-        const int uu = blockIdx.x * upw + j;
-        if (uu < NU) nmax = max(nmax, g_acnt[uu / pl.U8]);
-      }
-      const bool live = u < NU;
-      const int d = live ? u / pl.U8 : 0, r8 = live ? u % pl.U8 : 0;
-      const int e = g_act[d], p0 = g_aoff[d], n = live ? g_acnt[d] : 0;
-      GuCtx<1> cx;
-      gu_rows(pl, a, e, r8, i, q, KB, cx.wrow[0], cx.srow[0]);
-      cx.xr = xrs;
-      for (int c = 0; c * 16 < nmax; ++c) {
-        const int pj = c * 16 + i;
-        const bool tok_ok = live && pj < n;
-        cx.xoff = tok_ok ? ((uint32_t)g_ptok[p0 + pj] * pl.K + q * 128) * 2 : kOffNone;
-        f32x4 acc[1] = {{0.f, 0.f, 0.f, 0.f}};
-        if (live) {
-          gu_stream<1>(cx, ss0, ss1, acc);
-          if (tail) gu_tail<1>(cx, nss, KB, zero, acc);
-        }
-        if (KS == 1) {
-          if (live) gu_finish_wave(pl, hbuf, acc[0], p0 + pj, tok_ok, r8 * 8);
-        } else {
-          *reinterpret_cast<f32x4 *>(red + w * 256 + l * 4) = acc[0];
-          __syncthreads();
-          for (int t = tid; t < upw * 128; t += kDecThreads) {
-            const int ul = t >> 7, r = (t >> 4) & 7, j = t & 15;
-            const int uu = blockIdx.x * upw + ul;
-            if (uu >= NU) continue;
-            const int dd = uu / pl.U8, nn = g_acnt[dd];
-            if (c * 16 + j >= nn) continue;
-            float g = 0.f, uv = 0.f;
-            for (int sp = 0; sp < KS; ++sp) {
-              g += red[(ul * KS + sp) * 256 + tile_index(r, j)];
-              uv += red[(ul * KS + sp) * 256 + tile_index(r + 8, j)];
-            }
-            const float hv = apply_act(pl.act, round_bf16(g), round_bf16(uv));
-            hbuf[(size_t)(g_aoff[dd] + c * 16 + j) * pl.I + (uu % pl.U8) * 8 + r] = f32_to_bf16_bits(hv);
-          }
-          __syncthreads();
-        }
-      }
+    uint16_t *xs = reinterpret_cast<uint16_t *>(scr);  // staged activation rows (the scratch is free now)
+    const bool two = g_coff[D] * pl.U8 >= 2 * (int)gridDim.x;
+    const bool al = (pl.K / kBlockK) % 16 == 0;
+    if (two) {
+      if (al) gu_phase<2, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, D, hbuf);
+      else gu_phase<2, false>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, D, hbuf);
     } else {
-      // many units: each wave streams a contiguous run over full K, up to kGuW
-      // same-expert units at a time sharing the activation loads
-      const int ua = (int)((long)NU * gw / GW), ub = (int)((long)NU * (gw + 1) / GW);
-      const int nss = KB % 4 ? 0 : KB / 16;
-      for (int u = ua; u < ub;) {
-        const int d = u / pl.U8;
-        int cnt = min(kGuW, ub - u);
-        cnt = min(cnt, (d + 1) * pl.U8 - u);
-        const int e = g_act[d], p0 = g_aoff[d], n = g_acnt[d];
-        GuCtx<kGuW> cx;
-#pragma unroll
-        for (int j = 0; j < kGuW; ++j) {
-          gu_rows(pl, a, e, (u + min(j, cnt - 1)) % pl.U8, i, q, KB, cx.wrow[j], cx.srow[j]);
-          if (j >= cnt) {  // absent unit: zero rows (the lane offsets stay inside the zero area)
-            cx.wrow[j] = zero + q * 64;
-            cx.srow[j] = zero + q * 4;
-          }
-        }
-        cx.xr = xrs;
-        for (int c = 0; c * 16 < n; ++c) {
-          const int pj = c * 16 + i;
-          const bool tok_ok = pj < n;
-          cx.xoff = tok_ok ? ((uint32_t)g_ptok[p0 + pj] * pl.K + q * 128) * 2 : kOffNone;
-          f32x4 acc[kGuW];
-#pragma unroll
-          for (int j = 0; j < kGuW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-          gu_stream<kGuW>(cx, 0, nss, acc);
-          if (16 * nss < KB) gu_tail<kGuW>(cx, nss, KB, zero, acc);
-#pragma unroll
-          for (int j = 0; j < kGuW; ++j)
-            if (j < cnt) gu_finish_wave(pl, hbuf, acc[j], p0 + pj, tok_ok, ((u + j) % pl.U8) * 8);
-        }
-        u += cnt;
-      }
+      if (al) gu_phase<1, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, D, hbuf);
+      else gu_phase<1, false>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, D, hbuf);
     }
   }
   trace_mark(pl, a.ws, 6);

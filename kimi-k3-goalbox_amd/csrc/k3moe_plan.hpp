@@ -28,6 +28,7 @@ constexpr int kDecMaxTokens = 64;
 constexpr int kDecMaxPairs = 1024;
 constexpr int kDecMaxSplits = 8;   // router k-splits across workgroups
 constexpr int kDecMaxLds = 160 * 1024;   // gfx950: 160 KiB of LDS per workgroup
+constexpr int kDecStaticLds = 1024;  // decode kernel's static LDS (round table, counters), upper bound
 
 constexpr int kRedundantTokens = 16;   // decode: route every token in every workgroup up to this batch
 constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert) keys
@@ -63,6 +64,8 @@ struct Plan {
   int Srw;  // router k-splits across workgroups
   int U8;   // gate/up units per expert: 8 gate + 8 up rows each
   int lds_red, lds_grp, lds_scr, lds_total;  // dynamic LDS layout, bytes
+  int NX;      // gate/up: activation rows staged in LDS per round (also the chunk size in tokens)
+  int xpitch;  // staged row pitch in elements (K + 8: rows start in different banks)
   int trace;      // 1: the decode kernel records phase timestamps at o_trace
   int redundant;  // 1: every workgroup routes every token (no barrier before grouping)
   // workspace byte offsets
@@ -77,8 +80,8 @@ inline int align16(int v) { return (v + 15) & ~15; }
 
 // Decode-path LDS layout for plan p; returns the total bytes.
 inline int decode_lds(Plan &p) {
-  p.lds_red = kDecWaves * 256 * 4;                                  // per-wave 16x16 fp32 tiles
-  p.lds_grp = align16(4 * (3 * p.Dmax + 3 * p.P));                  // active list + pairs + pair index
+  p.lds_red = kDecWaves * 2 * 2 * 256 * 4;                          // per wave 2 x 2 16x16 fp32 tiles
+  p.lds_grp = align16(4 * (4 * p.Dmax + 1 + 3 * p.P));              // active list + chunk offsets + pairs
   p.redundant = p.B * p.E <= kRedundantKeys && p.B <= kRedundantTokens;
   const int nt = p.redundant ? p.B : 1;
   const int routed = 8 * p.P;                                       // ids + weights per pair
@@ -88,7 +91,14 @@ inline int decode_lds(Plan &p) {
   int scr = topk;
   if (group > scr) scr = group;
   if (down > scr) scr = down;
+  // gate/up stages activation rows in the same scratch: as many rows as fit, at most 16
+  p.xpitch = p.K + 8;
+  const int room = kDecMaxLds - kDecStaticLds - p.lds_red - p.lds_grp;
+  p.NX = room > 0 ? room / (p.xpitch * 2) : 0;
+  if (p.NX > 16) p.NX = 16;
+  if (p.NX * p.xpitch * 2 > scr) scr = p.NX * p.xpitch * 2;
   p.lds_scr = align16(scr);
+  if (p.NX < 1) return 1 << 30;  // no decode path
   p.lds_total = p.lds_red + p.lds_grp + p.lds_scr;
   return p.lds_total;
 }
@@ -123,7 +133,8 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   if (srw_cap < 1) srw_cap = 1;
   p.Srw = srw_cap;
   p.path = kPathGeneral;
-  if (d.path != K3MOE_PATH_GENERAL && p.B <= kDecMaxTokens && p.P <= kDecMaxPairs && decode_lds(p) <= kDecMaxLds)
+  if (d.path != K3MOE_PATH_GENERAL && p.B <= kDecMaxTokens && p.P <= kDecMaxPairs &&
+      decode_lds(p) <= kDecMaxLds - kDecStaticLds)
     p.path = kPathDecode;
   p.Srw = (int)(p.G / base);
   if (p.Srw > srw_cap) p.Srw = srw_cap;
