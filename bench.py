@@ -6,12 +6,15 @@ weighted combine) over one batch of seeded synthetic inputs resident in HBM.
 Default workload: one TP8 rank's expert shard (E=384, top-8, h=7168, I=256)
 at batch 1 (the headline line), with batches 8 and 64 reported beside it.
 
-Timing: the step is captured once in a HIP graph (torch.cuda.CUDAGraph) and
-replayed. Before every timed replay a 1 GiB buffer is read (summed) so that
-L2 and the 256 MB MALL hold none of the step's weights (cold cache); a read
-leaves no dirty lines whose write-back would land inside the timed region.
-HIP events on the replay stream bracket each replay. W untimed replays come
-first.
+Timing: HIP events on the stream bracket each run of the step: by default the
+step's kernel launch on the stream with its outputs and workspace allocated
+beforehand (--launch stream), or a replay of the step captured in a HIP graph
+(--launch graph; on this stack a one-kernel graph replay adds launch latency
+of its own). Before every timed run a 1 GiB buffer is read (summed) so that L2
+and the 256 MB MALL hold none of the step's weights (cold cache); a read
+leaves no dirty lines whose write-back would land inside the timed region. W
+untimed runs come first. The graph's outputs are checked bitwise against an
+eager step either way.
 
 Roofline: algorithmic bytes of the step (router + bias + x + the distinct
 experts' MXFP4 gate/up/down + outputs, k3moe.traffic.step_bytes) over the
@@ -87,6 +90,12 @@ def read_trace(cfg, device):
     out['start_spread_us'] = round(float((raw[:, 0].max() - t0)*0.01), 2)
     if float(full[:, 9].max()) > 0:   # expert-major down: stream end, then barrier 4 and the combine
         out['down_stream_done_at_us'] = round(float((full[:, 9].max() - t0)*0.01), 2)
+    sub = full[:, 10:12]   # inside top-k: logits gathered, selection done (workgroups that routed a token)
+    ok = (sub[:, 0] >= raw[:, 2]) & (sub[:, 1] >= sub[:, 0]) & (sub[:, 1] <= raw[:, 3])
+    if bool(ok.any()):
+        out['topk_parts'] = {'logits_med_us': round(float(((sub[ok, 0] - raw[ok, 2])*0.01).median()), 2),
+                             'select_med_us': round(float(((sub[ok, 1] - sub[ok, 0])*0.01).median()), 2),
+                             'tail_med_us': round(float(((raw[ok, 3] - sub[ok, 1])*0.01).median()), 2)}
     for n in range(4):   # inside each grid barrier: release+add, spin, acquire
         if float(full[:, 13 + 4*n].max()) <= 0:
             continue
@@ -117,8 +126,13 @@ def gpu_inputs(cfg, seed, layers, device, host_gen):
     return out
 
 
-def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True):
-    """Replay a captured graph of `layers` MoE layers; returns per-replay ms and the routing stats."""
+def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, launch='stream'):
+    """Time `steps` runs of `layers` MoE layers; returns per-run ms and the routing stats.
+
+    launch 'stream': each run is the layers' kernel launches on the stream (outputs and
+    workspace preallocated); 'graph': each run replays a captured HIP graph of them. Either
+    way HIP events on the stream bracket each run, and the graph's outputs are checked
+    bitwise against an eager step."""
     import torch
     import k3moe
     from k3moe import synthetic, traffic
@@ -147,6 +161,18 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True):
             torch.sum(flush, 0, out=sink)
         graph.replay()
     torch.cuda.synchronize(device)
+    run = graph.replay
+    if launch == 'stream':
+        calls = [(synthetic.step_args(inp), dict(kw, latent=inp.get('latent'), out=o)) for (inp, _), o in zip(data, outs)]
+
+        def run():
+            for a, k_ in calls:
+                k3moe.moe_step(*a, **k_)
+        for i in range(warmup):
+            if cold:
+                torch.sum(flush, 0, out=sink)
+            run()
+        torch.cuda.synchronize(device)
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     t0 = time.perf_counter()
@@ -154,7 +180,7 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True):
         if cold:
             torch.sum(flush, 0, out=sink)
         starts[i].record()
-        graph.replay()
+        run()
         ends[i].record()
     torch.cuda.synchronize(device)
     wall = time.perf_counter() - t0
@@ -216,6 +242,8 @@ def main():
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--warm-cache', action='store_true', help='skip the L2/MALL flush before each replay')
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--launch', default='stream', choices=['stream', 'graph'],
+                    help='time stream-ordered launches (default) or HIP-graph replays')
     ap.add_argument('--trace', action='store_true', help='record per-phase timestamps of the persistent kernel '
                     '(sets K3MOE_TRACE=1; adds a few stores per phase)')
     args = ap.parse_args()
@@ -246,7 +274,7 @@ def main():
     for cfg, layers, host_gen in runs:
         log(f'bench: {cfg.name} layers={layers} steps={args.steps} warmup={args.warmup} cold={cold}')
         m = measure(cfg, seed=args.seed, steps=args.steps, warmup=args.warmup, cold=cold, device=device,
-                    layers=layers, host_gen=host_gen)
+                    layers=layers, host_gen=host_gen, launch=args.launch)
         results[cfg.name] = summarize(cfg, m, layers)
         host[cfg.name] = m['host_inputs'][0]
         log(f'bench: {cfg.name} {results[cfg.name]}')
@@ -286,7 +314,8 @@ def main():
                    'hidden': head_cfg.hidden, 'inter': head_cfg.inter, 'tokens': head_cfg.tokens,
                    'layers': head_layers, 'weights': 'mxfp4 (e2m1 + e8m0/32), dequantized to bf16 in registers',
                    'accumulate': 'fp32', 'cache': 'cold (1 GiB read before each replay)' if cold else 'warm',
-                   'timing': 'HIP events around HIP-graph replays'},
+                   'timing': 'HIP events around ' + ('stream-ordered launches' if args.launch == 'stream'
+                                                      else 'HIP-graph replays')},
         'hbm_GBps': head['hbm_GBps'],
         'hbm_frac': head['hbm_frac'],
         'per_batch': results,

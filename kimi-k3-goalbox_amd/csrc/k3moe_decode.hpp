@@ -411,11 +411,36 @@ __device__ __forceinline__ void dnc_issue(DnTileBatch &bt, const Plan &pl, const
   }
 }
 
+// y of a pair's 16-row tile goes to a per-wave LDS buffer of kDnStage
+// entries (bf16 rows + a (pair, row tile) tag) instead of memory: stores in the
+// weight stream would queue behind (and hold up) its loads. The buffer is
+// written out with 16-byte stores when full and at the end of the wave's range.
+struct DnStage {
+  uint16_t *rows;  // [kDnStage][16] bf16
+  int *tag;        // [kDnStage] pair << 16 | row tile
+  int fill;
+};
+
+__device__ __forceinline__ void dn_flush(DnStage &st, const Plan &pl, uint16_t *ybuf) {
+  const int l = threadIdx.x & 63;
+  wave_lds_order();
+  for (int c = l; c < 2 * st.fill; c += 64) {
+    const int ent = c >> 1, half = c & 1, tag = st.tag[ent];
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(st.rows + ent * 16 + half * 8);
+    *reinterpret_cast<u32x4 *>(ybuf + (size_t)(tag >> 16) * pl.K + (tag & 0xFFFF) * 16 + half * 8) = v;
+  }
+  wave_lds_order();
+  st.fill = 0;
+}
+
+// Tiles rt .. of a batch for token chunk columns [0, ncol) (pairs p0c + column):
+// MFMA over the two k-steps, bf16 y rows into the stage.
 __device__ __forceinline__ void dnc_compute(const DnTileBatch &bt, const Plan &pl, const u32x4 (&hb)[2][4],
-                                            uint16_t *ybuf, int rt0, int rt1, int p, bool tok_ok) {
-  const int l = threadIdx.x & 63, q = l >> 4;
+                                            DnStage &st, uint16_t *ybuf, int rt0, int rt1, int p0c, int ncol) {
+  const int l = threadIdx.x & 63, i = l & 15, q = l >> 4;
 #pragma unroll
   for (int t = 0; t < kDnTiles; ++t) {
+    if (rt0 + t >= rt1) break;  // wave-uniform
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -424,11 +449,14 @@ __device__ __forceinline__ void dnc_compute(const DnTileBatch &bt, const Plan &p
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) acc = mfma16(av[kk], as_bf16x8(hb[ks][kk]), acc);
     }
-    if (tok_ok && rt0 + t < rt1) {
-      u32x2 packed = {(uint32_t)f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16),
-                      (uint32_t)f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16)};
-      *reinterpret_cast<u32x2 *>(ybuf + (size_t)p * pl.K + (rt0 + t) * 16 + 4 * q) = packed;
+    if (st.fill + ncol > kDnStage) dn_flush(st, pl, ybuf);
+    if (i < ncol) {
+      const u32x2 packed = {(uint32_t)f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16),
+                            (uint32_t)f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16)};
+      *reinterpret_cast<u32x2 *>(st.rows + (st.fill + i) * 16 + 4 * q) = packed;
+      if (q == 0) st.tag[st.fill + i] = ((p0c + i) << 16) | (rt0 + t);
     }
+    st.fill += ncol;
   }
 }
 
@@ -488,38 +516,54 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
   trace_mark(pl, a.ws, 0);
 
   // ------------------------------------------------------------ R: router --
+  // Workgroup unit = (16 router rows, k-split s) for every token tile: the 8
+  // waves take consecutive k-steps of the split, load the row tile once and
+  // every token tile with all loads in flight, and meet in LDS; the sum over
+  // waves is written as partial s of each logit.
   {
-    const int NU = pl.RTr * pl.TTr * pl.Srw;
+    const int NU = pl.RTr * pl.Srw;
     const int KB = pl.h / kBlockK;
     for (int u = blockIdx.x; u < NU; u += gridDim.x) {
-      const int s = u % pl.Srw, rest = u / pl.Srw;
-      const int rt = rest % pl.RTr, tt = rest / pl.RTr;
+      const int s = u % pl.Srw, rt = u / pl.Srw;
       const int k0 = (int)((long)s * pl.KSr / pl.Srw), k1 = (int)((long)(s + 1) * pl.KSr / pl.Srw);
       const int ka = k0 + (k1 - k0) * w / kDecWaves, kb1 = k0 + (k1 - k0) * (w + 1) / kDecWaves;
-      const int row = rt * 16 + i, tok = tt * 16 + i;
-      const bool row_ok = row < E, tok_ok = tok < B;
+      const int row = rt * 16 + i;
+      const bool row_ok = row < E;
       const uint16_t *arow = a.router + (size_t)(row_ok ? row : 0) * pl.h;
-      const uint16_t *brow = a.x + (size_t)(tok_ok ? tok : 0) * pl.h;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      f32x4 acc[kDecMaxTokens / 16];
+#pragma unroll
+      for (int tt = 0; tt < kDecMaxTokens / 16; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
       for (int ks = ka; ks < kb1; ++ks) {
         const int kb = ks * 4 + q;
         const bool ok = kb < KB;
-        u32x4 va[4], vb[4];
+        u32x4 va[4], vb[kDecMaxTokens / 16][4];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          va[kk] = (ok && row_ok) ? load16(arow + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
-          vb[kk] = (ok && tok_ok) ? load16(brow + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
+        for (int kk = 0; kk < 4; ++kk) va[kk] = (ok && row_ok) ? load16(arow + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int tt = 0; tt < kDecMaxTokens / 16; ++tt) {
+          const int tok = tt * 16 + i;
+          const bool tok_ok = ok && tt < pl.TTr && tok < B;
+          const uint16_t *brow = a.x + (size_t)(tok_ok ? tok : 0) * pl.h + kb * kBlockK;
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) vb[tt][kk] = tok_ok ? load16(brow + kk * 8) : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) acc = mfma16(as_bf16x8(va[kk]), as_bf16x8(vb[kk]), acc);
+        for (int tt = 0; tt < kDecMaxTokens / 16; ++tt) {
+          if (tt < pl.TTr) {
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) acc[tt] = mfma16(as_bf16x8(va[kk]), as_bf16x8(vb[tt][kk]), acc[tt]);
+          }
+        }
       }
-      *reinterpret_cast<f32x4 *>(red + w * 256 + l * 4) = acc;
+#pragma unroll
+      for (int tt = 0; tt < kDecMaxTokens / 16; ++tt)
+        if (tt < pl.TTr) *reinterpret_cast<f32x4 *>(red + (tt * kDecWaves + w) * 256 + l * 4) = acc[tt];
       __syncthreads();
-      if (tid < 256) {
-        const int ln = tid >> 2, v = tid & 3;
+      for (int j = tid; j < pl.TTr * 256; j += kDecThreads) {
+        const int tt = j >> 8, ln = (j >> 2) & 63, v = j & 3;
         const int r = 4 * (ln >> 4) + v, c = ln & 15;
         const int t = tt * 16 + c, e = rt * 16 + r;
-        if (t < B) part[((size_t)s * B + t) * pl.Epad + e] = red_sum(red, tid);
+        if (t < B) part[((size_t)s * B + t) * pl.Epad + e] = red_sum(red + tt * kDecWaves * 256, j & 255);
       }
       __syncthreads();
     }
@@ -579,6 +623,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
         }
       }
       __syncthreads();
+      trace_mark(pl, a.ws, 10);
       for (int tl = w; tl < nt; tl += kDecWaves) {
         const int t = t0 + tl;
         int *mysel = sel + w * kMaxTopk;
@@ -594,24 +639,24 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
         float wt = 0.f;
         if (pl.gating == K3MOE_GATING_SIGMOID_BIAS) {
           float sum = 0.f;
-          for (int r = 0; r < k; ++r) sum = __fadd_rn(sum, __shfl(my_score, r, 64));
+          for (int r = 0; r < k; ++r) sum = __fadd_rn(sum, lane_f32(my_score, r));
           wt = my_score / __fadd_rn(sum, 1e-20f);
         } else {
           float mx = -INFINITY;
-          for (int r = 0; r < k; ++r) mx = fmaxf(mx, __shfl(my_score, r, 64));
+          for (int r = 0; r < k; ++r) mx = fmaxf(mx, lane_f32(my_score, r));
           const float ex = (l < k) ? expf(my_score - mx) : 0.f;
           float sum = 0.f;
-          for (int r = 0; r < k; ++r) sum = __fadd_rn(sum, __shfl(ex, r, 64));
+          for (int r = 0; r < k; ++r) sum = __fadd_rn(sum, lane_f32(ex, r));
           wt = ex / sum;
         }
         const bool writer = redundant ? blockIdx.x == 0 : true;
         if (a.routes && a.out_short) {
           float mn = INFINITY;
-          for (int r = 0; r < k; ++r) mn = fminf(mn, __shfl(my_key, r, 64));
+          for (int r = 0; r < k; ++r) mn = fminf(mn, lane_f32(my_key, r));
           if (l == 0 && writer) a.out_short[t] = fmaxf(kyf[tl * E + mysel[k - 1]] - mn, 0.f);
         }
         int rank = 0;
-        for (int r = 0; r < k; ++r) rank += (__shfl(my_e, r, 64) < my_e) ? 1 : 0;
+        for (int r = 0; r < k; ++r) rank += ((int)lane_u32((uint32_t)my_e, r) < my_e) ? 1 : 0;
         if (l < k) {
           const size_t o = (size_t)t * k + rank;
           if (writer) {
@@ -627,6 +672,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
           }
         }
       }
+      trace_mark(pl, a.ws, 11);
       __syncthreads();
     }
   }
@@ -756,6 +802,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
     const int gw = blockIdx.x * kDecWaves + w;
     const int ta = (int)((long)NT * gw / GW), tb = (int)((long)NT * (gw + 1) / GW);
     const int KB = pl.I / kBlockK;
+    DnStage st;  // this wave's y stage in the scratch area (free after gate/up)
+    st.rows = reinterpret_cast<uint16_t *>(scr) + w * kDnStage * 16;
+    st.tag = reinterpret_cast<int *>(scr + kDecWaves * kDnStage * 32) + w * kDnStage;
+    st.fill = 0;
     for (int t = ta; t < tb;) {
       const int d = t / pl.RTd;
       const int rt0 = t % pl.RTd, rt1 = min(pl.RTd, rt0 + (tb - t));
@@ -766,6 +816,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
       for (int c = 0; c * 16 < n; ++c) {
         const int pj = c * 16 + i;
         const bool tok_ok = pj < n;
+        const int ncol = min(16, n - c * 16);
         // lane group q feeds blocks 2q (k-step 0) and 2q+1 (k-step 1) of the h row
         const uint32_t hoff = tok_ok ? (uint32_t)(p0 + pj) * pl.I * 2 + q * 128 : kOffNone;
         u32x4 hb[2][4];
@@ -780,16 +831,17 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
         for (int rt = rt0; rt < rt1; rt += 2 * kDnTiles) {
           const int o1 = rt + kDnTiles - rt0, o2 = rt + 2 * kDnTiles - rt0;
           if (rt + kDnTiles < rt1) dnc_issue(b1, pl, wrow + o1 * tstride, srow + o1 * sstride, zero, rt + kDnTiles, rt1);
-          dnc_compute(b0, pl, hb, ybuf, rt, rt1, p0 + pj, tok_ok);
+          dnc_compute(b0, pl, hb, st, ybuf, rt, rt1, p0 + c * 16, ncol);
           if (rt + kDnTiles < rt1) {
             if (rt + 2 * kDnTiles < rt1)
               dnc_issue(b0, pl, wrow + o2 * tstride, srow + o2 * sstride, zero, rt + 2 * kDnTiles, rt1);
-            dnc_compute(b1, pl, hb, ybuf, rt + kDnTiles, rt1, p0 + pj, tok_ok);
+            dnc_compute(b1, pl, hb, st, ybuf, rt + kDnTiles, rt1, p0 + c * 16, ncol);
           }
         }
       }
       t += rt1 - rt0;
     }
+    dn_flush(st, pl, ybuf);
     trace_mark(pl, a.ws, 9);
     grid_barrier(ctl, ++nbar, trace_slots(pl, a.ws, 24));
     // combine (kimi.py:318,323): expert_sum[t][col] = sum over the token's

@@ -223,33 +223,76 @@ __device__ __forceinline__ uint32_t ordered_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// k rounds of wave arg-max over the keys of experts e = lane + 64 m (m < 16,
-// e < E): selected experts in rank order go to sel[0..k) (lowest index first
-// among equal keys). Every lane must call it.
-__device__ __forceinline__ void wave_topk(const uint32_t *keys_lds, int E, int k, int *sel) {
+// Value of lane `src` (wave-uniform) in every lane.
+__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int src) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, src);
+}
+__device__ __forceinline__ float lane_f32(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+
+// One DPP step of a 64-bit wave maximum: max(v, v of the DPP source lane).
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
+  const uint32_t lo = dpp<Ctrl, RowMask>((uint32_t)v), hi = dpp<Ctrl, RowMask>((uint32_t)(v >> 32));
+  const uint64_t o = ((uint64_t)hi << 32) | lo;
+  return o > v ? o : v;
+}
+
+// Wave-wide maximum of a 64-bit value, in every lane (same DPP pattern as wave_max_u32).
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  v = dpp_max_u64<kDppQuadXor1, 0xF>(v);
+  v = dpp_max_u64<kDppQuadXor2, 0xF>(v);
+  v = dpp_max_u64<kDppHalfMirror, 0xF>(v);
+  v = dpp_max_u64<kDppMirror, 0xF>(v);
+  v = dpp_max_u64<kDppBcast15, 0xA>(v);
+  v = dpp_max_u64<kDppBcast31, 0xC>(v);
+  return ((uint64_t)lane_u32((uint32_t)(v >> 32), 63) << 32) | lane_u32((uint32_t)v, 63);
+}
+
+// Top-k of the ordered keys keys_lds[0..E), E <= 64 MM, 1 <= k <= min(E, 32):
+// larger keys first, equal keys in ascending expert order; sel[0..k) gets the
+// experts in that rank order. Lane l holds experts l + 64 m as 64-bit values
+// (key << 32 | ~expert) -- larger value = earlier rank, all distinct -- sorted
+// descending in registers (odd-even transposition network); each of the k
+// rounds takes the wave maximum of the lanes' heads and the winning lane drops
+// its head. All in VALU and DPP (no scalar dependency chains). Every lane must
+// call it. Returns the k-th largest key.
+template <int MM>
+__device__ __forceinline__ uint32_t wave_topk_m(const uint32_t *keys_lds, int E, int k, int *sel) {
   const int l = __lane_id();
-  uint32_t kv[16];
-  uint32_t live = 0;
+  uint64_t v[MM];
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
+  for (int m = 0; m < MM; ++m) {
     const int e = l + 64 * m;
-    kv[m] = e < E ? keys_lds[e] : 0u;
-    if (e < E) live |= 1u << m;
+    v[m] = e < E ? ((uint64_t)keys_lds[e] << 32) | (uint32_t)~e : 0ull;  // real keys are >= 0x007FFFFF
   }
-  for (int r = 0; r < k; ++r) {
-    uint32_t best = 0u;
-    int bm = -1;
 #pragma unroll
-    for (int m = 0; m < 16; ++m)
-      if (((live >> m) & 1u) && (bm < 0 || kv[m] > best)) {  // ascending m = ascending index
-        best = kv[m];
-        bm = m;
-      }
-    const uint32_t top = wave_max_u32(bm >= 0 ? best : 0u);
-    const uint32_t idx = wave_min_u32((bm >= 0 && best == top) ? (uint32_t)(l + 64 * bm) : 0xFFFFFFFFu);
-    if ((int)(idx & 63u) == l) live &= ~(1u << (idx >> 6));
-    if (l == 0) sel[r] = (int)idx;
+  for (int st = 0; st < MM; ++st) {
+#pragma unroll
+    for (int m = st & 1; m + 1 < MM; m += 2) {
+      const uint64_t hi = v[m] > v[m + 1] ? v[m] : v[m + 1];
+      const uint64_t lo = v[m] > v[m + 1] ? v[m + 1] : v[m];
+      v[m] = hi;
+      v[m + 1] = lo;
+    }
   }
+  uint64_t best = 0;
+  for (int r = 0; r < k; ++r) {
+    best = wave_max_u64(v[0]);
+    const bool win = v[0] == best;
+#pragma unroll
+    for (int m = 0; m < MM; ++m) v[m] = win ? (m + 1 < MM ? v[m + 1] : 0ull) : v[m];
+    if (l == 0) sel[r] = (int)~(uint32_t)best;
+  }
+  return (uint32_t)(best >> 32);
+}
+
+__device__ __forceinline__ uint32_t wave_topk(const uint32_t *keys_lds, int E, int k, int *sel) {
+  if (E <= 128) return wave_topk_m<2>(keys_lds, E, k, sel);
+  if (E <= 256) return wave_topk_m<4>(keys_lds, E, k, sel);
+  if (E <= 512) return wave_topk_m<8>(keys_lds, E, k, sel);
+  return wave_topk_m<16>(keys_lds, E, k, sel);
 }
 
 }  // namespace k3moe

@@ -115,24 +115,24 @@ __global__ __launch_bounds__(kThreads) void k_topk(Plan pl, const float *__restr
   float w = 0.f;
   if (pl.gating == K3MOE_GATING_SIGMOID_BIAS) {
     float sum = 0.f;
-    for (int r = 0; r < k; ++r) sum = __fadd_rn(sum, __shfl(my_score, r, kWave));
+    for (int r = 0; r < k; ++r) sum = __fadd_rn(sum, lane_f32(my_score, r));
     w = my_score / __fadd_rn(sum, 1e-20f);
   } else {
     float mx = -INFINITY;
-    for (int r = 0; r < k; ++r) mx = fmaxf(mx, __shfl(my_score, r, kWave));
+    for (int r = 0; r < k; ++r) mx = fmaxf(mx, lane_f32(my_score, r));
     const float ex = (l < k) ? expf(my_score - mx) : 0.f;
     float sum = 0.f;
-    for (int r = 0; r < k; ++r) sum = __fadd_rn(sum, __shfl(ex, r, kWave));
+    for (int r = 0; r < k; ++r) sum = __fadd_rn(sum, lane_f32(ex, r));
     w = ex / sum;
   }
   if (routes && out_short) {
     float mn = INFINITY;
-    for (int r = 0; r < k; ++r) mn = fminf(mn, __shfl(my_key, r, kWave));
+    for (int r = 0; r < k; ++r) mn = fminf(mn, lane_f32(my_key, r));
     if (l == 0) out_short[t] = fmaxf(s_key[wave][s_sel[wave][k - 1]] - mn, 0.f);
   }
   // ascending expert order
   int rank = 0;
-  for (int r = 0; r < k; ++r) rank += (__shfl(my_e, r, kWave) < my_e) ? 1 : 0;
+  for (int r = 0; r < k; ++r) rank += ((int)lane_u32((uint32_t)my_e, r) < my_e) ? 1 : 0;
   if (l < k) {
     const size_t o = (size_t)t * k + rank;
     out_ids[o] = my_e;

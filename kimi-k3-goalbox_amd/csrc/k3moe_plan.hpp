@@ -28,7 +28,8 @@ constexpr int kDecMaxTokens = 64;
 constexpr int kDecMaxPairs = 1024;
 constexpr int kDecMaxSplits = 8;   // router k-splits across workgroups
 constexpr int kDecMaxLds = 160 * 1024;   // gfx950: 160 KiB of LDS per workgroup
-constexpr int kDecStaticLds = 1024;  // decode kernel's static LDS (round table, counters), upper bound
+constexpr int kDecStaticLds = 1024;
+constexpr int kDnStage = 128;        // decode down: y rows staged per wave (32 B + a 4-byte tag each)  // decode kernel's static LDS (round table, counters), upper bound
 
 constexpr int kRedundantTokens = 16;   // decode: route every token in every workgroup up to this batch
 constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert) keys
@@ -87,7 +88,8 @@ inline int decode_lds(Plan &p) {
   const int routed = 8 * p.P;                                       // ids + weights per pair
   const int topk = routed + 4 * (3 * nt * p.E + kDecWaves * kMaxTopk);  // keys (u32, f32), scores, picks
   const int group = routed + 4 * (4 * p.E);                         // counts, offsets, bitmaps
-  const int down = kDecWaves * p.B * 16 * 4;                        // per-wave combine accumulators
+  int down = kDecWaves * p.B * 16 * 4;                              // per-wave combine accumulators
+  if (down < kDecWaves * kDnStage * 36) down = kDecWaves * kDnStage * 36;  // or per-wave y stages
   int scr = topk;
   if (group > scr) scr = group;
   if (down > scr) scr = down;
@@ -136,7 +138,7 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   if (d.path != K3MOE_PATH_GENERAL && p.B <= kDecMaxTokens && p.P <= kDecMaxPairs &&
       decode_lds(p) <= kDecMaxLds - kDecStaticLds)
     p.path = kPathDecode;
-  p.Srw = (int)(p.G / base);
+  p.Srw = (int)(p.G / p.RTr);  // decode router units: (row tile, split), every token tile
   if (p.Srw > srw_cap) p.Srw = srw_cap;
   if (p.Srw < 1) p.Srw = 1;
   decode_lds(p);
