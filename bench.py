@@ -54,6 +54,19 @@ def percentile(vals, q):
     return s[lo] + (s[min(lo + 1, len(s) - 1)] - s[lo])*(at - lo)
 
 
+# HBM bytes per launch of the step kernel from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
+# script, calibrated on a device copy of known size (k3moe.rocpd writes the file).
+TRAFFIC_FILE = 'profiles/hbm_traffic.json'
+
+
+def measured_traffic() -> dict:
+    path = os.path.join(REPO, TRAFFIC_FILE)
+    if not os.path.exists(path):
+        return {}
+    with open(path) as fh:
+        return json.load(fh).get('workloads', {})
+
+
 PHASES = ('router', 'barrier1', 'topk', 'barrier2', 'group', 'gate_up', 'barrier3', 'down_combine')
 
 
@@ -220,6 +233,9 @@ def cpu_baseline(cfg, host_inputs, reps=3):
     from oracle import moe_ref
     from k3moe import synthetic
     cores = len(os.sched_getaffinity(0))
+    share = os.environ.get('OMP_NUM_THREADS', '')
+    if share.isdigit() and int(share) > 0:   # the host share this process may use
+        cores = min(cores, int(share))
     torch.set_num_threads(cores)
     args = synthetic.step_args(host_inputs)
     kw = dict(topk=cfg.topk, gating=cfg.gating, activation=cfg.activation, latent=host_inputs.get('latent'))
@@ -242,6 +258,9 @@ def main():
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--warm-cache', action='store_true', help='skip the L2/MALL flush before each replay')
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--copy-probe', type=int, default=0, metavar='BYTES',
+                    help='first copy BYTES between two device buffers three times (a kernel of known '
+                         'traffic, to calibrate the FETCH_SIZE / WRITE_SIZE counters of a --pmc run)')
     ap.add_argument('--launch', default='stream', choices=['stream', 'graph'],
                     help='time stream-ordered launches (default) or HIP-graph replays')
     ap.add_argument('--trace', action='store_true', help='record per-phase timestamps of the persistent kernel '
@@ -270,6 +289,16 @@ def main():
         runs = [(configs.PREFILL, 1, False)]
         workload = 'unsharded-prefill-b4096'
 
+    if args.copy_probe:
+        n = args.copy_probe // 16 * 16
+        src = torch.ones(n // 4, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize(device)
+        log(f'bench: copy probe of {n} bytes x 3 done')
+        del src, dst
+
     results, host = {}, {}
     for cfg, layers, host_gen in runs:
         log(f'bench: {cfg.name} layers={layers} steps={args.steps} warmup={args.warmup} cold={cold}')
@@ -282,6 +311,10 @@ def main():
 
     head_cfg, head_layers, _ = runs[0]
     head = results[head_cfg.name]
+    measured = measured_traffic()
+    for name, r in results.items():
+        if name in measured and r['layers'] == 1:
+            r['hbm_traffic_bytes'] = measured[name]['traffic_bytes']
     cpu = None
     if not args.no_cpu_baseline and args.workload == 'tp8':
         per = {}
@@ -319,8 +352,10 @@ def main():
         'hbm_GBps': head['hbm_GBps'],
         'hbm_frac': head['hbm_frac'],
         'per_batch': results,
-        'roofline': {'bound': 'hbm', 'kernel': 'k3moe_moe_step (whole step)', 'achieved': head['hbm_GBps'],
-                     'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac'], 'traffic': None},
+        'roofline': {'bound': 'hbm', 'kernel': 'k3moe::k_moe_decode (the whole step, one launch)',
+                     'achieved': head['hbm_GBps'], 'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac'],
+                     'traffic': measured.get(head_cfg.name, {}).get('traffic_bytes') if head_layers == 1 else None,
+                     'traffic_source': TRAFFIC_FILE if measured else None},
         'cpu_baseline': cpu,
     }
     print(json.dumps(line), flush=True)

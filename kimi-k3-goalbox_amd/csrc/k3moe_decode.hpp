@@ -2,25 +2,28 @@
 //
 // One 512-thread workgroup (8 waves) per CU. Phases, separated by grid
 // barriers where a phase needs every workgroup's results:
-//   R   router logits on MFMA. Workgroup unit = (16 router rows, 16 tokens,
-//       k-range); the 8 waves split the k-range and meet in LDS, so at most
-//       Srw (<= 8) partials per logit reach memory.             (kimi.py:308)
+//   R   router logits on MFMA. Workgroup unit = (16 router rows, k-split s)
+//       for every token tile; each wave takes a 128-k step of the split with
+//       all its loads in flight, the waves meet in LDS and one partial per
+//       (split, logit) reaches memory.                          (kimi.py:308)
 //   --- barrier 1
-//   T   gating and top-k, one workgroup per token: partials summed in a fixed
-//       order, sigmoid + bias (or softmax), k wave arg-max rounds, weights
-//       renormalised, ids sorted.                               (kimi.py:308-316)
-//   --- barrier 2
+//   T   gating and top-k, one wave per token: partials summed in split
+//       order, sigmoid + bias (or softmax), a register-sorted DPP tournament
+//       for the k largest, weights renormalised, ids sorted. For B <= 16
+//       every workgroup routes every token itself.             (kimi.py:308-316)
+//   --- barrier 2 (only when tokens are routed by different workgroups)
 //   G   every workgroup rebuilds the expert grouping in its own LDS (active
-//       experts ascending, token pairs ascending inside an expert), so no
-//       barrier is needed after it.                             (kimi.py:319-320)
-//   GU  gate/up: workgroup unit = (active expert, 8 gate + 8 up rows); one
-//       16-row MFMA tile, the 8 waves split K and meet in LDS; SiTU/SiLU
-//       epilogue; bf16 h to memory.                             (kimi.py:321-322)
+//       experts ascending, token pairs ascending inside an expert, chunk
+//       offsets), so no barrier is needed after it.            (kimi.py:319-320)
+//   GU  gate/up: stream-K over groups of (expert, token chunk, 8 gate + 8 up
+//       rows) units with the chunks' activation rows staged in LDS; SiTU /
+//       SiLU epilogue; bf16 h to memory.                       (kimi.py:321-322)
 //   --- barrier 3
-//   DN  down + combine: workgroup unit = 16 output rows for every active
-//       expert, experts split over the waves; each wave accumulates
-//       w * bf16(y) per token in LDS in ascending expert order, the waves are
-//       summed in a fixed order and expert_sum is written once. (kimi.py:318-323)
+//   DN  many active experts: expert-major (expert, 16-row tile) ranges per
+//       wave, bf16 y per pair staged in LDS and written out in bulk, then
+//       barrier 4 and the combine (w * bf16(y), ascending expert order).
+//       Few active experts: each workgroup takes 16 output rows of every
+//       active expert and sums w * bf16(y) in LDS.             (kimi.py:318-323)
 // The barrier spin is bounded: a workgroup that waits too long sets the
 // error word and every workgroup runs to the end.
 #pragma once

@@ -233,3 +233,23 @@ def test_moe_layer_reads_reference_keys(gpu):
     want = k3moe.moe_step(*synthetic.step_args(to_dev(inp, gpu)), topk=cfg.topk)
     for k in want:
         assert torch.equal(got[k], want[k]), k
+
+
+@pytest.mark.gpu
+def test_submission_build_run_matches_moe_step(gpu):
+    from k3moe import submission
+    cfg = MoEConfig('submission', 24, 4, 128, 64, 5)
+    say(f'case: {cfg.name}')
+    inp = to_dev(synthetic.moe_layer_inputs(cfg, 1), gpu)
+    want = k3moe.moe_step(*synthetic.step_args(inp), topk=cfg.topk)
+    params = {'tokens': cfg.tokens, 'experts': cfg.experts, 'topk': cfg.topk, 'hidden': cfg.hidden,
+              'inter': cfg.inter}
+    run = submission.build({'params': params})
+    got = run({k: v for k, v in inp.items() if v is not None})
+    assert set(got) == set(want)
+    for k in want:
+        assert torch.equal(got[k], want[k]), k
+    run3 = submission.build({'params': params, 'layer': 3})
+    got3 = run3({('x' if k == 'x' else f'l3_{k}'): v for k, v in inp.items() if v is not None})
+    for k in want:
+        assert torch.equal(got3[k], want[k]), k

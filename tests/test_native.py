@@ -83,3 +83,18 @@ def test_product_package_does_not_import_the_oracle():
                 text = open(os.path.join(root, f)).read()
                 assert not re.search(r'^\s*(from|import)\s+oracle\b', text, flags=re.M), f
                 assert 'liborc' not in text, f
+
+
+def test_submission_build_validates_the_case():
+    from k3moe import submission
+    case = {'params': {'tokens': 2, 'experts': 16, 'topk': 4, 'hidden': 64, 'inter': 64}}
+    assert callable(submission.build(case))
+    with pytest.raises(ValueError, match='params'):
+        submission.build({'params': {'tokens': 2}})
+    with pytest.raises(ValueError, match='gating'):
+        submission.build(dict(case, gating='top1'))
+    with pytest.raises(ValueError, match='geometry'):
+        submission.build({'params': dict(case['params'], hidden=48)})
+    run = submission.build(case)
+    with pytest.raises(ValueError, match='x must be'):
+        run({'x': torch.zeros(3, 64, dtype=torch.bfloat16)})
