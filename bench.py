@@ -109,6 +109,18 @@ def read_trace(cfg, device):
         out['topk_parts'] = {'logits_med_us': round(float(((sub[ok, 0] - raw[ok, 2])*0.01).median()), 2),
                              'select_med_us': round(float(((sub[ok, 1] - sub[ok, 0])*0.01).median()), 2),
                              'tail_med_us': round(float(((raw[ok, 3] - sub[ok, 1])*0.01).median()), 2)}
+    def sub(a, b, name, rows=None):   # median of slot b - slot a over workgroups that wrote both in order
+        x, y = full[:, a], full[:, b]
+        ok = (x > 0) & (y >= x) & (x >= raw[:, 0])
+        if bool(ok.any()):
+            out.setdefault('sub_phases_med_us', {})[name] = round(float(((y[ok] - x[ok])*0.01).median()), 2)
+    sub(0, 31, 'router_loads_mfma')
+    sub(31, 1, 'router_reduce_store')
+    sub(10, 30, 'topk_select_only')
+    sub(30, 11, 'topk_weights_ids')
+    sub(4, 28, 'group_count')
+    sub(28, 29, 'group_scan')
+    sub(29, 5, 'group_place')
     for n in range(4):   # inside each grid barrier: release+add, spin, acquire
         if float(full[:, 13 + 4*n].max()) <= 0:
             continue

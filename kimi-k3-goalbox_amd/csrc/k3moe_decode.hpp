@@ -558,6 +558,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
           }
         }
       }
+      if (u == (int)blockIdx.x) trace_mark(pl, a.ws, 31);
 #pragma unroll
       for (int tt = 0; tt < kDecMaxTokens / 16; ++tt)
         if (tt < pl.TTr) *reinterpret_cast<f32x4 *>(red + (tt * kDecWaves + w) * 256 + l * 4) = acc[tt];
@@ -627,11 +628,31 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
       }
       __syncthreads();
       trace_mark(pl, a.ws, 10);
+      // one token per pass (E <= 512, k <= 8): every wave sorts 64 of the
+      // (key, ~expert) values with a bitonic network and offers its k best;
+      // wave 0 sorts the 8 k offers and keeps the first k
+      const bool coop = nt == 1 && E <= kDecWaves * 64 && k <= 8;
+      if (coop) {
+        uint64_t *cand = reinterpret_cast<uint64_t *>(
+            (reinterpret_cast<uintptr_t>(sel + kDecWaves * kMaxTopk) + 7) & ~(uintptr_t)7);  // [8 k]
+        const int e = w * 64 + l;
+        uint64_t v = e < E ? ((uint64_t)kyl[e] << 32) | (uint32_t)~e : 0ull;
+        v = wave_sort_desc(v);
+        if (l < k) cand[w * k + l] = v;
+        __syncthreads();
+        if (w == 0) {
+          uint64_t c = l < kDecWaves * k ? cand[l] : 0ull;
+          c = wave_sort_desc(c);
+          if (l < k) sel[l] = (int)~(uint32_t)c;
+          wave_lds_order();
+        }
+      }
       for (int tl = w; tl < nt; tl += kDecWaves) {
         const int t = t0 + tl;
         int *mysel = sel + w * kMaxTopk;
-        wave_topk(kyl + tl * E, E, k, mysel);
+        if (!coop) wave_topk(kyl + tl * E, E, k, mysel);
         wave_lds_order();
+        trace_mark(pl, a.ws, 30);
         int my_e = -1;
         float my_score = 0.f, my_key = 0.f;
         if (l < k) {
@@ -722,48 +743,58 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
       atomicOr(&bits[2 * e + (t >> 5)], 1u << (t & 31));
     }
     __syncthreads();
-    if (w == 0) {
-      // lane l owns experts [16 l, 16 l + 16): local sums, then a wave scan
-      int tot = 0, nac = 0, nch = 0;
-      for (int j = 0; j < 16; ++j) {
-        const int e = 16 * l + j;
-        const int c = e < E ? cnt[e] : 0;
-        tot += c;
-        nac += c > 0;
-        nch += (c + pl.NX - 1) / pl.NX;
-      }
-      int it = tot, ia = nac, ic = nch;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int ot = __shfl_up(it, d, 64), oa = __shfl_up(ia, d, 64), oc = __shfl_up(ic, d, 64);
-        if (l >= d) {
-          it += ot;
-          ia += oa;
-          ic += oc;
-        }
-      }
-      int base = it - tot, abase = ia - nac, cbase = ic - nch;
-      for (int j = 0; j < 16; ++j) {
-        const int e = 16 * l + j;
-        if (e >= E) break;
-        const int c = cnt[e];
-        off[e] = base;
-        if (c > 0) {
-          g_act[abase] = e;
-          g_aoff[abase] = base;
-          g_acnt[abase] = c;
-          g_coff[abase] = cbase;
-          ++abase;
-          cbase += (c + pl.NX - 1) / pl.NX;
-        }
-        base += c;
-      }
+    trace_mark(pl, a.ws, 28);
+    {
+      // exclusive prefix, in ascending expert order, of the pair counts, the
+      // active flags and the gate/up chunk counts: thread tid owns experts
+      // 2 tid and 2 tid + 1 (E <= 1024); wave scans, then the wave totals
+      int *wsum = reinterpret_cast<int *>(bits + 2 * E);  // [8 waves][3]
+      const int e0 = 2 * tid, e1 = e0 + 1;
+      const int c0 = e0 < E ? cnt[e0] : 0, c1 = e1 < E ? cnt[e1] : 0;
+      const int n0 = (c0 + pl.NX - 1) / pl.NX, n1 = (c1 + pl.NX - 1) / pl.NX;
+      const int tp = c0 + c1, ta = (c0 > 0) + (c1 > 0), tc = n0 + n1;
+      const int sp = wave_incl_scan(tp), sa = wave_incl_scan(ta), sc = wave_incl_scan(tc);
       if (l == 63) {
-        s_nact = ia;
-        g_coff[ia] = ic;
+        wsum[3 * w] = sp;
+        wsum[3 * w + 1] = sa;
+        wsum[3 * w + 2] = sc;
+      }
+      __syncthreads();
+      int bp = 0, ba = 0, bc = 0;
+      for (int ww = 0; ww < w; ++ww) {
+        bp += wsum[3 * ww];
+        ba += wsum[3 * ww + 1];
+        bc += wsum[3 * ww + 2];
+      }
+      int op = bp + sp - tp, oa = ba + sa - ta, oc = bc + sc - tc;
+      if (e0 < E) {
+        off[e0] = op;
+        if (c0 > 0) {
+          g_act[oa] = e0;
+          g_aoff[oa] = op;
+          g_acnt[oa] = c0;
+          g_coff[oa] = oc;
+          ++oa;
+          oc += n0;
+        }
+      }
+      op += c0;
+      if (e1 < E) {
+        off[e1] = op;
+        if (c1 > 0) {
+          g_act[oa] = e1;
+          g_aoff[oa] = op;
+          g_acnt[oa] = c1;
+          g_coff[oa] = oc;
+        }
+      }
+      if (tid == kDecThreads - 1) {  // totals
+        s_nact = ba + sa;
+        g_coff[ba + sa] = bc + sc;
       }
     }
     __syncthreads();
+    trace_mark(pl, a.ws, 29);
     for (int p = tid; p < pl.P; p += kDecThreads) {
       const int e = rid[p], t = p / k;
       const uint32_t lo = bits[2 * e], hi = bits[2 * e + 1];

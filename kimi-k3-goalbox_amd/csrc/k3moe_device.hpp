@@ -288,6 +288,52 @@ __device__ __forceinline__ uint32_t wave_topk_m(const uint32_t *keys_lds, int E,
   return (uint32_t)(best >> 32);
 }
 
+// Value of lane (lane ^ D) for D a power of two below 64: DPP quad permutes
+// for 1 and 2, ds_swizzle's xor mode for 4..16 (within 32-lane halves), a
+// cross-half shuffle for 32.
+template <int D>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+  if constexpr (D == 1) return dpp<kDppQuadXor1, 0xF>(v);
+  else if constexpr (D == 2) return dpp<kDppQuadXor2, 0xF>(v);
+  else if constexpr (D < 32) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (D << 10));
+  else return (uint32_t)__shfl_xor((int)v, 32, kWave);
+}
+
+template <int K, int J>
+__device__ __forceinline__ uint64_t bitonic_step(uint64_t v, int l) {
+  const uint64_t o = ((uint64_t)xor_lane<J>((uint32_t)(v >> 32)) << 32) | xor_lane<J>((uint32_t)v);
+  const bool keep_max = ((l & J) == 0) == ((l & K) == 0);
+  return keep_max ? (o > v ? o : v) : (o < v ? o : v);
+}
+
+template <int K, int J>
+__device__ __forceinline__ uint64_t bitonic_merge(uint64_t v, int l) {
+  v = bitonic_step<K, J>(v, l);
+  if constexpr (J > 1) v = bitonic_merge<K, J / 2>(v, l);
+  return v;
+}
+
+// Sorts one 64-bit value per lane across the wave, descending (lane 0 holds
+// the largest): the 21 compare-exchange stages of a bitonic network.
+template <int K = 2>
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v) {
+  v = bitonic_merge<K, K / 2>(v, __lane_id());
+  if constexpr (K < 64) v = wave_sort_desc<K * 2>(v);
+  return v;
+}
+
+// Inclusive prefix sum over the wave (lane l gets the sum of lanes 0..l):
+// DPP shifts inside rows of 16, then the row broadcasts.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += (int)__builtin_amdgcn_update_dpp(0, v, kDppBcast15, 0xA, 0xF, false);
+  v += (int)__builtin_amdgcn_update_dpp(0, v, kDppBcast31, 0xC, 0xF, false);
+  return v;
+}
+
 __device__ __forceinline__ uint32_t wave_topk(const uint32_t *keys_lds, int E, int k, int *sel) {
   if (E <= 128) return wave_topk_m<2>(keys_lds, E, k, sel);
   if (E <= 256) return wave_topk_m<4>(keys_lds, E, k, sel);
