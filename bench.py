@@ -81,7 +81,7 @@ def read_trace(cfg, device):
     d = torch.empty(cfg.experts, cfg.width, cfg.inter//32, 16, dtype=torch.uint8, device=device)
     r = torch.empty(cfg.experts, cfg.hidden, dtype=torch.bfloat16, device=device)
     total = k3moe.workspace_bytes(moe.dims_for(x, r, g, d, cfg.topk, cfg.gating, cfg.activation))
-    full = ws[total - 262144: total].cpu().view(torch.int64).view(1024, 32).double()
+    full = ws[total - 1024*48*8: total].cpu().view(torch.int64).view(1024, 48).double()
     G = int((full[:, 8] > 0).sum())
     full = full[:G]
     raw = full[:, :9]
@@ -121,6 +121,17 @@ def read_trace(cfg, device):
     sub(4, 28, 'group_count')
     sub(28, 29, 'group_scan')
     sub(29, 5, 'group_place')
+    sub(5, 32, 'gu_round_table')
+    sub(32, 33, 'gu_stage_x')
+    sub(33, 34, 'gu_stream_wave0')
+    sub(34, 35, 'gu_wait_all_waves')
+    sub(35, 6, 'gu_reduce_finish')
+    ends = full[:, 36:44]   # gate/up stream end of each wave, relative to the workgroup's staging barrier
+    okw = (ends > 0).all(1) & (full[:, 33] > 0)
+    if bool(okw.any()):
+        rel = (ends[okw] - full[okw, 33:34])*0.01
+        out['gu_stream_end_by_wave_med_us'] = [round(float(rel[:, j].median()), 1) for j in range(8)]
+        out['gu_stream_spread_med_us'] = round(float((rel.max(1).values - rel.min(1).values).median()), 1)
     for n in range(4):   # inside each grid barrier: release+add, spin, acquire
         if float(full[:, 13 + 4*n].max()) <= 0:
             continue

@@ -216,7 +216,8 @@ __device__ __forceinline__ void gu_finish_wave(const Plan &pl, uint16_t *hbuf, c
 template <int W, bool AL>
 __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, float *red, const int *g_act,
                                       const int *g_aoff, const int *g_acnt, const int *g_coff, const int *g_ptok,
-                                      uint16_t *xs, GuChunk *tab, int *s_round, int *s_rowtok, int D, uint16_t *hbuf) {
+                                      uint16_t *xs, GuChunk *tab, int *s_round, int *s_rowtok, int *s_prog, int D,
+                                      uint16_t *hbuf) {
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i = l & 15;
   const int KB = pl.K / kBlockK, NSS = (KB + 15) / 16, K8 = pl.K / 8;
   const int GPC = pl.U8 / W;  // groups per chunk
@@ -264,6 +265,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
       }
     }
     __syncthreads();
+    if (g0 == ga) trace_mark(pl, a.ws, 32);
     const int nch = s_round[0], rows = s_round[1];
     const int g1 = min(gb, (ci0 + nch) * GPC);
     const int work = (g1 - g0) * NSS;
@@ -296,6 +298,9 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
       rows_of(ig, iwr, isr);
       gu_issue<W, AL>(B0, iwr, isr, iss, KB);
     }
+    // progress of each wave's range in 1/4096 (empty ranges count as done);
+    // visible to the workgroup's other waves after the staging barrier
+    if (l == 0) __hip_atomic_store(s_prog + w, s < e ? 0 : 4096, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     // stage the round's activation rows (four rows per pass, every load in flight)
     for (int r0 = 0; r0 < rows; r0 += 4) {
       for (int c0 = 0; c0 < K8; c0 += 2 * kDecThreads) {
@@ -320,6 +325,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
       }
     }
     __syncthreads();
+    if (g0 == ga) trace_mark(pl, a.ws, 33);
     if (s < e) {
       int cg = ig, css = iss;  // compute cursor
       const uint16_t *xrow = xrow_of(cg);
@@ -335,6 +341,19 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
           gu_issue<W, AL>(nxt, iwr, isr, iss, KB);
         }
         gu_compute<W, AL>(cur, xrow, css, KB, acc);
+        // the memory pipeline serves older waves first: a wave behind the
+        // workgroup's mean progress raises its issue priority to catch up
+        {
+          const int mine = (pos + 1 - s) * 4096 / (e - s);
+          if (l == 0) __hip_atomic_store(s_prog + w, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+          const u32x4 p0 = *reinterpret_cast<const volatile u32x4 *>(s_prog);
+          const u32x4 p1 = *reinterpret_cast<const volatile u32x4 *>(s_prog + 4);
+          const int sum = (int)(p0[0] + p0[1] + p0[2] + p0[3] + p1[0] + p1[1] + p1[2] + p1[3]);
+          // wave-uniform (scalar) branch: s_setprio ignores the exec mask
+          if (__builtin_amdgcn_readfirstlane(mine * kDecWaves < sum ? 1 : 0)) __builtin_amdgcn_s_setprio(2);
+          else __builtin_amdgcn_s_setprio(0);
+        }
         if (++css == NSS || pos + 1 == e) {
           const bool started_here = cg * NSS >= s;
           if (started_here && css == NSS) {
@@ -356,7 +375,12 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
         if (pos + 1 < e) step(B1, B0, pos + 1);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
+    if (g0 == ga) trace_mark(pl, a.ws, 34);
+    if (g0 == ga && pl.o_trace && l == 0)  // every wave's stream end
+      reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + 36 + w] = __builtin_amdgcn_s_memrealtime();
     __syncthreads();
+    if (g0 == ga) trace_mark(pl, a.ws, 35);
     // a group cut by wave ranges: the wave holding its first part adds the rest in wave (= k) order
     if (s < e) {
       const int gl = (e - 1) / NSS;
@@ -506,6 +530,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
   __shared__ int s_nact;
   __shared__ GuChunk s_tab[16];
   __shared__ int s_round[2], s_rowtok[16];
+  __shared__ __attribute__((aligned(16))) int s_prog[kDecWaves];
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int i = l & 15, q = l >> 4;
@@ -815,11 +840,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
     const bool two = g_coff[D] * pl.U8 >= 2 * (int)gridDim.x;
     const bool al = (pl.K / kBlockK) % 16 == 0;
     if (two) {
-      if (al) gu_phase<2, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, D, hbuf);
-      else gu_phase<2, false>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, D, hbuf);
+      if (al) gu_phase<2, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf);
+      else gu_phase<2, false>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf);
     } else {
-      if (al) gu_phase<1, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, D, hbuf);
-      else gu_phase<1, false>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, D, hbuf);
+      if (al) gu_phase<1, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf);
+      else gu_phase<1, false>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf);
     }
   }
   trace_mark(pl, a.ws, 6);
