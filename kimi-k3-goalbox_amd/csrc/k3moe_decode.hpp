@@ -301,12 +301,12 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
     // progress of each wave's range in 1/4096 (empty ranges count as done);
     // visible to the workgroup's other waves after the staging barrier
     if (l == 0) __hip_atomic_store(s_prog + w, s < e ? 0 : 4096, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    // stage the round's activation rows (four rows per pass, every load in flight)
-    for (int r0 = 0; r0 < rows; r0 += 4) {
+    // stage the round's activation rows (eight rows per pass, every load in flight)
+    for (int r0 = 0; r0 < rows; r0 += 8) {
       for (int c0 = 0; c0 < K8; c0 += 2 * kDecThreads) {
-        u32x4 v[4][2];
+        u32x4 v[8][2];
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
+        for (int rr = 0; rr < 8; ++rr) {
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             const int c = c0 + hh * kDecThreads + tid;
@@ -315,7 +315,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
           }
         }
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
+        for (int rr = 0; rr < 8; ++rr) {
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             const int c = c0 + hh * kDecThreads + tid;
@@ -385,20 +385,27 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
     if (s < e) {
       const int gl = (e - 1) / NSS;
       if (gl * NSS >= s && e < (gl + 1) * NSS) {
-        f32x4 sum[W];
+        // the parts of later waves, all reads in flight, added in wave order
+        f32x4 sum[W], part[kDecWaves - 1][W];
+        bool has[kDecWaves - 1];
 #pragma unroll
-        for (int u = 0; u < W; ++u) sum[u] = *reinterpret_cast<const f32x4 *>(slot(w, 1, u));
-        for (int w2 = w + 1; w2 < kDecWaves; ++w2) {
+        for (int j = 0; j < kDecWaves - 1; ++j) {
+          const int w2 = w + 1 + j;
           const int s2 = (int)((long)work * w2 / kDecWaves), e2 = (int)((long)work * (w2 + 1) / kDecWaves);
-          if (s2 >= (gl + 1) * NSS) break;
-          if (e2 > s2) {
+          has[j] = w2 < kDecWaves && s2 < (gl + 1) * NSS && e2 > s2;
 #pragma unroll
-            for (int u = 0; u < W; ++u) {
-              const f32x4 v = *reinterpret_cast<const f32x4 *>(slot(w2, 0, u));
+          for (int u = 0; u < W; ++u)
+            part[j][u] = has[j] ? *reinterpret_cast<const f32x4 *>(slot(w2, 0, u)) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
-              for (int vv = 0; vv < 4; ++vv) sum[u][vv] += v[vv];
+        for (int u = 0; u < W; ++u) {
+          sum[u] = *reinterpret_cast<const f32x4 *>(slot(w, 1, u));
+#pragma unroll
+          for (int j = 0; j < kDecWaves - 1; ++j)
+            if (has[j]) {
+#pragma unroll
+              for (int vv = 0; vv < 4; ++vv) sum[u][vv] += part[j][u][vv];
             }
-          }
         }
         finish(gl, sum);
       }
@@ -653,26 +660,30 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
       }
       __syncthreads();
       trace_mark(pl, a.ws, 10);
-      // one token per pass (E <= 512, k <= 8): every wave sorts 64 of the
-      // (key, ~expert) values with a bitonic network and offers its k best;
-      // wave 0 sorts the 8 k offers and keeps the first k
+      // one token per pass with E <= 512, k <= 8: the 8 waves share its
+      // selection. Wave w sorts experts 64 w .. 64 w + 63 as (key, ~expert)
+      // values with a bitonic network and offers its k best; wave 0 sorts the
+      // 8 k offers and keeps the first k. Otherwise one wave per token runs
+      // wave_topk.
       const bool coop = nt == 1 && E <= kDecWaves * 64 && k <= 8;
-      if (coop) {
-        uint64_t *cand = reinterpret_cast<uint64_t *>(
-            (reinterpret_cast<uintptr_t>(sel + kDecWaves * kMaxTopk) + 7) & ~(uintptr_t)7);  // [8 k]
-        const int e = w * 64 + l;
-        uint64_t v = e < E ? ((uint64_t)kyl[e] << 32) | (uint32_t)~e : 0ull;
-        v = wave_sort_desc(v);
-        if (l < k) cand[w * k + l] = v;
-        __syncthreads();
-        if (w == 0) {
-          uint64_t c = l < kDecWaves * k ? cand[l] : 0ull;
-          c = wave_sort_desc(c);
-          if (l < k) sel[l] = (int)~(uint32_t)c;
-          wave_lds_order();
+      for (int tg = 0; tg < nt; tg += kDecWaves) {
+        if (coop) {
+          uint64_t *cand = reinterpret_cast<uint64_t *>(
+              (reinterpret_cast<uintptr_t>(sel + kDecWaves * kMaxTopk) + 7) & ~(uintptr_t)7);  // [8 k]
+          const int e = w * 64 + l;
+          uint64_t v = e < E ? ((uint64_t)kyl[e] << 32) | (uint32_t)~e : 0ull;
+          v = wave_sort_desc(v);
+          if (l < k) cand[w * k + l] = v;
+          __syncthreads();
+          if (w == 0) {
+            uint64_t c = l < kDecWaves * k ? cand[l] : 0ull;
+            c = wave_sort_desc(c);
+            if (l < k) sel[l] = (int)~(uint32_t)c;
+            wave_lds_order();
+          }
         }
-      }
-      for (int tl = w; tl < nt; tl += kDecWaves) {
+        const int tl = tg + w;
+        if (tl >= nt) continue;
         const int t = t0 + tl;
         int *mysel = sel + w * kMaxTopk;
         if (!coop) wave_topk(kyl + tl * E, E, k, mysel);
