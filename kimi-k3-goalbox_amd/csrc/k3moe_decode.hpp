@@ -937,14 +937,18 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
     float *acc_lds = reinterpret_cast<float *>(scr);  // [8 waves][B][16]
     float *mine = acc_lds + w * B * 16;
     const int da = D * w / kDecWaves, db = D * (w + 1) / kDecWaves;
+    // The wave walks items (expert d, 16-token chunk c, k-steps kc..kc+1) in
+    // order with the next item's loads in flight while the current one runs,
+    // across row tiles too (the next row tile's first item is issued before
+    // the current one's reduction).
+    DnLoad cur, nxt;
+    bool prefetched = false;
     for (int rt = blockIdx.x; rt < pl.RTd; rt += gridDim.x) {
       for (int j = l; j < B * 16; j += 64) mine[j] = 0.f;
       wave_lds_order();
-      // The wave walks items (expert d, 16-token chunk c, k-steps kc..kc+1) in
-      // order with the next item's loads in flight while the current one runs.
-      DnLoad cur, nxt;
       int d = da, c = 0, kc = 0;
-      if (d < db) dn_issue(pl, a, hbuf, g_act, g_aoff, g_acnt, rt, d, c, kc, KB, cur);
+      if (d < db && !prefetched) dn_issue(pl, a, hbuf, g_act, g_aoff, g_acnt, rt, d, c, kc, KB, cur);
+      prefetched = false;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
       while (d < db) {
         int nd = d, nc = c, nkc = kc + kDnDepth;
@@ -955,7 +959,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
             ++nd;
           }
         }
-        if (nd < db) dn_issue(pl, a, hbuf, g_act, g_aoff, g_acnt, rt, nd, nc, nkc, KB, nxt);
+        if (nd < db) {
+          dn_issue(pl, a, hbuf, g_act, g_aoff, g_acnt, rt, nd, nc, nkc, KB, nxt);
+        } else if (rt + (int)gridDim.x < pl.RTd) {
+          dn_issue(pl, a, hbuf, g_act, g_aoff, g_acnt, rt + gridDim.x, da, 0, 0, KB, nxt);
+          prefetched = true;
+        }
 #pragma unroll
         for (int j = 0; j < kDnDepth; ++j) {
           if (kc + j >= pl.KSd) break;
