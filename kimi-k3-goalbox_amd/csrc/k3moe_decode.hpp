@@ -55,9 +55,13 @@ struct DecodeArgs {
 // Grid barrier number `n` (1-based) over gridDim.x workgroups. Arrival is
 // two-level so that no counter sees more than kBarGroups arrivals per
 // barrier: workgroup b counts in on group counter b mod kBarGroups; the last
-// arrival of a group counts the group in on the top counter. Release before
-// arriving, acquire after the top counter shows every group.
+// arrival of a group counts the group in on the top counter. Data that crosses
+// a barrier is written with device-coherent stores (st_dev*), so arriving needs
+// only their completion (every wave waits for its vector memory operations)
+// and a relaxed increment; after the top counter shows every group, an
+// agent-scope acquire invalidates the local L2 for the reads that follow.
 __device__ __forceinline__ void grid_barrier(unsigned *ctl, unsigned n, uint64_t *trace = nullptr) {
+  wait_vmem();  // this wave's device-coherent stores are done
   __syncthreads();
   if (threadIdx.x == 0) {
     const unsigned G = gridDim.x;
@@ -65,7 +69,7 @@ __device__ __forceinline__ void grid_barrier(unsigned *ctl, unsigned n, uint64_t
     const unsigned g = blockIdx.x % groups;
     const unsigned members = (G - g + groups - 1) / groups;  // workgroups b < G with b mod groups == g
     if (trace) trace[0] = __builtin_amdgcn_s_memrealtime();
-    const unsigned old = __hip_atomic_fetch_add(ctl + kCtlGroup + g * kCtlStride, 1u, __ATOMIC_RELEASE,
+    const unsigned old = __hip_atomic_fetch_add(ctl + kCtlGroup + g * kCtlStride, 1u, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
     if (old == n * members - 1u)
       __hip_atomic_fetch_add(ctl + kCtlBar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -208,7 +212,8 @@ __device__ __forceinline__ void gu_finish_wave(const Plan &pl, uint16_t *hbuf, c
 #pragma unroll
     for (int v = 0; v < 4; ++v) hb[v] = f32_to_bf16_bits(apply_act(pl.act, round_bf16(acc[v]), round_bf16(up[v])));
     u32x2 packed = {(uint32_t)hb[0] | ((uint32_t)hb[1] << 16), (uint32_t)hb[2] | ((uint32_t)hb[3] << 16)};
-    *reinterpret_cast<u32x2 *>(hbuf + (size_t)p * pl.I + row0 + 4 * (l >> 4)) = packed;
+    st_dev64(make_rsrc(hbuf, (uint32_t)pl.P * pl.I * 2), (uint32_t)((size_t)p * pl.I + row0 + 4 * (l >> 4)) * 2,
+             packed);
   }
 }
 
@@ -461,7 +466,8 @@ __device__ __forceinline__ void dn_flush(DnStage &st, const Plan &pl, uint16_t *
   for (int c = l; c < 2 * st.fill; c += 64) {
     const int ent = c >> 1, half = c & 1, tag = st.tag[ent];
     const u32x4 v = *reinterpret_cast<const u32x4 *>(st.rows + ent * 16 + half * 8);
-    *reinterpret_cast<u32x4 *>(ybuf + (size_t)(tag >> 16) * pl.K + (tag & 0xFFFF) * 16 + half * 8) = v;
+    st_dev128(make_rsrc(ybuf, (uint32_t)pl.P * pl.K * 2),
+              (uint32_t)((size_t)(tag >> 16) * pl.K + (tag & 0xFFFF) * 16 + half * 8) * 2, v);
   }
   wave_lds_order();
   st.fill = 0;
@@ -599,7 +605,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
         const int tt = j >> 8, ln = (j >> 2) & 63, v = j & 3;
         const int r = 4 * (ln >> 4) + v, c = ln & 15;
         const int t = tt * 16 + c, e = rt * 16 + r;
-        if (t < B) part[((size_t)s * B + t) * pl.Epad + e] = red_sum(red + tt * kDecWaves * 256, j & 255);
+        if (t < B)
+          st_dev32(make_rsrc(part, (uint32_t)(pl.Srw * B * pl.Epad * 4)), (uint32_t)(((size_t)s * B + t) * pl.Epad + e) * 4,
+                   __float_as_uint(red_sum(red + tt * kDecWaves * 256, j & 255)));
       }
       __syncthreads();
     }
@@ -624,38 +632,76 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
     float *scl = kyf + nt * E;                           // [nt][E] scores (sigmoid or logits)
     int *sel = reinterpret_cast<int *>(scl + nt * E);    // [8 waves][kMaxTopk]
     for (int t0 = redundant ? 0 : blockIdx.x; t0 < B; t0 += redundant ? B : gridDim.x) {
-      // logits of (t0 + f / E, f % E): partials summed in split order, four
-      // flat items per thread with every load in flight together
-      for (int f0 = tid; f0 < nt * E; f0 += 4 * kDecThreads) {
-        float ps[4][kDecMaxSplits];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int f = f0 + j * kDecThreads;
-          const int t = t0 + f / E, e = f % E;
-#pragma unroll
-          for (int sp = 0; sp < kDecMaxSplits; ++sp)
-            ps[j][sp] = (f < nt * E && sp < pl.Srw) ? part[((size_t)sp * B + t) * pl.Epad + e] : 0.f;
+      // logits of (t0 + f / E, f % E): partials summed in split order. With
+      // E % 4 == 0 a thread takes 4 consecutive experts of a token per item
+      // group (one 16-byte load per split; partial rows are 64-byte aligned)
+      // and two groups at a time, every load in flight together.
+      auto gate = [&](int f, float logit, float bias) {
+        float score, key;
+        if (pl.gating == K3MOE_GATING_SIGMOID_BIAS) {
+          score = 1.0f / (1.0f + expf(-logit));
+          key = a.bias ? __fadd_rn(score, bias) : score;
+        } else {
+          score = logit;
+          key = logit;
         }
+        scl[f] = score;
+        kyf[f] = key;
+        kyl[f] = ordered_key(key);
+      };
+      if ((E & 3) == 0) {
+        const int NG4 = nt * E / 4;
+        for (int g0 = tid; g0 < NG4; g0 += 2 * kDecThreads) {
+          f32x4 ps[2][kDecMaxSplits];
+          float bv[2][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int f = f0 + j * kDecThreads;
-          if (f >= nt * E) break;
-          float logit = ps[j][0];
+          for (int j = 0; j < 2; ++j) {
+            const int g = g0 + j * kDecThreads;
+            const bool ok = g < NG4;
+            const int f = 4 * (ok ? g : 0), t = t0 + f / E, e = f % E;
 #pragma unroll
-          for (int sp = 1; sp < kDecMaxSplits; ++sp)
-            if (sp < pl.Srw) logit += ps[j][sp];
-          const int e = f % E;
-          float score, key;
-          if (pl.gating == K3MOE_GATING_SIGMOID_BIAS) {
-            score = 1.0f / (1.0f + expf(-logit));
-            key = a.bias ? __fadd_rn(score, a.bias[e]) : score;
-          } else {
-            score = logit;
-            key = logit;
+            for (int sp = 0; sp < kDecMaxSplits; ++sp)
+              ps[j][sp] = (ok && sp < pl.Srw)
+                              ? *reinterpret_cast<const f32x4 *>(part + ((size_t)sp * B + t) * pl.Epad + e)
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) bv[j][v] = (ok && a.bias) ? a.bias[e + v] : 0.f;
           }
-          scl[f] = score;
-          kyf[f] = key;
-          kyl[f] = ordered_key(key);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int g = g0 + j * kDecThreads;
+            if (g >= NG4) break;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              float logit = ps[j][0][v];
+#pragma unroll
+              for (int sp = 1; sp < kDecMaxSplits; ++sp)
+                if (sp < pl.Srw) logit += ps[j][sp][v];
+              gate(4 * g + v, logit, bv[j][v]);
+            }
+          }
+        }
+      } else {
+        for (int f0 = tid; f0 < nt * E; f0 += 4 * kDecThreads) {
+          float ps[4][kDecMaxSplits];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int f = f0 + j * kDecThreads;
+            const int t = t0 + f / E, e = f % E;
+#pragma unroll
+            for (int sp = 0; sp < kDecMaxSplits; ++sp)
+              ps[j][sp] = (f < nt * E && sp < pl.Srw) ? part[((size_t)sp * B + t) * pl.Epad + e] : 0.f;
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int f = f0 + j * kDecThreads;
+            if (f >= nt * E) break;
+            float logit = ps[j][0];
+#pragma unroll
+            for (int sp = 1; sp < kDecMaxSplits; ++sp)
+              if (sp < pl.Srw) logit += ps[j][sp];
+            gate(f, logit, a.bias ? a.bias[f % E] : 0.f);
+          }
         }
       }
       __syncthreads();
@@ -727,8 +773,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
             rid[o] = my_e;
             rw[o] = wt;
           } else {
-            ws_ids[o] = my_e;
-            ws_w[o] = wt;
+            st_dev32(make_rsrc(ws_ids, (uint32_t)pl.P * 4), (uint32_t)o * 4, (uint32_t)my_e);
+            st_dev32(make_rsrc(ws_w, (uint32_t)pl.P * 4), (uint32_t)o * 4, __float_as_uint(wt));
           }
         }
       }

@@ -151,6 +151,26 @@ __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
 // the line must stay in L2 in between: plain loads, not non-temporal ones.
 __device__ __forceinline__ u32x4 load16_nt(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
+// Device-coherent stores (cache policy sc1, the encoding of an agent-scope
+// atomic store): written through past the XCD's L2, so data that other
+// workgroups read after a grid barrier needs no L2 write-back at the barrier,
+// only the completion of the stores (vmcnt). `r` is a buffer resource over
+// the destination array, `off` a byte offset.
+constexpr int kCpolDevice = 16;
+
+__device__ __forceinline__ void st_dev32(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kCpolDevice);
+}
+__device__ __forceinline__ void st_dev64(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, kCpolDevice);
+}
+__device__ __forceinline__ void st_dev128(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCpolDevice);
+}
+
+// Wait until every vector memory operation of this wave has completed.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // ------------------------------------------------------------- activations --
 
 // SiTU (kimi.py:194-196) on bf16-rounded gate/up values, in FP32 with the
