@@ -81,7 +81,7 @@ def read_trace(cfg, device):
     d = torch.empty(cfg.experts, cfg.width, cfg.inter//32, 16, dtype=torch.uint8, device=device)
     r = torch.empty(cfg.experts, cfg.hidden, dtype=torch.bfloat16, device=device)
     total = k3moe.workspace_bytes(moe.dims_for(x, r, g, d, cfg.topk, cfg.gating, cfg.activation))
-    full = ws[total - 1024*48*8: total].cpu().view(torch.int64).view(1024, 48).double()
+    full = ws[total - 1024*56*8: total].cpu().view(torch.int64).view(1024, 56).double()
     G = int((full[:, 8] > 0).sum())
     full = full[:G]
     raw = full[:, :9]
@@ -132,6 +132,12 @@ def read_trace(cfg, device):
         rel = (ends[okw] - full[okw, 33:34])*0.01
         out['gu_stream_end_by_wave_med_us'] = [round(float(rel[:, j].median()), 1) for j in range(8)]
         out['gu_stream_spread_med_us'] = round(float((rel.max(1).values - rel.min(1).values).median()), 1)
+    ends = full[:, 48:56]   # expert-major down: stream end of each wave, relative to barrier 3's exit
+    okw = (ends > 0).all(1) & (ends.min(1).values >= raw[:, 7])
+    if bool(okw.any()):
+        rel = (ends[okw] - full[okw, 7:8])*0.01
+        out['dn_stream_end_by_wave_med_us'] = [round(float(rel[:, j].median()), 1) for j in range(8)]
+        out['dn_stream_end_max_us'] = round(float(rel.max()), 1)
     for n in range(4):   # inside each grid barrier: release+add, spin, acquire
         if float(full[:, 13 + 4*n].max()) <= 0:
             continue

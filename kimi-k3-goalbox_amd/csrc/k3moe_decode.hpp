@@ -93,6 +93,23 @@ __device__ __forceinline__ void grid_barrier(unsigned *ctl, unsigned n, uint64_t
   __syncthreads();
 }
 
+// The memory pipeline serves older waves first, so in a stream split evenly
+// over the waves the younger ones fall behind. Each wave publishes its
+// progress (in 1/4096 of its range) in prog[8] and raises its issue priority
+// while it is behind the workgroup's mean. The branch is wave-uniform:
+// s_setprio ignores the exec mask.
+__device__ __forceinline__ void balance_waves(int *prog, int done, int total) {
+  const int w = threadIdx.x >> 6;
+  const int mine = total > 0 ? done * 4096 / total : 4096;
+  if ((threadIdx.x & 63) == 0) __hip_atomic_store(prog + w, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  const u32x4 p0 = *reinterpret_cast<const volatile u32x4 *>(prog);
+  const u32x4 p1 = *reinterpret_cast<const volatile u32x4 *>(prog + 4);
+  const int sum = (int)(p0[0] + p0[1] + p0[2] + p0[3] + p1[0] + p1[1] + p1[2] + p1[3]);
+  if (__builtin_amdgcn_readfirstlane(mine * kDecWaves < sum ? 1 : 0)) __builtin_amdgcn_s_setprio(2);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 // Trace slots of workgroup blockIdx.x starting at `slot`, or null when not tracing.
 __device__ __forceinline__ uint64_t *trace_slots(const Plan &pl, char *ws, int slot) {
   return pl.o_trace ? reinterpret_cast<uint64_t *>(ws + pl.o_trace) + blockIdx.x * kTraceSlots + slot : nullptr;
@@ -346,19 +363,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
           gu_issue<W, AL>(nxt, iwr, isr, iss, KB);
         }
         gu_compute<W, AL>(cur, xrow, css, KB, acc);
-        // the memory pipeline serves older waves first: a wave behind the
-        // workgroup's mean progress raises its issue priority to catch up
-        {
-          const int mine = (pos + 1 - s) * 4096 / (e - s);
-          if (l == 0) __hip_atomic_store(s_prog + w, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-          const u32x4 p0 = *reinterpret_cast<const volatile u32x4 *>(s_prog);
-          const u32x4 p1 = *reinterpret_cast<const volatile u32x4 *>(s_prog + 4);
-          const int sum = (int)(p0[0] + p0[1] + p0[2] + p0[3] + p1[0] + p1[1] + p1[2] + p1[3]);
-          // wave-uniform (scalar) branch: s_setprio ignores the exec mask
-          if (__builtin_amdgcn_readfirstlane(mine * kDecWaves < sum ? 1 : 0)) __builtin_amdgcn_s_setprio(2);
-          else __builtin_amdgcn_s_setprio(0);
-        }
+        balance_waves(s_prog, pos + 1 - s, e - s);
         if (++css == NSS || pos + 1 == e) {
           const bool started_here = cg * NSS >= s;
           if (started_here && css == NSS) {
@@ -957,6 +962,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
       }
       t += rt1 - rt0;
     }
+    if (pl.o_trace && l == 0)  // every wave's stream end (before its y flush)
+      reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + 48 + w] = __builtin_amdgcn_s_memrealtime();
     dn_flush(st, pl, ybuf);
     trace_mark(pl, a.ws, 9);
     grid_barrier(ctl, ++nbar, trace_slots(pl, a.ws, 24));

@@ -45,7 +45,7 @@ constexpr int kCtlBytes = 4 * (kCtlGroup + kBarGroups * kCtlStride);  // 2176
 // (K <= 16384 activations: 32 KiB + lane offsets).
 constexpr int kZeroBytes = 64 * 1024;
 constexpr int kInitBytes = 4096 + kZeroBytes;  // control block (page-padded) + zero area
-constexpr int kTraceSlots = 48;    // phase timestamps per workgroup when tracing
+constexpr int kTraceSlots = 56;    // phase timestamps per workgroup when tracing
 constexpr int kErrBarrierTimeout = 1;
 
 enum Path { kPathGeneral = 0, kPathDecode = 1 };
