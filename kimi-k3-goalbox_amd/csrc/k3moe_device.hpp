@@ -168,6 +168,13 @@ __device__ __forceinline__ void st_dev128(__amdgpu_buffer_rsrc_t r, uint32_t off
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCpolDevice);
 }
 
+// Address of the next instruction.
+__device__ __forceinline__ uint64_t program_counter() {
+  uint64_t pc;
+  asm volatile("s_getpc_b64 %0" : "=s"(pc));
+  return pc;
+}
+
 // Wait until every vector memory operation of this wave has completed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 

@@ -35,8 +35,10 @@ constexpr int kRedundantTokens = 16;   // decode: route every token in every wor
 constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert) keys
 
 // Control block (uint32 words): top barrier counter, exit counter, sticky
-// error word, then kBarGroups group counters kCtlStride words (128 B) apart.
+// error word, the decode kernel's code range (words 4-7), then kBarGroups
+// group counters kCtlStride words (128 B) apart.
 constexpr int kCtlBar = 0, kCtlExit = 1, kCtlErr = 2;
+constexpr int kCtlCode = 4;  // 2 x uint64: the decode kernel's code range (start, end) of its last launch
 constexpr int kBarGroups = 16, kCtlGroup = 32, kCtlStride = 32;
 constexpr int kCtlBytes = 4 * (kCtlGroup + kBarGroups * kCtlStride);  // 2176
 // A zero area follows the control block: loads of inactive lanes and of k-steps
