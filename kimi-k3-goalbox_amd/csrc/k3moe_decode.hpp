@@ -569,17 +569,22 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
   // workgroups b, b + 8, .. of an XCD cover up to 256 KiB, one 1 KiB chunk per
   // wave). The range is read only if its recorded start is this launch's and
   // never past its recorded end.
+  // The warm-up loads are issued after the router's own loads, so that the
+  // router's waits do not include them.
   uint64_t *crange = reinterpret_cast<uint64_t *>(ctl + kCtlCode);
   const uint64_t pc0 = program_counter();
   u32x4 code_probe = {0, 0, 0, 0};
-  {
+  bool warm = false;
+  auto warm_code = [&]() {
+    if (warm) return;
+    warm = true;
     const uint64_t c0 = crange[0], c1 = crange[1];
     if (c0 == pc0 && c1 > pc0 && c1 - pc0 < (1u << 20)) {
       const uint64_t lo = pc0 & ~(uint64_t)1023;
       const uint64_t addr = lo + (uint64_t)((blockIdx.x >> 3) + 32 * w) * 1024 + l * 16;
       if (addr + 16 <= c1) code_probe = *reinterpret_cast<const volatile u32x4 *>(addr);
     }
-  }
+  };
 
   // ------------------------------------------------------------ R: router --
   // Workgroup unit = (16 router rows, k-split s) for every token tile: the 8
@@ -613,6 +618,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) vb[tt][kk] = tok_ok ? load16(brow + kk * 8) : u32x4{0, 0, 0, 0};
         }
+        warm_code();
 #pragma unroll
         for (int tt = 0; tt < kDecMaxTokens / 16; ++tt) {
           if (tt < pl.TTr) {
@@ -637,6 +643,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
       __syncthreads();
     }
   }
+  warm_code();  // workgroups without router work
   trace_mark(pl, a.ws, 1);
   asm volatile("" ::"v"(code_probe));  // the warm-up loads complete here
   unsigned nbar = 0;  // barriers passed so far (barrier n waits for n * G arrivals)

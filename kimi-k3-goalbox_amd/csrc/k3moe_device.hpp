@@ -31,12 +31,9 @@ __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
 // ---------------------------------------------------------------- bf16 bits --
 
-// FP32 -> BF16 with round-to-nearest-even; NaN -> quiet NaN with the sign kept.
+// FP32 -> BF16 with round-to-nearest-even (the hardware conversion); NaN -> a quiet NaN.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
-  uint32_t rounding = 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)((u + rounding) >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);  // v_cvt_pk_bf16_f32: round to nearest even
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
