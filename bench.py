@@ -116,6 +116,8 @@ def read_trace(cfg, device):
             out.setdefault('sub_phases_med_us', {})[name] = round(float(((y[ok] - x[ok])*0.01).median()), 2)
     sub(0, 31, 'router_loads_mfma')
     sub(31, 1, 'router_reduce_store')
+    sub(2, 44, 'topk_gather_loads')
+    sub(44, 10, 'topk_gather_compute')
     sub(10, 30, 'topk_select_only')
     sub(30, 11, 'topk_weights_ids')
     sub(4, 28, 'group_count')
