@@ -644,6 +644,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
     }
   }
   warm_code();  // workgroups without router work
+  unsigned *ecnt = reinterpret_cast<unsigned *>(a.ws + pl.o_ecnt);  // gate/up units done per active expert
+  {
+    const __amdgpu_buffer_rsrc_t er = make_rsrc(ecnt, (uint32_t)pl.Dmax * 4);
+    for (int j = blockIdx.x * kDecThreads + tid; j < pl.Dmax; j += gridDim.x * kDecThreads) st_dev32(er, j * 4, 0u);
+  }
   trace_mark(pl, a.ws, 1);
   asm volatile("" ::"v"(code_probe));  // the warm-up loads complete here
   unsigned nbar = 0;  // barriers passed so far (barrier n waits for n * G arrivals)
@@ -938,11 +943,39 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
     }
   }
   trace_mark(pl, a.ws, 6);
-  grid_barrier(ctl, ++nbar, trace_slots(pl, a.ws, 20));
+  // Expert-major down needs an expert's h only: instead of a grid barrier,
+  // each workgroup counts the gate/up units it finished per expert (after its
+  // h stores have completed), and a down wave waits for its expert's count.
+  // The row-tile down path needs every expert and keeps the barrier.
+  const bool expert_major = D > kDnExpertMajorMin && pl.I == 256 && pl.o_y;
+  if (expert_major) {
+    wait_vmem();
+    __syncthreads();
+    const int W = g_coff[D] * pl.U8 >= 2 * (int)gridDim.x ? 2 : 1;  // as in the gate/up phase
+    const int NG = g_coff[D] * (pl.U8 / W);
+    const int ga = (int)((long)NG * blockIdx.x / gridDim.x), gb = (int)((long)NG * (blockIdx.x + 1) / gridDim.x);
+    if (ga < gb) {
+      const int ua = ga * W, ub = gb * W;  // this workgroup's units, chunk-major (chunk * U8 + unit)
+      auto expert_of = [&](int ci) {
+        int lo = 0, hi = D - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (g_coff[mid] <= ci) lo = mid; else hi = mid - 1;
+        }
+        return lo;
+      };
+      const int d0 = expert_of(ua / pl.U8), d1 = expert_of((ub - 1) / pl.U8);
+      for (int d = d0 + tid; d <= d1; d += kDecThreads) {
+        const int n = min(ub, g_coff[d + 1] * pl.U8) - max(ua, g_coff[d] * pl.U8);
+        if (n > 0) __hip_atomic_fetch_add(ecnt + d, (unsigned)n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  } else {
+    grid_barrier(ctl, ++nbar, trace_slots(pl, a.ws, 20));
+  }
   trace_mark(pl, a.ws, 7);
 
   // ------------------------------------------------------- DN: down+combine --
-  const bool expert_major = D > kDnExpertMajorMin && pl.I == 256 && pl.o_y;
   if (expert_major) {
     uint16_t *ybuf = reinterpret_cast<uint16_t *>(a.ws + pl.o_y);
     const __amdgpu_buffer_rsrc_t hrs = make_rsrc(hbuf, (uint32_t)pl.P * pl.I * 2);
@@ -968,15 +1001,30 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
         const int ncol = min(16, n - c * 16);
         // lane group q feeds blocks 2q (k-step 0) and 2q+1 (k-step 1) of the h row
         const uint32_t hoff = tok_ok ? (uint32_t)(p0 + pj) * pl.I * 2 + q * 128 : kOffNone;
+        DnTileBatch b0, b1;
+        dnc_issue(b0, pl, wrow, srow, zero, rt0, rt1);  // weights do not depend on h
+        if (c == 0) {  // the expert's gate/up units are all done (bounded wait)
+          const unsigned need = (unsigned)(g_coff[d + 1] - g_coff[d]) * pl.U8;
+          unsigned spins = 0;
+          while (__hip_atomic_load(ecnt + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+            if (++spins > kSpinLimit) {
+              __hip_atomic_store(ctl + kCtlErr, (unsigned)kErrBarrierTimeout, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+          // the h loads below stay after the wait (the hardware issues in
+          // order; this keeps the compiler from hoisting them)
+          asm volatile("" ::: "memory");
+        }
         u32x4 hb[2][4];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           const uint32_t ho = hoff + ks * 64;
 #pragma unroll
-          for (int kk = 0; kk < 4; ++kk) hb[ks][kk] = bload16(hrs, ho + kk * 16);
+          for (int kk = 0; kk < 4; ++kk) hb[ks][kk] = bload16_dev(hrs, ho + kk * 16);  // device-coherent
         }
-        DnTileBatch b0, b1;
-        dnc_issue(b0, pl, wrow, srow, zero, rt0, rt1);
         for (int rt = rt0; rt < rt1; rt += 2 * kDnTiles) {
           const int o1 = rt + kDnTiles - rt0, o2 = rt + 2 * kDnTiles - rt0;
           if (rt + kDnTiles < rt1) dnc_issue(b1, pl, wrow + o1 * tstride, srow + o1 * sstride, zero, rt + kDnTiles, rt1);

@@ -172,6 +172,12 @@ __device__ __forceinline__ uint64_t program_counter() {
   return pc;
 }
 
+// Device-coherent 16-byte load (sc1): sees device-coherent stores of other
+// workgroups without an L2 invalidate.
+__device__ __forceinline__ u32x4 bload16_dev(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kCpolDevice));
+}
+
 // Wait until every vector memory operation of this wave has completed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 

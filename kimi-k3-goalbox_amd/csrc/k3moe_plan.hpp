@@ -73,7 +73,7 @@ struct Plan {
   int redundant;  // 1: every workgroup routes every token (no barrier before grouping)
   // workspace byte offsets
   size_t o_ctl, o_zero, o_logit, o_ids, o_w, o_nact, o_active, o_aoff, o_acnt, o_ptok, o_pw, o_pof, o_gpart, o_gcnt,
-      o_h, o_y, o_trace, total;
+      o_h, o_y, o_ecnt, o_trace, total;
 };
 
 __host__ __device__ inline int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
@@ -178,6 +178,7 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   // pair outputs: the general path, and the decode path's expert-major down (I == 256)
   p.o_y = take((general || p.I == 256) ? (size_t)p.P * p.K * 2 : 0);
   p.trace = trace && p.path == kPathDecode;
+  p.o_ecnt = take((size_t)p.Dmax * 4);  // decode: gate/up units done per active expert
   p.o_trace = p.trace ? take((size_t)1024 * kTraceSlots * 8) : 0;  // last area of the workspace
   p.total = o;
 }
