@@ -292,15 +292,17 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
     const int g1 = min(gb, (ci0 + nch) * GPC);
     const int work = (g1 - g0) * NSS;
     const int s = (int)((long)work * w / kDecWaves), e = (int)((long)work * (w + 1) / kDecWaves);
-    // unit rows of group gg of the round (relative to g0)
+    // unit rows of group gg of the round (relative to g0); lanes 0-7 gate, 8-15 up
+    const uint8_t *const lane_blk = i >= 8 ? a.ublk : a.gblk;
+    const uint8_t *const lane_scl = i >= 8 ? a.uscl : a.gscl;
     auto rows_of = [&](int gg, const uint8_t *(&wr)[W], const uint8_t *(&sr)[W]) {
       const int G = g0 + gg, j = G / GPC - ci0, pg = G % GPC;
       const int ex = tab[j].e;
 #pragma unroll
       for (int u = 0; u < W; ++u) {
         const size_t row = (size_t)ex * pl.I + (pg * W + u) * 8 + (i & 7);
-        wr[u] = (i >= 8 ? a.ublk : a.gblk) + row * KB * 16;
-        sr[u] = (i >= 8 ? a.uscl : a.gscl) + row * KB;
+        wr[u] = lane_blk + row * KB * 16;
+        sr[u] = lane_scl + row * KB;
       }
     };
     auto xrow_of = [&](int gg) {
@@ -534,7 +536,15 @@ __device__ __forceinline__ void dn_issue(const Plan &pl, const DecodeArgs &a, co
   }
 }
 
-__global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeArgs a) {
+static_assert(sizeof(Plan) % alignof(DecodeArgs) == 0, "DecodeArgs follows Plan in the argument segment");
+
+__global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, DecodeArgs a_arg) {
+  // The arguments, read through the touched segment (pl_arg at offset 0, a_arg after it).
+  const uint64_t kargs = touch_kernargs<sizeof(Plan) + sizeof(DecodeArgs)>();
+  const Plan pl = load_const<Plan>(kargs);
+  const DecodeArgs a = load_const<DecodeArgs>(kargs + sizeof(Plan));
+  (void)pl_arg;
+  (void)a_arg;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   float *red = reinterpret_cast<float *>(lds);
   int *g_act = reinterpret_cast<int *>(lds + pl.lds_red);
@@ -1131,10 +1141,13 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl, DecodeAr
   }
 
   // ------------------------------------------------ exit: reset the counters --
+  // A workgroup counts itself out only after its last barrier wait has
+  // returned, so the last to arrive may reset the counters after a relaxed
+  // count; the outputs are published by the kernel's completion.
   __syncthreads();
   trace_mark(pl, a.ws, 8);
   if (tid == 0) {
-    const unsigned old = __hip_atomic_fetch_add(ctl + kCtlExit, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned old = __hip_atomic_fetch_add(ctl + kCtlExit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old == gridDim.x - 1) {
       __hip_atomic_store(ctl + kCtlBar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       for (unsigned g = 0; g < kBarGroups; ++g)
