@@ -656,8 +656,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   warm_code();  // workgroups without router work
   unsigned *ecnt = reinterpret_cast<unsigned *>(a.ws + pl.o_ecnt);  // gate/up units done per active expert
   {
-    const __amdgpu_buffer_rsrc_t er = make_rsrc(ecnt, (uint32_t)pl.Dmax * 4);
-    for (int j = blockIdx.x * kDecThreads + tid; j < pl.Dmax; j += gridDim.x * kDecThreads) st_dev32(er, j * 4, 0u);
+    const __amdgpu_buffer_rsrc_t er = make_rsrc(ecnt, (uint32_t)pl.Dmax * kCntStride * 4);
+    for (int j = blockIdx.x * kDecThreads + tid; j < pl.Dmax; j += gridDim.x * kDecThreads)
+      st_dev32(er, j * kCntStride * 4, 0u);
   }
   trace_mark(pl, a.ws, 1);
   asm volatile("" ::"v"(code_probe));  // the warm-up loads complete here
@@ -953,11 +954,28 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     }
   }
   trace_mark(pl, a.ws, 6);
-  // Expert-major down needs an expert's h only: instead of a grid barrier,
-  // each workgroup counts the gate/up units it finished per expert (after its
-  // h stores have completed), and a down wave waits for its expert's count.
-  // The row-tile down path needs every expert and keeps the barrier.
+  // Expert-major down reads an expert's h only after its gate/up units are
+  // done: instead of a grid barrier, each workgroup counts the gate/up units it
+  // finished per expert (after its h stores have completed), and a down wave
+  // waits for its expert's count. Each count has a 128-byte line of its own:
+  // increments of one line are serialised where they are performed. The
+  // row-tile down path needs every expert in every workgroup and keeps the
+  // barrier (with few experts all workgroups would count on a few lines).
   const bool expert_major = D > kDnExpertMajorMin && pl.I == 256 && pl.o_y;
+  auto wait_expert = [&](int d) {  // bounded: a timeout sets the status word
+    const unsigned need = (unsigned)(g_coff[d + 1] - g_coff[d]) * pl.U8;
+    unsigned spins = 0;
+    while (__hip_atomic_load(ecnt + d * kCntStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(ctl + kCtlErr, (unsigned)kErrBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    // the h loads after the wait stay after it (the hardware issues in
+    // order; this keeps the compiler from hoisting them)
+    asm volatile("" ::: "memory");
+  };
   if (expert_major) {
     wait_vmem();
     __syncthreads();
@@ -977,7 +995,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       const int d0 = expert_of(ua / pl.U8), d1 = expert_of((ub - 1) / pl.U8);
       for (int d = d0 + tid; d <= d1; d += kDecThreads) {
         const int n = min(ub, g_coff[d + 1] * pl.U8) - max(ua, g_coff[d] * pl.U8);
-        if (n > 0) __hip_atomic_fetch_add(ecnt + d, (unsigned)n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (n > 0)
+          __hip_atomic_fetch_add(ecnt + d * kCntStride, (unsigned)n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   } else {
@@ -1013,21 +1032,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
         const uint32_t hoff = tok_ok ? (uint32_t)(p0 + pj) * pl.I * 2 + q * 128 : kOffNone;
         DnTileBatch b0, b1;
         dnc_issue(b0, pl, wrow, srow, zero, rt0, rt1);  // weights do not depend on h
-        if (c == 0) {  // the expert's gate/up units are all done (bounded wait)
-          const unsigned need = (unsigned)(g_coff[d + 1] - g_coff[d]) * pl.U8;
-          unsigned spins = 0;
-          while (__hip_atomic_load(ecnt + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
-            if (++spins > kSpinLimit) {
-              __hip_atomic_store(ctl + kCtlErr, (unsigned)kErrBarrierTimeout, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-              break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-          }
-          // the h loads below stay after the wait (the hardware issues in
-          // order; this keeps the compiler from hoisting them)
-          asm volatile("" ::: "memory");
-        }
+        if (c == 0) wait_expert(d);  // the expert's gate/up units are all done
         u32x4 hb[2][4];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {

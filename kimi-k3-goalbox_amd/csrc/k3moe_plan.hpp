@@ -38,6 +38,7 @@ constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert
 // error word, the decode kernel's code range (words 4-7), then kBarGroups
 // group counters kCtlStride words (128 B) apart.
 constexpr int kCtlBar = 0, kCtlExit = 1, kCtlErr = 2;
+constexpr int kCntStride = 32;  // 32-bit words between per-expert counters: one 128-byte line each
 constexpr int kCtlCode = 4;  // 2 x uint64: the decode kernel's code range (start, end) of its last launch
 constexpr int kBarGroups = 16, kCtlGroup = 32, kCtlStride = 32;
 constexpr int kCtlBytes = 4 * (kCtlGroup + kBarGroups * kCtlStride);  // 2176
@@ -178,7 +179,7 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   // pair outputs: the general path, and the decode path's expert-major down (I == 256)
   p.o_y = take((general || p.I == 256) ? (size_t)p.P * p.K * 2 : 0);
   p.trace = trace && p.path == kPathDecode;
-  p.o_ecnt = take((size_t)p.Dmax * 4);  // decode: gate/up units done per active expert
+  p.o_ecnt = take((size_t)p.Dmax * kCntStride * 4);  // decode: gate/up units done per active expert
   p.o_trace = p.trace ? take((size_t)1024 * kTraceSlots * 8) : 0;  // last area of the workspace
   p.total = o;
 }
