@@ -52,31 +52,49 @@ struct DecodeArgs {
   char *ws;
 };
 
-// Grid barrier number `n` (1-based) over gridDim.x workgroups. Arrival is
-// two-level so that no counter sees more than kBarGroups arrivals per
-// barrier: workgroup b counts in on group counter b mod kBarGroups; the last
-// arrival of a group counts the group in on the top counter. Data that crosses
-// a barrier is written with device-coherent stores (st_dev*), so arriving needs
-// only their completion (every wave waits for its vector memory operations)
-// and a relaxed increment; after the top counter shows every group, an
-// agent-scope acquire invalidates the local L2 for the reads that follow.
-__device__ __forceinline__ void grid_barrier(unsigned *ctl, unsigned n, uint64_t *trace = nullptr) {
-  wait_vmem();  // this wave's device-coherent stores are done
+// Grid barrier number `n` (1-based) of this launch over gridDim.x (a power of
+// two) workgroups. Arrival is two-level so that no counter sees more than
+// kBarGroups arrivals per barrier: workgroup b counts in on group counter
+// b mod kBarGroups; the last arrival of a group counts the group in on the top
+// counter. The counters are never reset: `bb` holds their values before this
+// launch's first barrier, and every count is a power of two, so the 32-bit
+// wrap keeps whole barriers whole. Data that crosses a barrier is written with
+// device-coherent stores (st_dev*), so arriving needs only their completion
+// (every wave waits for its vector memory operations) and a relaxed
+// increment; after the top counter shows every group, an agent-scope acquire
+// invalidates the local L2 for the reads that follow.
+struct BarrierBase {
+  unsigned top, grp;  // the top counter and this workgroup's group counter before barrier 1
+};
+
+__device__ __forceinline__ unsigned bar_groups() { return gridDim.x < kBarGroups ? gridDim.x : kBarGroups; }
+
+// Thread 0, at the kernel's start: no barrier of this launch can complete
+// before this workgroup arrives, so the counters hold whole barriers of
+// earlier launches plus arrivals of this launch's barrier 1 (fewer than a
+// group's members, or fewer than all groups); rounding down removes those.
+__device__ __forceinline__ BarrierBase barrier_base(const unsigned *ctl) {
+  const unsigned groups = bar_groups(), members = gridDim.x / groups, g = blockIdx.x % groups;
+  const unsigned t = __hip_atomic_load(ctl + kCtlTop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned c = __hip_atomic_load(ctl + kCtlGroup + g * kCtlStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return BarrierBase{t & ~(groups - 1u), c & ~(members - 1u)};
+}
+
+__device__ __forceinline__ void grid_barrier(unsigned *ctl, const BarrierBase &bb, unsigned n,
+                                             uint64_t *trace = nullptr) {
+  wait_vmem();  // this wave's device-coherent stores are done (and thread 0's base loads)
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned G = gridDim.x;
-    const unsigned groups = G < kBarGroups ? G : kBarGroups;
-    const unsigned g = blockIdx.x % groups;
-    const unsigned members = (G - g + groups - 1) / groups;  // workgroups b < G with b mod groups == g
+    const unsigned groups = bar_groups(), members = gridDim.x / groups, g = blockIdx.x % groups;
     if (trace) trace[0] = __builtin_amdgcn_s_memrealtime();
     const unsigned old = __hip_atomic_fetch_add(ctl + kCtlGroup + g * kCtlStride, 1u, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
-    if (old == n * members - 1u)
-      __hip_atomic_fetch_add(ctl + kCtlBar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == bb.grp + n * members - 1u)
+      __hip_atomic_fetch_add(ctl + kCtlTop, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (trace) trace[1] = __builtin_amdgcn_s_memrealtime();
-    const unsigned target = n * groups;
+    const unsigned target = bb.top + n * groups;
     unsigned spins = 0;
-    while (__hip_atomic_load(ctl + kCtlBar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+    while ((int)(__hip_atomic_load(ctl + kCtlTop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
       if ((++spins & 63u) == 0u) {
         if (__hip_atomic_load(ctl + kCtlErr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
         if (spins > kSpinLimit) {
@@ -570,6 +588,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   const uint8_t *zero = reinterpret_cast<const uint8_t *>(a.ws + pl.o_zero);  // kZeroBytes of zeros
   const int B = pl.B, E = pl.E, k = pl.k;
   trace_mark(pl, a.ws, 0);
+  // this launch's barrier targets (thread 0 arrives for the workgroup)
+  const BarrierBase bb = tid == 0 ? barrier_base(ctl) : BarrierBase{0u, 0u};
 
   // Code warm-up: a step runs much of this kernel's code once, and after other
   // work has evicted it every new stretch stalls on instruction fetches from
@@ -662,8 +682,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   }
   trace_mark(pl, a.ws, 1);
   asm volatile("" ::"v"(code_probe));  // the warm-up loads complete here
-  unsigned nbar = 0;  // barriers passed so far (barrier n waits for n * G arrivals)
-  grid_barrier(ctl, ++nbar, trace_slots(pl, a.ws, 12));
+  unsigned nbar = 0;  // barriers of this launch passed so far
+  grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 12));
   trace_mark(pl, a.ws, 2);
 
   // -------------------------------------------------------- T: top-k/gating --
@@ -833,7 +853,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   }
   trace_mark(pl, a.ws, 3);
   if (!redundant) {
-    grid_barrier(ctl, ++nbar, trace_slots(pl, a.ws, 16));
+    grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 16));
     for (int p0 = tid; p0 < pl.P; p0 += 4 * kDecThreads) {
       int iv[4];
       float wv[4];
@@ -1000,7 +1020,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       }
     }
   } else {
-    grid_barrier(ctl, ++nbar, trace_slots(pl, a.ws, 20));
+    grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 20));
   }
   trace_mark(pl, a.ws, 7);
 
@@ -1057,7 +1077,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + 48 + w] = __builtin_amdgcn_s_memrealtime();
     dn_flush(st, pl, ybuf);
     trace_mark(pl, a.ws, 9);
-    grid_barrier(ctl, ++nbar, trace_slots(pl, a.ws, 24));
+    grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 24));
     // combine (kimi.py:318,323): expert_sum[t][col] = sum over the token's
     // experts in ascending id order of w * bf16(y), from zero, FP32 adds
     const int K4 = pl.K / 4;
@@ -1145,22 +1165,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     }
   }
 
-  // ------------------------------------------------ exit: reset the counters --
-  // A workgroup counts itself out only after its last barrier wait has
-  // returned, so the last to arrive may reset the counters after a relaxed
-  // count; the outputs are published by the kernel's completion.
+  // ------------------------------------------------------------------ exit --
   __syncthreads();
   trace_mark(pl, a.ws, 8);
-  if (tid == 0) {
-    const unsigned old = __hip_atomic_fetch_add(ctl + kCtlExit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == gridDim.x - 1) {
-      __hip_atomic_store(ctl + kCtlBar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (unsigned g = 0; g < kBarGroups; ++g)
-        __hip_atomic_store(ctl + kCtlGroup + g * kCtlStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ctl + kCtlExit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      crange[0] = pc0;  // this kernel's code range, for the next launch's warm-up
-      crange[1] = program_counter();
-    }
+  if (blockIdx.x == 0 && tid == 0) {  // this kernel's code range, for the next launch's warm-up
+    crange[0] = pc0;
+    crange[1] = program_counter();
   }
 }
 

@@ -4,9 +4,10 @@
 //   decode   B <= 64 tokens: one persistent kernel, one 512-thread workgroup
 //            per CU, phases separated by grid barriers (k3moe_decode.hpp)
 //   general  any B: a chain of six kernels (k3moe_general.hpp)
-// The workspace starts with a control block (kCtlBytes): barrier and exit
-// counters of the persistent kernel and a sticky error word. It must be zero
-// before the first step; every step leaves the counters at zero on exit.
+// The workspace starts with a control block (kCtlBytes): the barrier counters
+// of the persistent kernel and a sticky error word. It must be zero before the
+// first step; the barrier counters only grow (32-bit, wrapping), and each
+// launch takes its barrier targets from their values at its start.
 #pragma once
 
 #include <stddef.h>
@@ -34,14 +35,15 @@ constexpr int kDnStage = 128;        // decode down: y rows staged per wave (32 
 constexpr int kRedundantTokens = 16;   // decode: route every token in every workgroup up to this batch
 constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert) keys
 
-// Control block (uint32 words): top barrier counter, exit counter, sticky
-// error word, the decode kernel's code range (words 4-7), then kBarGroups
-// group counters kCtlStride words (128 B) apart.
-constexpr int kCtlBar = 0, kCtlExit = 1, kCtlErr = 2;
-constexpr int kCntStride = 32;  // 32-bit words between per-expert counters: one 128-byte line each
+// Control block (uint32 words): the sticky error word and the decode kernel's
+// code range (words 4-7) in the first 128-byte line, the top barrier counter
+// in the second, then kBarGroups group counters kCtlStride words (128 B) apart.
+constexpr int kCtlErr = 2;
 constexpr int kCtlCode = 4;  // 2 x uint64: the decode kernel's code range (start, end) of its last launch
-constexpr int kBarGroups = 16, kCtlGroup = 32, kCtlStride = 32;
-constexpr int kCtlBytes = 4 * (kCtlGroup + kBarGroups * kCtlStride);  // 2176
+constexpr int kCtlTop = 32;
+constexpr int kBarGroups = 16, kCtlGroup = 64, kCtlStride = 32;
+constexpr int kCtlBytes = 4 * (kCtlGroup + kBarGroups * kCtlStride);  // 2304
+constexpr int kCntStride = 32;  // 32-bit words between per-expert counters: one 128-byte line each
 // A zero area follows the control block: loads of inactive lanes and of k-steps
 // past a range read it instead of branching. Zeroed with the control block by
 // the workspace init and never written by a step. Holds any row offset used
@@ -131,7 +133,11 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   // choice and the workspace size use the largest router split (srw_cap), so
   // they do not depend on the device's CU count; the split used is smaller
   // when the grid is small.
-  p.G = n_cus > 0 ? (n_cus < 1024 ? n_cus : 1024) : 1;
+  // persistent grid: the largest power of two <= the CU count (at most 1024),
+  // so that the barrier's group and member counts are powers of two and its
+  // wrapping counters stay consistent (MI355X: all 256 CUs)
+  p.G = 1;
+  while (p.G * 2 <= n_cus && p.G * 2 <= 1024) p.G *= 2;
   long base = (long)p.RTr * p.TTr;
   int srw_cap = p.KSr / kDecWaves;
   if (srw_cap > kDecMaxSplits) srw_cap = kDecMaxSplits;

@@ -253,3 +253,40 @@ def test_submission_build_run_matches_moe_step(gpu):
     got3 = run3({('x' if k == 'x' else f'l3_{k}'): v for k, v in inp.items() if v is not None})
     for k in want:
         assert torch.equal(got3[k], want[k]), k
+
+
+@pytest.mark.parametrize('cfg', [configs.TP8_B1, configs.TP8_B8], ids=lambda c: c.name)
+def test_decode_barrier_counters_wrap(gpu, cfg):
+    """The persistent kernel's barrier counters are never reset; they grow by
+    whole barriers and wrap at 2**32. Preset them (consistently) two barriers
+    before the wrap and run steps across it: results equal a fresh workspace's
+    and no barrier times out. A wrong target would only hit the barrier's
+    bounded wait, which sets the status word."""
+    say(f'case: {cfg.name} seed=5, barrier counters preset 2 barriers before the 32-bit wrap')
+    g = to_dev(synthetic.moe_layer_inputs(cfg, 5), gpu)
+    from k3moe.moe import dims_for, workspace_bytes
+    need = workspace_bytes(dims_for(g['x'], g['router'], g['gate_blocks'], g['down_blocks'], cfg.topk, cfg.gating,
+                                    cfg.activation, g.get('latent'), 'decode'))
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    G = 1
+    while G * 2 <= min(cus, 1024):
+        G *= 2                                  # the persistent grid: largest power of two <= CUs
+    groups = min(G, 16)
+    members = G // groups
+    fresh = k3moe.new_workspace(need, gpu)
+    ref = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, path='decode', workspace=fresh)
+    ws = k3moe.new_workspace(need, gpu)
+    ctl = ws[:4096].view(torch.int32)            # control block: top counter word 32, group g at 64 + 32 g
+    ctl[32] = -2 * groups
+    for gi in range(groups):
+        ctl[64 + 32 * gi] = -2 * members
+    torch.cuda.synchronize(gpu)
+    for step in range(4):
+        got = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, path='decode', workspace=ws)
+        torch.cuda.synchronize(gpu)
+        say(f'  step {step}: top counter {int(ctl[32].item()) & 0xFFFFFFFF:#x}')
+        for key in ('expert_sum', 'expert_ids', 'route_weights'):
+            assert torch.equal(got[key], ref[key]), key
+    assert k3moe.workspace_status(ws) == 0
+    assert k3moe.workspace_status(fresh) == 0
+    assert int(ctl[32].item()) & 0xFFFFFFFF < 1 << 16, 'the top counter crossed the wrap'
