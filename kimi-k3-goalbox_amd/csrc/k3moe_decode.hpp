@@ -28,6 +28,10 @@
 // error word and every workgroup runs to the end.
 #pragma once
 
+#include <stddef.h>
+
+#include <type_traits>
+
 #include "k3moe_device.hpp"
 #include "k3moe_general.hpp"
 #include "k3moe_plan.hpp"
@@ -556,11 +560,36 @@ __device__ __forceinline__ void dn_issue(const Plan &pl, const DecodeArgs &a, co
 
 static_assert(sizeof(Plan) % alignof(DecodeArgs) == 0, "DecodeArgs follows Plan in the argument segment");
 
+// The DecodeArgs at constant address `at`; every pointer is device (global) memory.
+__device__ __forceinline__ DecodeArgs load_args(uint64_t at) {
+  DecodeArgs a;
+#define K3_FIELD(f) a.f = global_field<std::remove_pointer_t<decltype(a.f)>>(at + offsetof(DecodeArgs, f))
+  K3_FIELD(x);
+  K3_FIELD(xin);
+  K3_FIELD(router);
+  K3_FIELD(bias);
+  K3_FIELD(gblk);
+  K3_FIELD(gscl);
+  K3_FIELD(ublk);
+  K3_FIELD(uscl);
+  K3_FIELD(dblk);
+  K3_FIELD(dscl);
+  K3_FIELD(routes);
+  K3_FIELD(out);
+  K3_FIELD(out_ids);
+  K3_FIELD(out_w);
+  K3_FIELD(out_short);
+  K3_FIELD(ws);
+#undef K3_FIELD
+  static_assert(sizeof(DecodeArgs) == 16 * sizeof(void *), "every field read");
+  return a;
+}
+
 __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, DecodeArgs a_arg) {
   // The arguments, read through the touched segment (pl_arg at offset 0, a_arg after it).
   const uint64_t kargs = touch_kernargs<sizeof(Plan) + sizeof(DecodeArgs)>();
   const Plan pl = load_const<Plan>(kargs);
-  const DecodeArgs a = load_const<DecodeArgs>(kargs + sizeof(Plan));
+  const DecodeArgs a = load_args(kargs + sizeof(Plan));
   (void)pl_arg;
   (void)a_arg;
   extern __shared__ __attribute__((aligned(16))) char lds[];

@@ -209,6 +209,19 @@ __device__ __forceinline__ T load_const(uint64_t addr) {
   return v;
 }
 
+// The pointer stored at constant-memory address `addr` (the kernel-argument
+// segment), read as a global-memory pointer: the compiler's address-space
+// inference then emits global loads and stores through it and everything
+// derived from it, not flat ones (a flat access also counts as an LDS access,
+// so waits for LDS results would wait for it too).
+template <class T>
+__device__ __forceinline__ T *global_field(uint64_t addr) {
+  typedef T __attribute__((address_space(1))) GT;
+  GT *const __attribute__((address_space(4))) *slot =
+      reinterpret_cast<GT *const __attribute__((address_space(4))) *>(addr);
+  return (T *)*slot;
+}
+
 // Address of the next instruction.
 __device__ __forceinline__ uint64_t program_counter() {
   uint64_t pc;
