@@ -32,7 +32,7 @@ constexpr int kDecMaxLds = 160 * 1024;   // gfx950: 160 KiB of LDS per workgroup
 constexpr int kDecStaticLds = 1024;
 constexpr int kDnStage = 128;        // decode down: y rows staged per wave (32 B + a 4-byte tag each)  // decode kernel's static LDS (round table, counters), upper bound
 
-constexpr int kRedundantTokens = 16;   // decode: route every token in every workgroup up to this batch
+constexpr int kRedundantTokens = 1;    // decode: route every token in every workgroup up to this batch
 constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert) keys
 
 // Control block (uint32 words): the sticky error word and the decode kernel's
