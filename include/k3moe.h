@@ -41,10 +41,17 @@ extern "C" {
 /* Execution path. AUTO runs the single persistent kernel for decode-sized
  * batches (tokens <= 64, tokens*topk <= 1024) and the multi-kernel path
  * otherwise; the other values force one (DECODE fails with K3MOE_EINVAL when
- * the shape does not fit it). Both give the same expert sets. */
+ * the shape does not fit it). All give the same expert sets. The multi-kernel
+ * path (GENERAL) runs the expert projections as grouped GEMMs (weights read
+ * once per 128 tokens of an expert) when the experts average at least 16
+ * tokens and hidden/latent and inter are multiples of 128, and as per-16-token
+ * streams otherwise; GROUPED and STREAMED force one of the two (GROUPED fails
+ * with K3MOE_EINVAL when the widths are not multiples of 128). */
 #define K3MOE_PATH_AUTO 0
 #define K3MOE_PATH_GENERAL 1
 #define K3MOE_PATH_DECODE 2
+#define K3MOE_PATH_GROUPED 3
+#define K3MOE_PATH_STREAMED 4
 
 /* Element type codes. */
 #define K3MOE_DTYPE_BF16 0

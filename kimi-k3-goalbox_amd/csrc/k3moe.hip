@@ -19,6 +19,7 @@
 #include "k3moe_device.hpp"
 #include "k3moe_general.hpp"
 #include "k3moe_plan.hpp"
+#include "k3moe_xgemm.hpp"
 
 using namespace k3moe;
 
@@ -53,8 +54,10 @@ int check_dims(const k3moe_dims *d) {
   if (d->activation != K3MOE_ACT_SITU && d->activation != K3MOE_ACT_SILU)
     return fail(K3MOE_EINVAL, "unknown activation %d", d->activation);
   if (d->x_dtype != K3MOE_DTYPE_BF16) return fail(K3MOE_EINVAL, "x_dtype must be bf16 (%d)", K3MOE_DTYPE_BF16);
-  if (d->path != K3MOE_PATH_AUTO && d->path != K3MOE_PATH_GENERAL && d->path != K3MOE_PATH_DECODE)
-    return fail(K3MOE_EINVAL, "unknown path %d", d->path);
+  if (d->path < K3MOE_PATH_AUTO || d->path > K3MOE_PATH_STREAMED) return fail(K3MOE_EINVAL, "unknown path %d", d->path);
+  if (d->path == K3MOE_PATH_GROUPED && (d->latent % 128 || d->inter % 128))
+    return fail(K3MOE_EINVAL, "the grouped GEMM path needs latent (%d) and inter (%d) multiples of 128", d->latent,
+                d->inter);
   if ((long)d->tokens * d->topk > (1L << 30)) return fail(K3MOE_EINVAL, "tokens*topk too large");
   return K3MOE_OK;
 }
@@ -102,16 +105,27 @@ int launch_check(const char *what) {
 }
 
 // Lets the decode kernel use more than 64 KiB of dynamic LDS (once per process).
-int allow_lds(int bytes) {
-  static int granted = 0;
-  if (bytes <= 65536 || bytes <= granted) return K3MOE_OK;
-  // dynamic + static LDS must fit the 160 KiB of a workgroup
-  const int limit = kDecMaxLds - kDecStaticLds;
-  if (hipFuncSetAttribute(reinterpret_cast<const void *>(&k_moe_decode), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          limit) != hipSuccess)
-    return fail(K3MOE_EHIP, "setting the decode kernel's LDS limit failed: %s", hipGetErrorString(hipGetLastError()));
+// Raises kernel fn's dynamic LDS limit to `limit` bytes (once per kernel and process).
+int grant_lds(const void *fn, int limit, int &granted, const char *what) {
+  if (granted >= limit) return K3MOE_OK;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, limit) != hipSuccess)
+    return fail(K3MOE_EHIP, "setting the %s kernel's LDS limit failed: %s", what, hipGetErrorString(hipGetLastError()));
   granted = limit;
   return K3MOE_OK;
+}
+
+int allow_lds(int bytes) {
+  static int granted = 0;
+  if (bytes <= 65536) return K3MOE_OK;
+  // dynamic + static LDS must fit the 160 KiB of a workgroup
+  return grant_lds(reinterpret_cast<const void *>(&k_moe_decode), kDecMaxLds - kDecStaticLds, granted, "decode");
+}
+
+int allow_xgemm_lds() {
+  static int granted_gu = 0, granted_dn = 0;
+  int rc = grant_lds(reinterpret_cast<const void *>(&k_xgemm<true>), kXLds, granted_gu, "gate/up GEMM");
+  if (!rc) rc = grant_lds(reinterpret_cast<const void *>(&k_xgemm<false>), kXLds, granted_dn, "down GEMM");
+  return rc;
 }
 
 __global__ void k_zero_words(uint32_t *p, int n) {
@@ -218,14 +232,24 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
   if ((rc = launch_check("topk"))) return rc;
   hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, st, p, ws);
   if ((rc = launch_check("group"))) return rc;
-  const long ng = (long)p.Dmax * p.RTg * p.Sg;
-  hipLaunchKernelGGL(k_gateup, dim3(cdiv(ng, kWavesPerBlock)), dim3(kThreads), 0, st, p, xin, gate_blocks,
-                     gate_scales, up_blocks, up_scales, ws);
-  if ((rc = launch_check("gateup"))) return rc;
-  const long nd = (long)p.Dmax * p.RGd;
-  hipLaunchKernelGGL(k_down, dim3(cdiv(nd, kWavesPerBlock)), dim3(kThreads), 0, st, p, down_blocks, down_scales,
-                     ws);
-  if ((rc = launch_check("down"))) return rc;
+  if (p.xgemm) {  // many tokens per expert: grouped GEMMs, weights read once per 128 tokens
+    if ((rc = allow_xgemm_lds())) return rc;
+    hipLaunchKernelGGL(k_xgemm<true>, dim3(p.G), dim3(kXThreads), kXLds, st, p, xin, gate_blocks, gate_scales,
+                       up_blocks, up_scales, ws);
+    if ((rc = launch_check("gate/up GEMM"))) return rc;
+    hipLaunchKernelGGL(k_xgemm<false>, dim3(p.G), dim3(kXThreads), kXLds, st, p,
+                       reinterpret_cast<const uint16_t *>(ws + p.o_h), down_blocks, down_scales, nullptr, nullptr, ws);
+    if ((rc = launch_check("down GEMM"))) return rc;
+  } else {
+    const long ng = (long)p.Dmax * p.RTg * p.Sg;
+    hipLaunchKernelGGL(k_gateup, dim3(cdiv(ng, kWavesPerBlock)), dim3(kThreads), 0, st, p, xin, gate_blocks,
+                       gate_scales, up_blocks, up_scales, ws);
+    if ((rc = launch_check("gateup"))) return rc;
+    const long nd = (long)p.Dmax * p.RGd;
+    hipLaunchKernelGGL(k_down, dim3(cdiv(nd, kWavesPerBlock)), dim3(kThreads), 0, st, p, down_blocks, down_scales,
+                       ws);
+    if ((rc = launch_check("down"))) return rc;
+  }
   const long nc = (long)p.B * (p.K / 4);
   hipLaunchKernelGGL(k_combine, dim3(cdiv(nc, 256)), dim3(256), 0, st, p, ws, expert_sum);
   return launch_check("combine");

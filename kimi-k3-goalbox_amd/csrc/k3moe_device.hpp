@@ -124,6 +124,8 @@ __device__ __forceinline__ void convert_block_fast(const u32x4 &w, uint32_t s, b
   out[3] = fp4x8_to_bf16(w[3], sc);
 }
 
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 &v) { return __builtin_bit_cast(bf16x8, v); }
+
 __device__ __forceinline__ f32x4 mfma16(const bf16x8 &a, const bf16x8 &b, const f32x4 &c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

@@ -15,8 +15,6 @@
 
 namespace k3moe {
 
-__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 &v) { return __builtin_bit_cast(bf16x8, v); }
-
 // a ranks before b: NaN first, then the larger value, then the lower index
 __device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib) {
   const bool na = va != va, nb = vb != vb;

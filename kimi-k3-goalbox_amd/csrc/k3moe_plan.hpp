@@ -22,6 +22,7 @@ constexpr int kThreads = kWavesPerBlock * 64;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopk = 32;
 constexpr int kGroupChunk = 128;   // tokens per placement chunk in k_group
+constexpr int kXMinPairsPerExpert = 16;  // general path: grouped GEMMs from this many token-expert pairs per expert
 
 constexpr int kDecWaves = 8;       // decode path: waves per workgroup
 constexpr int kDecThreads = kDecWaves * 64;
@@ -74,6 +75,7 @@ struct Plan {
   int xpitch;  // staged row pitch in elements (K + 8: rows start in different banks)
   int trace;      // 1: the decode kernel records phase timestamps at o_trace
   int redundant;  // 1: every workgroup routes every token (no barrier before grouping)
+  int xgemm;      // general path: 1 = grouped-GEMM expert kernels, 0 = per-16-token streams
   // workspace byte offsets
   size_t o_ctl, o_zero, o_logit, o_ids, o_w, o_nact, o_active, o_aoff, o_acnt, o_ptok, o_pw, o_pof, o_gpart, o_gcnt,
       o_h, o_y, o_ecnt, o_trace, total;
@@ -144,9 +146,14 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   if (srw_cap < 1) srw_cap = 1;
   p.Srw = srw_cap;
   p.path = kPathGeneral;
-  if (d.path != K3MOE_PATH_GENERAL && p.B <= kDecMaxTokens && p.P <= kDecMaxPairs &&
+  if ((d.path == K3MOE_PATH_AUTO || d.path == K3MOE_PATH_DECODE) && p.B <= kDecMaxTokens && p.P <= kDecMaxPairs &&
       decode_lds(p) <= kDecMaxLds - kDecStaticLds)
     p.path = kPathDecode;
+  // general path expert kernels: grouped GEMMs when the experts average at
+  // least kXMinPairsPerExpert tokens (and the widths allow 128-k steps)
+  const bool widths = p.K % 128 == 0 && p.I % 128 == 0;
+  p.xgemm = d.path == K3MOE_PATH_GROUPED ||
+            (d.path != K3MOE_PATH_STREAMED && widths && (long)p.P >= (long)kXMinPairsPerExpert * p.E);
   p.Srw = (int)(p.G / p.RTr);  // decode router units: (row tile, split), every token tile
   if (p.Srw > srw_cap) p.Srw = srw_cap;
   if (p.Srw < 1) p.Srw = 1;

@@ -142,7 +142,8 @@ def moe_step(x: torch.Tensor, router: torch.Tensor, router_bias: torch.Tensor | 
     written. `out` may supply preallocated output tensors by the same keys;
     `workspace` an initialised workspace (new_workspace), else the device's
     cached one is used. `path` forces an execution path ('auto', 'general',
-    'decode'); the default picks the persistent kernel for decode batches.
+    'decode', or the general path with 'grouped' GEMM or 'streamed' expert
+    kernels); the default picks the persistent kernel for decode batches.
     """
     if fp32:
         raise NotImplementedError('fp32=True is the FP32 truth mode of the CPU oracle; '

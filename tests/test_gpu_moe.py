@@ -290,3 +290,49 @@ def test_decode_barrier_counters_wrap(gpu, cfg):
     assert k3moe.workspace_status(ws) == 0
     assert k3moe.workspace_status(fresh) == 0
     assert int(ctl[32].item()) & 0xFFFFFFFF < 1 << 16, 'the top counter crossed the wrap'
+
+
+# ---- the general path's grouped-GEMM expert kernels (many tokens per expert) ----
+
+GROUPED_B512 = MoEConfig('grouped-b512', 32, 4, 1024, 1024, 512, gating='softmax')  # ~64 tokens per expert
+
+
+@pytest.mark.parametrize('path', ['grouped', 'streamed'])
+def test_general_expert_kernels_plumbing(gpu, path):
+    """Both expert-kernel variants of the general path on the small case (1-2 tokens per expert)."""
+    cfg = configs.CPU_PLUMBING
+    say(f'case: {cfg.name} seed=4 path={path}')
+    run_and_check(cfg, synthetic.moe_layer_inputs(cfg, 4), gpu, path=path)
+
+
+def test_grouped_gemm_b512_sampled_rows(gpu):
+    cfg = GROUPED_B512
+    say(f'case: {cfg.name} seed=2 path=grouped (oracle on 8 sampled rows)')
+    rows = torch.tensor([0, 1, 100, 255, 256, 300, 510, 511])
+    run_and_check(cfg, synthetic.moe_layer_inputs(cfg, 2), gpu, rows=rows, path='grouped')
+
+
+def test_grouped_vs_streamed_b512(gpu):
+    """Same routing kernels, so the expert sets are identical; the two expert-kernel
+    variants differ only in FP32 summation order inside the dot products."""
+    cfg = GROUPED_B512
+    say(f'case: {cfg.name} seed=6, grouped vs streamed expert kernels')
+    g = to_dev(synthetic.moe_layer_inputs(cfg, 6), gpu)
+    outs = {}
+    for path in ('grouped', 'streamed'):
+        outs[path] = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, gating=cfg.gating, path=path)
+        torch.cuda.synchronize(gpu)
+    a, b = outs['grouped'], outs['streamed']
+    assert torch.equal(a['expert_ids'], b['expert_ids'])
+    assert torch.equal(a['route_weights'], b['route_weights'])
+    assert bool(torch.isfinite(a['expert_sum']).all())
+    assert moe_ref.rel_l2(a['expert_sum'].cpu(), b['expert_sum'].cpu()) < 5e-3
+
+
+def test_grouped_gemm_experts_over_128_tokens(gpu):
+    """Forced routes put all 512 tokens on experts 0-3: four 128-token tiles per expert."""
+    cfg = GROUPED_B512
+    say(f'case: {cfg.name} seed=7 path=grouped, every token routed to experts 0-3')
+    routes = torch.tensor([[0, 1, 2, 3], [3, 2, 1, 0]]).repeat(cfg.tokens // 2, 1).contiguous()
+    rows = torch.tensor([0, 127, 128, 129, 255, 383, 384, 511])
+    run_and_check(cfg, synthetic.moe_layer_inputs(cfg, 7), gpu, routes=routes, rows=rows, path='grouped')

@@ -49,8 +49,8 @@ def test_workspace_bytes_for_every_config(name):
 @pytest.mark.parametrize('field,value,msg', [
     ('experts', 0, 'experts'), ('experts', 2000, 'experts'), ('topk', 0, 'topk'), ('topk', 33, 'topk'),
     ('hidden', 100, 'hidden'), ('latent', 48, 'latent'), ('inter', 40, 'inter'), ('gating', 7, 'gating'),
-    ('activation', 9, 'activation'), ('x_dtype', 1, 'x_dtype'), ('path', 7, 'path'),
-    ('tokens', 0, 'tokens')])
+    ('activation', 9, 'activation'), ('x_dtype', 1, 'x_dtype'), ('path', 7, 'path'), ('path', -1, 'path'),
+    ('path', 3, 'grouped GEMM path needs latent'), ('tokens', 0, 'tokens')])
 def test_invalid_dims_are_rejected_with_a_message(field, value, msg):
     d = _native.Dims(tokens=2, experts=16, topk=4, hidden=64, latent=64, inter=64, gating=0, activation=0,
                      x_dtype=0, path=0)
