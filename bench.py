@@ -279,6 +279,24 @@ def cpu_baseline(cfg, host_inputs, reps=3):
     return {'us_per_layer': round(statistics.median(ts)*1e6, 1), 'cores': torch.get_num_threads(), 'reps': reps}
 
 
+MFMA_BF16_DENSE_TFLOPS = 2500.0  # MI355X dense bf16 MFMA peak (the instruction type the GEMMs use)
+
+
+def roofline_entry(head, cfg, layers, measured, workload):
+    """The roofline object of the JSON line: HBM for the decode-sized steps (one persistent kernel),
+    bf16 MFMA for the prefill step (grouped GEMMs; its HBM rate is given beside it)."""
+    if workload == 'prefill':
+        return {'bound': 'mfma', 'kernel': 'k3moe::k_xgemm<gate/up> + k3moe::k_xgemm<down> (grouped GEMMs) '
+                                           'with the router, top-k, grouping and combine kernels',
+                'achieved': head['tflops'], 'peak': MFMA_BF16_DENSE_TFLOPS, 'unit': 'TFLOP/s',
+                'frac': round(head['tflops'] / MFMA_BF16_DENSE_TFLOPS, 4), 'traffic': None,
+                'hbm': {'achieved': head['hbm_GBps'], 'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac']}}
+    return {'bound': 'hbm', 'kernel': 'k3moe::k_moe_decode (the whole step, one launch)',
+            'achieved': head['hbm_GBps'], 'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac'],
+            'traffic': measured.get(cfg.name, {}).get('traffic_bytes') if layers == 1 else None,
+            'traffic_source': TRAFFIC_FILE if measured else None}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
     ap.add_argument('--gpus', type=int, default=1)
@@ -383,10 +401,7 @@ def main():
         'hbm_GBps': head['hbm_GBps'],
         'hbm_frac': head['hbm_frac'],
         'per_batch': results,
-        'roofline': {'bound': 'hbm', 'kernel': 'k3moe::k_moe_decode (the whole step, one launch)',
-                     'achieved': head['hbm_GBps'], 'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac'],
-                     'traffic': measured.get(head_cfg.name, {}).get('traffic_bytes') if head_layers == 1 else None,
-                     'traffic_source': TRAFFIC_FILE if measured else None},
+        'roofline': roofline_entry(head, head_cfg, head_layers, measured, args.workload),
         'cpu_baseline': cpu,
     }
     print(json.dumps(line), flush=True)
