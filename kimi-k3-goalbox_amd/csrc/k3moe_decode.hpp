@@ -261,7 +261,7 @@ template <int W, bool AL>
 __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, float *red, const int *g_act,
                                       const int *g_aoff, const int *g_acnt, const int *g_coff, const int *g_ptok,
                                       uint16_t *xs, GuChunk *tab, int *s_round, int *s_rowtok, int *s_prog, int D,
-                                      uint16_t *hbuf) {
+                                      uint16_t *hbuf, const u32x4 (&xpre)[2], bool xpre_ok) {
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i = l & 15;
   const int KB = pl.K / kBlockK, NSS = (KB + 15) / 16, K8 = pl.K / 8;
   const int GPC = pl.U8 / W;  // groups per chunk
@@ -347,8 +347,17 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
     // progress of each wave's range in 1/4096 (empty ranges count as done);
     // visible to the workgroup's other waves after the staging barrier
     if (l == 0) __hip_atomic_store(s_prog + w, s < e ? 0 : 4096, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    // stage the round's activation rows (eight rows per pass, every load in flight)
-    for (int r0 = 0; r0 < rows; r0 += 8) {
+    // stage the round's activation rows (eight rows per pass, every load in flight);
+    // a single token's row was loaded into xpre after the first barrier (every
+    // staged row of a round is then that token's)
+    for (int r = 0; xpre_ok && r < rows; ++r) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int c = hh * kDecThreads + tid;
+        if (c < K8) *reinterpret_cast<u32x4 *>(xs + (size_t)r * pl.xpitch + c * 8) = xpre[hh];
+      }
+    }
+    for (int r0 = 0; !xpre_ok && r0 < rows; r0 += 8) {
       for (int c0 = 0; c0 < K8; c0 += 2 * kDecThreads) {
         u32x4 v[8][2];
 #pragma unroll
@@ -714,6 +723,19 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   unsigned nbar = 0;  // barriers of this launch passed so far
   grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 12));
   trace_mark(pl, a.ws, 2);
+  // A single token's expert-input row is known from the start: its loads are
+  // issued here and arrive during the top-k and grouping phases; gate/up then
+  // writes it to LDS instead of loading it (two 16-byte chunks per thread, the
+  // chunk mapping of the gate/up staging).
+  const bool xpre_ok = B == 1 && pl.K / 8 <= 2 * kDecThreads;
+  u32x4 xpre[2] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
+  if (xpre_ok) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int c = hh * kDecThreads + tid;
+      if (c < pl.K / 8) xpre[hh] = load16(a.xin + c * 8);
+    }
+  }
 
   // -------------------------------------------------------- T: top-k/gating --
   // Small batches: every workgroup routes every token itself (no barrier, the
@@ -995,11 +1017,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     const bool two = g_coff[D] * pl.U8 >= 2 * (int)gridDim.x;
     const bool al = (pl.K / kBlockK) % 16 == 0;
     if (two) {
-      if (al) gu_phase<2, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf);
-      else gu_phase<2, false>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf);
+      if (al) gu_phase<2, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
+      else gu_phase<2, false>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
     } else {
-      if (al) gu_phase<1, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf);
-      else gu_phase<1, false>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf);
+      if (al) gu_phase<1, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
+      else gu_phase<1, false>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
     }
   }
   trace_mark(pl, a.ws, 6);
