@@ -118,9 +118,10 @@ int k3moe_moe_step(const k3moe_dims *dims,
                    float *shortfall,
                    void *workspace, size_t workspace_bytes, void *stream);
 
-/* Zero the workspace's first 69632 bytes (the control block with the barrier
- * counters and the sticky status word, and a zero area the kernels read in
- * place of inactive data) with a small kernel on `stream`. A workspace must be
+/* Zero the workspace's first 86016 bytes (the control block with the barrier
+ * counters and the sticky status word, a zero area the kernels read in place
+ * of inactive data, and the latent block's row-tile counters) with a small
+ * kernel on `stream`. A workspace must be
  * initialised once before its first step; each step leaves the counters at
  * zero, so one workspace serves any number of consecutive steps on one
  * stream (steps that overlap on one workspace race). No reference
@@ -131,6 +132,58 @@ int k3moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
  * completed normally; 1 = a persistent step's grid barrier timed out, its
  * outputs are invalid). Synchronises `stream`. No reference counterpart. */
 int k3moe_workspace_status(const void *workspace, int32_t *status, void *stream);
+
+/* Geometry of the latent MoE block around the routed experts of a Kimi K3
+ * layer (kimi.py:317, 325-328; weight shapes kimi.py:112-121):
+ *   tokens      B <= 64: rows of x
+ *   hidden      h: width of x and of the block's output (7168)
+ *   latent      lh: width of the experts' input and of expert_sum (3584)
+ *   shared      S: this rank's shared-expert width (intermediate x
+ *               shared_experts / tp: 768 on a TP8 rank)
+ *   activation  K3MOE_ACT_*: the shared experts' activation (SiTU, kimi.py:326)
+ * h, lh and S are multiples of 128. Weights are bf16, row-major:
+ *   latent_down [lh, h]   latent_up [h, lh]   latent_norm [lh]
+ *   shared_gate, shared_up [S, h]             shared_down [h, S]
+ * Both entry points share one workspace (and may share the MoE step's, which
+ * is then sized for the larger of the two); it must be initialised by
+ * k3moe_workspace_init. */
+typedef struct k3moe_latent_dims {
+    int32_t tokens;
+    int32_t hidden;
+    int32_t latent;
+    int32_t shared;
+    int32_t activation; /* K3MOE_ACT_* */
+} k3moe_latent_dims;
+
+/* Device workspace bytes k3moe_latent_in and k3moe_latent_out need for `dims`.
+ * Replaces the temporaries of kimi.py:317, 325-327. */
+int k3moe_latent_workspace_bytes(const k3moe_latent_dims *dims, size_t *bytes);
+
+/* The block's projections of the normalised layer input, before the experts
+ * (kimi.py:317 and the inner part of 326-327, one rank, no all-reduce):
+ *   x          [B, h]   bf16   `normalized`
+ * Outputs (written, never read):
+ *   latent     [B, lh]  bf16   bf16(x @ latent_down.T): the experts' input
+ *                              (k3moe_moe_step's `latent`)
+ *   shared_h   [B, S]   bf16   bf16(act(bf16(x @ shared_gate.T), bf16(x @ shared_up.T)))
+ * FP32 accumulation, rounded where kimi.py:246-247 and 326 cast. */
+int k3moe_latent_in(const k3moe_latent_dims *dims, const void *x, const void *latent_down,
+                    const void *shared_gate, const void *shared_up, void *latent, void *shared_h,
+                    void *workspace, size_t workspace_bytes, void *stream);
+
+/* The block's output from the experts' sum and the shared activation
+ * (kimi.py:325-328, one rank, no all-reduce):
+ *   expert_sum [B, lh]  fp32   k3moe_moe_step's expert_sum
+ *   shared_h   [B, S]   bf16   k3moe_latent_in's shared_h
+ * Output (written, never read):
+ *   out        [B, h]   bf16   bf16(routed + shared) with
+ *                              routed = bf16(rms(bf16(expert_sum), latent_norm, eps 1e-5) @ latent_up.T),
+ *                              rms as common.py:13-21 (normalised value cast
+ *                              to bf16, then times the bf16 weight),
+ *                              shared = bf16(shared_h @ shared_down.T) */
+int k3moe_latent_out(const k3moe_latent_dims *dims, const float *expert_sum, const void *latent_norm,
+                     const void *latent_up, const void *shared_h, const void *shared_down, void *out,
+                     void *workspace, size_t workspace_bytes, void *stream);
 
 /* MXFP4 decode, unpack_mxfp4 (megabench/tasks/quantization.py:40-51) plus the
  * `.to(act)` cast of kimi.py:321: n_blocks blocks of 16 bytes and n_blocks

@@ -18,6 +18,7 @@
 #include "k3moe_decode.hpp"
 #include "k3moe_device.hpp"
 #include "k3moe_general.hpp"
+#include "k3moe_latent.hpp"
 #include "k3moe_plan.hpp"
 #include "k3moe_xgemm.hpp"
 
@@ -126,6 +127,53 @@ int allow_xgemm_lds() {
   int rc = grant_lds(reinterpret_cast<const void *>(&k_xgemm<true>), kXLds, granted_gu, "gate/up GEMM");
   if (!rc) rc = grant_lds(reinterpret_cast<const void *>(&k_xgemm<false>), kXLds, granted_dn, "down GEMM");
   return rc;
+}
+
+int check_latent_dims(const k3moe_latent_dims *d) {
+  if (!d) return fail(K3MOE_EINVAL, "dims is NULL");
+  if (d->tokens < 1 || d->tokens > kLatMaxTokens)
+    return fail(K3MOE_EINVAL, "the latent block takes 1 to %d tokens, got %d", kLatMaxTokens, d->tokens);
+  if (d->hidden < 128 || d->hidden % 128 || d->latent < 128 || d->latent % 128 || d->shared < 128 ||
+      d->shared % 128)
+    return fail(K3MOE_EINVAL, "hidden (%d), latent (%d) and shared (%d) must be positive multiples of 128",
+                d->hidden, d->latent, d->shared);
+  if (d->activation != K3MOE_ACT_SITU && d->activation != K3MOE_ACT_SILU)
+    return fail(K3MOE_EINVAL, "unknown activation %d", d->activation);
+  return K3MOE_OK;
+}
+
+// Plans of both latent kernels (the workspace covers the larger).
+int latent_plans(const k3moe_latent_dims *d, int n_cus, LatPlan &pin, LatPlan &pout) {
+  int rc = check_latent_dims(d);
+  if (rc) return rc;
+  const char *why = latent_plan(*d, n_cus, 0, pin);
+  if (!why) why = latent_plan(*d, n_cus, 1, pout);
+  if (why) return fail(K3MOE_EINVAL, "latent block geometry B=%d h=%d lh=%d S=%d: %s", d->tokens, d->hidden,
+                       d->latent, d->shared, why);
+  return K3MOE_OK;
+}
+
+int allow_latent_lds(int out, int bytes) {
+  static int granted[2] = {0, 0};
+  if (bytes <= 65536) return K3MOE_OK;
+  const void *fn = out ? reinterpret_cast<const void *>(&k_latent<1>) : reinterpret_cast<const void *>(&k_latent<0>);
+  return grant_lds(fn, kLatMaxLds, granted[out], "latent block");
+}
+
+int latent_launch(const k3moe_latent_dims *dims, int out, const LatArgs &a, size_t workspace_bytes, void *stream) {
+  LatPlan pin, pout;
+  int rc = latent_plans(dims, device_cus(), pin, pout);
+  if (rc) return rc;
+  const size_t need = (size_t)(pin.total > pout.total ? pin.total : pout.total);
+  if (!a.ws || workspace_bytes < need)
+    return fail(K3MOE_EWORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(a.ws) % 256) return fail(K3MOE_EWORKSPACE, "workspace must be 256-byte aligned");
+  const LatPlan &p = out ? pout : pin;
+  if ((rc = allow_latent_lds(out, p.lds_total))) return rc;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (out) hipLaunchKernelGGL(k_latent<1>, dim3(p.G), dim3(kLatThreads), p.lds_total, st, p, a);
+  else hipLaunchKernelGGL(k_latent<0>, dim3(p.G), dim3(kLatThreads), p.lds_total, st, p, a);
+  return launch_check(out ? "latent_out" : "latent_in");
 }
 
 __global__ void k_zero_words(uint32_t *p, int n) {
@@ -253,6 +301,50 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
   const long nc = (long)p.B * (p.K / 4);
   hipLaunchKernelGGL(k_combine, dim3(cdiv(nc, 256)), dim3(256), 0, st, p, ws, expert_sum);
   return launch_check("combine");
+}
+
+int k3moe_latent_workspace_bytes(const k3moe_latent_dims *dims, size_t *bytes) {
+  g_err[0] = 0;
+  LatPlan pin, pout;
+  int rc = latent_plans(dims, kDefaultCus, pin, pout);
+  if (rc) return rc;
+  if (!bytes) return fail(K3MOE_EINVAL, "bytes is NULL");
+  *bytes = (size_t)(pin.total > pout.total ? pin.total : pout.total);
+  return K3MOE_OK;
+}
+
+int k3moe_latent_in(const k3moe_latent_dims *dims, const void *x, const void *latent_down, const void *shared_gate,
+                    const void *shared_up, void *latent, void *shared_h, void *workspace, size_t workspace_bytes,
+                    void *stream) {
+  g_err[0] = 0;
+  if (!x || !latent_down || !shared_gate || !shared_up || !latent || !shared_h)
+    return fail(K3MOE_EINVAL, "a required pointer is NULL");
+  LatArgs a{};
+  a.x = reinterpret_cast<const uint16_t *>(x);
+  a.wa = reinterpret_cast<const uint16_t *>(latent_down);
+  a.wb = reinterpret_cast<const uint16_t *>(shared_gate);
+  a.wc = reinterpret_cast<const uint16_t *>(shared_up);
+  a.ya = reinterpret_cast<uint16_t *>(latent);
+  a.yb = reinterpret_cast<uint16_t *>(shared_h);
+  a.ws = reinterpret_cast<char *>(workspace);
+  return latent_launch(dims, 0, a, workspace_bytes, stream);
+}
+
+int k3moe_latent_out(const k3moe_latent_dims *dims, const float *expert_sum, const void *latent_norm,
+                     const void *latent_up, const void *shared_h, const void *shared_down, void *out,
+                     void *workspace, size_t workspace_bytes, void *stream) {
+  g_err[0] = 0;
+  if (!expert_sum || !latent_norm || !latent_up || !shared_h || !shared_down || !out)
+    return fail(K3MOE_EINVAL, "a required pointer is NULL");
+  LatArgs a{};
+  a.x = reinterpret_cast<const uint16_t *>(shared_h);
+  a.esum = expert_sum;
+  a.norm = reinterpret_cast<const uint16_t *>(latent_norm);
+  a.wa = reinterpret_cast<const uint16_t *>(latent_up);
+  a.wb = reinterpret_cast<const uint16_t *>(shared_down);
+  a.ya = reinterpret_cast<uint16_t *>(out);
+  a.ws = reinterpret_cast<char *>(workspace);
+  return latent_launch(dims, 1, a, workspace_bytes, stream);
 }
 
 int k3moe_mxfp4_decode(const uint8_t *blocks, const uint8_t *scales, int64_t n_blocks, int32_t out_dtype,

@@ -240,6 +240,24 @@ __device__ __forceinline__ u32x4 bload16_dev(__amdgpu_buffer_rsrc_t r, uint32_t 
 // Wait until every vector memory operation of this wave has completed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Waits until at most N of this wave's vector memory operations are in flight
+// (direct-to-LDS loads are not tracked by the compiler's own waits).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier for hand-offs through LDS, without the memory fence of
+// __syncthreads (whose release would also wait for the global loads still in
+// flight for later steps). It orders LDS only: each wave's LDS reads and
+// writes before it are complete (lgkmcnt) at it. Data loaded directly to LDS
+// must be waited for (wait_vm) before it.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // ------------------------------------------------------------- activations --
 
 // SiTU (kimi.py:194-196) on bf16-rounded gate/up values, in FP32 with the

@@ -50,7 +50,11 @@ constexpr int kCntStride = 32;  // 32-bit words between per-expert counters: one
 // the workspace init and never written by a step. Holds any row offset used
 // (K <= 16384 activations: 32 KiB + lane offsets).
 constexpr int kZeroBytes = 64 * 1024;
-constexpr int kInitBytes = 4096 + kZeroBytes;  // control block (page-padded) + zero area
+// Then the latent block's arrival counters (one uint32 per output row tile,
+// k3moe_latent.hpp): zero between launches; the launch that completes a tile
+// puts its counter back to zero.
+constexpr int kLatCntBytes = 16384;
+constexpr int kInitBytes = 4096 + kZeroBytes + kLatCntBytes;  // control block (page-padded), zero area, counters
 constexpr int kTraceSlots = 56;    // phase timestamps per workgroup when tracing
 constexpr int kErrBarrierTimeout = 1;
 
@@ -175,6 +179,7 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   auto take = [&](size_t bytes) { size_t at = o; o = align256(o + bytes); return at; };
   p.o_ctl = take(4096);
   p.o_zero = take(kZeroBytes);
+  take(kLatCntBytes);  // the latent block's counters, kept by MoE steps on a shared workspace
   p.o_logit = take((size_t)logit_splits * p.B * p.Epad * 4);
   p.o_ids = take((size_t)p.P * 4);
   p.o_w = take((size_t)p.P * 4);

@@ -42,24 +42,6 @@ constexpr int kXSlotW = 16 * 1024;                      // weight tiles
 constexpr int kXSlot = kXSlotX + kXSlotW + 4 * 256;     // + scales: 50176 bytes
 constexpr int kXLds = kXRing * kXSlot;                  // dynamic LDS, 150528 bytes
 
-// Waits until at most N of this wave's vector memory operations are in flight
-// (direct-to-LDS loads are not tracked by the compiler's own waits).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Workgroup barrier for the ring, without the memory fence of __syncthreads
-// (whose release would also wait for the direct-to-LDS loads still in flight
-// for later k-steps). What the ring needs is explicit: each wave's loads of
-// the step about to be read are waited for (wait_vm) before it, and its LDS
-// reads of the slot about to be refilled are complete (lgkmcnt) at it.
-__device__ __forceinline__ void ring_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // 16 (or 4) bytes per lane from global memory to LDS: lane L's bytes land at
 // dst + L * size; dst is the same for the whole wave.
 template <int Size>

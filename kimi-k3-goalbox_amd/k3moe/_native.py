@@ -31,8 +31,15 @@ class Dims(ctypes.Structure):
                 ('path', ctypes.c_int32)]
 
 
+class LatentDims(ctypes.Structure):
+    """Mirror of k3moe_latent_dims in include/k3moe.h."""
+    _fields_ = [('tokens', ctypes.c_int32), ('hidden', ctypes.c_int32), ('latent', ctypes.c_int32),
+                ('shared', ctypes.c_int32), ('activation', ctypes.c_int32)]
+
+
 EXPORTS = ('k3moe_workspace_bytes', 'k3moe_workspace_init', 'k3moe_workspace_status', 'k3moe_moe_step',
-           'k3moe_mxfp4_decode', 'k3moe_last_error', 'k3moe_version')
+           'k3moe_mxfp4_decode', 'k3moe_last_error', 'k3moe_version', 'k3moe_latent_workspace_bytes',
+           'k3moe_latent_in', 'k3moe_latent_out')
 
 _lib = None
 
@@ -62,6 +69,12 @@ def load(path: str | None = None):
     lib.k3moe_moe_step.restype = ctypes.c_int
     lib.k3moe_mxfp4_decode.argtypes = [p, p, i64, i32, p, p]
     lib.k3moe_mxfp4_decode.restype = ctypes.c_int
+    lib.k3moe_latent_workspace_bytes.argtypes = [ctypes.POINTER(LatentDims), ctypes.POINTER(sz)]
+    lib.k3moe_latent_workspace_bytes.restype = ctypes.c_int
+    lib.k3moe_latent_in.argtypes = [ctypes.POINTER(LatentDims)] + [p]*6 + [p, sz, p]
+    lib.k3moe_latent_in.restype = ctypes.c_int
+    lib.k3moe_latent_out.argtypes = [ctypes.POINTER(LatentDims)] + [p]*6 + [p, sz, p]
+    lib.k3moe_latent_out.restype = ctypes.c_int
     lib.k3moe_last_error.argtypes = []
     lib.k3moe_last_error.restype = ctypes.c_char_p
     lib.k3moe_version.argtypes = []

@@ -19,7 +19,7 @@ from . import _native
 from ._native import ACTIVATION, GATING, Dims, check
 
 MX_BLOCK = 32
-INIT_BYTES = 4096 + 65536  # control block + zero area zeroed by k3moe_workspace_init
+INIT_BYTES = 4096 + 65536 + 16384  # control block, zero area and latent-block counters zeroed by k3moe_workspace_init
 
 
 def _dev_ptr(t: torch.Tensor | None):
@@ -72,11 +72,18 @@ def get_workspace(dims: Dims, device: torch.device) -> torch.Tensor:
     """The cached step workspace of `device`, grown to fit `dims`.
 
     A new workspace is zero-initialised by k3moe_workspace_init (a kernel on
-    the current stream, never a memset). Steps leave its control words at
-    zero, so one workspace serves consecutive steps in stream order; steps
-    that may run concurrently on other streams must pass their own workspace.
+    the current stream, never a memset). Each launch takes its barrier targets
+    from the counters' values at its start and the latent block's tile
+    counters return to zero, so one workspace serves consecutive steps in
+    stream order; steps that may run concurrently on other streams must pass
+    their own workspace.
     """
-    need = max(workspace_bytes(dims), INIT_BYTES)
+    return cached_workspace(workspace_bytes(dims), device)
+
+
+def cached_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """The device's cached workspace, grown to at least `nbytes` (shared by the MoE step and the latent block)."""
+    need = max(int(nbytes), INIT_BYTES)
     key = (device.type, device.index)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < need:

@@ -34,13 +34,14 @@ def seed_for(seed: int, name: str) -> int:
     return int.from_bytes(hashlib.blake2b(f"{seed}:{name}".encode(), digest_size=8).digest(), "little")
 
 
-def randn(seed: int, name: str, shape, scale: float, *, dtype=torch.bfloat16, device='cpu') -> torch.Tensor:
-    """N(0, scale) in float32 cast to dtype (kimi.py:56-58 without the shift)."""
+def randn(seed: int, name: str, shape, scale: float, *, dtype=torch.bfloat16, device='cpu',
+          shift: float = 0.0) -> torch.Tensor:
+    """N(shift, scale) in float32 cast to dtype (kimi.py:56-58)."""
     if str(device).startswith('cuda'):
         g = torch.Generator(device=device).manual_seed(seed_for(seed, name) & ((1 << 63) - 1))
-        return (torch.randn(shape, generator=g, device=device)*scale).to(dtype)
+        return (torch.randn(shape, generator=g, device=device)*scale + shift).to(dtype)
     g = torch.Generator().manual_seed(seed_for(seed, name))
-    return (torch.randn(shape, generator=g)*scale).to(dtype).to(device)
+    return (torch.randn(shape, generator=g)*scale + shift).to(dtype).to(device)
 
 
 def kimi_exponent(fan_in: int) -> int:
@@ -108,3 +109,28 @@ STEP_KEYS = ('x', 'router', 'router_bias', 'gate_blocks', 'gate_scales', 'up_blo
 def step_args(inputs: dict) -> tuple:
     """Positional arguments of k3moe.moe_step (and the oracle's moe_step) from an input dict."""
     return tuple(inputs[k] for k in STEP_KEYS)
+
+
+def latent_block_inputs(cfg, seed: int, *, shared: int, shared_fan: int | None = None, layer: int = 0,
+                        device='cpu', scale_mode: str = 'kimi') -> dict:
+    """Inputs of one latent MoE block (kimi.py:112-121, 317-328) of `cfg` (cfg.latent set).
+
+    The expert tensors and router of moe_layer_inputs, plus latent_down [lh, h],
+    latent_up [h, lh], latent_norm [lh], shared_gate / shared_up [shared, h] and
+    shared_down [h, shared], all bf16 with the reference generator's
+    distributions (kimi.py:134-144): N(0, fan_in^-1/2), norm weights N(1, 0.1).
+    shared_fan is shared_down's fan-in, the unsharded shared width for a TP
+    shard (kimi.py:121: intermediate x shared_experts; 6144 for Kimi K3).
+    `x` is the normalized layer input [B, h]; there is no separate `latent`.
+    """
+    if not cfg.latent:
+        raise ValueError('latent_block_inputs needs a configuration with a latent width')
+    out = moe_layer_inputs(cfg, seed, layer=layer, device=device, scale_mode=scale_mode)
+    out.pop('latent')
+    h, lh, p = cfg.hidden, cfg.latent, f'l{layer}_'
+    for name, shape, fan in (('latent_down', (lh, h), h), ('latent_up', (h, lh), lh),
+                             ('shared_gate', (shared, h), h), ('shared_up', (shared, h), h),
+                             ('shared_down', (h, shared), shared_fan or shared)):
+        out[name] = randn(seed, p + name, shape, fan**-0.5, device=device)
+    out['latent_norm'] = randn(seed, p + 'latent_norm', (lh,), 0.1, shift=1.0, device=device)
+    return out

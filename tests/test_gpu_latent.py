@@ -1,0 +1,195 @@
+"""GPU parity of the latent MoE block (kimi.py:317, 325-328) against the CPU restatement (run with -m gpu).
+
+Bar: every float output within the oracle band rel-L2(gpu, truth) <= 2 rel-L2(bf16
+oracle, truth) + 0.002 (truth = the FP32 mode on the same inputs), elementwise next
+to the BF16 oracle (same rounding points: at most a rounding step apart), expert sets
+exact (or certified FP64 near-ties) in the whole block, no input mutated, repeated
+launches on one workspace bitwise identical. Each test prints its case first.
+"""
+
+import pytest
+import torch
+
+import k3moe
+from k3moe import configs, synthetic
+from k3moe.configs import MoEConfig
+from oracle import grading, latent_ref, moe_ref
+
+pytestmark = pytest.mark.gpu
+
+# (B, h, lh, S): the Kimi K3 TP8 rank (h 7168, latent 3584, shared 768 = 3072 x 2 / 8) at the
+# reference's batches, and small or ragged shapes (token tiles, splits and row tiles partly filled)
+SHAPES = [(1, 7168, 3584, 768), (8, 7168, 3584, 768), (64, 7168, 3584, 768), (3, 256, 128, 128),
+          (17, 512, 256, 128), (33, 1024, 512, 256), (40, 2048, 1024, 384), (1, 128, 128, 128)]
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def block_weights(B, h, lh, S, seed):
+    r = lambda name, shape, scale, **kw: synthetic.randn(seed, name, shape, scale, **kw)
+    return {'x': r('x', (B, h), 1.0), 'latent_down': r('latent_down', (lh, h), h**-0.5),
+            'shared_gate': r('shared_gate', (S, h), h**-0.5), 'shared_up': r('shared_up', (S, h), h**-0.5),
+            'latent_up': r('latent_up', (h, lh), lh**-0.5), 'shared_down': r('shared_down', (h, S), S**-0.5),
+            'latent_norm': r('latent_norm', (lh,), 0.1, shift=1.0),
+            'expert_sum': r('expert_sum', (B, lh), 0.5, dtype=torch.float32)}
+
+
+def near_oracle(got, oracle, steps=1, floor=2e-4):
+    """bf16 values at most `steps` rounding steps (2^-7 relative) from the BF16 oracle, mostly equal.
+
+    The absolute term (floor x the oracle's RMS) covers values that cancel to
+    near zero, where the FP32 sums' different orders, or the roundings of
+    addends, differ by more than the value's own rounding step.
+    """
+    g, o = got.float().cpu(), oracle.float()
+    tol = o.abs()*(steps*2.0**-7) + floor*o.pow(2).mean().sqrt()
+    bad = (g - o).abs() > tol
+    if bool(bad.any()):
+        i = int(((g - o).abs() - tol).flatten().argmax())
+        raise AssertionError(f'{int(bad.sum())} values further than {steps} rounding steps from the oracle; '
+                             f'worst at {i}: {float(g.flatten()[i])} vs {float(o.flatten()[i])}')
+    same = float((g == o).float().mean())
+    assert same >= 0.9, same
+
+
+@pytest.mark.parametrize('B,h,lh,S', SHAPES)
+def test_latent_in_matches_oracle(B, h, lh, S):
+    say(f'latent_in B={B} h={h} lh={lh} S={S}')
+    dev = torch.device('cuda:0')
+    w = block_weights(B, h, lh, S, seed=B + h)
+    g = {k: v.to(dev) for k, v in w.items()}
+    before = grading.snapshot(g)
+    lat, sh = k3moe.latent_in(g['x'], g['latent_down'], g['shared_gate'], g['shared_up'])
+    torch.cuda.synchronize(dev)
+    grading.check_unchanged(g, before)
+    args = (w['x'], w['latent_down'], w['shared_gate'], w['shared_up'])
+    o_lat, o_sh = latent_ref.latent_in(*args)
+    t_lat, t_sh = latent_ref.latent_in(*args, fp32=True)
+    # shared_h = bf16(act(bf16(g), bf16(u))): a flipped rounding of g or u moves the
+    # activation by about one step before its own rounding
+    for name, got, o, t, steps in (('latent', lat, o_lat, t_lat, 1), ('shared_h', sh, o_sh, t_sh, 2)):
+        assert got.dtype == torch.bfloat16
+        detail = grading.band_check(got.cpu(), o, t, t, name=name)
+        say(f'  {name}: {detail}')
+        near_oracle(got, o, steps)
+
+
+@pytest.mark.parametrize('B,h,lh,S', SHAPES)
+def test_latent_out_matches_oracle(B, h, lh, S):
+    say(f'latent_out B={B} h={h} lh={lh} S={S}')
+    dev = torch.device('cuda:0')
+    w = block_weights(B, h, lh, S, seed=B + 2*h)
+    w['shared_h'] = synthetic.randn(B + 2*h, 'shared_h', (B, S), 0.5)
+    keys = ('expert_sum', 'latent_norm', 'latent_up', 'shared_h', 'shared_down')
+    g = {k: w[k].to(dev) for k in keys}
+    before = grading.snapshot(g)
+    out = k3moe.latent_out(*(g[k] for k in keys))
+    torch.cuda.synchronize(dev)
+    grading.check_unchanged(g, before)
+    o = latent_ref.latent_out(*(w[k] for k in keys))
+    t = latent_ref.latent_out(*(w[k] for k in keys), fp32=True)
+    assert out.dtype == torch.bfloat16
+    detail = grading.band_check(out.cpu(), o, t, t, name='output')
+    say(f'  output: {detail}')
+    # the normalised row is rounded twice before the product, and the output is the
+    # rounded sum of two rounded addends (routed + shared): a flipped rounding there
+    # moves an output by a step of the addends, not of the (possibly cancelled) sum
+    near_oracle(out, o, steps=2, floor=2.0**-7)
+
+
+def test_latent_rms_small_expert_sum_uses_epsilon():
+    """An expert sum near 1e-3 makes eps = 1e-5 dominate the RMS (kimi.py:325)."""
+    B, h, lh, S = 2, 256, 128, 128
+    say(f'latent_out tiny expert_sum B={B} h={h} lh={lh} S={S}')
+    dev = torch.device('cuda:0')
+    w = block_weights(B, h, lh, S, seed=5)
+    w['expert_sum'] = w['expert_sum']*2e-3
+    w['shared_h'] = torch.zeros(B, S, dtype=torch.bfloat16)
+    keys = ('expert_sum', 'latent_norm', 'latent_up', 'shared_h', 'shared_down')
+    out = k3moe.latent_out(*(w[k].to(dev) for k in keys)).cpu()
+    o = latent_ref.latent_out(*(w[k] for k in keys))
+    no_eps = latent_ref.latent_out(w['expert_sum']*1e3, *(w[k] for k in keys[1:]))
+    assert moe_ref.rel_l2(out, o) < 0.01
+    # without the epsilon the rows would be scale-free: visibly larger
+    assert float(out.float().abs().mean()) < 0.7*float(no_eps.float().abs().mean())
+
+
+def test_latent_repeated_launches_are_identical():
+    B, h, lh, S = 8, 7168, 3584, 768
+    say(f'latent repeat B={B} h={h} lh={lh} S={S}')
+    dev = torch.device('cuda:0')
+    w = {k: v.to(dev) for k, v in block_weights(B, h, lh, S, seed=3).items()}
+    w['shared_h'] = synthetic.randn(3, 'shared_h', (B, S), 0.5, device=dev)
+    ws = k3moe.new_workspace(32 << 20, dev)
+    first = None
+    for _ in range(4):
+        lat, sh = k3moe.latent_in(w['x'], w['latent_down'], w['shared_gate'], w['shared_up'], workspace=ws)
+        out = k3moe.latent_out(w['expert_sum'], w['latent_norm'], w['latent_up'], w['shared_h'], w['shared_down'],
+                               workspace=ws)
+        got = (lat.clone(), sh.clone(), out.clone())
+        if first is None:
+            first = got
+        else:
+            assert all(torch.equal(a, b) for a, b in zip(first, got))
+    torch.cuda.synchronize(dev)
+    assert k3moe.workspace_status(ws) == 0
+    # the tile counters are back at zero
+    cnt = ws[4096 + 65536:4096 + 65536 + 16384].view(torch.int32)
+    assert int(cnt.abs().sum()) == 0
+
+
+def block_case(cfg, seed, shared, shared_fan=None):
+    return synthetic.latent_block_inputs(cfg, seed, shared=shared, shared_fan=shared_fan)
+
+
+@pytest.mark.parametrize('cfg,shared,seed', [
+    (MoEConfig('latent-small', 64, 8, 1024, 256, 5, latent=512), 256, 0),
+    (MoEConfig('kimi-rank-e128-b8', 128, 16, 7168, 384, 8, latent=3584), 768, 1),
+    (MoEConfig('kimi-rank-e128-b1', 128, 16, 7168, 384, 1, latent=3584), 768, 2),
+])
+def test_latent_block_matches_oracle(cfg, shared, seed):
+    """latent_in -> moe_step on the latent -> latent_out against the restatement of kimi.py:317-328."""
+    run_block(cfg, shared, seed)
+
+
+def test_latent_block_kimi_rank_geometry():
+    """The full Kimi K3 TP8 rank: 896 experts, top-16, I=384, latent 3584, shared 768, B=8."""
+    run_block(configs.KIMI_K3_TP8, 768, 0, shared_fan=6144)
+
+
+def run_block(cfg, shared, seed, shared_fan=None):
+    say(f'latent_block {cfg.name} shared={shared} seed={seed}')
+    dev = torch.device('cuda:0')
+    w = block_case(cfg, seed, shared, shared_fan)
+    g = {k: (v.to(dev) if v is not None else None) for k, v in w.items()}
+    before = grading.snapshot({k: v for k, v in g.items() if v is not None})
+    got = k3moe.latent_block(g['x'], g, topk=cfg.topk)
+    torch.cuda.synchronize(dev)
+    grading.check_unchanged({k: v for k, v in g.items() if v is not None}, before)
+    got = {k: v.cpu() for k, v in got.items()}
+    oracle = latent_ref.latent_block(w['x'], w, topk=cfg.topk)
+    sets = grading.route_sets(got['expert_ids'], oracle['expert_ids'], w['x'], w['router'], w['router_bias'],
+                              cfg.topk)
+    assert sets['ok'], sets
+    truth_o = latent_ref.latent_block(w['x'], w, topk=cfg.topk, fp32=True, routes=oracle['expert_ids'])
+    truth_c = truth_o if sets['exact'] else latent_ref.latent_block(w['x'], w, topk=cfg.topk, fp32=True,
+                                                                    routes=got['expert_ids'])
+    for name in ('latent', 'shared_h', 'expert_sum', 'output'):
+        detail = grading.band_check(got[name], oracle[name], truth_o[name], truth_c[name], name=name)
+        say(f'  {name}: {detail}')
+
+
+def test_latent_moe_layer_reads_reference_keys():
+    cfg = MoEConfig('latent-small', 64, 8, 1024, 256, 4, latent=512)
+    say(f'latent_moe_layer {cfg.name}')
+    dev = torch.device('cuda:0')
+    w = synthetic.latent_block_inputs(cfg, 7, shared=256)
+    x = w.pop('x')
+    values = {f'l3_{k}': (v.to(dev) if v is not None else None) for k, v in w.items()}
+    got = k3moe.latent_moe_layer(values, 3, x.to(dev), topk=cfg.topk)
+    direct = k3moe.latent_block(x.to(dev), {k: values['l3_' + k] for k in w}, topk=cfg.topk)
+    torch.cuda.synchronize(dev)
+    for k in ('output', 'expert_ids', 'expert_sum'):
+        assert torch.equal(got[k], direct[k]), k

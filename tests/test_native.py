@@ -98,3 +98,40 @@ def test_submission_build_validates_the_case():
     run = submission.build(case)
     with pytest.raises(ValueError, match='x must be'):
         run({'x': torch.zeros(3, 64, dtype=torch.bfloat16)})
+
+
+def test_latent_dims_struct_matches_header():
+    text = open(HEADER).read()
+    body = re.search(r'typedef struct k3moe_latent_dims \{(.*?)\} k3moe_latent_dims;', text, flags=re.S).group(1)
+    fields = re.findall(r'int32_t\s+(\w+);', body)
+    assert fields == [f for f, _ in _native.LatentDims._fields_]
+
+
+@pytest.mark.parametrize('B', [1, 8, 64])
+def test_latent_workspace_bytes_kimi_rank(B):
+    from k3moe import latent
+    n = latent.latent_workspace_bytes(latent.latent_dims(B, 7168, 3584, 768))
+    # at least the counters' area and one split's fp32 partials of every output row
+    assert n % 256 == 0 and n >= 4096 + 65536 + 16384 + B*7168*4
+
+
+@pytest.mark.parametrize('dims,msg', [
+    ((0, 7168, 3584, 768), 'tokens'), ((65, 7168, 3584, 768), 'tokens'), ((8, 7100, 3584, 768), 'multiples of 128'),
+    ((8, 7168, 3500, 768), 'multiples of 128'), ((8, 7168, 3584, 0), 'multiples of 128'),
+    ((64, 16384, 8192, 1024), 'does not fit')])
+def test_latent_invalid_dims_are_rejected(dims, msg):
+    from k3moe import latent
+    with pytest.raises(ValueError, match=msg):
+        latent.latent_workspace_bytes(latent.latent_dims(*dims))
+    with pytest.raises(ValueError, match='activation'):
+        latent.latent_dims(8, 7168, 3584, 768, activation='gelu')
+
+
+def test_latent_rejects_host_tensors():
+    from k3moe import latent
+    x = torch.zeros(2, 256, dtype=torch.bfloat16)
+    w = torch.zeros(128, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match='ROCm GPU'):
+        latent.latent_in(x, w, w, w)
+    with pytest.raises(NotImplementedError):
+        latent.latent_block(x, {}, topk=2, fp32=True)

@@ -247,3 +247,94 @@ def test_golden_tiny_case_regression():
     assert np.allclose(bf['route_weights'].numpy(), data['route_weights'], rtol=1e-6, atol=0)
     assert moe_ref.rel_l2(bf['expert_sum'], torch.from_numpy(data['expert_sum_bf16'])) < 1e-6
     assert moe_ref.rel_l2(fp['expert_sum'], torch.from_numpy(data['expert_sum_fp32'])) < 1e-6
+
+
+# ----------------------------------------------------------- latent block --
+
+def latent_case(seed=0, B=3, h=64, lh=32, S=16, E=8, k=2, I=64):
+    from k3moe import synthetic
+    from k3moe.configs import MoEConfig
+    cfg = MoEConfig('tiny-latent', E, k, h, I, B, latent=lh)
+    return cfg, synthetic.latent_block_inputs(cfg, seed, shared=S)
+
+
+@pytest.mark.parametrize('seed', [0, 1])
+def test_latent_in_matches_float64_brute_force(seed):
+    from oracle import latent_ref
+    _, w = latent_case(seed)
+    args = (w['x'], w['latent_down'], w['shared_gate'], w['shared_up'])
+    lat64, sh64 = latent_ref.latent_in_f64(*args)
+    lat, sh = latent_ref.latent_in(*args, fp32=True)
+    assert lat.dtype == sh.dtype == torch.float32
+    assert moe_ref.rel_l2(lat, lat64) < 2e-6 and moe_ref.rel_l2(sh, sh64) < 2e-6
+    lat, sh = latent_ref.latent_in(*args)
+    assert lat.dtype == sh.dtype == torch.bfloat16
+    for got, want in ((lat, lat64), (sh, sh64)):
+        assert 1e-4 < moe_ref.rel_l2(got, want) < 2e-2
+
+
+@pytest.mark.parametrize('seed', [0, 1])
+def test_latent_out_matches_float64_brute_force(seed):
+    from oracle import latent_ref
+    from k3moe import synthetic
+    _, w = latent_case(seed)
+    es = synthetic.randn(seed, 'expert_sum', (3, 32), 0.3, dtype=torch.float32)
+    sh = synthetic.randn(seed, 'shared_h', (3, 16), 0.5, dtype=torch.float32)
+    want = latent_ref.latent_out_f64(es, w['latent_norm'], w['latent_up'], sh, w['shared_down'])
+    got = latent_ref.latent_out(es, w['latent_norm'], w['latent_up'], sh, w['shared_down'], fp32=True)
+    assert got.dtype == torch.float32 and moe_ref.rel_l2(got, want) < 2e-6
+    got = latent_ref.latent_out(es, w['latent_norm'], w['latent_up'], sh.bfloat16(), w['shared_down'])
+    assert got.dtype == torch.bfloat16 and 1e-4 < moe_ref.rel_l2(got, want) < 2e-2
+
+
+def test_latent_rms_epsilon_closed_form():
+    """A constant row c has RMS |c|: the normalized value is c/sqrt(c^2 + 1e-5) (kimi.py:325)."""
+    from oracle import latent_ref
+    for c in (1e-3, 3e-3, 0.5):
+        x = torch.full((2, 64), c)
+        got = latent_ref.rms(x, torch.ones(64), latent_ref.RMS_EPS)
+        assert torch.allclose(got, torch.full_like(got, c/(c*c + 1e-5)**0.5), rtol=1e-6, atol=0)
+    # at c = 1e-3 the epsilon dominates: 0.3015 rather than 1
+    assert abs(float(latent_ref.rms(torch.full((1, 8), 1e-3), torch.ones(8), latent_ref.RMS_EPS)[0, 0]) - 0.30151) < 1e-4
+
+
+def test_latent_planted_mistakes_fail_brute_force(monkeypatch):
+    from oracle import latent_ref
+    from k3moe import synthetic
+    _, w = latent_case(0)
+    lat64, sh64 = latent_ref.latent_in_f64(w['x'], w['latent_down'], w['shared_gate'], w['shared_up'])
+    _, bad = latent_ref.latent_in(w['x'], w['latent_down'], w['shared_up'], w['shared_gate'], fp32=True)
+    assert moe_ref.rel_l2(bad, sh64) > 0.05             # gate and up swapped
+    es = synthetic.randn(0, 'expert_sum', (3, 32), 0.3, dtype=torch.float32)
+    sh = torch.from_numpy(sh64).float()
+    want = latent_ref.latent_out_f64(es, w['latent_norm'], w['latent_up'], sh, w['shared_down'])
+    rms = latent_ref.rms
+    plants = {
+        'norm weight dropped': lambda x, weight, eps: rms(x, torch.ones_like(weight), eps),
+        'mean over tokens': lambda x, weight, eps: (x.float()*torch.rsqrt(x.float().square().mean(0, keepdim=True)
+                                                                         + eps)).to(x.dtype)*weight.to(x.dtype),
+    }
+    for name, fn in plants.items():
+        monkeypatch.setattr(latent_ref, 'rms', fn)
+        got = latent_ref.latent_out(es, w['latent_norm'], w['latent_up'], sh, w['shared_down'], fp32=True)
+        assert moe_ref.rel_l2(got, want) > 0.02, name
+    monkeypatch.setattr(latent_ref, 'rms', rms)
+
+
+@pytest.mark.parametrize('seed', [0, 2])
+def test_latent_block_chains_float64_pieces(seed):
+    """The whole block in FP32 against latent_in_f64 -> moe_step_f64 on the latent -> latent_out_f64."""
+    from oracle import latent_ref
+    cfg, w = latent_case(seed)
+    before = {k: v.clone() for k, v in w.items() if v is not None}
+    r = latent_ref.latent_block(w['x'], w, topk=cfg.topk, fp32=True)
+    assert all(torch.equal(before[k], w[k]) for k in before)
+    lat64, sh64 = latent_ref.latent_in_f64(w['x'], w['latent_down'], w['shared_gate'], w['shared_up'])
+    es64 = moe_ref.moe_step_f64(w['x'], w['router'], w['router_bias'], w['gate_blocks'], w['gate_scales'],
+                                w['up_blocks'], w['up_scales'], w['down_blocks'], w['down_scales'],
+                                routes=r['expert_ids'], weights=r['route_weights'], latent=torch.from_numpy(lat64))
+    out64 = latent_ref.latent_out_f64(torch.from_numpy(es64), w['latent_norm'], w['latent_up'],
+                                      torch.from_numpy(sh64), w['shared_down'])
+    assert moe_ref.rel_l2(r['output'], out64) < 1e-5
+    bf = latent_ref.latent_block(w['x'], w, topk=cfg.topk, routes=r['expert_ids'])
+    assert bf['output'].dtype == torch.bfloat16 and 1e-4 < moe_ref.rel_l2(bf['output'], out64) < 3e-2
