@@ -24,7 +24,14 @@ CPU baseline: the CPU oracle's BF16 MoE step (oracle/moe_ref.py, the
 restatement of megabench/tasks/kimi.py:307-323) on the same inputs on the host
 cores, warmup 1, median of 3.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--workload tp8|tp8-l8|prefill]
+Workload kimi-latent: the whole latent MoE block of a Kimi K3 TP8 rank
+(kimi.py:317-328: latent_down and the shared experts' gate/up, the MoE step on
+the 3584-wide latent with 896 experts top-16 and I=384, then the RMS norm,
+latent_up and shared_down; bf16 weights outside the experts), its three kernels
+timed separately with events between them; CPU baseline: the restatement of the
+block (oracle/latent_ref.py).
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--workload tp8|tp8-l8|prefill|kimi-latent]
 """
 
 from __future__ import annotations
@@ -244,6 +251,98 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, 
             'graph_matches_eager': same, 'host_inputs': [h for _, h in data], 'trace': trace}
 
 
+KIMI_SHARED, KIMI_SHARED_FAN = 768, 6144  # shared-expert width of a TP8 rank (3072 x 2 / 8), unsharded fan-in
+
+
+def measure_latent(cfg, *, seed, steps, warmup, cold, device):
+    """Time the latent block (latent_in, moe_step on the latent, latent_out) with events between
+    its three launches; returns per-stage and whole-block ms per run."""
+    import torch
+    import k3moe
+    from k3moe import synthetic, traffic
+
+    w = synthetic.latent_block_inputs(cfg, seed, shared=KIMI_SHARED, shared_fan=KIMI_SHARED_FAN, device=device)
+    x = w['x']
+    kw = dict(topk=cfg.topk, gating=cfg.gating, activation=cfg.activation)
+    r = k3moe.latent_block(x, w, **kw)
+    torch.cuda.synchronize(device)
+    distinct = int(r['expert_ids'].unique().numel())
+    lat, sh, out = r['latent'], r['shared_h'], r['output']
+    moe_out = {k: r[k] for k in ('expert_sum', 'expert_ids', 'route_weights')}
+    step = synthetic.step_args(dict(w, x=x))
+    stages = [
+        ('latent_in', lambda: k3moe.latent_in(x, w['latent_down'], w['shared_gate'], w['shared_up'],
+                                              out={'latent': lat, 'shared_h': sh})),
+        ('moe_step', lambda: k3moe.moe_step(*step, **kw, latent=lat, out=moe_out)),
+        ('latent_out', lambda: k3moe.latent_out(moe_out['expert_sum'], w['latent_norm'], w['latent_up'], sh,
+                                                w['shared_down'], out=out)),
+    ]
+    flush = torch.ones(1 << 28, dtype=torch.float32, device=device) if cold else None
+    sink = torch.zeros((), dtype=torch.float32, device=device)
+    for _ in range(warmup):
+        if cold:
+            torch.sum(flush, 0, out=sink)
+        for _, f in stages:
+            f()
+    torch.cuda.synchronize(device)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(steps)]
+    for i in range(steps):
+        if cold:
+            torch.sum(flush, 0, out=sink)
+        ev[i][0].record()
+        for j, (_, f) in enumerate(stages):
+            f()
+            ev[i][j + 1].record()
+    torch.cuda.synchronize(device)
+    block_ms = [e[0].elapsed_time(e[-1]) for e in ev]
+    stage_ms = {name: [e[j].elapsed_time(e[j + 1]) for e in ev] for j, (name, _) in enumerate(stages)}
+    same = torch.equal(out, k3moe.latent_block(x, w, **kw)['output'])
+    B, h, lh, S = cfg.tokens, cfg.hidden, cfg.latent, KIMI_SHARED
+    nbytes = {'latent_in': traffic.latent_in_bytes(B=B, h=h, lh=lh, S=S),
+              'moe_step': traffic.step_bytes(B=B, E=cfg.experts, k=cfg.topk, h=h, I=cfg.inter, distinct=distinct,
+                                             K=lh),
+              'latent_out': traffic.latent_out_bytes(B=B, h=h, lh=lh, S=S)}
+    host = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in w.items()}
+    del flush
+    return {'ms': block_ms, 'stage_ms': stage_ms, 'distinct': distinct, 'bytes': sum(nbytes.values()),
+            'stage_bytes': nbytes, 'repeat_matches': same, 'host': host}
+
+
+def summarize_latent(cfg, m):
+    ms_mean = statistics.fmean(m['ms'])
+    gbps = m['bytes']/(ms_mean*1e-3)/1e9
+    stages = {}
+    for name, ms in m['stage_ms'].items():
+        t = statistics.fmean(ms)
+        g = m['stage_bytes'][name]/(t*1e-3)/1e9
+        stages[name] = {'us': round(t*1000, 3), 'us_p50': round(statistics.median(ms)*1000, 3),
+                        'algorithmic_bytes': m['stage_bytes'][name], 'hbm_GBps': round(g, 1),
+                        'hbm_frac': round(g/8000.0, 4)}
+    return {'tokens': cfg.tokens, 'layers': 1, 'us_per_layer': round(ms_mean*1000, 3),
+            'us_per_layer_p50': round(statistics.median(m['ms'])*1000, 3),
+            'us_per_layer_p95': round(percentile(m['ms'], 0.95)*1000, 3), 'distinct_experts': m['distinct'],
+            'algorithmic_bytes': m['bytes'], 'hbm_GBps': round(gbps, 1), 'hbm_frac': round(gbps/8000.0, 4),
+            'stages': stages, 'repeat_matches': m['repeat_matches']}
+
+
+def cpu_baseline_latent(cfg, host, reps=3):
+    """The CPU restatement of the latent block (BF16 mode) on the same inputs (warmup 1, median of reps)."""
+    import torch
+    from oracle import latent_ref
+    cores = len(os.sched_getaffinity(0))
+    share = os.environ.get('OMP_NUM_THREADS', '')
+    if share.isdigit() and int(share) > 0:
+        cores = min(cores, int(share))
+    torch.set_num_threads(cores)
+    latent_ref.latent_block(host['x'], host, topk=cfg.topk)
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        latent_ref.latent_block(host['x'], host, topk=cfg.topk)
+        ts.append(time.perf_counter() - t)
+    return {'us_per_layer': round(statistics.median(ts)*1e6, 1), 'cores': torch.get_num_threads(), 'reps': reps}
+
+
 def summarize(cfg, m, layers):
     ms_mean = statistics.fmean(m['ms'])
     ms_p50 = statistics.median(m['ms'])
@@ -285,6 +384,11 @@ MFMA_BF16_DENSE_TFLOPS = 2500.0  # MI355X dense bf16 MFMA peak (the instruction 
 def roofline_entry(head, cfg, layers, measured, workload):
     """The roofline object of the JSON line: HBM for the decode-sized steps (one persistent kernel),
     bf16 MFMA for the prefill step (grouped GEMMs; its HBM rate is given beside it)."""
+    if workload == 'kimi-latent':
+        return {'bound': 'hbm', 'kernel': 'k3moe::k_latent<0> + k3moe::k_moe_decode + k3moe::k_latent<1> '
+                                          '(the whole block; per-kernel rates in per_batch stages)',
+                'achieved': head['hbm_GBps'], 'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac'],
+                'traffic': None}
     if workload == 'prefill':
         return {'bound': 'mfma', 'kernel': 'k3moe::k_xgemm<gate/up> + k3moe::k_xgemm<down> (grouped GEMMs) '
                                            'with the router, top-k, grouping and combine kernels',
@@ -302,7 +406,7 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=2)
-    ap.add_argument('--workload', default='tp8', choices=['tp8', 'tp8-l8', 'prefill'])
+    ap.add_argument('--workload', default='tp8', choices=['tp8', 'tp8-l8', 'prefill', 'kimi-latent'])
     ap.add_argument('--batches', default='1,8,64', help='batches of the tp8 workload; the first is the headline')
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--warm-cache', action='store_true', help='skip the L2/MALL flush before each replay')
@@ -334,6 +438,10 @@ def main():
     elif args.workload == 'tp8-l8':
         runs = [(configs.TP8_B64_L8, 8, False)]
         workload = 'tp8-rank-b64-8-stacked-layers'
+    elif args.workload == 'kimi-latent':
+        batches = [int(b) for b in args.batches.split(',')]
+        runs = [(configs.KIMI_K3_TP8.with_tokens(b), 1, False) for b in batches]
+        workload = f'kimi-k3-tp8-rank-latent-block-b{batches[0]}'
     else:
         runs = [(configs.PREFILL, 1, False)]
         workload = 'unsharded-prefill-b4096'
@@ -351,10 +459,15 @@ def main():
     results, host = {}, {}
     for cfg, layers, host_gen in runs:
         log(f'bench: {cfg.name} layers={layers} steps={args.steps} warmup={args.warmup} cold={cold}')
-        m = measure(cfg, seed=args.seed, steps=args.steps, warmup=args.warmup, cold=cold, device=device,
-                    layers=layers, host_gen=host_gen, launch=args.launch)
-        results[cfg.name] = summarize(cfg, m, layers)
-        host[cfg.name] = m['host_inputs'][0]
+        if args.workload == 'kimi-latent':
+            m = measure_latent(cfg, seed=args.seed, steps=args.steps, warmup=args.warmup, cold=cold, device=device)
+            results[cfg.name] = summarize_latent(cfg, m)
+            host[cfg.name] = m['host']
+        else:
+            m = measure(cfg, seed=args.seed, steps=args.steps, warmup=args.warmup, cold=cold, device=device,
+                        layers=layers, host_gen=host_gen, launch=args.launch)
+            results[cfg.name] = summarize(cfg, m, layers)
+            host[cfg.name] = m['host_inputs'][0]
         log(f'bench: {cfg.name} {results[cfg.name]}')
         torch.cuda.empty_cache()
 
@@ -365,16 +478,19 @@ def main():
         if name in measured and r['layers'] == 1:
             r['hbm_traffic_bytes'] = measured[name]['traffic_bytes']
     cpu = None
-    if not args.no_cpu_baseline and args.workload == 'tp8':
+    if not args.no_cpu_baseline and args.workload in ('tp8', 'kimi-latent'):
         per = {}
-        for cfg, _, _ in runs:
+        # the latent block's oracle decodes every routed expert (up to 896 at b64): head batch only
+        for cfg, _, _ in (runs[:1] if args.workload == 'kimi-latent' else runs):
             log(f'cpu baseline: {cfg.name}')
-            per[cfg.name] = cpu_baseline(cfg, host[cfg.name])
+            per[cfg.name] = (cpu_baseline_latent if args.workload == 'kimi-latent' else cpu_baseline)(
+                cfg, host[cfg.name])
             results[cfg.name]['cpu_us_per_layer'] = per[cfg.name]['us_per_layer']
         c0 = per[head_cfg.name]
         cpu = {'value': c0['us_per_layer'], 'unit': 'us/layer', 'cores': c0['cores'], 'kind': 'port',
-               'sample': f'{head_cfg.name} seed {args.seed}: one full MoE layer of the CPU oracle '
-                         f'(BF16 mode), median of 3 after 1 warmup; batches '
+               'sample': f'{head_cfg.name} seed {args.seed}: one full '
+                         + ('latent MoE block' if args.workload == 'kimi-latent' else 'MoE layer')
+                         + ' of the CPU oracle (BF16 mode), median of 3 after 1 warmup; batches '
                          + ', '.join(f'{k}: {v["us_per_layer"]} us' for k, v in per.items()),
                'cpu': platform.processor() or platform.machine()}
 

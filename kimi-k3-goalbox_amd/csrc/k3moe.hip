@@ -150,6 +150,11 @@ int latent_plans(const k3moe_latent_dims *d, int n_cus, LatPlan &pin, LatPlan &p
   if (!why) why = latent_plan(*d, n_cus, 1, pout);
   if (why) return fail(K3MOE_EINVAL, "latent block geometry B=%d h=%d lh=%d S=%d: %s", d->tokens, d->hidden,
                        d->latent, d->shared, why);
+  if (trace_enabled()) {  // one trace area for both kernels, the last 1024 x kTraceSlots x 8 bytes
+    const long at = pin.total > pout.total ? pin.total : pout.total;
+    pin.o_trace = pout.o_trace = at;
+    pin.total = pout.total = at + 1024L * kTraceSlots * 8;
+  }
   return K3MOE_OK;
 }
 

@@ -258,6 +258,20 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// 16 (or 4) bytes per lane from global memory to LDS: lane L's bytes land at
+// dst + L * size; dst is the same for the whole wave. Aux is the cache policy
+// (kCpolDevice: a device-coherent read). The compiler counts these loads in
+// vmcnt but does not wait for them before LDS reads: wait_vm first.
+template <int Size, int Aux = 0>
+__device__ __forceinline__ void load_lds(const void *src, char *dst) {
+  static_assert(Size == 16 || Size == 4, "16- or 4-byte lanes");
+  typedef __attribute__((address_space(3))) void lds_void;
+  if constexpr (Size == 16)
+    __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 16, 0, Aux);
+  else
+    __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 4, 0, Aux);
+}
+
 // ------------------------------------------------------------- activations --
 
 // SiTU (kimi.py:194-196) on bf16-rounded gate/up values, in FP32 with the

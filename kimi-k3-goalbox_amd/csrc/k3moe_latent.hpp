@@ -11,33 +11,35 @@
 //
 // Both are skinny bf16 GEMMs: B <= 64 tokens against 10-50 MB weight
 // matrices, HBM-bound, every weight byte read once. The output rows form 16-row
-// tiles (k_latent<0>: latent_down, shared_gate, shared_up rows in turn;
-// k_latent<1>: the h output rows, each with two parts: k over latent_up then
-// k over shared_down, rounded separately). The k axis is cut into SP splits
-// of 128-k steps. Workgroup b takes split s = b mod SP and the row tiles
-// b / SP + j G / SP ("units"):
+// tiles (k_latent<0>: the latent_down rows, then "pair" tiles of 8 shared_gate
+// rows and the same 8 shared_up rows; k_latent<1>: the h output rows, each with
+// two parts: k over latent_up then k over shared_down, rounded separately). The
+// k axis is cut into SP splits of 128-k steps. Workgroup b takes split
+// s = b mod SP and the row tiles b / SP + j G / SP ("units"), so the SP
+// consecutive workgroups of a group share their tiles:
 //   - it stages the activation rows of its split (all tokens) in LDS once;
 //   - the 8 waves take the split's k-steps in turn (wave w: k0 + w, k0 + w + 8),
 //     each loading 16 rows x 128 k of bf16 weights per k-step (64 bytes per
-//     lane) into a register ring three units deep, so the weight stream of
-//     the next two units is in flight while one is multiplied (MFMA
-//     16x16x32 bf16, token tiles of 16 as the B operand from LDS);
+//     lane, 4 loads of 16 rows x 64 contiguous bytes) into a register ring three units deep,
+//     refilled as soon as a unit is multiplied, so three units' weights are in
+//     flight (MFMA 16x16x32 bf16, token tiles of 16 as the B operand from LDS);
 //   - the waves' fp32 tiles meet in LDS (wave order) and the split's partial
 //     of each (token, row) goes to the workspace with device-coherent stores.
-// At the end each workgroup counts its units in on a per-tile counter; the
-// workgroup that completes a tile sums its partials in split order and writes
-// the bf16 outputs (with the activation for a shared gate/up tile pair, which
-// shares one counter), then puts the counter back to zero. k_latent<1> first
-// normalises the expert sum: workgroup t < B computes token t's en row into
-// the workspace (followed by a copy of its shared_h row), while every
-// workgroup already streams its first two units' weights, and a grid barrier
-// separates that from the staging.
+// After its units the group meets at a counter of its own (a barrier of SP
+// workgroups); member s then sums the partials of the group's tiles
+// j = s, s + SP, .. in split order and writes the bf16 outputs (with the
+// activation for a pair tile). k_latent<1> normalises the expert sum first:
+// for up to 8 tokens every workgroup does it itself for its split's k range,
+// for more workgroup t < B writes token t's row to the workspace and a grid
+// barrier separates that from the staging.
 //
 // Accumulation order is fixed (k-step order per wave, wave order, split
 // order), so results do not depend on timing.
 #pragma once
 
 #include <stddef.h>
+
+#include <type_traits>
 
 #include "k3moe_barrier.hpp"
 #include "k3moe_decode.hpp"
@@ -50,12 +52,14 @@ constexpr int kLatMaxTokens = 64;
 constexpr int kLatWaves = 8;
 constexpr int kLatThreads = kLatWaves * 64;
 constexpr int kLatKW = 2;          // k-steps per wave and unit, at most
-constexpr int kLatXChunks = 16;    // 16-byte activation chunks per thread when staging, at most
 constexpr int kLatMaxLds = kDecMaxLds - 1024;  // dynamic LDS (the static LDS stays under 1 KiB)
 constexpr int kLatMaxUnits = 64;   // units per workgroup, at most
 constexpr int kLatMaxSplits = 16;  // k-splits, at most
-constexpr int kLatNormPairs = 8;   // k_latent<1>: expert-sum pairs per thread of a normalising workgroup
+constexpr int kLatLocalNorm = 8;   // k_latent<1>: up to this many tokens every workgroup normalises
+constexpr int kLatNormChunks = 16; // ... from 16-byte chunks, 64 lanes x 16 x 4 = latent widths up to 4096
 constexpr float kLatRmsEps = 1e-5f;  // kimi.py:325
+constexpr int kLatGrpStride = 16;    // words between group counters (64 bytes)
+constexpr unsigned kLatGrpTotal = 1024;  // a group counter grows by this much per launch, whatever SP is
 
 struct LatPlan {
   int B, h, lh, S, act;
@@ -69,8 +73,9 @@ struct LatPlan {
   int kwmax;   // k-steps of the largest split
   int xpitch;  // staged activation row pitch, elements
   int lds_x, lds_total;
-  int ntile0;  // k_latent<0>: latent_down row tiles (the shared tiles follow)
-  long o_cnt, o_part0, o_part1, o_en, total;
+  int ntile0;  // k_latent<0>: latent_down row tiles (the shared pair tiles follow)
+  int local_norm;  // k_latent<1>: every workgroup normalises the expert sum (no grid barrier)
+  long o_cnt, o_part0, o_part1, o_en, o_trace, total;
 };
 
 // The arguments of both kernels.
@@ -96,16 +101,13 @@ inline const char *latent_plan(const k3moe_latent_dims &d, int n_cus, int out, L
   p.G = 1;
   while (p.G * 2 <= n_cus && p.G * 2 <= 1024) p.G *= 2;
   p.ntile0 = p.lh / 16;
-  int ncnt;
   if (!out) {
-    p.RT = (p.lh + 2 * p.S) / 16; p.KS0 = p.KS = p.h / kStepK;
-    ncnt = p.lh / 16 + p.S / 16;
+    p.RT = p.lh / 16 + p.S / 8; p.KS0 = p.KS = p.h / kStepK;
   } else {
     p.RT = p.h / 16; p.KS0 = p.lh / kStepK; p.KS = p.KS0 + p.S / kStepK;
-    ncnt = p.RT;
-    if (p.lh > 2 * kLatNormPairs * kLatThreads || p.S > 2 * kLatNormPairs * kLatThreads)
-      return "latent or shared width too large for the normalisation";
   }
+  p.local_norm = out && p.B <= kLatLocalNorm && p.lh <= 64 * 4 * kLatNormChunks;
+
   const int parts = out ? 2 : 1;
   const int red = parts * p.TT * kLatWaves * 1024;
   p.SP = 0;
@@ -114,7 +116,7 @@ inline const char *latent_plan(const k3moe_latent_dims &d, int n_cus, int out, L
     while (s > p.KS) s >>= 1;  // at least one k-step per split
     const int kw = cdiv(p.KS, s);
     const int lx = p.B * (kw * kStepK + 8) * 2;
-    if (kw <= kLatWaves * kLatKW && p.B * kw <= kLatXChunks * kLatThreads / 16 && lx + red <= kLatMaxLds) p.SP = s;
+    if (kw <= kLatWaves * kLatKW && lx + red <= kLatMaxLds) p.SP = s;
     if (s < sp) break;
   }
   if (!p.SP) return "the staged activation slice does not fit in LDS";
@@ -125,7 +127,7 @@ inline const char *latent_plan(const k3moe_latent_dims &d, int n_cus, int out, L
   p.lds_total = p.lds_x + red;
   p.J = cdiv(p.RT, p.G / p.SP);
   if (p.J > kLatMaxUnits) return "too many row tiles per workgroup";
-  if (ncnt * 4 > kLatCntBytes) return "too many row tiles for the counter area";
+  if ((p.G / p.SP) * kLatGrpStride * 4 > kLatCntBytes) return "too many workgroup groups for the counter area";
   long o = 0;
   auto take = [&](long bytes) { long at = o; o = (long)align256((size_t)(o + bytes)); return at; };
   take(kInitBytes - kLatCntBytes);
@@ -134,18 +136,24 @@ inline const char *latent_plan(const k3moe_latent_dims &d, int n_cus, int out, L
   p.o_part0 = take(part);
   p.o_part1 = out ? take(part) : 0;
   p.o_en = out ? take((long)p.B * (p.lh + p.S) * 2) : 0;
+  p.o_trace = 0;  // a trace area, when wanted, follows the larger of the two kernels' layouts
   p.total = o;
   return nullptr;
 }
 
-// The first bf16 of lane (row i, block q)'s 64 bytes of k-step ks of row tile rt.
-__device__ __forceinline__ const uint16_t *lat_src(const LatPlan &pl, const LatArgs &a, int rt, int ks, int i, int q) {
+// Lane (row i, group q) of k-step ks of row tile rt: MFMA kk of the step takes
+// k = 32 kk + 8 q .. + 7, so the 4 lanes of a row read 64 contiguous bytes per
+// load (half a 128-byte line). Returns the lane's first bf16 (kk = 0). `pair`
+// is this lane's matrix in a <0> pair tile (shared_gate for rows i < 8,
+// shared_up for i >= 8), chosen once per lane by the caller.
+__device__ __forceinline__ const uint16_t *lat_src(const LatPlan &pl, const LatArgs &a, const uint16_t *pair, int rt,
+                                                   int ks, int i, int q) {
   const long r = (long)rt * 16 + i;
-  const int kq = q * 32;
+  const int kq = q * 8;
   if (!pl.out) {
-    const uint16_t *row = r < pl.lh ? a.wa + r * pl.h
-                          : r < pl.lh + pl.S ? a.wb + (r - pl.lh) * pl.h
-                                             : a.wc + (r - pl.lh - pl.S) * pl.h;
+    // pair tile p: rows i < 8 are shared_gate row 8 p + i, rows i >= 8 shared_up row 8 p + i - 8
+    const long sr = 8L * (rt - pl.ntile0) + (i & 7);
+    const uint16_t *row = rt < pl.ntile0 ? a.wa + r * pl.h : pair + sr * pl.h;
     return row + ks * kStepK + kq;
   }
   return ks < pl.KS0 ? a.wa + r * pl.lh + ks * kStepK + kq : a.wb + r * pl.S + (ks - pl.KS0) * kStepK + kq;
@@ -155,131 +163,216 @@ __device__ __forceinline__ float bload4_dev(__amdgpu_buffer_rsrc_t r, uint32_t o
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, kCpolDevice));
 }
 
+static_assert(sizeof(LatPlan) % alignof(LatArgs) == 0, "LatArgs follows LatPlan in the argument segment");
+
+// The LatArgs at constant address `at`; every pointer is device (global) memory.
+__device__ __forceinline__ LatArgs lat_args(uint64_t at) {
+  LatArgs a;
+#define K3_FIELD(f) a.f = global_field<std::remove_pointer_t<decltype(a.f)>>(at + offsetof(LatArgs, f))
+  K3_FIELD(x);
+  K3_FIELD(esum);
+  K3_FIELD(norm);
+  K3_FIELD(wa);
+  K3_FIELD(wb);
+  K3_FIELD(wc);
+  K3_FIELD(ya);
+  K3_FIELD(yb);
+  K3_FIELD(ws);
+#undef K3_FIELD
+  static_assert(sizeof(LatArgs) == 9 * sizeof(void *), "every field read");
+  return a;
+}
+
 template <int OUT>
-__global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl, LatArgs a) {
+__global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatArgs a_arg) {
+  // the arguments, read through the touched segment (all its lines requested at once)
+  const uint64_t kargs = touch_kernargs<sizeof(LatPlan) + sizeof(LatArgs)>();
+  const LatPlan pl = load_const<LatPlan>(kargs);
+  const LatArgs a = lat_args(kargs + sizeof(LatPlan));
+  (void)pl_arg;
+  (void)a_arg;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   uint16_t *xs = reinterpret_cast<uint16_t *>(lds);                 // [B][xpitch] activation slice
   float *red = reinterpret_cast<float *>(lds + pl.lds_x);          // [parts][TT][8 waves][256]
-  __shared__ int s_fin[kLatMaxUnits];
-  __shared__ int s_nfin;
   __shared__ float s_wsum[kLatWaves];
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int i = l & 15, q = l >> 4;
   const int B = pl.B, TT = pl.TT, SP = pl.SP;
-  const int s = blockIdx.x % SP;
-  const int k0 = lat_k0(s, pl.KS, SP), k1 = lat_k0(s + 1, pl.KS, SP), nk = k1 - k0;
-  const int rstep = gridDim.x / SP, rt0 = blockIdx.x / SP;
-  const int J = rt0 < pl.RT ? cdiv(pl.RT - rt0, rstep) : 0;
+  const int lsp = __builtin_ctz(SP), lstep = __builtin_ctz(gridDim.x) - lsp;  // SP and the grid are powers of two
+  const int s = blockIdx.x & (SP - 1);
+  const int k0 = (s * pl.KS) >> lsp, k1 = ((s + 1) * pl.KS) >> lsp, nk = k1 - k0;
+  const int rstep = 1 << lstep, rt0 = blockIdx.x >> lsp;
+  const int J = rt0 < pl.RT ? (pl.RT - rt0 + rstep - 1) >> lstep : 0;
   const bool touch0 = k0 < pl.KS0, touch1 = OUT && k1 > pl.KS0;  // parts with k-steps in this split
+  const bool local = OUT && pl.local_norm;  // <1>: every workgroup normalises the expert sum itself
   unsigned *ctl = reinterpret_cast<unsigned *>(a.ws);
-  unsigned *cnt = reinterpret_cast<unsigned *>(a.ws + pl.o_cnt);
+  unsigned *gcnt = reinterpret_cast<unsigned *>(a.ws + pl.o_cnt) + rt0 * kLatGrpStride;  // this group's counter
   const uint16_t *zlane = reinterpret_cast<const uint16_t *>(a.ws + 4096 + l * 64);  // 64 zero bytes
   const uint32_t part_bytes = (uint32_t)((long)SP * pl.RT * B * 64);
   const __amdgpu_buffer_rsrc_t rp0 = make_rsrc(a.ws + pl.o_part0, part_bytes);
   const __amdgpu_buffer_rsrc_t rp1 = make_rsrc(a.ws + (OUT ? pl.o_part1 : pl.o_part0), part_bytes);
   BarrierBase bb{0u, 0u};
-  if (OUT && tid == 0) bb = barrier_base(ctl);
+  if (OUT && !local && tid == 0) bb = barrier_base(ctl);
+  // the group counter before this launch: no member can have added a whole kLatGrpTotal yet
+  const unsigned gbase =
+      tid == 0 ? __hip_atomic_load(gcnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & ~(kLatGrpTotal - 1u) : 0u;
+  // phase timestamps (100 MHz) when the plan carries a trace area: 0 start, 1 staged,
+  // 2 + j unit j done (j < 40), 45 units done, 46 group met, 47 end; <1>: 48 normalised, 49 barrier
+  auto mark = [&](int n) {
+    if (pl.o_trace && tid == 0)
+      reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + n] = __builtin_amdgcn_s_memrealtime();
+  };
+  mark(0);
 
+  const uint16_t *pair = i < 8 ? a.wb : a.wc;  // <0>: this lane's matrix in a pair tile
   // weight ring: unit j's k-steps of this wave; past the units or the split, the zero area
   auto issue = [&](int j, u32x4 (&buf)[kLatKW][4]) {
     const int rt = rt0 + rstep * j;
 #pragma unroll
     for (int m = 0; m < kLatKW; ++m) {
       const int ks = k0 + w + kLatWaves * m;
-      const uint16_t *src = (j < J && ks < k1) ? lat_src(pl, a, rt, ks, i, q) : zlane;
+      const uint16_t *src = (j < J && ks < k1) ? lat_src(pl, a, pair, rt, ks, i, q) : zlane;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) buf[m][kk] = load16(src + kk * 8);
+      for (int kk = 0; kk < 4; ++kk) buf[m][kk] = load16(src + kk * 32);
     }
   };
 
-  // the activation slice of this split: x (<0>) or [en | shared_h] (<1>), all tokens
-  const int cpt = nk * (kStepK / 8);  // 16-byte chunks per token
-  u32x4 xc[kLatXChunks];
-  const int erow = pl.lh + pl.S;  // <1>: workspace row of a token, [en | shared_h]
-  const __amdgpu_buffer_rsrc_t ren = make_rsrc(a.ws + pl.o_en, OUT ? (uint32_t)(B * erow * 2) : 0u);
-  auto stage_load = [&]() {
-#pragma unroll
-    for (int c = 0; c < kLatXChunks; ++c) {
-      const int idx = tid + c * kLatThreads;
-      const int t = idx / cpt, cc = idx - t * cpt;
+  // The activation slice of this split (all tokens) loaded straight into LDS,
+  // one 16-byte chunk per lane: wave u takes (token t, group g), the chunks
+  // 64 g .. 64 g + 63 of token t's cpt chunks. <0>: x; <1>: [en | shared_h]
+  // from the workspace rows, or with local normalisation the shared_h chunks
+  // only (the normalisation writes the en chunks). Waited for with wait_vm.
+  const int cpt = nk * (kStepK / 8);  // chunks per token
+  const int ngrp = (cpt + 63) >> 6;
+  const int erow = pl.lh + pl.S;      // <1>: workspace row of a token, [en | shared_h]
+  auto stage = [&]() {
+    for (int u = w; u < B * ngrp; u += kLatWaves) {
+      const int t = u / ngrp, g = u - t * ngrp;
+      const int cc = g * 64 + l;
       const int ks = k0 + (cc >> 4), e = (cc & 15) * 8;
-      if (!OUT) {
-        const uint16_t *src = t < B ? a.x + (long)t * pl.h + ks * kStepK + e : zlane;
-        xc[c] = load16(src);
-      } else {
-        xc[c] = bload16_dev(ren, t < B ? (uint32_t)(((long)t * erow + ks * kStepK + e) * 2) : kOffNone);
+      char *dst = reinterpret_cast<char *>(xs + t * pl.xpitch) + g * 64 * 16;
+      if (cc < cpt) {
+        if (!OUT)
+          load_lds<16>(a.x + (long)t * pl.h + ks * kStepK + e, dst);
+        else if (!local)
+          load_lds<16, kCpolDevice>(a.ws + pl.o_en + ((long)t * erow + ks * kStepK + e) * 2, dst);
+        else if (ks >= pl.KS0)
+          load_lds<16>(a.x + (long)t * pl.S + (ks - pl.KS0) * kStepK + e, dst);
       }
     }
   };
-  auto stage_store = [&]() {
-#pragma unroll
-    for (int c = 0; c < kLatXChunks; ++c) {
-      const int idx = tid + c * kLatThreads;
-      const int t = idx / cpt, cc = idx - t * cpt;
-      if (t < B) *reinterpret_cast<u32x4 *>(xs + t * pl.xpitch + cc * 8) = xc[c];
-    }
-  };
+  constexpr int kRingLoads = 3 * kLatKW * 4;  // weight loads of the three prologue units, per wave
 
   u32x4 b0[kLatKW][4], b1[kLatKW][4], b2[kLatKW][4];
   if (!OUT) {
-    stage_load();  // first, so that its wait below does not include the weight loads
+    stage();  // first, so that its wait below does not include the weight loads
     issue(0, b0);
     issue(1, b1);
-    stage_store();
+    issue(2, b2);
+    wait_vm<kRingLoads>();
     ring_barrier();
-  } else {
-    // Workgroup t < B normalises token t's expert sum: en = bf16(bf16(e r) w),
-    // e = bf16(expert_sum), r = 1/sqrt(mean(e^2) + eps), and writes the
-    // workspace row [en | shared_h] the splits stage from. Its loads go first,
-    // then the first two units' weight loads.
-    const bool norm_wg = (int)blockIdx.x < B;
-    const int t = norm_wg ? (int)blockIdx.x : 0;
-    float2 ev[kLatNormPairs];
-    uint32_t wv[kLatNormPairs], hv[kLatNormPairs];
-    if (norm_wg) {
+  } else if (local) {
+    // Small batches: wave t < B normalises token t in every workgroup, from
+    // 16-byte chunks k = 4 (l + 64 m) of its expert-sum row:
+    //   en = bf16(bf16(e r) w), e = bf16(expert_sum), r = 1/sqrt(mean(e^2) + eps),
+    // and writes the chunks in this split's latent range to the slice. The
+    // expert sum, the norm weights of the range and the shared_h chunks are
+    // loaded before the first units' weights.
+    const int t = w;
+    const int kr0 = k0 * kStepK, kr1 = (touch0 ? (k1 < pl.KS0 ? k1 : pl.KS0) : k0) * kStepK;
+    f32x4 ec[kLatNormChunks];
 #pragma unroll
-      for (int m = 0; m < kLatNormPairs; ++m) {
-        const int k = 2 * (tid + m * kLatThreads);
-        const int kc = k < pl.lh ? k : 0, kh = k < pl.S ? k : 0;
-        ev[m] = *reinterpret_cast<const float2 *>(a.esum + (long)t * pl.lh + kc);
-        wv[m] = *reinterpret_cast<const uint32_t *>(a.norm + kc);
-        hv[m] = *reinterpret_cast<const uint32_t *>(a.x + (long)t * pl.S + kh);
-      }
+    for (int m = 0; m < kLatNormChunks; ++m) {
+      const int k = 4 * (l + 64 * m);
+      ec[m] = *reinterpret_cast<const f32x4 *>(t < B && k < pl.lh ? a.esum + (long)t * pl.lh + k
+                                                                  : reinterpret_cast<const float *>(zlane));
     }
+    const u32x4 wnv = load16(tid * 8 < kr1 - kr0 ? a.norm + kr0 + tid * 8 : zlane);
+    stage();
     issue(0, b0);
     issue(1, b1);
-    if (norm_wg) {
+    issue(2, b2);
+    float r = 0.f;
+    if (t < B) {
       float ss = 0.f;
 #pragma unroll
-      for (int m = 0; m < kLatNormPairs; ++m) {
-        if (2 * (tid + m * kLatThreads) < pl.lh) {
-          const float e0 = round_bf16(ev[m].x), e1 = round_bf16(ev[m].y);
-          ss += e0 * e0;
-          ss += e1 * e1;
+      for (int m = 0; m < kLatNormChunks; ++m) {
+        if (4 * (l + 64 * m) < pl.lh) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float e = round_bf16(ec[m][v]);
+            ss += e * e;
+          }
         }
       }
 #pragma unroll
       for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
+      r = 1.0f / __fsqrt_rn(ss / (float)pl.lh + kLatRmsEps);
+    }
+    uint16_t *wn_lds = reinterpret_cast<uint16_t *>(red);  // the range's norm weights (red is free until the units)
+    if (tid * 8 < kr1 - kr0) *reinterpret_cast<u32x4 *>(wn_lds + tid * 8) = wnv;
+    wait_vm<kRingLoads>();
+    ring_barrier();
+    if (t < B) {
+#pragma unroll
+      for (int m = 0; m < kLatNormChunks; ++m) {
+        const int k = 4 * (l + 64 * m);
+        if (k >= kr0 && k < kr1) {
+          const u32x2 wp = *reinterpret_cast<const u32x2 *>(wn_lds + (k - kr0));
+          uint32_t o[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const uint32_t wb = v & 1 ? wp[v >> 1] >> 16 : wp[v >> 1] & 0xFFFFu;
+            o[v] = f32_to_bf16_bits(round_bf16(round_bf16(ec[m][v]) * r) * bf16_bits_to_f32(wb));
+          }
+          *reinterpret_cast<u32x2 *>(xs + t * pl.xpitch + (k - kr0)) = u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+        }
+      }
+    }
+    ring_barrier();
+    mark(48);
+  } else {
+    issue(0, b0);
+    issue(1, b1);
+    issue(2, b2);
+    if ((int)blockIdx.x < B) {
+      // Workgroup t < B normalises token t's expert sum into the workspace row
+      // [en | shared_h] the splits stage from (as above, one workgroup per token).
+      const int t = blockIdx.x;
+      float ss = 0.f;
+      for (int k = 2 * tid; k < pl.lh; k += 2 * kLatThreads) {
+        const float2 v = *reinterpret_cast<const float2 *>(a.esum + (long)t * pl.lh + k);
+        const float e0 = round_bf16(v.x), e1 = round_bf16(v.y);
+        ss += e0 * e0;
+        ss += e1 * e1;
+      }
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
       if (l == 0) s_wsum[w] = ss;
-      ring_barrier();
+      __syncthreads();
       float tot = s_wsum[0];
 #pragma unroll
       for (int v = 1; v < kLatWaves; ++v) tot += s_wsum[v];
       const float r = 1.0f / __fsqrt_rn(tot / (float)pl.lh + kLatRmsEps);
-#pragma unroll
-      for (int m = 0; m < kLatNormPairs; ++m) {
-        const int k = 2 * (tid + m * kLatThreads);
-        const float n0 = round_bf16(round_bf16(ev[m].x) * r), n1 = round_bf16(round_bf16(ev[m].y) * r);
-        const uint32_t o0 = f32_to_bf16_bits(n0 * bf16_bits_to_f32(wv[m] & 0xFFFFu));
-        const uint32_t o1 = f32_to_bf16_bits(n1 * bf16_bits_to_f32(wv[m] >> 16));
-        st_dev32(ren, k < pl.lh ? (uint32_t)(((long)t * erow + k) * 2) : kOffNone, o0 | (o1 << 16));
-        st_dev32(ren, k < pl.S ? (uint32_t)(((long)t * erow + pl.lh + k) * 2) : kOffNone, hv[m]);
+      const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.ws + pl.o_en, (uint32_t)(B * erow * 2));
+      for (int k = 2 * tid; k < pl.lh; k += 2 * kLatThreads) {
+        const float2 v = *reinterpret_cast<const float2 *>(a.esum + (long)t * pl.lh + k);
+        const uint32_t wn = *reinterpret_cast<const uint32_t *>(a.norm + k);
+        const float n0 = round_bf16(round_bf16(v.x) * r), n1 = round_bf16(round_bf16(v.y) * r);
+        const uint32_t o0 = f32_to_bf16_bits(n0 * bf16_bits_to_f32(wn & 0xFFFFu));
+        const uint32_t o1 = f32_to_bf16_bits(n1 * bf16_bits_to_f32(wn >> 16));
+        st_dev32(rw, (uint32_t)(((long)t * erow + k) * 2), o0 | (o1 << 16));
       }
+      for (int k = 2 * tid; k < pl.S; k += 2 * kLatThreads)
+        st_dev32(rw, (uint32_t)(((long)t * erow + pl.lh + k) * 2),
+                 *reinterpret_cast<const uint32_t *>(a.x + (long)t * pl.S + k));
     }
+    mark(48);
     grid_barrier(ctl, bb, 1);
-    stage_load();
-    stage_store();
+    mark(49);
+    stage();
+    wait_vm<0>();
     ring_barrier();
   }
 
@@ -294,7 +387,7 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl, LatArgs a
       const int ks = k0 + w + kLatWaves * m;
       if (ks >= k1) continue;
       const bool p1 = OUT && ks >= pl.KS0;
-      const uint16_t *xrow = xs + (ks - k0) * kStepK + q * 32;
+      const uint16_t *xrow = xs + (ks - k0) * kStepK + q * 8;
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         if (tt >= TT) continue;
@@ -302,7 +395,7 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl, LatArgs a
         u32x4 bv[4];
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk)
-          bv[kk] = tok < B ? *reinterpret_cast<const u32x4 *>(xrow + tok * pl.xpitch + kk * 8) : u32x4{0, 0, 0, 0};
+          bv[kk] = tok < B ? *reinterpret_cast<const u32x4 *>(xrow + tok * pl.xpitch + kk * 32) : u32x4{0, 0, 0, 0};
         if (p1) {
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) acc1[tt] = mfma16(as_bf16x8(buf[m][kk]), as_bf16x8(bv[kk]), acc1[tt]);
@@ -333,82 +426,83 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl, LatArgs a
       }
     }
     ring_barrier();
+    if (j < 40) mark(2 + j);
   };
 
+  mark(1);
+  // three units in flight: a buffer is refilled with unit j + 3 once unit j is multiplied
   for (int j = 0; j < J; j += 3) {
-    issue(j + 2, b2);
     unit(j, b0);
+    if (j + 3 < J) issue(j + 3, b0);
     if (j + 1 >= J) break;
-    issue(j + 3, b0);
     unit(j + 1, b1);
+    if (j + 4 < J) issue(j + 4, b1);
     if (j + 2 >= J) break;
-    issue(j + 4, b1);
     unit(j + 2, b2);
+    if (j + 5 < J) issue(j + 5, b2);
   }
+  mark(45);
 
-  // count the units in (one lane of wave 0 per unit, all atomics in flight
-  // together); the workgroup that completes a tile finishes it
-  if (tid == 0) s_nfin = 0;
-  wait_vmem();  // this wave's partial stores are complete
+  // the group's barrier: every member's partial stores are complete
+  wait_vmem();
   __syncthreads();
-  if (tid < J) {
-    const int rt = rt0 + rstep * tid;
-    int ci = rt, need = SP;
-    if (!OUT && rt >= pl.ntile0) {  // a shared gate tile and its up tile share a counter
-      ci = pl.ntile0 + (rt - pl.ntile0) % (pl.S / 16);
-      need = 2 * SP;
+  if (tid == 0) {
+    __hip_atomic_fetch_add(gcnt, kLatGrpTotal >> lsp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned target = gbase + kLatGrpTotal;
+    unsigned spins = 0;
+    while ((int)(__hip_atomic_load(gcnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(ctl + kCtlErr, (unsigned)kErrBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
     }
-    const unsigned old = __hip_atomic_fetch_add(cnt + ci, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == (unsigned)need - 1u) {
-      __hip_atomic_store(cnt + ci, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_fin[atomicAdd(&s_nfin, 1)] = ci;
-    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
-  const int nfin = s_nfin;
-  if (nfin) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  mark(46);
   int s0 = 0, last0 = SP;  // <1>: splits [0, last0) have part-0 k-steps, [s0, SP) part-1 k-steps
   if (OUT) {
-    while (s0 < SP && lat_k0(s0 + 1, pl.KS, SP) <= pl.KS0) ++s0;
-    last0 = lat_k0(s0, pl.KS, SP) < pl.KS0 ? s0 + 1 : s0;
+    while (s0 < SP && (((s0 + 1) * pl.KS) >> lsp) <= pl.KS0) ++s0;
+    last0 = ((s0 * pl.KS) >> lsp) < pl.KS0 ? s0 + 1 : s0;
   }
-  for (int f = 0; f < nfin; ++f) {
-    const int ci = s_fin[f];
+  // member s finishes the group's tiles j = s, s + SP, ..: per output, every
+  // split's partial is loaded before the sum (in split order)
+  for (int j = s; j < J; j += SP) {
+    const int rt = rt0 + rstep * j;
+    const bool pair = !OUT && rt >= pl.ntile0;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {  // B * 16 <= 2 * kLatThreads outputs
       const int it = tid + c * kLatThreads;
-      if (it >= B * 16) continue;
       const int t = it >> 4, r = it & 15;
-      // every split's partials are loaded first, then summed in split order
-      auto off = [&](int ss, int rt) { return (uint32_t)((((long)ss * pl.RT + rt) * B + t) * 64 + r * 4); };
+      const bool ok = t < B && (!pair || r < 8);
       float va[kLatMaxSplits], vb[kLatMaxSplits];
-      const int rta = ci, rtb = !OUT ? ci + pl.S / 16 : ci;
-      const bool two = OUT || ci >= pl.ntile0;
 #pragma unroll
       for (int ss = 0; ss < kLatMaxSplits; ++ss) {
         va[ss] = vb[ss] = 0.f;
         if (ss < SP) {
-          va[ss] = bload4_dev(rp0, off(ss, rta));
-          if (two) vb[ss] = bload4_dev(OUT ? rp1 : rp0, off(ss, rtb));
+          const uint32_t o = (uint32_t)((((long)ss * pl.RT + rt) * B + t) * 64 + r * 4);
+          va[ss] = bload4_dev(rp0, ok ? o : kOffNone);
+          vb[ss] = bload4_dev(OUT ? rp1 : rp0, ok && (OUT || pair) ? o + (OUT ? 0 : 32) : kOffNone);
         }
       }
+      if (!ok) continue;
       float sa = 0.f, sb = 0.f;
 #pragma unroll
       for (int ss = 0; ss < kLatMaxSplits; ++ss) {
         if (ss < SP && ss < last0) sa += va[ss];
-        if (ss < SP && (OUT ? ss >= s0 : two)) sb += vb[ss];
+        if (ss < SP && ss >= s0) sb += vb[ss];
       }
-      if (!OUT) {
-        if (ci < pl.ntile0)
-          a.ya[(long)t * pl.lh + ci * 16 + r] = f32_to_bf16_bits(sa);
-        else
-          a.yb[(long)t * pl.S + (ci - pl.ntile0) * 16 + r] =
-              f32_to_bf16_bits(apply_act(pl.act, round_bf16(sa), round_bf16(sb)));
-      } else {
-        a.ya[(long)t * pl.h + ci * 16 + r] = f32_to_bf16_bits(round_bf16(sa) + round_bf16(sb));
-      }
+      if (OUT)
+        a.ya[(long)t * pl.h + rt * 16 + r] = f32_to_bf16_bits(round_bf16(sa) + round_bf16(sb));
+      else if (!pair)
+        a.ya[(long)t * pl.lh + rt * 16 + r] = f32_to_bf16_bits(sa);
+      else
+        a.yb[(long)t * pl.S + (rt - pl.ntile0) * 8 + r] =
+            f32_to_bf16_bits(apply_act(pl.act, round_bf16(sa), round_bf16(sb)));
     }
   }
+  mark(47);
 }
 
 }  // namespace k3moe

@@ -42,17 +42,6 @@ constexpr int kXSlotW = 16 * 1024;                      // weight tiles
 constexpr int kXSlot = kXSlotX + kXSlotW + 4 * 256;     // + scales: 50176 bytes
 constexpr int kXLds = kXRing * kXSlot;                  // dynamic LDS, 150528 bytes
 
-// 16 (or 4) bytes per lane from global memory to LDS: lane L's bytes land at
-// dst + L * size; dst is the same for the whole wave.
-template <int Size>
-__device__ __forceinline__ void load_lds(const void *src, char *dst) {
-  static_assert(Size == 16 || Size == 4, "16- or 4-byte lanes");
-  typedef __attribute__((address_space(3))) void lds_void;
-  if constexpr (Size == 16)
-    __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 16, 0, 0);
-  else
-    __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 4, 0, 0);
-}
 
 // GU: gate/up -> h (act = pl.act); otherwise down -> y.
 template <bool GU>

@@ -39,3 +39,14 @@ def step_flops(*, B: int, E: int, k: int, h: int, I: int, K: int | None = None) 
     """2 B E h (router) + 2 B k 3 I K (gate, up, down)."""
     K = h if K is None else K
     return 2*B*E*h + 2*B*k*3*I*K
+
+
+def latent_in_bytes(*, B: int, h: int, lh: int, S: int) -> int:
+    """latent_down lh h + shared gate/up 2 S h bf16 weights, x B h in, latent B lh and shared_h B S out."""
+    return (lh + 2*S)*h*2 + B*h*2 + B*(lh + S)*2
+
+
+def latent_out_bytes(*, B: int, h: int, lh: int, S: int) -> int:
+    """latent_up h lh + shared_down h S bf16 weights + latent_norm lh, expert_sum B lh fp32 and
+    shared_h B S in, output B h bf16 out."""
+    return h*(lh + S)*2 + lh*2 + B*lh*4 + B*S*2 + B*h*2
