@@ -106,7 +106,7 @@ __device__ __forceinline__ int tile_index(int row, int col) { return (col + 16 *
 // ---------------------------------------------------------------- gate/up --
 // A unit is 8 gate + 8 up rows of one (active expert, chunk of up to NX
 // tokens): one 16x16 MFMA tile. Units form groups of W (W = 2 when the grid
-// has at least two units per workgroup, else 1), ordered expert-major, chunk,
+// has at least two units per workgroup and pairs balance, gu_pairs; else 1), ordered expert-major, chunk,
 // unit. Workgroup b takes groups [NG b / G, NG (b + 1) / G) in rounds; a round
 // is a run of whole chunks whose token rows fit the LDS staging area (NX
 // rows), copied there once, so the MFMA B operand comes from LDS. Inside a
@@ -176,6 +176,16 @@ __device__ __forceinline__ void gu_compute(const GuSS<W> &B, const uint16_t *xro
       for (int kk = 0; kk < 4; ++kk) acc[u] = mfma16(av[kk], as_bf16x8(b[kk]), acc[u]);
     }
   }
+}
+
+// Gate/up groups of two units (W = 2) for nu units over the grid: when there
+// are at least two units per workgroup, and the whole groups balance as well
+// as single units or there are at least 8 units per workgroup (one group more
+// or less then costs at most an eighth).
+__device__ __forceinline__ bool gu_pairs(int nu) {
+  const int G = (int)gridDim.x;
+  if (nu < 2 * G) return false;
+  return cdiv(cdiv(nu, 2), G) * 2 <= cdiv(nu, G) || nu >= 8 * G;
 }
 
 // Activation epilogue of a full-K unit tile held by one wave: lanes 0-31 hold
@@ -767,13 +777,38 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       }
       __syncthreads();
       trace_mark(pl, a.ws, 10);
-      // one token per pass with E <= 512, k <= 8: the 8 waves share its
-      // selection. Wave w sorts experts 64 w .. 64 w + 63 as (key, ~expert)
+      // One token per pass: the 8 waves share its selection. With E <= 512
+      // and k <= 8, wave w sorts experts 64 w .. 64 w + 63 as (key, ~expert)
       // values with a bitonic network and offers its k best; wave 0 sorts the
-      // 8 k offers and keeps the first k. Otherwise one wave per token runs
-      // wave_topk.
+      // 8 k offers and keeps the first k. With E <= 1024 and k <= 32, wave w
+      // sorts experts 64 w .. and 64 (w + 8) .. and merges them into its 32
+      // best; wave 0 merges the 8 offers in a tree of three levels. Otherwise
+      // one wave per token runs wave_topk.
       const bool coop = nt == 1 && E <= kDecWaves * 64 && k <= 8;
+      const bool coop2 = nt == 1 && !coop && E <= 2 * kDecWaves * 64 && k <= 32;
       for (int tg = 0; tg < nt; tg += kDecWaves) {
+        if (coop2) {
+          uint64_t *cand = reinterpret_cast<uint64_t *>(
+              (reinterpret_cast<uintptr_t>(sel + kDecWaves * kMaxTopk) + 7) & ~(uintptr_t)7);  // [8][32]
+          const int e0 = w * 64 + l, e1 = (w + kDecWaves) * 64 + l;
+          uint64_t v0 = e0 < E ? ((uint64_t)kyl[e0] << 32) | (uint32_t)~e0 : 0ull;
+          uint64_t v1 = e1 < E ? ((uint64_t)kyl[e1] << 32) | (uint32_t)~e1 : 0ull;
+          v0 = wave_sort_desc(v0);
+          v1 = wave_sort_desc(v1);
+          const uint64_t mine = merge_top32(v0, v1);
+          if (l < 32) cand[w * 32 + l] = mine;
+          __syncthreads();
+          if (w == 0) {
+            uint64_t c[kDecWaves];
+#pragma unroll
+            for (int j = 0; j < kDecWaves; ++j) c[j] = cand[j * 32 + (l & 31)];
+            const uint64_t c01 = merge_top32(c[0], c[1]), c23 = merge_top32(c[2], c[3]);
+            const uint64_t c45 = merge_top32(c[4], c[5]), c67 = merge_top32(c[6], c[7]);
+            const uint64_t top = merge_top32(merge_top32(c01, c23), merge_top32(c45, c67));
+            if (l < k) sel[l] = (int)~(uint32_t)top;
+            wave_lds_order();
+          }
+        }
         if (coop) {
           uint64_t *cand = reinterpret_cast<uint64_t *>(
               (reinterpret_cast<uintptr_t>(sel + kDecWaves * kMaxTopk) + 7) & ~(uintptr_t)7);  // [8 k]
@@ -793,7 +828,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
         if (tl >= nt) continue;
         const int t = t0 + tl;
         int *mysel = sel + w * kMaxTopk;
-        if (!coop) wave_topk(kyl + tl * E, E, k, mysel);
+        if (!coop && !coop2) wave_topk(kyl + tl * E, E, k, mysel);
         wave_lds_order();
         trace_mark(pl, a.ws, 30);
         int my_e = -1;
@@ -955,7 +990,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   // ------------------------------------------------------------ GU: gate/up --
   {
     uint16_t *xs = reinterpret_cast<uint16_t *>(scr);  // staged activation rows (the scratch is free now)
-    const bool two = g_coff[D] * pl.U8 >= 2 * (int)gridDim.x;
+    const bool two = gu_pairs(g_coff[D] * pl.U8);
     const bool al = (pl.K / kBlockK) % 16 == 0;
     if (two) {
       if (al) gu_phase<2, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
@@ -991,7 +1026,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   if (expert_major) {
     wait_vmem();
     __syncthreads();
-    const int W = g_coff[D] * pl.U8 >= 2 * (int)gridDim.x ? 2 : 1;  // as in the gate/up phase
+    const int W = gu_pairs(g_coff[D] * pl.U8) ? 2 : 1;  // as in the gate/up phase
     const int NG = g_coff[D] * (pl.U8 / W);
     const int ga = (int)((long)NG * blockIdx.x / gridDim.x), gb = (int)((long)NG * (blockIdx.x + 1) / gridDim.x);
     if (ga < gb) {

@@ -443,6 +443,17 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v) {
   return v;
 }
 
+// Top 32 of two lists sorted descending in lanes 0..31 (a and b), sorted
+// descending in lanes 0..31: b reversed into lanes 32..63 makes a bitonic
+// sequence of 64, which one 6-stage merge sorts.
+__device__ __forceinline__ uint64_t merge_top32(uint64_t a, uint64_t b) {
+  const int l = __lane_id();
+  const uint32_t bl = (uint32_t)__shfl((int)(uint32_t)b, 63 - l, kWave);
+  const uint32_t bh = (uint32_t)__shfl((int)(uint32_t)(b >> 32), 63 - l, kWave);
+  const uint64_t c = l < 32 ? a : (((uint64_t)bh << 32) | bl);
+  return bitonic_merge<64, 32>(c, l);
+}
+
 // Inclusive prefix sum over the wave (lane l gets the sum of lanes 0..l):
 // DPP shifts inside rows of 16, then the row broadcasts.
 __device__ __forceinline__ int wave_incl_scan(int v) {

@@ -97,7 +97,7 @@ inline int decode_lds(Plan &p) {
   p.redundant = p.B * p.E <= kRedundantKeys && p.B <= kRedundantTokens;
   const int nt = p.redundant ? p.B : 1;
   const int routed = 8 * p.P;                                       // ids + weights per pair
-  const int topk = routed + 4 * (3 * nt * p.E + kDecWaves * kMaxTopk) + 8 * 64 + 8;  // keys, scores, picks, offers
+  const int topk = routed + 4 * (3 * nt * p.E + kDecWaves * kMaxTopk) + 8 * kDecWaves * 32 + 8;  // keys, scores, picks, offers
   const int group = routed + 4 * (4 * p.E + 32);                    // counts, offsets, bitmaps, wave sums
   int down = kDecWaves * p.B * 16 * 4;                              // per-wave combine accumulators
   if (down < kDecWaves * kDnStage * 36) down = kDecWaves * kDnStage * 36;  // or per-wave y stages

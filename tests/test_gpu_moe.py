@@ -121,6 +121,10 @@ TINY = [
     MoEConfig('k1', 16, 1, 128, 64, 33),
     MoEConfig('k32', 48, 32, 96, 32, 5),
     MoEConfig('many-tokens', 24, 4, 256, 128, 70),
+    # wide expert sets: the workgroup-cooperative selection (up to 1024 experts, top-32)
+    MoEConfig('e1024-k32', 1024, 32, 64, 32, 2),
+    MoEConfig('e600-k12', 600, 12, 96, 64, 7),
+    MoEConfig('e896-k16', 896, 16, 128, 64, 9),
 ]
 
 
