@@ -87,7 +87,8 @@ def read_trace(cfg, device):
     g = torch.empty(cfg.experts, cfg.inter, cfg.width//32, 16, dtype=torch.uint8, device=device)
     d = torch.empty(cfg.experts, cfg.width, cfg.inter//32, 16, dtype=torch.uint8, device=device)
     r = torch.empty(cfg.experts, cfg.hidden, dtype=torch.bfloat16, device=device)
-    total = k3moe.workspace_bytes(moe.dims_for(x, r, g, d, cfg.topk, cfg.gating, cfg.activation))
+    lat = torch.empty(cfg.tokens, cfg.width, dtype=torch.bfloat16, device=device) if cfg.latent else None
+    total = k3moe.workspace_bytes(moe.dims_for(x, r, g, d, cfg.topk, cfg.gating, cfg.activation, lat))
     full = ws[total - 1024*56*8: total].cpu().view(torch.int64).view(1024, 56).double()
     G = int((full[:, 8] > 0).sum())
     full = full[:G]

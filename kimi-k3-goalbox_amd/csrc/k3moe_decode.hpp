@@ -410,29 +410,41 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
 
 // ---------------------------------------------------- down, expert-major --
 // For many active experts: a wave streams a contiguous run of (expert, 16-row
-// tile) items; the B operand (the expert's h rows, at most two k-steps) is
+// tile) items; the B operand (the expert's h rows, KSD = I / 128 k-steps) is
 // loaded once per expert and token chunk; bf16 y goes to the pair buffer and
-// a combine phase sums it. Tiles come in batches of kDnTiles, two in flight.
-constexpr int kDnTiles = 4;
+// a combine phase sums it. Tiles come in batches of dn_tiles(KSD), two in flight.
+__host__ __device__ constexpr int dn_tiles(int ksd) { return ksd == 2 ? 4 : ksd == 3 ? 3 : 2; }
+// I of the expert-major down path: 256, 384 or 512 (2-4 k-steps per row)
+__host__ __device__ inline bool dn_expert_major_ok(int I) { return I == 256 || I == 384 || I == 512; }
 
+template <int KSD>
 struct DnTileBatch {
-  u32x4 a[kDnTiles][2];
-  uint32_t s[kDnTiles][2];
+  u32x4 a[dn_tiles(KSD)][KSD];
+  uint32_t s[dn_tiles(KSD)][KSD];
 };
 
-// wrow/srow: this lane's row (tile rt0) + 32 q / + 2 q bytes: lane group q
-// owns blocks 2q and 2q+1 of the row (k-steps 0 and 1), so both scales are one
-// 16-bit load. Rows of later tiles are 16 rows further each; tiles at or past
-// rt1 read the zero area. Requires I == 256 (8 blocks per row).
-__device__ __forceinline__ void dnc_issue(DnTileBatch &bt, const Plan &pl, const uint8_t *wrow,
+// wrow/srow: this lane's row (tile rt0) + 16 KSD q / + KSD q bytes: lane
+// group q owns blocks KSD q .. KSD q + KSD - 1 of the row (k-step ks takes
+// block KSD q + ks), so a row's 4 lane groups read it whole and contiguous.
+// Rows of later tiles are 16 rows further each; tiles at or past rt1 read the
+// zero area.
+template <int KSD>
+__device__ __forceinline__ void dnc_issue(DnTileBatch<KSD> &bt, const Plan &pl, const uint8_t *wrow,
                                           const uint8_t *srow, const uint8_t *zero, int rt0, int rt1) {
-  constexpr size_t tstride = (size_t)16 * 8 * 16, sstride = (size_t)16 * 8;
+  constexpr int T = dn_tiles(KSD), KB = 4 * KSD;
+  constexpr size_t tstride = (size_t)16 * KB * 16, sstride = (size_t)16 * KB;
 #pragma unroll
-  for (int t = 0; t < kDnTiles; ++t) {
+  for (int t = 0; t < T; ++t) {
     const bool ok = rt0 + t < rt1;  // wave-uniform
-    const uint32_t sc = ok ? *reinterpret_cast<const uint16_t *>(srow + t * sstride) : 0u;
+    uint32_t sc = 0u;
+    if (ok) {
+      if constexpr (KSD == 2) sc = *reinterpret_cast<const uint16_t *>(srow + t * sstride);
+      else if constexpr (KSD == 4) sc = *reinterpret_cast<const uint32_t *>(srow + t * sstride);
+      else sc = (uint32_t)srow[t * sstride] | ((uint32_t)srow[t * sstride + 1] << 8) |
+                ((uint32_t)srow[t * sstride + 2] << 16);
+    }
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < KSD; ++ks) {
       bt.a[t][ks] = load16(ok ? wrow + t * tstride + ks * 16 : zero);
       bt.s[t][ks] = (sc >> (8 * ks)) & 0xFFu;
     }
@@ -463,16 +475,17 @@ __device__ __forceinline__ void dn_flush(DnStage &st, const Plan &pl, uint16_t *
 }
 
 // Tiles rt .. of a batch for token chunk columns [0, ncol) (pairs p0c + column):
-// MFMA over the two k-steps, bf16 y rows into the stage.
-__device__ __forceinline__ void dnc_compute(const DnTileBatch &bt, const Plan &pl, const u32x4 (&hb)[2][4],
+// MFMA over the KSD k-steps, bf16 y rows into the stage.
+template <int KSD>
+__device__ __forceinline__ void dnc_compute(const DnTileBatch<KSD> &bt, const Plan &pl, const u32x4 (&hb)[KSD][4],
                                             DnStage &st, uint16_t *ybuf, int rt0, int rt1, int p0c, int ncol) {
   const int l = threadIdx.x & 63, i = l & 15, q = l >> 4;
 #pragma unroll
-  for (int t = 0; t < kDnTiles; ++t) {
+  for (int t = 0; t < dn_tiles(KSD); ++t) {
     if (rt0 + t >= rt1) break;  // wave-uniform
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < KSD; ++ks) {
       bf16x8 av[4];
       convert_block_fast(bt.a[t][ks], bt.s[t][ks], av);
 #pragma unroll
@@ -486,6 +499,54 @@ __device__ __forceinline__ void dnc_compute(const DnTileBatch &bt, const Plan &p
       if (q == 0) st.tag[st.fill + i] = ((p0c + i) << 16) | (rt0 + t);
     }
     st.fill += ncol;
+  }
+}
+
+// One wave's expert-major down range: items t in [ta, tb) of (active expert,
+// 16-row tile), expert-major; for each expert and 16-token chunk the h rows
+// (B operand) are loaded once, and the weight tiles stream in batches.
+template <int KSD, class WaitExpert>
+__device__ __forceinline__ void dn_expert_major(const Plan &pl, const DecodeArgs &a, const int *g_act,
+                                                const int *g_aoff, const int *g_acnt, const uint8_t *zero,
+                                                __amdgpu_buffer_rsrc_t hrs, DnStage &st, uint16_t *ybuf, int ta,
+                                                int tb, const WaitExpert &wait_expert) {
+  constexpr int T = dn_tiles(KSD), KB = 4 * KSD;
+  const int l = threadIdx.x & 63, i = l & 15, q = l >> 4;
+  for (int t = ta; t < tb;) {
+    const int d = t / pl.RTd;
+    const int rt0 = t % pl.RTd, rt1 = min(pl.RTd, rt0 + (tb - t));
+    const int e = g_act[d], p0 = g_aoff[d], n = g_acnt[d];
+    const size_t row0 = (size_t)e * pl.K + rt0 * 16 + i;
+    const uint8_t *wrow = a.dblk + row0 * KB * 16 + q * 16 * KSD, *srow = a.dscl + row0 * KB + q * KSD;
+    const size_t tstride = (size_t)16 * KB * 16, sstride = (size_t)16 * KB;
+    for (int c = 0; c * 16 < n; ++c) {
+      const int pj = c * 16 + i;
+      const bool tok_ok = pj < n;
+      const int ncol = min(16, n - c * 16);
+      // lane group q feeds blocks KSD q + ks (k-step ks) of the h row (64 bytes each)
+      const uint32_t hoff = tok_ok ? (uint32_t)(p0 + pj) * pl.I * 2 + q * 64 * KSD : kOffNone;
+      DnTileBatch<KSD> b0, b1;
+      dnc_issue<KSD>(b0, pl, wrow, srow, zero, rt0, rt1);  // weights do not depend on h
+      if (c == 0) wait_expert(d);  // the expert's gate/up units are all done
+      u32x4 hb[KSD][4];
+#pragma unroll
+      for (int ks = 0; ks < KSD; ++ks) {
+        const uint32_t ho = hoff + ks * 64;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) hb[ks][kk] = bload16_dev(hrs, ho + kk * 16);  // device-coherent
+      }
+      for (int rt = rt0; rt < rt1; rt += 2 * T) {
+        const int o1 = rt + T - rt0, o2 = rt + 2 * T - rt0;
+        if (rt + T < rt1) dnc_issue<KSD>(b1, pl, wrow + o1 * tstride, srow + o1 * sstride, zero, rt + T, rt1);
+        dnc_compute<KSD>(b0, pl, hb, st, ybuf, rt, rt1, p0 + c * 16, ncol);
+        if (rt + T < rt1) {
+          if (rt + 2 * T < rt1)
+            dnc_issue<KSD>(b0, pl, wrow + o2 * tstride, srow + o2 * sstride, zero, rt + 2 * T, rt1);
+          dnc_compute<KSD>(b1, pl, hb, st, ybuf, rt + T, rt1, p0 + c * 16, ncol);
+        }
+      }
+    }
+    t += rt1 - rt0;
   }
 }
 
@@ -1008,7 +1069,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   // increments of one line are serialised where they are performed. The
   // row-tile down path needs every expert in every workgroup and keeps the
   // barrier (with few experts all workgroups would count on a few lines).
-  const bool expert_major = D > kDnExpertMajorMin && pl.I == 256 && pl.o_y;
+  const bool expert_major = D > kDnExpertMajorMin && dn_expert_major_ok(pl.I) && pl.o_y;
   auto wait_expert = [&](int d) {  // bounded: a timeout sets the status word
     const unsigned need = (unsigned)(g_coff[d + 1] - g_coff[d]) * pl.U8;
     unsigned spins = 0;
@@ -1059,47 +1120,13 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     const int GW = gridDim.x * kDecWaves;
     const int gw = blockIdx.x * kDecWaves + w;
     const int ta = (int)((long)NT * gw / GW), tb = (int)((long)NT * (gw + 1) / GW);
-    const int KB = pl.I / kBlockK;
     DnStage st;  // this wave's y stage in the scratch area (free after gate/up)
     st.rows = reinterpret_cast<uint16_t *>(scr) + w * kDnStage * 16;
     st.tag = reinterpret_cast<int *>(scr + kDecWaves * kDnStage * 32) + w * kDnStage;
     st.fill = 0;
-    for (int t = ta; t < tb;) {
-      const int d = t / pl.RTd;
-      const int rt0 = t % pl.RTd, rt1 = min(pl.RTd, rt0 + (tb - t));
-      const int e = g_act[d], p0 = g_aoff[d], n = g_acnt[d];
-      const size_t row0 = (size_t)e * pl.K + rt0 * 16 + i;
-      const uint8_t *wrow = a.dblk + row0 * KB * 16 + q * 32, *srow = a.dscl + row0 * KB + q * 2;
-      const size_t tstride = (size_t)16 * KB * 16, sstride = (size_t)16 * KB;
-      for (int c = 0; c * 16 < n; ++c) {
-        const int pj = c * 16 + i;
-        const bool tok_ok = pj < n;
-        const int ncol = min(16, n - c * 16);
-        // lane group q feeds blocks 2q (k-step 0) and 2q+1 (k-step 1) of the h row
-        const uint32_t hoff = tok_ok ? (uint32_t)(p0 + pj) * pl.I * 2 + q * 128 : kOffNone;
-        DnTileBatch b0, b1;
-        dnc_issue(b0, pl, wrow, srow, zero, rt0, rt1);  // weights do not depend on h
-        if (c == 0) wait_expert(d);  // the expert's gate/up units are all done
-        u32x4 hb[2][4];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const uint32_t ho = hoff + ks * 64;
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) hb[ks][kk] = bload16_dev(hrs, ho + kk * 16);  // device-coherent
-        }
-        for (int rt = rt0; rt < rt1; rt += 2 * kDnTiles) {
-          const int o1 = rt + kDnTiles - rt0, o2 = rt + 2 * kDnTiles - rt0;
-          if (rt + kDnTiles < rt1) dnc_issue(b1, pl, wrow + o1 * tstride, srow + o1 * sstride, zero, rt + kDnTiles, rt1);
-          dnc_compute(b0, pl, hb, st, ybuf, rt, rt1, p0 + c * 16, ncol);
-          if (rt + kDnTiles < rt1) {
-            if (rt + 2 * kDnTiles < rt1)
-              dnc_issue(b0, pl, wrow + o2 * tstride, srow + o2 * sstride, zero, rt + 2 * kDnTiles, rt1);
-            dnc_compute(b1, pl, hb, st, ybuf, rt + kDnTiles, rt1, p0 + c * 16, ncol);
-          }
-        }
-      }
-      t += rt1 - rt0;
-    }
+    if (pl.I == 256) dn_expert_major<2>(pl, a, g_act, g_aoff, g_acnt, zero, hrs, st, ybuf, ta, tb, wait_expert);
+    else if (pl.I == 384) dn_expert_major<3>(pl, a, g_act, g_aoff, g_acnt, zero, hrs, st, ybuf, ta, tb, wait_expert);
+    else dn_expert_major<4>(pl, a, g_act, g_aoff, g_acnt, zero, hrs, st, ybuf, ta, tb, wait_expert);
     if (pl.o_trace && l == 0)  // every wave's stream end (before its y flush)
       reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + 48 + w] = __builtin_amdgcn_s_memrealtime();
     dn_flush(st, pl, ybuf);

@@ -194,8 +194,8 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   p.o_gpart = take(general && p.Sg > 1 ? (size_t)p.Sg * p.P * 2 * p.I * 4 : 0);
   p.o_gcnt = take(general ? (size_t)p.Dmax * p.RTg * 4 : 0);
   p.o_h = take((size_t)p.P * p.I * 2);
-  // pair outputs: the general path, and the decode path's expert-major down (I == 256)
-  p.o_y = take((general || p.I == 256) ? (size_t)p.P * p.K * 2 : 0);
+  // pair outputs: the general path, and the decode path's expert-major down (I = 256, 384, 512)
+  p.o_y = take((general || p.I == 256 || p.I == 384 || p.I == 512) ? (size_t)p.P * p.K * 2 : 0);
   p.trace = trace && p.path == kPathDecode;
   p.o_ecnt = take((size_t)p.Dmax * kCntStride * 4);  // decode: gate/up units done per active expert
   p.o_trace = p.trace ? take((size_t)1024 * kTraceSlots * 8) : 0;  // last area of the workspace

@@ -125,6 +125,9 @@ TINY = [
     MoEConfig('e1024-k32', 1024, 32, 64, 32, 2),
     MoEConfig('e600-k12', 600, 12, 96, 64, 7),
     MoEConfig('e896-k16', 896, 16, 128, 64, 9),
+    # more than 32 active experts with I = 384 and 512: the expert-major down path's 3 and 4 k-steps
+    MoEConfig('i384-wide', 96, 8, 128, 384, 7),
+    MoEConfig('i512-wide', 64, 8, 128, 512, 9),
 ]
 
 
