@@ -115,11 +115,24 @@ int grant_lds(const void *fn, int limit, int &granted, const char *what) {
   return K3MOE_OK;
 }
 
-int allow_lds(int bytes) {
-  static int granted = 0;
+// The decode kernel instantiation for a plan: whole gate/up super-steps (K a
+// multiple of 512) and the expert-major down variant of its I.
+typedef void (*DecodeKernel)(Plan, DecodeArgs);
+DecodeKernel decode_kernel(const Plan &p, int &slot) {
+  static const DecodeKernel table[2][4] = {
+      {k_moe_decode<false, 0>, k_moe_decode<false, 2>, k_moe_decode<false, 3>, k_moe_decode<false, 4>},
+      {k_moe_decode<true, 0>, k_moe_decode<true, 2>, k_moe_decode<true, 3>, k_moe_decode<true, 4>}};
+  const int al = (p.K / kBlockK) % 16 == 0 ? 1 : 0;
+  const int v = p.I == 256 ? 1 : p.I == 384 ? 2 : p.I == 512 ? 3 : 0;
+  slot = al * 4 + v;
+  return table[al][v];
+}
+
+int allow_lds(DecodeKernel fn, int slot, int bytes) {
+  static int granted[8] = {0};
   if (bytes <= 65536) return K3MOE_OK;
   // dynamic + static LDS must fit the 160 KiB of a workgroup
-  return grant_lds(reinterpret_cast<const void *>(&k_moe_decode), kDecMaxLds - kDecStaticLds, granted, "decode");
+  return grant_lds(reinterpret_cast<const void *>(fn), kDecMaxLds - kDecStaticLds, granted[slot], "decode");
 }
 
 int allow_xgemm_lds() {
@@ -271,8 +284,10 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
     a.out_w = route_weights;
     a.out_short = shortfall;
     a.ws = ws;
-    if ((rc = allow_lds(p.lds_total))) return rc;
-    hipLaunchKernelGGL(k_moe_decode, dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
+    int slot = 0;
+    const DecodeKernel fn = decode_kernel(p, slot);
+    if ((rc = allow_lds(fn, slot, p.lds_total))) return rc;
+    hipLaunchKernelGGL(fn, dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
     return launch_check("decode step");
   }
 

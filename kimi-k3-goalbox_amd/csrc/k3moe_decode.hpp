@@ -219,9 +219,41 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
   const int NG = g_coff[D] * GPC;
   const int ga = (int)((long)NG * blockIdx.x / gridDim.x), gb = (int)((long)NG * (blockIdx.x + 1) / gridDim.x);
   auto slot = [&](int wv, int which, int u) { return red + ((wv * 2 + which) * 2 + u) * 256 + l * 4; };
+  // unit rows: lanes 0-7 gate, 8-15 up
+  const uint8_t *const lane_blk = i >= 8 ? a.ublk : a.gblk;
+  const uint8_t *const lane_scl = i >= 8 ? a.uscl : a.gscl;
+  // A single token's groups are one round when there are at most min(16, NX)
+  // of them (a chunk is one row): each wave's range and first expert are known
+  // before the round table, so its first super-step's weight loads are issued
+  // first and the table is built while they are in flight.
+  GuSS<W> B0, B1;
+  bool pre = false;
+  if (pl.B == 1 && ga < gb && gb - ga <= min(16, pl.NX)) {
+    const int work = (gb - ga) * NSS;
+    const int s = (int)((long)work * w / kDecWaves), e = (int)((long)work * (w + 1) / kDecWaves);
+    if (s < e) {
+      const int G = ga + s / NSS, ci = G / GPC, pg = G % GPC;
+      int lo = 0, hi = D - 1;  // active expert of chunk ci
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (g_coff[mid] <= ci) lo = mid; else hi = mid - 1;
+      }
+      const uint8_t *wr[W], *sr[W];
+#pragma unroll
+      for (int u = 0; u < W; ++u) {
+        const size_t row = (size_t)g_act[lo] * pl.I + (pg * W + u) * 8 + (i & 7);
+        wr[u] = lane_blk + row * KB * 16;
+        sr[u] = lane_scl + row * KB;
+      }
+      gu_issue<W, AL>(B0, wr, sr, s % NSS, KB);
+      pre = true;
+    }
+  }
   for (int g0 = ga; g0 < gb;) {
     const int ci0 = g0 / GPC;
-    __syncthreads();  // the previous round is done with the table, the staged rows and the partial tiles
+    // LDS-only barriers in the round (no vector-memory wait): the previous round is
+    // done with the table, the staged rows and the partial tiles
+    ring_barrier();
     if (w == 0) {
       // lane j < 16 takes chunk ci0 + j; the round is the prefix of chunks whose rows fit
       const int ci = ci0 + l;
@@ -259,15 +291,13 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
         s_round[1] = rows;
       }
     }
-    __syncthreads();
+    ring_barrier();
     if (g0 == ga) trace_mark(pl, a.ws, 32);
     const int nch = s_round[0], rows = s_round[1];
     const int g1 = min(gb, (ci0 + nch) * GPC);
     const int work = (g1 - g0) * NSS;
     const int s = (int)((long)work * w / kDecWaves), e = (int)((long)work * (w + 1) / kDecWaves);
-    // unit rows of group gg of the round (relative to g0); lanes 0-7 gate, 8-15 up
-    const uint8_t *const lane_blk = i >= 8 ? a.ublk : a.gblk;
-    const uint8_t *const lane_scl = i >= 8 ? a.uscl : a.gscl;
+    // unit rows of group gg of the round (relative to g0)
     auto rows_of = [&](int gg, const uint8_t *(&wr)[W], const uint8_t *(&sr)[W]) {
       const int G = g0 + gg, j = G / GPC - ci0, pg = G % GPC;
       const int ex = tab[j].e;
@@ -288,13 +318,13 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
 #pragma unroll
       for (int u = 0; u < W; ++u) gu_finish_wave(pl, hbuf, acc[u], ch.pbase + i, i < ch.n, (pg * W + u) * 8);
     };
-    GuSS<W> B0, B1;
     const uint8_t *iwr[W], *isr[W];
     int ig = s / NSS, iss = s % NSS;  // issue cursor
     if (s < e) {
       rows_of(ig, iwr, isr);
-      gu_issue<W, AL>(B0, iwr, isr, iss, KB);
+      if (!pre) gu_issue<W, AL>(B0, iwr, isr, iss, KB);  // else issued before the table, the same loads
     }
+    pre = false;
     // progress of each wave's range in 1/4096 (empty ranges count as done);
     // visible to the workgroup's other waves after the staging barrier
     if (l == 0) __hip_atomic_store(s_prog + w, s < e ? 0 : 4096, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -330,7 +360,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
         }
       }
     }
-    __syncthreads();
+    ring_barrier();  // staged rows visible; each wave's compute waits for its own weight loads
     if (g0 == ga) trace_mark(pl, a.ws, 33);
     if (s < e) {
       int cg = ig, css = iss;  // compute cursor
@@ -414,8 +444,6 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
 // loaded once per expert and token chunk; bf16 y goes to the pair buffer and
 // a combine phase sums it. Tiles come in batches of dn_tiles(KSD), two in flight.
 __host__ __device__ constexpr int dn_tiles(int ksd) { return ksd == 2 ? 4 : ksd == 3 ? 3 : 2; }
-// I of the expert-major down path: 256, 384 or 512 (2-4 k-steps per row)
-__host__ __device__ inline bool dn_expert_major_ok(int I) { return I == 256 || I == 384 || I == 512; }
 
 template <int KSD>
 struct DnTileBatch {
@@ -606,6 +634,11 @@ __device__ __forceinline__ DecodeArgs load_args(uint64_t at) {
   return a;
 }
 
+// AL: K is a multiple of 512 (whole 16-block super-steps in gate/up); KSD: the
+// expert-major down path's k-steps per row (I / 128 for I = 256, 384, 512; 0:
+// that path is not used). Each instantiation holds one variant of each, which
+// keeps the kernel's code (and its instruction-cache footprint) small.
+template <bool AL, int KSD>
 __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, DecodeArgs a_arg) {
   // The arguments, read through the touched segment (pl_arg at offset 0, a_arg after it).
   const uint64_t kargs = touch_kernargs<sizeof(Plan) + sizeof(DecodeArgs)>();
@@ -1051,15 +1084,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   // ------------------------------------------------------------ GU: gate/up --
   {
     uint16_t *xs = reinterpret_cast<uint16_t *>(scr);  // staged activation rows (the scratch is free now)
-    const bool two = gu_pairs(g_coff[D] * pl.U8);
-    const bool al = (pl.K / kBlockK) % 16 == 0;
-    if (two) {
-      if (al) gu_phase<2, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
-      else gu_phase<2, false>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
-    } else {
-      if (al) gu_phase<1, true>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
-      else gu_phase<1, false>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
-    }
+    if (gu_pairs(g_coff[D] * pl.U8))
+      gu_phase<2, AL>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
+    else
+      gu_phase<1, AL>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
   }
   trace_mark(pl, a.ws, 6);
   // Expert-major down reads an expert's h only after its gate/up units are
@@ -1069,7 +1097,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   // increments of one line are serialised where they are performed. The
   // row-tile down path needs every expert in every workgroup and keeps the
   // barrier (with few experts all workgroups would count on a few lines).
-  const bool expert_major = D > kDnExpertMajorMin && dn_expert_major_ok(pl.I) && pl.o_y;
+  const bool expert_major = KSD > 0 && D > kDnExpertMajorMin && pl.o_y;
   auto wait_expert = [&](int d) {  // bounded: a timeout sets the status word
     const unsigned need = (unsigned)(g_coff[d + 1] - g_coff[d]) * pl.U8;
     unsigned spins = 0;
@@ -1124,9 +1152,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     st.rows = reinterpret_cast<uint16_t *>(scr) + w * kDnStage * 16;
     st.tag = reinterpret_cast<int *>(scr + kDecWaves * kDnStage * 32) + w * kDnStage;
     st.fill = 0;
-    if (pl.I == 256) dn_expert_major<2>(pl, a, g_act, g_aoff, g_acnt, zero, hrs, st, ybuf, ta, tb, wait_expert);
-    else if (pl.I == 384) dn_expert_major<3>(pl, a, g_act, g_aoff, g_acnt, zero, hrs, st, ybuf, ta, tb, wait_expert);
-    else dn_expert_major<4>(pl, a, g_act, g_aoff, g_acnt, zero, hrs, st, ybuf, ta, tb, wait_expert);
+    if constexpr (KSD > 0) dn_expert_major<KSD>(pl, a, g_act, g_aoff, g_acnt, zero, hrs, st, ybuf, ta, tb, wait_expert);
     if (pl.o_trace && l == 0)  // every wave's stream end (before its y flush)
       reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + 48 + w] = __builtin_amdgcn_s_memrealtime();
     dn_flush(st, pl, ybuf);
