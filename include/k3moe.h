@@ -135,7 +135,8 @@ int k3moe_workspace_status(const void *workspace, int32_t *status, void *stream)
 
 /* Geometry of the latent MoE block around the routed experts of a Kimi K3
  * layer (kimi.py:317, 325-328; weight shapes kimi.py:112-121):
- *   tokens      B <= 64: rows of x
+ *   tokens      B: rows of x (up to 64 per kernel launch; larger batches run as
+ *               consecutive launches of 64 token rows on the same stream)
  *   hidden      h: width of x and of the block's output (7168)
  *   latent      lh: width of the experts' input and of expert_sum (3584)
  *   shared      S: this rank's shared-expert width (intermediate x

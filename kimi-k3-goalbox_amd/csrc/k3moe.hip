@@ -144,8 +144,7 @@ int allow_xgemm_lds() {
 
 int check_latent_dims(const k3moe_latent_dims *d) {
   if (!d) return fail(K3MOE_EINVAL, "dims is NULL");
-  if (d->tokens < 1 || d->tokens > kLatMaxTokens)
-    return fail(K3MOE_EINVAL, "the latent block takes 1 to %d tokens, got %d", kLatMaxTokens, d->tokens);
+  if (d->tokens < 1) return fail(K3MOE_EINVAL, "tokens must be >= 1, got %d", d->tokens);
   if (d->hidden < 128 || d->hidden % 128 || d->latent < 128 || d->latent % 128 || d->shared < 128 ||
       d->shared % 128)
     return fail(K3MOE_EINVAL, "hidden (%d), latent (%d) and shared (%d) must be positive multiples of 128",
@@ -155,12 +154,17 @@ int check_latent_dims(const k3moe_latent_dims *d) {
   return K3MOE_OK;
 }
 
-// Plans of both latent kernels (the workspace covers the larger).
+// Plans of both latent kernels for a launch of min(tokens, kLatMaxTokens)
+// tokens (larger batches run as consecutive launches of up to that many; the
+// workspace covers the larger plan of the full launch, which also covers a
+// shorter last one).
 int latent_plans(const k3moe_latent_dims *d, int n_cus, LatPlan &pin, LatPlan &pout) {
   int rc = check_latent_dims(d);
   if (rc) return rc;
-  const char *why = latent_plan(*d, n_cus, 0, pin);
-  if (!why) why = latent_plan(*d, n_cus, 1, pout);
+  k3moe_latent_dims c = *d;
+  if (c.tokens > kLatMaxTokens) c.tokens = kLatMaxTokens;
+  const char *why = latent_plan(c, n_cus, 0, pin);
+  if (!why) why = latent_plan(c, n_cus, 1, pout);
   if (why) return fail(K3MOE_EINVAL, "latent block geometry B=%d h=%d lh=%d S=%d: %s", d->tokens, d->hidden,
                        d->latent, d->shared, why);
   if (trace_enabled()) {  // one trace area for both kernels, the last 1024 x kTraceSlots x 8 bytes
@@ -186,12 +190,32 @@ int latent_launch(const k3moe_latent_dims *dims, int out, const LatArgs &a, size
   if (!a.ws || workspace_bytes < need)
     return fail(K3MOE_EWORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);
   if (reinterpret_cast<uintptr_t>(a.ws) % 256) return fail(K3MOE_EWORKSPACE, "workspace must be 256-byte aligned");
-  const LatPlan &p = out ? pout : pin;
-  if ((rc = allow_latent_lds(out, p.lds_total))) return rc;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (out) hipLaunchKernelGGL(k_latent<1>, dim3(p.G), dim3(kLatThreads), p.lds_total, st, p, a);
-  else hipLaunchKernelGGL(k_latent<0>, dim3(p.G), dim3(kLatThreads), p.lds_total, st, p, a);
-  return launch_check(out ? "latent_out" : "latent_in");
+  const long h = dims->hidden, lh = dims->latent, S = dims->shared;
+  for (int b0 = 0; b0 < dims->tokens; b0 += kLatMaxTokens) {  // token rows b0 .. b0 + nb - 1
+    k3moe_latent_dims c = *dims;
+    c.tokens = dims->tokens - b0 < kLatMaxTokens ? dims->tokens - b0 : kLatMaxTokens;
+    LatPlan p;
+    const char *why = latent_plan(c, device_cus(), out, p);
+    if (why) return fail(K3MOE_EINVAL, "latent block geometry B=%d h=%d lh=%d S=%d: %s", c.tokens, c.hidden,
+                         c.latent, c.shared, why);
+    p.o_trace = (out ? pout : pin).o_trace;
+    LatArgs ac = a;
+    if (!out) {
+      ac.x = a.x + b0 * h;
+      ac.ya = a.ya + b0 * lh;
+      ac.yb = a.yb + b0 * S;
+    } else {
+      ac.x = a.x + b0 * S;
+      ac.esum = a.esum + b0 * lh;
+      ac.ya = a.ya + b0 * h;
+    }
+    if ((rc = allow_latent_lds(out, p.lds_total))) return rc;
+    if (out) hipLaunchKernelGGL(k_latent<1>, dim3(p.G), dim3(kLatThreads), p.lds_total, st, p, ac);
+    else hipLaunchKernelGGL(k_latent<0>, dim3(p.G), dim3(kLatThreads), p.lds_total, st, p, ac);
+    if ((rc = launch_check(out ? "latent_out" : "latent_in"))) return rc;
+  }
+  return K3MOE_OK;
 }
 
 __global__ void k_zero_words(uint32_t *p, int n) {

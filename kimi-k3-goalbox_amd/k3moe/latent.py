@@ -23,8 +23,6 @@ from . import _native
 from ._native import ACTIVATION, LatentDims, check
 from .moe import _dev_ptr, _expect, cached_workspace, moe_step
 
-MAX_TOKENS = 64
-
 
 def latent_dims(tokens: int, hidden: int, latent: int, shared: int, activation: str = 'situ') -> LatentDims:
     if activation not in ACTIVATION:

@@ -20,7 +20,8 @@ pytestmark = pytest.mark.gpu
 # (B, h, lh, S): the Kimi K3 TP8 rank (h 7168, latent 3584, shared 768 = 3072 x 2 / 8) at the
 # reference's batches, and small or ragged shapes (token tiles, splits and row tiles partly filled)
 SHAPES = [(1, 7168, 3584, 768), (8, 7168, 3584, 768), (64, 7168, 3584, 768), (3, 256, 128, 128),
-          (17, 512, 256, 128), (33, 1024, 512, 256), (40, 2048, 1024, 384), (1, 128, 128, 128)]
+          (17, 512, 256, 128), (33, 1024, 512, 256), (40, 2048, 1024, 384), (1, 128, 128, 128),
+          (100, 1024, 512, 256), (130, 512, 256, 128)]   # more than 64 tokens: launches of 64 rows
 
 
 def say(*a):
@@ -148,6 +149,7 @@ def block_case(cfg, seed, shared, shared_fan=None):
 
 @pytest.mark.parametrize('cfg,shared,seed', [
     (MoEConfig('latent-small', 64, 8, 1024, 256, 5, latent=512), 256, 0),
+    (MoEConfig('latent-b80', 64, 8, 1024, 256, 80, latent=512), 256, 3),   # general MoE path, two latent launches
     (MoEConfig('kimi-rank-e128-b8', 128, 16, 7168, 384, 8, latent=3584), 768, 1),
     (MoEConfig('kimi-rank-e128-b1', 128, 16, 7168, 384, 1, latent=3584), 768, 2),
 ])
@@ -161,19 +163,33 @@ def test_latent_block_kimi_rank_geometry():
     run_block(configs.KIMI_K3_TP8, 768, 0, shared_fan=6144)
 
 
-def run_block(cfg, shared, seed, shared_fan=None):
-    say(f'latent_block {cfg.name} shared={shared} seed={seed}')
+def test_latent_block_forced_routes():
+    """Forced expert sets (kimi.py:311-313) through the whole block."""
+    cfg = MoEConfig('latent-routes', 48, 6, 512, 128, 7, latent=256)
+    w = block_case(cfg, 4, 128)
+    g = torch.Generator().manual_seed(11)
+    routes = torch.stack([torch.randperm(cfg.experts, generator=g)[:cfg.topk] for _ in range(cfg.tokens)])
+    run_block(cfg, 128, 4, routes=routes, w=w)
+
+
+def run_block(cfg, shared, seed, shared_fan=None, routes=None, w=None):
+    say(f'latent_block {cfg.name} shared={shared} seed={seed} routes={routes is not None}')
     dev = torch.device('cuda:0')
-    w = block_case(cfg, seed, shared, shared_fan)
+    w = w if w is not None else block_case(cfg, seed, shared, shared_fan)
     g = {k: (v.to(dev) if v is not None else None) for k, v in w.items()}
     before = grading.snapshot({k: v for k, v in g.items() if v is not None})
-    got = k3moe.latent_block(g['x'], g, topk=cfg.topk)
+    got = k3moe.latent_block(g['x'], g, topk=cfg.topk, routes=None if routes is None else routes.to(dev))
     torch.cuda.synchronize(dev)
     grading.check_unchanged({k: v for k, v in g.items() if v is not None}, before)
     got = {k: v.cpu() for k, v in got.items()}
-    oracle = latent_ref.latent_block(w['x'], w, topk=cfg.topk)
-    sets = grading.route_sets(got['expert_ids'], oracle['expert_ids'], w['x'], w['router'], w['router_bias'],
-                              cfg.topk)
+    oracle = latent_ref.latent_block(w['x'], w, topk=cfg.topk, routes=routes)
+    if routes is not None:
+        assert torch.equal(got['expert_ids'], routes.sort(-1).values)
+        assert torch.allclose(got['route_shortfall'], oracle['route_shortfall'], rtol=1e-5, atol=1e-6)
+        sets = {'ok': True, 'exact': True}
+    else:
+        sets = grading.route_sets(got['expert_ids'], oracle['expert_ids'], w['x'], w['router'], w['router_bias'],
+                                  cfg.topk)
     assert sets['ok'], sets
     truth_o = latent_ref.latent_block(w['x'], w, topk=cfg.topk, fp32=True, routes=oracle['expert_ids'])
     truth_c = truth_o if sets['exact'] else latent_ref.latent_block(w['x'], w, topk=cfg.topk, fp32=True,

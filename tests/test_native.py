@@ -107,16 +107,18 @@ def test_latent_dims_struct_matches_header():
     assert fields == [f for f, _ in _native.LatentDims._fields_]
 
 
-@pytest.mark.parametrize('B', [1, 8, 64])
+@pytest.mark.parametrize('B', [1, 8, 64, 200])
 def test_latent_workspace_bytes_kimi_rank(B):
     from k3moe import latent
     n = latent.latent_workspace_bytes(latent.latent_dims(B, 7168, 3584, 768))
     # at least the counters' area and one split's fp32 partials of every output row
-    assert n % 256 == 0 and n >= 4096 + 65536 + 16384 + B*7168*4
+    assert n % 256 == 0 and n >= 4096 + 65536 + 16384 + min(B, 64)*7168*4
+    if B > 64:   # launches of 64 token rows: the 64-row workspace serves them
+        assert n == latent.latent_workspace_bytes(latent.latent_dims(64, 7168, 3584, 768))
 
 
 @pytest.mark.parametrize('dims,msg', [
-    ((0, 7168, 3584, 768), 'tokens'), ((65, 7168, 3584, 768), 'tokens'), ((8, 7100, 3584, 768), 'multiples of 128'),
+    ((0, 7168, 3584, 768), 'tokens'), ((-3, 7168, 3584, 768), 'tokens'), ((8, 7100, 3584, 768), 'multiples of 128'),
     ((8, 7168, 3500, 768), 'multiples of 128'), ((8, 7168, 3584, 0), 'multiples of 128'),
     ((64, 16384, 8192, 1024), 'does not fit')])
 def test_latent_invalid_dims_are_rejected(dims, msg):
