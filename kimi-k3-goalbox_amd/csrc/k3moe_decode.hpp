@@ -222,13 +222,15 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
   // unit rows: lanes 0-7 gate, 8-15 up
   const uint8_t *const lane_blk = i >= 8 ? a.ublk : a.gblk;
   const uint8_t *const lane_scl = i >= 8 ? a.uscl : a.gscl;
-  // A single token's groups are one round when there are at most min(16, NX)
-  // of them (a chunk is one row): each wave's range and first expert are known
-  // before the round table, so its first super-step's weight loads are issued
-  // first and the table is built while they are in flight.
+  // The first round usually holds all of this workgroup's groups: assuming it
+  // does, each wave's range and first expert are known before the round table,
+  // so its first super-step's weight loads are issued first and the table is
+  // built while they are in flight. They are the loads the round needs when
+  // the wave's range starts at the same position (always when the assumption
+  // holds); otherwise they are issued again.
   GuSS<W> B0, B1;
-  bool pre = false;
-  if (pl.B == 1 && ga < gb && gb - ga <= min(16, pl.NX)) {
+  int s_pre = -1;
+  if (ga < gb) {
     const int work = (gb - ga) * NSS;
     const int s = (int)((long)work * w / kDecWaves), e = (int)((long)work * (w + 1) / kDecWaves);
     if (s < e) {
@@ -246,7 +248,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
         sr[u] = lane_scl + row * KB;
       }
       gu_issue<W, AL>(B0, wr, sr, s % NSS, KB);
-      pre = true;
+      s_pre = s;
     }
   }
   for (int g0 = ga; g0 < gb;) {
@@ -322,9 +324,9 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
     int ig = s / NSS, iss = s % NSS;  // issue cursor
     if (s < e) {
       rows_of(ig, iwr, isr);
-      if (!pre) gu_issue<W, AL>(B0, iwr, isr, iss, KB);  // else issued before the table, the same loads
+      if (s != s_pre) gu_issue<W, AL>(B0, iwr, isr, iss, KB);  // else issued before the table, the same loads
     }
-    pre = false;
+    s_pre = -1;  // later rounds issue their own
     // progress of each wave's range in 1/4096 (empty ranges count as done);
     // visible to the workgroup's other waves after the staging barrier
     if (l == 0) __hip_atomic_store(s_prog + w, s < e ? 0 : 4096, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
