@@ -90,7 +90,11 @@ def read_trace(cfg, device):
     lat = torch.empty(cfg.tokens, cfg.width, dtype=torch.bfloat16, device=device) if cfg.latent else None
     total = k3moe.workspace_bytes(moe.dims_for(x, r, g, d, cfg.topk, cfg.gating, cfg.activation, lat))
     full = ws[total - 1024*56*8: total].cpu().view(torch.int64).view(1024, 56).double()
-    G = int((full[:, 8] > 0).sum())
+    # rows of the persistent grid: the largest power of two <= the CU count
+    # (rows past it hold other launches' stamps or never-written memory)
+    G = 1
+    while G*2 <= min(torch.cuda.get_device_properties(device).multi_processor_count, 1024):
+        G *= 2
     full = full[:G]
     raw = full[:, :9]
     dump = os.environ.get('K3MOE_TRACE_DUMP')

@@ -178,6 +178,19 @@ __device__ __forceinline__ void gu_compute(const GuSS<W> &B, const uint16_t *xro
   }
 }
 
+// n * b / gridDim.x, rounded down, for the persistent grid (a power of two):
+// a shift instead of a 64-bit division (whose expansion is long, and first
+// executed code costs instruction fetches).
+__device__ __forceinline__ int grid_share(int n, unsigned b) {
+  return (int)(((uint64_t)(unsigned)n * b) >> __builtin_ctz(gridDim.x));
+}
+
+// n * w / kDecWaves, rounded down (n >= 0).
+__device__ __forceinline__ int wave_share(int n, int w) {
+  return (int)(((uint64_t)(unsigned)n * (unsigned)w) >> 3);
+}
+static_assert(kDecWaves == 8, "wave_share divides by 8");
+
 // Gate/up groups of two units (W = 2) for nu units over the grid: when there
 // are at least two units per workgroup, and the whole groups balance as well
 // as single units or there are at least 8 units per workgroup (one group more
@@ -217,7 +230,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
   const int KB = pl.K / kBlockK, NSS = (KB + 15) / 16, K8 = pl.K / 8;
   const int GPC = pl.U8 / W;  // groups per chunk
   const int NG = g_coff[D] * GPC;
-  const int ga = (int)((long)NG * blockIdx.x / gridDim.x), gb = (int)((long)NG * (blockIdx.x + 1) / gridDim.x);
+  const int ga = grid_share(NG, blockIdx.x), gb = grid_share(NG, blockIdx.x + 1);
   auto slot = [&](int wv, int which, int u) { return red + ((wv * 2 + which) * 2 + u) * 256 + l * 4; };
   // unit rows: lanes 0-7 gate, 8-15 up
   const uint8_t *const lane_blk = i >= 8 ? a.ublk : a.gblk;
@@ -232,7 +245,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
   int s_pre = -1;
   if (ga < gb) {
     const int work = (gb - ga) * NSS;
-    const int s = (int)((long)work * w / kDecWaves), e = (int)((long)work * (w + 1) / kDecWaves);
+    const int s = wave_share(work, w), e = wave_share(work, w + 1);
     if (s < e) {
       const int G = ga + s / NSS, ci = G / GPC, pg = G % GPC;
       int lo = 0, hi = D - 1;  // active expert of chunk ci
@@ -298,7 +311,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
     const int nch = s_round[0], rows = s_round[1];
     const int g1 = min(gb, (ci0 + nch) * GPC);
     const int work = (g1 - g0) * NSS;
-    const int s = (int)((long)work * w / kDecWaves), e = (int)((long)work * (w + 1) / kDecWaves);
+    const int s = wave_share(work, w), e = wave_share(work, w + 1);
     // unit rows of group gg of the round (relative to g0)
     auto rows_of = [&](int gg, const uint8_t *(&wr)[W], const uint8_t *(&sr)[W]) {
       const int G = g0 + gg, j = G / GPC - ci0, pg = G % GPC;
@@ -417,7 +430,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
 #pragma unroll
         for (int j = 0; j < kDecWaves - 1; ++j) {
           const int w2 = w + 1 + j;
-          const int s2 = (int)((long)work * w2 / kDecWaves), e2 = (int)((long)work * (w2 + 1) / kDecWaves);
+          const int s2 = wave_share(work, w2), e2 = wave_share(work, w2 + 1);
           has[j] = w2 < kDecWaves && s2 < (gl + 1) * NSS && e2 > s2;
 #pragma unroll
           for (int u = 0; u < W; ++u)
@@ -711,7 +724,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     const int KB = pl.h / kBlockK;
     for (int u = blockIdx.x; u < NU; u += gridDim.x) {
       const int s = u % pl.Srw, rt = u / pl.Srw;
-      const int k0 = (int)((long)s * pl.KSr / pl.Srw), k1 = (int)((long)(s + 1) * pl.KSr / pl.Srw);
+      const int k0 = (int)((unsigned)(s * pl.KSr) / (unsigned)pl.Srw), k1 = (int)((unsigned)((s + 1) * pl.KSr) / (unsigned)pl.Srw);
       const int ka = k0 + (k1 - k0) * w / kDecWaves, kb1 = k0 + (k1 - k0) * (w + 1) / kDecWaves;
       const int row = rt * 16 + i;
       const bool row_ok = row < E;
@@ -1119,7 +1132,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     __syncthreads();
     const int W = gu_pairs(g_coff[D] * pl.U8) ? 2 : 1;  // as in the gate/up phase
     const int NG = g_coff[D] * (pl.U8 / W);
-    const int ga = (int)((long)NG * blockIdx.x / gridDim.x), gb = (int)((long)NG * (blockIdx.x + 1) / gridDim.x);
+    const int ga = grid_share(NG, blockIdx.x), gb = grid_share(NG, blockIdx.x + 1);
     if (ga < gb) {
       const int ua = ga * W, ub = gb * W;  // this workgroup's units, chunk-major (chunk * U8 + unit)
       auto expert_of = [&](int ci) {
@@ -1147,9 +1160,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     uint16_t *ybuf = reinterpret_cast<uint16_t *>(a.ws + pl.o_y);
     const __amdgpu_buffer_rsrc_t hrs = make_rsrc(hbuf, (uint32_t)pl.P * pl.I * 2);
     const int NT = D * pl.RTd;  // (expert, 16-row tile) items, expert-major
-    const int GW = gridDim.x * kDecWaves;
     const int gw = blockIdx.x * kDecWaves + w;
-    const int ta = (int)((long)NT * gw / GW), tb = (int)((long)NT * (gw + 1) / GW);
+    const int ta = grid_share(NT, gw) >> 3, tb = grid_share(NT, gw + 1) >> 3;  // NT * gw / (8 G)
     DnStage st;  // this wave's y stage in the scratch area (free after gate/up)
     st.rows = reinterpret_cast<uint16_t *>(scr) + w * kDnStage * 16;
     st.tag = reinterpret_cast<int *>(scr + kDecWaves * kDnStage * 32) + w * kDnStage;
@@ -1163,8 +1175,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     // combine (kimi.py:318,323): expert_sum[t][col] = sum over the token's
     // experts in ascending id order of w * bf16(y), from zero, FP32 adds
     const int K4 = pl.K / 4;
-    for (long idx = (long)blockIdx.x * kDecThreads + tid; idx < (long)B * K4; idx += (long)gridDim.x * kDecThreads) {
-      const int t = (int)(idx / K4), c4 = (int)(idx % K4) * 4;
+    for (unsigned idx = blockIdx.x * kDecThreads + tid; idx < (unsigned)(B * K4); idx += gridDim.x * kDecThreads) {
+      const int t = (int)(idx / (unsigned)K4), c4 = ((int)idx - t * K4) * 4;
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
       for (int sl = 0; sl < k; ++sl) {
         const int p = g_pof[t * k + sl];

@@ -91,8 +91,10 @@ struct LatArgs {
   char *ws;
 };
 
-// Split s covers k-steps [lat_k0(s), lat_k0(s + 1)).
-__host__ __device__ inline int lat_k0(int s, int KS, int SP) { return (int)((long)s * KS / SP); }
+// Split s covers k-steps [lat_k0(s), lat_k0(s + 1)) (SP a power of two: a shift).
+__host__ __device__ inline int lat_k0(int s, int KS, int SP) {
+  return (int)(((unsigned)s * (unsigned)KS) >> __builtin_ctz((unsigned)SP));
+}
 
 // Plan of k_latent<out> for the given geometry; null on success, else why it does not fit.
 inline const char *latent_plan(const k3moe_latent_dims &d, int n_cus, int out, LatPlan &p) {
