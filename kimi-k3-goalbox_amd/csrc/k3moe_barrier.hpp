@@ -38,33 +38,67 @@ __device__ __forceinline__ BarrierBase barrier_base(const unsigned *ctl) {
   return BarrierBase{t & ~(groups - 1u), c & ~(members - 1u)};
 }
 
-__device__ __forceinline__ void grid_barrier(unsigned *ctl, const BarrierBase &bb, unsigned n,
-                                             uint64_t *trace = nullptr) {
-  wait_vmem();  // this wave's device-coherent stores are done (and thread 0's base loads)
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned groups = bar_groups(), members = gridDim.x / groups, g = blockIdx.x % groups;
-    if (trace) trace[0] = __builtin_amdgcn_s_memrealtime();
-    const unsigned old = __hip_atomic_fetch_add(ctl + kCtlGroup + g * kCtlStride, 1u, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-    if (old == bb.grp + n * members - 1u)
-      __hip_atomic_fetch_add(ctl + kCtlTop, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (trace) trace[1] = __builtin_amdgcn_s_memrealtime();
-    const unsigned target = bb.top + n * groups;
-    unsigned spins = 0;
-    while ((int)(__hip_atomic_load(ctl + kCtlTop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-      if ((++spins & 63u) == 0u) {
-        if (__hip_atomic_load(ctl + kCtlErr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
-        if (spins > kSpinLimit) {
-          __hip_atomic_store(ctl + kCtlErr, (unsigned)kErrBarrierTimeout, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
+struct NoArrival {
+  __device__ void operator()() const {}
+};
+
+// Thread 0's arrival: counts this workgroup in on its group counter, and the
+// group in on the top counter when it is the group's last.
+__device__ __forceinline__ void barrier_arrive(unsigned *ctl, const BarrierBase &bb, unsigned n, uint64_t *trace) {
+  const unsigned groups = bar_groups(), members = gridDim.x / groups, g = blockIdx.x % groups;
+  if (trace) trace[0] = __builtin_amdgcn_s_memrealtime();
+  const unsigned old = __hip_atomic_fetch_add(ctl + kCtlGroup + g * kCtlStride, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+  if (old == bb.grp + n * members - 1u)
+    __hip_atomic_fetch_add(ctl + kCtlTop, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (trace) trace[1] = __builtin_amdgcn_s_memrealtime();
+}
+
+// Thread 0: spins until the top counter shows every group (bounded: a timeout
+// or another workgroup's error ends it), then acquires at agent scope.
+__device__ __forceinline__ void barrier_wait(unsigned *ctl, const BarrierBase &bb, unsigned n, uint64_t *trace) {
+  const unsigned target = bb.top + n * bar_groups();
+  unsigned spins = 0;
+  while ((int)(__hip_atomic_load(ctl + kCtlTop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+    if ((++spins & 63u) == 0u) {
+      if (__hip_atomic_load(ctl + kCtlErr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+      if (spins > kSpinLimit) {
+        __hip_atomic_store(ctl + kCtlErr, (unsigned)kErrBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
       }
     }
-    if (trace) trace[2] = __builtin_amdgcn_s_memrealtime();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (trace) trace[3] = __builtin_amdgcn_s_memrealtime();
+  }
+  if (trace) trace[2] = __builtin_amdgcn_s_memrealtime();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (trace) trace[3] = __builtin_amdgcn_s_memrealtime();
+}
+
+// Pending >= 0: loads may cross the barrier in flight. A wave w >= 1 that has
+// issued exactly Pending vector-memory loads after its last store (`pending`)
+// waits only for the operations before them (the counter completes in
+// order), the waves meet without the workgroup fence's full wait, and wave 0
+// runs `arrived` (its own loads) between its arrival and the spin.
+template <int Pending = -1, class Arrived = NoArrival>
+__device__ __forceinline__ void grid_barrier(unsigned *ctl, const BarrierBase &bb, unsigned n,
+                                             uint64_t *trace = nullptr, bool pending = false,
+                                             const Arrived &arrived = Arrived()) {
+  if constexpr (Pending < 0) {
+    wait_vmem();  // this wave's device-coherent stores are done (and thread 0's base loads)
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      barrier_arrive(ctl, bb, n, trace);
+      barrier_wait(ctl, bb, n, trace);
+    }
+  } else {
+    if (Pending > 0 && pending) wait_vm<Pending>();  // this wave's stores are done
+    else wait_vmem();
+    ring_barrier();
+    if (threadIdx.x < 64) {
+      if (threadIdx.x == 0) barrier_arrive(ctl, bb, n, trace);
+      asm volatile("" ::: "memory");  // after the arrival
+      arrived();
+      if (threadIdx.x == 0) barrier_wait(ctl, bb, n, trace);
+    }
   }
   __syncthreads();
 }

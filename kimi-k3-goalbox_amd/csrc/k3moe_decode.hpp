@@ -601,25 +601,46 @@ struct DnLoad {
   u32x4 b[kDnDepth][4];
 };
 
-__device__ __forceinline__ void dn_issue(const Plan &pl, const DecodeArgs &a, const uint16_t *hbuf,
-                                         const int *g_act, const int *g_aoff, const int *g_acnt, int rt, int d,
-                                         int c, int kc, int KB, DnLoad &L) {
+// Weights and scales of a down item (they do not depend on h): exactly
+// 2 kDnDepth loads per lane, k-steps past I and row tiles past the last read
+// from the zero area.
+__device__ __forceinline__ void dn_issue_w(const Plan &pl, const DecodeArgs &a, const uint8_t *zero,
+                                           const int *g_act, int rt, int d, int kc, int KB, DnLoad &L) {
   const int l = threadIdx.x & 63, i = l & 15, q = l >> 4;
-  const int e = g_act[d], p0 = g_aoff[d], n = g_acnt[d];
+  const bool rt_ok = rt < pl.RTd;
+  const size_t row = (size_t)g_act[d] * pl.K + (rt_ok ? rt : 0) * 16 + i;
+#pragma unroll
+  for (int j = 0; j < kDnDepth; ++j) {
+    const int kb = (kc + j) * 4 + q;
+    const bool ok = rt_ok && kc + j < pl.KSd && kb < KB;
+    L.w[j] = load16(ok ? a.dblk + (row * KB + kb) * 16 : zero);
+    L.s[j] = *(ok ? a.dscl + row * KB + kb : zero);
+  }
+}
+
+// The activated h rows (B operand) of a down item: token chunk c of active expert d.
+__device__ __forceinline__ void dn_issue_h(const Plan &pl, const uint16_t *hbuf, const int *g_aoff,
+                                           const int *g_acnt, int d, int c, int kc, int KB, DnLoad &L) {
+  const int l = threadIdx.x & 63, i = l & 15, q = l >> 4;
+  const int p0 = g_aoff[d], n = g_acnt[d];
   const int pj = c * 16 + i;
   const bool tok_ok = pj < n;
-  const size_t row = (size_t)e * pl.K + rt * 16 + i;
   const uint16_t *hr = hbuf + (size_t)(p0 + (tok_ok ? pj : 0)) * pl.I;
 #pragma unroll
   for (int j = 0; j < kDnDepth; ++j) {
     const int kb = (kc + j) * 4 + q;
     const bool ok = kc + j < pl.KSd && kb < KB;
-    L.w[j] = ok ? load16(a.dblk + (row * KB + kb) * 16) : u32x4{0, 0, 0, 0};
-    L.s[j] = ok ? a.dscl[row * KB + kb] : 127u;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
       L.b[j][kk] = (ok && tok_ok) ? load16(hr + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
   }
+}
+
+__device__ __forceinline__ void dn_issue(const Plan &pl, const DecodeArgs &a, const uint16_t *hbuf,
+                                         const uint8_t *zero, const int *g_act, const int *g_aoff,
+                                         const int *g_acnt, int rt, int d, int c, int kc, int KB, DnLoad &L) {
+  dn_issue_w(pl, a, zero, g_act, rt, d, kc, KB, L);
+  dn_issue_h(pl, hbuf, g_aoff, g_acnt, d, c, kc, KB, L);
 }
 
 static_assert(sizeof(Plan) % alignof(DecodeArgs) == 0, "DecodeArgs follows Plan in the argument segment");
@@ -1150,7 +1171,30 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
           __hip_atomic_fetch_add(ecnt + d * kCntStride, (unsigned)n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-  } else {
+  }
+  // Row-tile down with at most one active expert per wave, one token chunk
+  // per expert, I <= 256 and at most two row tiles per workgroup (small
+  // batches): wave w takes its expert's item in both row tiles. The weights do
+  // not depend on h, so their loads are issued before barrier 3 (wave 0's just
+  // after its arrival) and arrive while it completes; only h follows it.
+  const int dn_da = D * w / kDecWaves, dn_db = D * (w + 1) / kDecWaves;
+  const bool dn_pair = !expert_major && D <= kDecWaves && B <= 16 && pl.KSd <= kDnDepth &&
+                       pl.RTd <= 2 * (int)gridDim.x;
+  DnLoad pf[2];
+  auto dn_pair_issue = [&]() {
+    if (dn_da < dn_db) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)  // a row tile past the last reads the zero area
+        dn_issue_w(pl, a, zero, g_act, (int)blockIdx.x + tt * (int)gridDim.x, dn_da, 0, pl.I / kBlockK, pf[tt]);
+    }
+  };
+  if (dn_pair) {
+    if (w > 0) {
+      asm volatile("" ::: "memory");  // after this wave's h stores
+      dn_pair_issue();
+    }
+    grid_barrier<4 * kDnDepth>(ctl, bb, ++nbar, trace_slots(pl, a.ws, 20), w > 0 && dn_da < dn_db, dn_pair_issue);
+  } else if (!expert_major) {
     grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 20));
   }
   trace_mark(pl, a.ws, 7);
@@ -1189,6 +1233,54 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       }
       *reinterpret_cast<f32x4 *>(a.out + (size_t)t * pl.K + c4) = f32x4{acc[0], acc[1], acc[2], acc[3]};
     }
+  } else if (dn_pair) {
+    // wave w: its expert's item in both row tiles, h loaded once after the barrier
+    float *acc_lds = reinterpret_cast<float *>(scr);  // [2 row tiles][8 waves][B][16]
+    const int BS = B * 16;
+    for (int j = l; j < 2 * BS; j += 64) {
+      const int tt = j >= BS ? 1 : 0;
+      acc_lds[(tt * kDecWaves + w) * BS + j - tt * BS] = 0.f;
+    }
+    wave_lds_order();
+    if (dn_da < dn_db) {
+      const int d = dn_da;
+      dn_issue_h(pl, hbuf, g_aoff, g_acnt, d, 0, 0, pl.I / kBlockK, pf[0]);
+      f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+        for (int j = 0; j < kDnDepth; ++j) {
+          if (j >= pl.KSd) break;
+          bf16x8 av[4];
+          convert_block_fast(pf[tt].w[j], pf[tt].s[j], av);
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) acc[tt] = mfma16(av[kk], as_bf16x8(pf[0].b[j][kk]), acc[tt]);
+        }
+      }
+      const int p0 = g_aoff[d];
+      if (i < g_acnt[d]) {  // w * bf16(y) of the expert's token i, from zero
+        const int t = g_ptok[p0 + i];
+        const float wt = g_pw[p0 + i];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          float *dst = acc_lds + (tt * kDecWaves + w) * BS + t * 16 + 4 * q;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) dst[v] = __fadd_rn(dst[v], __fmul_rn(round_bf16(acc[tt][v]), wt));
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int rt = (int)blockIdx.x + tt * (int)gridDim.x;
+      if (rt >= pl.RTd) break;
+      for (int j = tid; j < BS; j += kDecThreads) {
+        float sum = acc_lds[tt * kDecWaves * BS + j];
+#pragma unroll
+        for (int ww = 1; ww < kDecWaves; ++ww) sum = __fadd_rn(sum, acc_lds[(tt * kDecWaves + ww) * BS + j]);
+        a.out[(size_t)(j >> 4) * pl.K + rt * 16 + (j & 15)] = sum;
+      }
+    }
   } else
   {
     const int KB = pl.I / kBlockK;
@@ -1205,7 +1297,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       for (int j = l; j < B * 16; j += 64) mine[j] = 0.f;
       wave_lds_order();
       int d = da, c = 0, kc = 0;
-      if (d < db && !prefetched) dn_issue(pl, a, hbuf, g_act, g_aoff, g_acnt, rt, d, c, kc, KB, cur);
+      if (d < db && !prefetched) dn_issue(pl, a, hbuf, zero, g_act, g_aoff, g_acnt, rt, d, c, kc, KB, cur);
       prefetched = false;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
       while (d < db) {
@@ -1218,9 +1310,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
           }
         }
         if (nd < db) {
-          dn_issue(pl, a, hbuf, g_act, g_aoff, g_acnt, rt, nd, nc, nkc, KB, nxt);
+          dn_issue(pl, a, hbuf, zero, g_act, g_aoff, g_acnt, rt, nd, nc, nkc, KB, nxt);
         } else if (rt + (int)gridDim.x < pl.RTd) {
-          dn_issue(pl, a, hbuf, g_act, g_aoff, g_acnt, rt + gridDim.x, da, 0, 0, KB, nxt);
+          dn_issue(pl, a, hbuf, zero, g_act, g_aoff, g_acnt, rt + gridDim.x, da, 0, 0, KB, nxt);
           prefetched = true;
         }
 #pragma unroll

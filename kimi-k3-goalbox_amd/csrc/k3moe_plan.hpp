@@ -99,7 +99,7 @@ inline int decode_lds(Plan &p) {
   const int routed = 8 * p.P;                                       // ids + weights per pair
   const int topk = routed + 4 * (3 * nt * p.E + kDecWaves * kMaxTopk) + 8 * kDecWaves * 32 + 8;  // keys, scores, picks, offers
   const int group = routed + 4 * (4 * p.E + 32);                    // counts, offsets, bitmaps, wave sums
-  int down = kDecWaves * p.B * 16 * 4;                              // per-wave combine accumulators
+  int down = (p.B <= 16 ? 2 : 1) * kDecWaves * p.B * 16 * 4;       // per-wave combine accumulators (2 row tiles up to 16 tokens)
   if (down < kDecWaves * kDnStage * 36) down = kDecWaves * kDnStage * 36;  // or per-wave y stages
   int scr = topk;
   if (group > scr) scr = group;

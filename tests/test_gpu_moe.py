@@ -128,6 +128,8 @@ TINY = [
     # more than 32 active experts with I = 384 and 512: the expert-major down path's 3 and 4 k-steps
     MoEConfig('i384-wide', 96, 8, 128, 384, 7),
     MoEConfig('i512-wide', 64, 8, 128, 512, 9),
+    # at most 8 active experts with up to 16 tokens each: the paired row-tile down path
+    MoEConfig('e8-b16', 8, 2, 512, 256, 16),
 ]
 
 
