@@ -128,8 +128,11 @@ TINY = [
     # more than 32 active experts with I = 384 and 512: the expert-major down path's 3 and 4 k-steps
     MoEConfig('i384-wide', 96, 8, 128, 384, 7),
     MoEConfig('i512-wide', 64, 8, 128, 512, 9),
-    # at most 8 active experts with up to 16 tokens each: the paired row-tile down path
+    # at most 8 active experts with up to 16 tokens each: the paired row-tile down path;
+    # 9 to 12 active experts at small batches: the row-tile path's multi-expert waves
     MoEConfig('e8-b16', 8, 2, 512, 256, 16),
+    MoEConfig('e16-k4', 16, 4, 256, 128, 3),
+    MoEConfig('e12-k6', 12, 6, 384, 256, 2),
 ]
 
 
