@@ -1034,7 +1034,24 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   trace_mark(pl, a.ws, 4);
 
   // ------------------------------------------------- G: grouping (in LDS) --
-  {
+  if (B == 1) {
+    // one token: its k distinct experts, ascending, are the active list, with
+    // one pair and one chunk each
+    if (tid < k) {
+      g_act[tid] = rid[tid];
+      g_aoff[tid] = tid;
+      g_acnt[tid] = 1;
+      g_coff[tid] = tid;
+      g_ptok[tid] = 0;
+      g_pw[tid] = rw[tid];
+      g_pof[tid] = tid;
+    }
+    if (tid == 0) {
+      s_nact = k;
+      g_coff[k] = k;
+    }
+    __syncthreads();
+  } else {
     int *cnt = reinterpret_cast<int *>(scr2);  // [E]
     int *off = cnt + E;                        // [E]
     uint32_t *bits = reinterpret_cast<uint32_t *>(off + E);  // [E][2] token bitmaps (B <= 64)
