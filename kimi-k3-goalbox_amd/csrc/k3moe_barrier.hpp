@@ -38,10 +38,6 @@ __device__ __forceinline__ BarrierBase barrier_base(const unsigned *ctl) {
   return BarrierBase{t & ~(groups - 1u), c & ~(members - 1u)};
 }
 
-struct NoArrival {
-  __device__ void operator()() const {}
-};
-
 // Thread 0's arrival: counts this workgroup in on its group counter, and the
 // group in on the top counter when it is the group's last.
 __device__ __forceinline__ void barrier_arrive(unsigned *ctl, const BarrierBase &bb, unsigned n, uint64_t *trace) {
@@ -73,32 +69,13 @@ __device__ __forceinline__ void barrier_wait(unsigned *ctl, const BarrierBase &b
   if (trace) trace[3] = __builtin_amdgcn_s_memrealtime();
 }
 
-// Pending >= 0: loads may cross the barrier in flight. A wave w >= 1 that has
-// issued exactly Pending vector-memory loads after its last store (`pending`)
-// waits only for the operations before them (the counter completes in
-// order), the waves meet without the workgroup fence's full wait, and wave 0
-// runs `arrived` (its own loads) between its arrival and the spin.
-template <int Pending = -1, class Arrived = NoArrival>
 __device__ __forceinline__ void grid_barrier(unsigned *ctl, const BarrierBase &bb, unsigned n,
-                                             uint64_t *trace = nullptr, bool pending = false,
-                                             const Arrived &arrived = Arrived()) {
-  if constexpr (Pending < 0) {
-    wait_vmem();  // this wave's device-coherent stores are done (and thread 0's base loads)
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      barrier_arrive(ctl, bb, n, trace);
-      barrier_wait(ctl, bb, n, trace);
-    }
-  } else {
-    if (Pending > 0 && pending) wait_vm<Pending>();  // this wave's stores are done
-    else wait_vmem();
-    ring_barrier();
-    if (threadIdx.x < 64) {
-      if (threadIdx.x == 0) barrier_arrive(ctl, bb, n, trace);
-      asm volatile("" ::: "memory");  // after the arrival
-      arrived();
-      if (threadIdx.x == 0) barrier_wait(ctl, bb, n, trace);
-    }
+                                             uint64_t *trace = nullptr) {
+  wait_vmem();  // this wave's device-coherent stores are done (and thread 0's base loads)
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    barrier_arrive(ctl, bb, n, trace);
+    barrier_wait(ctl, bb, n, trace);
   }
   __syncthreads();
 }

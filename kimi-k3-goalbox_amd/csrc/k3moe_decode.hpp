@@ -636,6 +636,24 @@ __device__ __forceinline__ void dn_issue_h(const Plan &pl, const uint16_t *hbuf,
   }
 }
 
+// The same h rows (k-steps 0 .. kDnDepth - 1) with device-coherent loads, for
+// a wave that waited on the expert's count instead of a grid barrier.
+__device__ __forceinline__ void dn_issue_h_dev(const Plan &pl, const uint16_t *hbuf, const int *g_aoff,
+                                               const int *g_acnt, int d, DnLoad &L) {
+  const int l = threadIdx.x & 63, i = l & 15, q = l >> 4;
+  const __amdgpu_buffer_rsrc_t hrs = make_rsrc(hbuf, (uint32_t)pl.P * pl.I * 2);
+  const int KB = pl.I / kBlockK;
+  const bool tok_ok = i < g_acnt[d];
+#pragma unroll
+  for (int j = 0; j < kDnDepth; ++j) {
+    const int kb = j * 4 + q;
+    const bool ok = tok_ok && j < pl.KSd && kb < KB;
+    const uint32_t off = ok ? (uint32_t)(((g_aoff[d] + i) * pl.I + kb * kBlockK) * 2) : kOffNone;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) L.b[j][kk] = bload16_dev(hrs, off + kk * 16);
+  }
+}
+
 __device__ __forceinline__ void dn_issue(const Plan &pl, const DecodeArgs &a, const uint16_t *hbuf,
                                          const uint8_t *zero, const int *g_act, const int *g_aoff,
                                          const int *g_acnt, int rt, int d, int c, int kc, int KB, DnLoad &L) {
@@ -1148,9 +1166,18 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   // finished per expert (after its h stores have completed), and a down wave
   // waits for its expert's count. Each count has a 128-byte line of its own:
   // increments of one line are serialised where they are performed. The
-  // row-tile down path needs every expert in every workgroup and keeps the
-  // barrier (with few experts all workgroups would count on a few lines).
+  // paired row-tile path below (at most one expert per wave) waits the same
+  // way; the general row-tile path needs every expert in every workgroup and
+  // keeps the barrier.
   const bool expert_major = KSD > 0 && D > kDnExpertMajorMin && pl.o_y;
+  // Paired row-tile down: at most one active expert per wave, one token
+  // chunk per expert, I <= 256 and at most two row tiles per workgroup (small
+  // batches). Wave w takes its expert's item in both row tiles; the weights
+  // do not depend on h, so they are loaded while the expert's gate/up units
+  // complete.
+  const int dn_da = D * w / kDecWaves, dn_db = D * (w + 1) / kDecWaves;
+  const bool dn_pair = !expert_major && D <= kDecWaves && B <= 16 && pl.KSd <= kDnDepth &&
+                       pl.RTd <= 2 * (int)gridDim.x;
   auto wait_expert = [&](int d) {  // bounded: a timeout sets the status word
     const unsigned need = (unsigned)(g_coff[d + 1] - g_coff[d]) * pl.U8;
     unsigned spins = 0;
@@ -1165,7 +1192,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     // order; this keeps the compiler from hoisting them)
     asm volatile("" ::: "memory");
   };
-  if (expert_major) {
+  if (expert_major || dn_pair) {
     wait_vmem();
     __syncthreads();
     const int W = gu_pairs(g_coff[D] * pl.U8) ? 2 : 1;  // as in the gate/up phase
@@ -1189,29 +1216,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       }
     }
   }
-  // Row-tile down with at most one active expert per wave, one token chunk
-  // per expert, I <= 256 and at most two row tiles per workgroup (small
-  // batches): wave w takes its expert's item in both row tiles. The weights do
-  // not depend on h, so their loads are issued before barrier 3 (wave 0's just
-  // after its arrival) and arrive while it completes; only h follows it.
-  const int dn_da = D * w / kDecWaves, dn_db = D * (w + 1) / kDecWaves;
-  const bool dn_pair = !expert_major && D <= kDecWaves && B <= 16 && pl.KSd <= kDnDepth &&
-                       pl.RTd <= 2 * (int)gridDim.x;
   DnLoad pf[2];
-  auto dn_pair_issue = [&]() {
-    if (dn_da < dn_db) {
+  if (dn_pair && dn_da < dn_db) {
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)  // a row tile past the last reads the zero area
-        dn_issue_w(pl, a, zero, g_act, (int)blockIdx.x + tt * (int)gridDim.x, dn_da, 0, pl.I / kBlockK, pf[tt]);
-    }
-  };
-  if (dn_pair) {
-    if (w > 0) {
-      asm volatile("" ::: "memory");  // after this wave's h stores
-      dn_pair_issue();
-    }
-    grid_barrier<4 * kDnDepth>(ctl, bb, ++nbar, trace_slots(pl, a.ws, 20), w > 0 && dn_da < dn_db, dn_pair_issue);
-  } else if (!expert_major) {
+    for (int tt = 0; tt < 2; ++tt)  // a row tile past the last reads the zero area
+      dn_issue_w(pl, a, zero, g_act, (int)blockIdx.x + tt * (int)gridDim.x, dn_da, 0, pl.I / kBlockK, pf[tt]);
+  } else if (!expert_major && !dn_pair) {
     grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 20));
   }
   trace_mark(pl, a.ws, 7);
@@ -1261,7 +1271,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     wave_lds_order();
     if (dn_da < dn_db) {
       const int d = dn_da;
-      dn_issue_h(pl, hbuf, g_aoff, g_acnt, d, 0, 0, pl.I / kBlockK, pf[0]);
+      wait_expert(d);  // the expert's gate/up units are all done
+      dn_issue_h_dev(pl, hbuf, g_aoff, g_acnt, d, pf[0]);
       f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
