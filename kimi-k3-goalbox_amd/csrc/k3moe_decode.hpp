@@ -18,12 +18,15 @@
 //   GU  gate/up: stream-K over groups of (expert, token chunk, 8 gate + 8 up
 //       rows) units with the chunks' activation rows staged in LDS; SiTU /
 //       SiLU epilogue; bf16 h to memory.                       (kimi.py:321-322)
-//   --- barrier 3
+//   --- barrier 3 (general row-tile down only; the other down paths wait on
+//       per-expert counts of finished gate/up units)
 //   DN  many active experts: expert-major (expert, 16-row tile) ranges per
 //       wave, bf16 y per pair staged in LDS and written out in bulk, then
 //       barrier 4 and the combine (w * bf16(y), ascending expert order).
 //       Few active experts: each workgroup takes 16 output rows of every
-//       active expert and sums w * bf16(y) in LDS.             (kimi.py:318-323)
+//       active expert and sums w * bf16(y) in LDS; with at most 8 (one per
+//       wave) and two row tiles per workgroup, a wave's weights for both
+//       tiles are loaded while its expert's gate/up completes.  (kimi.py:318-323)
 // The barrier spin is bounded: a workgroup that waits too long sets the
 // error word and every workgroup runs to the end.
 #pragma once
