@@ -226,7 +226,8 @@ __device__ __forceinline__ void gu_finish_wave(const Plan &pl, uint16_t *hbuf, c
 // The gate/up phase of one workgroup (see the comment above GuSS).
 template <int W, bool AL>
 __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, float *red, const int *g_act,
-                                      const int *g_aoff, const int *g_acnt, const int *g_coff, const int *g_ptok,
+                                      const int *g_aoff, const int *g_acnt, const int *g_coff, const int *g_cexp,
+                                      const int *g_ptok,
                                       uint16_t *xs, GuChunk *tab, int *s_round, int *s_rowtok, int *s_prog, int D,
                                       uint16_t *hbuf, const u32x4 (&xpre)[2], bool xpre_ok) {
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i = l & 15;
@@ -251,11 +252,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
     const int s = wave_share(work, w), e = wave_share(work, w + 1);
     if (s < e) {
       const int G = ga + s / NSS, ci = G / GPC, pg = G % GPC;
-      int lo = 0, hi = D - 1;  // active expert of chunk ci
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (g_coff[mid] <= ci) lo = mid; else hi = mid - 1;
-      }
+      const int lo = g_cexp[ci];  // active expert of chunk ci
       const uint8_t *wr[W], *sr[W];
 #pragma unroll
       for (int u = 0; u < W; ++u) {
@@ -278,32 +275,22 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
       const bool in = l < 16 && ci * GPC < gb;
       int n = 0, e = 0, pbase = 0;
       if (in) {
-        int lo = 0, hi = D - 1;  // active expert of chunk ci: largest lo with g_coff[lo] <= ci
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if (g_coff[mid] <= ci) lo = mid; else hi = mid - 1;
-        }
+        const int lo = g_cexp[ci];  // active expert of chunk ci
         const int c = ci - g_coff[lo];
         e = g_act[lo];
         pbase = g_aoff[lo] + c * pl.NX;
         n = min(pl.NX, g_acnt[lo] - c * pl.NX);
       }
-      int pre = n;  // inclusive prefix of the token counts
-#pragma unroll
-      for (int dd = 1; dd < 16; dd <<= 1) {
-        const int o = __shfl_up(pre, dd, 64);
-        if (l >= dd) pre += o;
-      }
+      const int pre = wave_incl_scan(n);  // inclusive prefix of the token counts (lanes >= 16 add 0)
       const bool fits = in && pre <= pl.NX;
       const int nch = __popcll(__ballot(fits));  // >= 1: one chunk never exceeds NX rows
-      const int rows = __shfl(pre, nch - 1, 64);
+      const int rows = __builtin_amdgcn_readlane(pre, nch - 1);
       if (fits) tab[l] = GuChunk{e, pbase, n, pre - n};
+      // staged row l's chunk: the number of chunks that end at or before it
+      int j = 0;
+      for (int jj = 0; jj + 1 < nch; ++jj) j += __builtin_amdgcn_readlane(pre, jj) <= l ? 1 : 0;
       wave_lds_order();
-      if (l < rows) {  // staged row l: token of its chunk
-        int j = 0;
-        while (j + 1 < nch && tab[j + 1].xrow <= l) ++j;
-        s_rowtok[l] = g_ptok[tab[j].pbase + l - tab[j].xrow];
-      }
+      if (l < rows) s_rowtok[l] = g_ptok[tab[j].pbase + l - tab[j].xrow];  // staged row l: token of its chunk
       if (l == 0) {
         s_round[0] = nch;
         s_round[1] = rows;
@@ -712,6 +699,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   int *g_ptok = g_coff + pl.Dmax + 1;
   float *g_pw = reinterpret_cast<float *>(g_ptok + pl.P);
   int *g_pof = reinterpret_cast<int *>(g_pw + pl.P);  // pair index of (token, slot)
+  int *g_cexp = g_pof + pl.P;  // [P] active expert (index into g_act) of each gate/up chunk
   char *scr = lds + pl.lds_red + pl.lds_grp;
   __shared__ int s_nact;
   __shared__ GuChunk s_tab[16];
@@ -1066,6 +1054,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       g_ptok[tid] = 0;
       g_pw[tid] = rw[tid];
       g_pof[tid] = tid;
+      g_cexp[tid] = tid;
     }
     if (tid == 0) {
       s_nact = k;
@@ -1120,6 +1109,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
           g_aoff[oa] = op;
           g_acnt[oa] = c0;
           g_coff[oa] = oc;
+          for (int c = 0; c < n0; ++c) g_cexp[oc + c] = oa;
           ++oa;
           oc += n0;
         }
@@ -1132,6 +1122,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
           g_aoff[oa] = op;
           g_acnt[oa] = c1;
           g_coff[oa] = oc;
+          for (int c = 0; c < n1; ++c) g_cexp[oc + c] = oa;
         }
       }
       if (tid == kDecThreads - 1) {  // totals
@@ -1159,9 +1150,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   {
     uint16_t *xs = reinterpret_cast<uint16_t *>(scr);  // staged activation rows (the scratch is free now)
     if (gu_pairs(g_coff[D] * pl.U8))
-      gu_phase<2, AL>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
+      gu_phase<2, AL>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_cexp, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
     else
-      gu_phase<1, AL>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
+      gu_phase<1, AL>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_cexp, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
   }
   trace_mark(pl, a.ws, 6);
   // Expert-major down reads an expert's h only after its gate/up units are
@@ -1203,15 +1194,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     const int ga = grid_share(NG, blockIdx.x), gb = grid_share(NG, blockIdx.x + 1);
     if (ga < gb) {
       const int ua = ga * W, ub = gb * W;  // this workgroup's units, chunk-major (chunk * U8 + unit)
-      auto expert_of = [&](int ci) {
-        int lo = 0, hi = D - 1;
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if (g_coff[mid] <= ci) lo = mid; else hi = mid - 1;
-        }
-        return lo;
-      };
-      const int d0 = expert_of(ua / pl.U8), d1 = expert_of((ub - 1) / pl.U8);
+      const int d0 = g_cexp[ua / pl.U8], d1 = g_cexp[(ub - 1) / pl.U8];
       for (int d = d0 + tid; d <= d1; d += kDecThreads) {
         const int n = min(ub, g_coff[d + 1] * pl.U8) - max(ua, g_coff[d] * pl.U8);
         if (n > 0)

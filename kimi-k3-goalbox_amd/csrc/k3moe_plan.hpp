@@ -93,7 +93,7 @@ inline int align16(int v) { return (v + 15) & ~15; }
 // Decode-path LDS layout for plan p; returns the total bytes.
 inline int decode_lds(Plan &p) {
   p.lds_red = kDecWaves * 2 * 2 * 256 * 4;                          // per wave 2 x 2 16x16 fp32 tiles
-  p.lds_grp = align16(4 * (4 * p.Dmax + 1 + 3 * p.P));              // active list + chunk offsets + pairs
+  p.lds_grp = align16(4 * (4 * p.Dmax + 1 + 4 * p.P));              // active list + chunk offsets + pairs + chunk experts
   p.redundant = p.B * p.E <= kRedundantKeys && p.B <= kRedundantTokens;
   const int nt = p.redundant ? p.B : 1;
   const int routed = 8 * p.P;                                       // ids + weights per pair
