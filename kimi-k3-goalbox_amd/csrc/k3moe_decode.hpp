@@ -917,9 +917,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       __syncthreads();
       trace_mark(pl, a.ws, 10);
       // One token per pass: the 8 waves share its selection. With E <= 512
-      // and k <= 8, wave w sorts experts 64 w .. 64 w + 63 as (key, ~expert)
-      // values with a bitonic network and offers its k best; wave 0 sorts the
-      // 8 k offers and keeps the first k. With E <= 1024 and k <= 32, wave w
+      // and k <= 8, wave w selects the 8 best of experts 64 w .. 64 w + 63 as
+      // (key, ~expert) values with a bitonic network (8-lane sorts, three
+      // merge levels) and offers its k best; wave 0 merges the 8 sorted
+      // offers the same way and keeps the first k. With E <= 1024 and k <= 32, wave w
       // sorts experts 64 w .. and 64 (w + 8) .. and merges them into its 32
       // best; wave 0 merges the 8 offers in a tree of three levels. Otherwise
       // one wave per token runs wave_topk.
@@ -953,12 +954,13 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
               (reinterpret_cast<uintptr_t>(sel + kDecWaves * kMaxTopk) + 7) & ~(uintptr_t)7);  // [8 k]
           const int e = w * 64 + l;
           uint64_t v = e < E ? ((uint64_t)kyl[e] << 32) | (uint32_t)~e : 0ull;
-          v = wave_sort_desc(v);
+          v = wave_top8_desc(v);
           if (l < k) cand[w * k + l] = v;
           __syncthreads();
           if (w == 0) {
-            uint64_t c = l < kDecWaves * k ? cand[l] : 0ull;
-            c = wave_sort_desc(c);
+            // offer j in lanes 8 j .. 8 j + 7, descending, zeros past its k
+            uint64_t c = (l & 7) < k ? cand[(l >> 3) * k + (l & 7)] : 0ull;
+            c = wave_merge8_desc(c);
             if (l < k) sel[l] = (int)~(uint32_t)c;
             wave_lds_order();
           }
