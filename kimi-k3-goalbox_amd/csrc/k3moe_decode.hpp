@@ -843,9 +843,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     int *sel = reinterpret_cast<int *>(scl + nt * E);    // [8 waves][kMaxTopk]
     for (int t0 = redundant ? 0 : blockIdx.x; t0 < B; t0 += redundant ? B : gridDim.x) {
       // logits of (t0 + f / E, f % E): partials summed in split order. With
-      // E % 4 == 0 a thread takes 4 consecutive experts of a token per item
-      // group (one 16-byte load per split; partial rows are 64-byte aligned)
-      // and two groups at a time, every load in flight together.
+      // E % 4 == 0 and more logits than threads a thread takes 4 consecutive
+      // experts of a token per item group (one 16-byte load per split;
+      // partial rows are 64-byte aligned) and two groups at a time, every load
+      // in flight together; otherwise one logit per thread (the gating math
+      // spread over the most threads).
       auto gate = [&](int f, float logit, float bias) {
         float score, key;
         if (pl.gating == K3MOE_GATING_SIGMOID_BIAS) {
@@ -859,7 +861,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
         kyf[f] = key;
         kyl[f] = ordered_key(key);
       };
-      if ((E & 3) == 0) {
+      if ((E & 3) == 0 && nt * E > kDecThreads) {
         const int NG4 = nt * E / 4;
         for (int g0 = tid; g0 < NG4; g0 += 2 * kDecThreads) {
           f32x4 ps[2][kDecMaxSplits];
