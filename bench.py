@@ -4,7 +4,16 @@
 A step is one MoE layer (router top-k, MXFP4 gate/up, activation, down,
 weighted combine) over one batch of seeded synthetic inputs resident in HBM.
 Default workload: one TP8 rank's expert shard (E=384, top-8, h=7168, I=256)
-at batch 1 (the headline line), with batches 8 and 64 reported beside it.
+at batch 1 (the headline line), with batches 8 and 64 reported beside it, and
+(unless --no-extra) 8 stacked batch-64 layers of that shard with fresh weights
+per layer, and the unsharded prefill chunk (I=2048, 4096 tokens), both with
+inputs made on the device.
+
+Self-check: the last timed run's outputs are checked against the CPU oracle
+(expert sets exact or FP64-certified near-ties, the band ratio of kimi.py's
+grader <= 1, finite values; all rows of the batches, sampled rows of the
+stacked and prefill configurations), and the workspace status word is read
+after each timed loop. A failure prints the JSON line, then exits with 3.
 
 Timing: HIP events on the stream bracket each run of the step: by default the
 step's kernel launch on the stream with its outputs and workspace allocated
@@ -32,6 +41,7 @@ timed separately with events between them; CPU baseline: the restatement of the
 block (oracle/latent_ref.py).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--workload tp8|tp8-l8|prefill|kimi-latent]
+                       [--no-extra] [--no-check] [--no-cpu-baseline]
 """
 
 from __future__ import annotations
@@ -241,8 +251,15 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, 
     torch.cuda.synchronize(device)
     wall = time.perf_counter() - t0
     ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    # the graph's outputs equal an eager step on the same inputs (bitwise)
+    # the last timed run's outputs, for the oracle checks
+    timed = [{k: v.cpu() for k, v in o.items()} for o in outs]
+    # the step's workspace status: 0 unless a wait timed out or a forced-route row was invalid
     inp0 = data[0][0]
+    ws = k3moe.moe.get_workspace(k3moe.moe.dims_for(inp0['x'], inp0['router'], inp0['gate_blocks'],
+                                                    inp0['down_blocks'], cfg.topk, cfg.gating, cfg.activation,
+                                                    inp0.get('latent')), device)
+    status = k3moe.workspace_status(ws)
+    # the graph's outputs equal an eager step on the same inputs (bitwise)
     eager = k3moe.moe_step(*synthetic.step_args(inp0), **kw, latent=inp0.get('latent'))
     torch.cuda.synchronize(device)
     same = all(torch.equal(outs[0][k], eager[k]) for k in eager)
@@ -253,7 +270,8 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, 
     trace = read_trace(cfg, device) if os.environ.get('K3MOE_TRACE') == '1' and layers == 1 else None
     del graph, outs, flush
     return {'ms': ms, 'wall_s': wall, 'distinct': distinct, 'bytes': nbytes, 'flops': flops,
-            'graph_matches_eager': same, 'host_inputs': [h for _, h in data], 'trace': trace}
+            'graph_matches_eager': same, 'host_inputs': [h for _, h in data], 'trace': trace,
+            'timed': timed, 'status': status, 'device_inputs': [d for d, _ in data]}
 
 
 KIMI_SHARED, KIMI_SHARED_FAN = 768, 6144  # shared-expert width of a TP8 rank (3072 x 2 / 8), unsharded fan-in
@@ -374,13 +392,85 @@ def cpu_baseline(cfg, host_inputs, reps=3):
     torch.set_num_threads(cores)
     args = synthetic.step_args(host_inputs)
     kw = dict(topk=cfg.topk, gating=cfg.gating, activation=cfg.activation, latent=host_inputs.get('latent'))
-    moe_ref.moe_step(*args, **kw)
+    result = moe_ref.moe_step(*args, **kw)
     ts = []
     for _ in range(reps):
         t = time.perf_counter()
         moe_ref.moe_step(*args, **kw)
         ts.append(time.perf_counter() - t)
-    return {'us_per_layer': round(statistics.median(ts)*1e6, 1), 'cores': torch.get_num_threads(), 'reps': reps}
+    return {'us_per_layer': round(statistics.median(ts)*1e6, 1), 'cores': torch.get_num_threads(), 'reps': reps,
+            'oracle': result}
+
+
+class _DeviceExperts:
+    """An expert tensor left on the GPU, indexed by expert id on the host: the oracle reads
+    only the routed experts, so each one's slice is copied to the CPU on first use."""
+
+    def __init__(self, t):
+        self.t, self.cache = t, {}
+
+    def __getitem__(self, e):
+        e = int(e)
+        if e not in self.cache:
+            self.cache[e] = self.t[e].cpu()
+        return self.cache[e]
+
+
+def host_view(g):
+    """Oracle inputs for device-resident step inputs: small tensors copied, experts lazy."""
+    import torch
+    return {k: (_DeviceExperts(v) if k.endswith(('_blocks', '_scales')) else
+                v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in g.items()}
+
+
+def oracle_check(cfg, got, host, rows=None, oracle_bf16=None) -> dict:
+    """The timed outputs against the CPU oracle (the grader of kimi.py:413-455): per-row expert
+    sets (exact, or FP64-certified near-ties), route weights, and the band ratio
+    rel-L2(got, FP32 truth) / (2 rel-L2(BF16 oracle, FP32 truth) + 0.002), which must be <= 1.
+    `rows` restricts the oracle to sampled token rows (the large configurations)."""
+    import torch
+    from oracle import grading, moe_ref
+    from k3moe import synthetic
+    kw = dict(topk=cfg.topk, gating=cfg.gating, activation=cfg.activation)
+    ref_in = dict(host)
+    if rows is not None:
+        rows = torch.as_tensor(rows)
+        ref_in['x'] = host['x'][rows]
+        if host.get('latent') is not None:
+            ref_in['latent'] = host['latent'][rows]
+        got = {k: v[rows] for k, v in got.items()}
+    args = synthetic.step_args(ref_in)
+    lat = ref_in.get('latent')
+    bf = oracle_bf16 if oracle_bf16 is not None else moe_ref.moe_step(*args, **kw, latent=lat)
+    sets = grading.route_sets(got['expert_ids'], bf['expert_ids'], ref_in['x'], ref_in['router'],
+                              ref_in['router_bias'], cfg.topk, cfg.gating)
+    truth_o = moe_ref.moe_step(*args, **kw, fp32=True, routes=bf['expert_ids'], latent=lat)
+    truth_c = truth_o if sets['exact'] else moe_ref.moe_step(*args, **kw, fp32=True, routes=got['expert_ids'],
+                                                             latent=lat)
+    oracle_err = moe_ref.rel_l2(bf['expert_sum'], truth_o['expert_sum'])
+    cand_err = moe_ref.rel_l2(got['expert_sum'], truth_c['expert_sum'])
+    finite = bool(torch.isfinite(got['expert_sum']).all())
+    ratio = cand_err/(grading.BAND*oracle_err + grading.FLOOR)
+    out = {'rows': 'all' if rows is None else [int(r) for r in rows], 'sets_exact': sets['exact'],
+           'sets_differing': sets['differing'], 'sets_certified': sets['certified'],
+           'band_ratio': round(ratio, 4), 'candidate_rel_l2': cand_err, 'oracle_rel_l2': oracle_err,
+           'finite': finite}
+    if sets['exact']:
+        out['route_weight_max_err'] = float((got['route_weights'] - bf['route_weights']).abs().max())
+    out['ok'] = bool(sets['ok'] and finite and ratio <= 1.0)
+    return out
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), else the platform's processor string."""
+    try:
+        with open('/proc/cpuinfo') as fh:
+            for line in fh:
+                if line.startswith('model name'):
+                    return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 MFMA_BF16_DENSE_TFLOPS = 2500.0  # MI355X dense bf16 MFMA peak (the instruction type the GEMMs use)
@@ -423,6 +513,9 @@ def main():
                     help='time stream-ordered launches (default) or HIP-graph replays')
     ap.add_argument('--trace', action='store_true', help='record per-phase timestamps of the persistent kernel '
                     '(sets K3MOE_TRACE=1; adds a few stores per phase)')
+    ap.add_argument('--no-extra', action='store_true', help='tp8 workload: leave out the 8-stacked-layer and '
+                    'prefill configurations (reported beside the batches by default)')
+    ap.add_argument('--no-check', action='store_true', help='skip the oracle checks of the timed outputs')
     args = ap.parse_args()
     if args.trace:
         os.environ['K3MOE_TRACE'] = '1'
@@ -436,19 +529,23 @@ def main():
     device = torch.device('cuda:0')
     cold = not args.warm_cache
 
+    # (config, layers, inputs made on the host, oracle rows: None = every row)
     if args.workload == 'tp8':
         batches = [int(b) for b in args.batches.split(',')]
-        runs = [(configs.TP8_B1.with_tokens(b), 1, True) for b in batches]
+        runs = [(configs.TP8_B1.with_tokens(b), 1, True, None) for b in batches]
+        if not args.no_extra:
+            runs += [(configs.TP8_B64_L8, 8, False, [0, 21, 42, 63]),
+                     (configs.PREFILL, 1, False, [0, 1, 2047, 4095])]
         workload = f'tp8-rank-b{batches[0]}'
     elif args.workload == 'tp8-l8':
-        runs = [(configs.TP8_B64_L8, 8, False)]
+        runs = [(configs.TP8_B64_L8, 8, False, [0, 21, 42, 63])]
         workload = 'tp8-rank-b64-8-stacked-layers'
     elif args.workload == 'kimi-latent':
         batches = [int(b) for b in args.batches.split(',')]
-        runs = [(configs.KIMI_K3_TP8.with_tokens(b), 1, False) for b in batches]
+        runs = [(configs.KIMI_K3_TP8.with_tokens(b), 1, False, None) for b in batches]
         workload = f'kimi-k3-tp8-rank-latent-block-b{batches[0]}'
     else:
-        runs = [(configs.PREFILL, 1, False)]
+        runs = [(configs.PREFILL, 1, False, [0, 1, 2047, 4095])]
         workload = 'unsharded-prefill-b4096'
 
     if args.copy_probe:
@@ -461,8 +558,8 @@ def main():
         log(f'bench: copy probe of {n} bytes x 3 done')
         del src, dst
 
-    results, host = {}, {}
-    for cfg, layers, host_gen in runs:
+    results, host, timed, failures = {}, {}, {}, []
+    for cfg, layers, host_gen, rows in runs:
         log(f'bench: {cfg.name} layers={layers} steps={args.steps} warmup={args.warmup} cold={cold}')
         if args.workload == 'kimi-latent':
             m = measure_latent(cfg, seed=args.seed, steps=args.steps, warmup=args.warmup, cold=cold, device=device)
@@ -472,21 +569,36 @@ def main():
             m = measure(cfg, seed=args.seed, steps=args.steps, warmup=args.warmup, cold=cold, device=device,
                         layers=layers, host_gen=host_gen, launch=args.launch)
             results[cfg.name] = summarize(cfg, m, layers)
+            results[cfg.name]['workspace_status'] = m['status']
+            if m['status'] != 0:
+                failures.append(f'{cfg.name}: workspace status {m["status"]} after the timed runs')
             host[cfg.name] = m['host_inputs'][0]
+            timed[cfg.name] = m['timed']
+            if not host_gen and not args.no_check:
+                # inputs made on the device: the oracle on sampled rows of the last layer, now,
+                # while the inputs are resident (its routed experts copied to the host)
+                log(f'bench: oracle check of {cfg.name}, rows {rows}')
+                chk = oracle_check(cfg, m['timed'][-1], host_view(m['device_inputs'][-1]), rows=rows)
+                chk['layer'] = layers - 1
+                results[cfg.name]['check'] = chk
+            del m
         log(f'bench: {cfg.name} {results[cfg.name]}')
         torch.cuda.empty_cache()
 
-    head_cfg, head_layers, _ = runs[0]
+    head_cfg, head_layers, _, _ = runs[0]
     head = results[head_cfg.name]
     measured = measured_traffic()
     for name, r in results.items():
         if name in measured and r['layers'] == 1:
             r['hbm_traffic_bytes'] = measured[name]['traffic_bytes']
-    cpu = None
+    cpu, per = None, {}
     if not args.no_cpu_baseline and args.workload in ('tp8', 'kimi-latent'):
-        per = {}
-        # the latent block's oracle decodes every routed expert (up to 896 at b64): head batch only
-        for cfg, _, _ in (runs[:1] if args.workload == 'kimi-latent' else runs):
+        # the latent block's oracle decodes every routed expert (up to 896 at b64): head batch only;
+        # the CPU baseline covers the configurations made on the host (the batches of one layer)
+        for cfg, _, host_gen, _ in (runs[:1] if args.workload == 'kimi-latent' else runs):
+            if args.workload != 'kimi-latent' and not host_gen:
+                results[cfg.name]['cpu_us_per_layer'] = None
+                continue
             log(f'cpu baseline: {cfg.name}')
             per[cfg.name] = (cpu_baseline_latent if args.workload == 'kimi-latent' else cpu_baseline)(
                 cfg, host[cfg.name])
@@ -496,8 +608,22 @@ def main():
                'sample': f'{head_cfg.name} seed {args.seed}: one full '
                          + ('latent MoE block' if args.workload == 'kimi-latent' else 'MoE layer')
                          + ' of the CPU oracle (BF16 mode), median of 3 after 1 warmup; batches '
-                         + ', '.join(f'{k}: {v["us_per_layer"]} us' for k, v in per.items()),
-               'cpu': platform.processor() or platform.machine()}
+                         + ', '.join(f'{k}: {v["us_per_layer"]} us' for k, v in per.items())
+                         + ('' if args.workload == 'kimi-latent' else
+                            '; not measured for the stacked-layer and prefill configurations (a stacked '
+                            'layer is the b64 layer\'s work; the prefill oracle decodes every expert)'),
+               'cpu': cpu_model()}
+    if args.workload != 'kimi-latent' and not args.no_check:
+        for cfg, layers, host_gen, rows in runs:
+            if not host_gen:
+                continue
+            log(f'bench: oracle check of {cfg.name}')
+            orc = per[cfg.name]['oracle'] if cfg.name in per else None
+            results[cfg.name]['check'] = oracle_check(cfg, timed[cfg.name][0], host[cfg.name], rows=rows,
+                                                      oracle_bf16=orc)
+    for name, r in results.items():
+        if 'check' in r and not r['check']['ok']:
+            failures.append(f'{name}: timed outputs fail the oracle check {r["check"]}')
 
     ms_step = head['us_per_layer']*head_layers/1000.0
     line = {
@@ -521,11 +647,16 @@ def main():
                                                       else 'HIP-graph replays')},
         'hbm_GBps': head['hbm_GBps'],
         'hbm_frac': head['hbm_frac'],
+        'checks_ok': None if args.no_check else not failures,
         'per_batch': results,
         'roofline': roofline_entry(head, head_cfg, head_layers, measured, args.workload),
         'cpu_baseline': cpu,
     }
     print(json.dumps(line), flush=True)
+    if failures:
+        for f in failures:
+            log('bench: FAILED ' + f)
+        sys.exit(3)
 
 
 if __name__ == '__main__':

@@ -95,7 +95,9 @@ int k3moe_workspace_bytes(const k3moe_dims *dims, size_t *bytes);
  *   router_bias  [E]     fp32   or NULL for zero bias (kimi.py:115, 309)
  *   expert tensors as in k3moe_dims
  *   routes       [B, k]  int64  forced expert sets (kimi.py:311-313), or NULL;
- *                               ids must be in range and distinct per row
+ *                               ids must be in range and distinct per row (a row
+ *                               that is not keeps its own top-k and sets
+ *                               K3MOE_STATUS_ROUTES in the workspace status)
  * Outputs (written, never read):
  *   expert_sum   [B, K]  fp32   routing-weighted sum of expert outputs (kimi.py:318, 323)
  *   expert_ids   [B, k]  int64  chosen experts, ascending per row (kimi.py:316)
@@ -118,6 +120,36 @@ int k3moe_moe_step(const k3moe_dims *dims,
                    float *shortfall,
                    void *workspace, size_t workspace_bytes, void *stream);
 
+/* Where a step of the multi-kernel path leaves its token grouping
+ * (kimi.py:319-320: `indices.unique()` and the `(indices == e).nonzero()`
+ * lists) in the workspace, as byte offsets from its base. For tests and tools
+ * that inspect a step; after a step on the GENERAL, GROUPED or STREAMED path
+ * (or AUTO above the decode limits) the workspace holds:
+ *   active_count  int32          D, the number of distinct experts chosen
+ *   active        int32 [D]      those experts, ascending
+ *   offsets       int32 [D]      first pair of each active expert
+ *   counts        int32 [D]      pairs of each active expert
+ *   pair_token    int32 [B k]    token of each pair: expert-major, tokens ascending
+ *   pair_weight   fp32  [B k]    routing weight of each pair
+ *   pair_of       int32 [B k]    pair of (token t, slot j), slots in expert_ids order
+ *   pair_h        bf16  [B k, I] each pair's activation output, cast(act(gate, up))
+ *   pair_y        bf16  [B k, K] each pair's down projection, cast(h @ down.T)
+ * The persistent decode path keeps its grouping in LDS; for dims that select
+ * it this returns K3MOE_EINVAL. */
+typedef struct k3moe_layout {
+    int64_t active_count;
+    int64_t active;
+    int64_t offsets;
+    int64_t counts;
+    int64_t pair_token;
+    int64_t pair_weight;
+    int64_t pair_of;
+    int64_t pair_h;
+    int64_t pair_y;
+} k3moe_layout;
+
+int k3moe_workspace_layout(const k3moe_dims *dims, k3moe_layout *layout);
+
 /* Zero the workspace's first 86016 bytes (the control block with the barrier
  * counters and the sticky status word, a zero area the kernels read in place
  * of inactive data, and the latent block's row-tile counters) with a small
@@ -128,9 +160,22 @@ int k3moe_moe_step(const k3moe_dims *dims,
  * counterpart: the reference allocates its temporaries per call. */
 int k3moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 
+/* Status bits of the workspace's sticky status word (an OR over every step
+ * since k3moe_workspace_init). */
+#define K3MOE_STATUS_TIMEOUT 1 /* a persistent step's wait timed out (its workgroups
+                                * were not all resident): that step's outputs are
+                                * invalid, and the workspace's barrier counters must
+                                * be re-initialised (k3moe_workspace_init) before
+                                * later steps on it are trusted */
+#define K3MOE_STATUS_ROUTES 2  /* forced routes held an id out of [0, experts) or a
+                                * repeated id in a row: such rows used their own
+                                * top-k selection instead (kimi.py:364-367) */
+
 /* Copy the workspace's sticky status word to *status (0 = every step so far
- * completed normally; 1 = a persistent step's grid barrier timed out, its
- * outputs are invalid). Synchronises `stream`. No reference counterpart. */
+ * completed normally, else K3MOE_STATUS_* bits). Synchronises `stream`.
+ * k3moe_moe_step and the latent entry points never synchronise, so a caller
+ * that needs the guarantee reads the status after its steps. No reference
+ * counterpart. */
 int k3moe_workspace_status(const void *workspace, int32_t *status, void *stream);
 
 /* Geometry of the latent MoE block around the routed experts of a Kimi K3

@@ -242,6 +242,27 @@ int k3moe_workspace_bytes(const k3moe_dims *dims, size_t *bytes) {
   return K3MOE_OK;
 }
 
+int k3moe_workspace_layout(const k3moe_dims *dims, k3moe_layout *layout) {
+  g_err[0] = 0;
+  int rc = check_dims(dims);
+  if (rc) return rc;
+  if (!layout) return fail(K3MOE_EINVAL, "layout is NULL");
+  Plan p;
+  make_plan(*dims, device_cus(), p, trace_enabled());
+  if (p.path == kPathDecode)
+    return fail(K3MOE_EINVAL, "the persistent decode path keeps its grouping in LDS (tokens %d, pairs %d)", p.B, p.P);
+  layout->active_count = (int64_t)p.o_nact;
+  layout->active = (int64_t)p.o_active;
+  layout->offsets = (int64_t)p.o_aoff;
+  layout->counts = (int64_t)p.o_acnt;
+  layout->pair_token = (int64_t)p.o_ptok;
+  layout->pair_weight = (int64_t)p.o_pw;
+  layout->pair_of = (int64_t)p.o_pof;
+  layout->pair_h = (int64_t)p.o_h;
+  layout->pair_y = (int64_t)p.o_y;
+  return K3MOE_OK;
+}
+
 int k3moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {
   g_err[0] = 0;
   if (!workspace || workspace_bytes < (size_t)kInitBytes)

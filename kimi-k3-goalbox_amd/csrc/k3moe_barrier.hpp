@@ -23,7 +23,34 @@ constexpr unsigned kSpinLimit = 1u << 21;  // bounded barrier wait (about 0.1-1 
 // invalidates the local L2 for the reads that follow.
 struct BarrierBase {
   unsigned top, grp;  // the top counter and this workgroup's group counter before barrier 1
+  unsigned abort;     // the abort counter at this workgroup's start
 };
+
+// A wait of this launch gave up: record it in the sticky status word and move
+// the abort counter, so that the launch's other waits stop early.
+__device__ __forceinline__ void raise_timeout(unsigned *ctl) {
+  __hip_atomic_fetch_or(ctl + kCtlErr, (unsigned)kErrBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_add(ctl + kCtlAbort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A launch that gave up a wait leaves NaN in its output, so that a caller
+// that does not read the status word still cannot take it for a result: each
+// workgroup that gave up, or that ends after another one did, fills its share
+// [n b / G, n (b + 1) / G) of the output's n elements (fp32, or bf16 when
+// BF16). Kernels call it from every thread.
+template <bool BF16>
+__device__ __forceinline__ void poison_share(void *out, long n) {
+  const long lo = n * (long)blockIdx.x / (long)gridDim.x, hi = n * ((long)blockIdx.x + 1) / (long)gridDim.x;
+  for (long j = lo + threadIdx.x; j < hi; j += blockDim.x) {
+    if (BF16) reinterpret_cast<uint16_t *>(out)[j] = 0x7FC0u;
+    else reinterpret_cast<uint32_t *>(out)[j] = 0x7FC00000u;
+  }
+}
+
+// The abort counter moved since `base`: a wait of this launch gave up.
+__device__ __forceinline__ bool aborted(const unsigned *ctl, unsigned base) {
+  return __hip_atomic_load(ctl + kCtlAbort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != base;
+}
 
 __device__ __forceinline__ unsigned bar_groups() { return gridDim.x < kBarGroups ? gridDim.x : kBarGroups; }
 
@@ -35,7 +62,8 @@ __device__ __forceinline__ BarrierBase barrier_base(const unsigned *ctl) {
   const unsigned groups = bar_groups(), members = gridDim.x / groups, g = blockIdx.x % groups;
   const unsigned t = __hip_atomic_load(ctl + kCtlTop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const unsigned c = __hip_atomic_load(ctl + kCtlGroup + g * kCtlStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return BarrierBase{t & ~(groups - 1u), c & ~(members - 1u)};
+  const unsigned ab = __hip_atomic_load(ctl + kCtlAbort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return BarrierBase{t & ~(groups - 1u), c & ~(members - 1u), ab};
 }
 
 // Thread 0's arrival: counts this workgroup in on its group counter, and the
@@ -50,16 +78,22 @@ __device__ __forceinline__ void barrier_arrive(unsigned *ctl, const BarrierBase 
   if (trace) trace[1] = __builtin_amdgcn_s_memrealtime();
 }
 
-// Thread 0: spins until the top counter shows every group (bounded: a timeout
-// or another workgroup's error ends it), then acquires at agent scope.
-__device__ __forceinline__ void barrier_wait(unsigned *ctl, const BarrierBase &bb, unsigned n, uint64_t *trace) {
+// Thread 0: spins until the top counter shows every group, then acquires at
+// agent scope. Bounded: it gives up after kSpinLimit polls (a timeout), or
+// when another wait of this launch gave up. Returns false when it gave up.
+__device__ __forceinline__ bool barrier_wait(unsigned *ctl, const BarrierBase &bb, unsigned n, uint64_t *trace) {
   const unsigned target = bb.top + n * bar_groups();
   unsigned spins = 0;
+  bool ok = true;
   while ((int)(__hip_atomic_load(ctl + kCtlTop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
     if ((++spins & 63u) == 0u) {
-      if (__hip_atomic_load(ctl + kCtlErr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+      if (aborted(ctl, bb.abort)) {
+        ok = false;
+        break;
+      }
       if (spins > kSpinLimit) {
-        __hip_atomic_store(ctl + kCtlErr, (unsigned)kErrBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        raise_timeout(ctl);
+        ok = false;
         break;
       }
     }
@@ -67,17 +101,23 @@ __device__ __forceinline__ void barrier_wait(unsigned *ctl, const BarrierBase &b
   if (trace) trace[2] = __builtin_amdgcn_s_memrealtime();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (trace) trace[3] = __builtin_amdgcn_s_memrealtime();
+  return ok;
 }
 
-__device__ __forceinline__ void grid_barrier(unsigned *ctl, const BarrierBase &bb, unsigned n,
+// Returns false in every thread of the workgroup when the wait gave up: the
+// data the barrier should publish may be incomplete, so the caller leaves
+// (every later wait of the launch then gives up early too).
+__device__ __forceinline__ bool grid_barrier(unsigned *ctl, const BarrierBase &bb, unsigned n,
                                              uint64_t *trace = nullptr) {
+  __shared__ int s_ok;
   wait_vmem();  // this wave's device-coherent stores are done (and thread 0's base loads)
   __syncthreads();
   if (threadIdx.x == 0) {
     barrier_arrive(ctl, bb, n, trace);
-    barrier_wait(ctl, bb, n, trace);
+    s_ok = barrier_wait(ctl, bb, n, trace) ? 1 : 0;
   }
   __syncthreads();
+  return s_ok != 0;
 }
 
 }  // namespace k3moe

@@ -717,7 +717,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   const int B = pl.B, E = pl.E, k = pl.k;
   trace_mark(pl, a.ws, 0);
   // this launch's barrier targets (thread 0 arrives for the workgroup)
-  const BarrierBase bb = tid == 0 ? barrier_base(ctl) : BarrierBase{0u, 0u};
+  const BarrierBase bb = tid == 0 ? barrier_base(ctl) : BarrierBase{0u, 0u, 0u};
+  __shared__ unsigned s_abort0;  // the abort counter at the start, for every thread's bounded waits
+  if (tid == 0) s_abort0 = bb.abort;
 
   // Code warm-up: a step runs much of this kernel's code once, and after other
   // work has evicted it every new stretch stalls on instruction fetches from
@@ -811,7 +813,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   trace_mark(pl, a.ws, 1);
   asm volatile("" ::"v"(code_probe));  // the warm-up loads complete here
   unsigned nbar = 0;  // barriers of this launch passed so far
-  grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 12));
+  // a wait of this launch gave up: NaN in this workgroup's share of the output, and leave
+  auto give_up = [&]() { poison_share<false>(a.out, (long)B * pl.K); };
+  if (!grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 12))) return give_up();
   trace_mark(pl, a.ws, 2);
   // A single token's expert-input row is known from the start: its loads are
   // issued here and arrive during the top-k and grouping phases; gate/up then
@@ -974,10 +978,17 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
         if (!coop && !coop2) wave_topk(kyl + tl * E, E, k, mysel);
         wave_lds_order();
         trace_mark(pl, a.ws, 30);
+        const bool writer = redundant ? blockIdx.x == 0 : true;
+        // forced routes replace the selection when the row is valid; an invalid
+        // row keeps its own top-k and sets the status word
+        int fid = 0;
+        const bool forced = a.routes && forced_route(a.routes, t, k, E, &fid);
+        if (a.routes && !forced && l == 0 && writer)
+          __hip_atomic_fetch_or(ctl + kCtlErr, (unsigned)kErrRoutes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         int my_e = -1;
         float my_score = 0.f, my_key = 0.f;
         if (l < k) {
-          my_e = a.routes ? (int)a.routes[(size_t)t * k + l] : mysel[l];
+          my_e = forced ? fid : mysel[l];
           my_score = scl[tl * E + my_e];
           my_key = kyf[tl * E + my_e];
         }
@@ -994,7 +1005,6 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
           for (int r = 0; r < k; ++r) sum = __fadd_rn(sum, lane_f32(ex, r));
           wt = ex / sum;
         }
-        const bool writer = redundant ? blockIdx.x == 0 : true;
         if (a.routes && a.out_short) {
           float mn = INFINITY;
           for (int r = 0; r < k; ++r) mn = fminf(mn, lane_f32(my_key, r));
@@ -1023,7 +1033,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   }
   trace_mark(pl, a.ws, 3);
   if (!redundant) {
-    grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 16));
+    if (!grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 16))) return give_up();
     for (int p0 = tid; p0 < pl.P; p0 += 4 * kDecThreads) {
       int iv[4];
       float wv[4];
@@ -1176,12 +1186,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   const int dn_da = D * w / kDecWaves, dn_db = D * (w + 1) / kDecWaves;
   const bool dn_pair = !expert_major && D <= kDecWaves && B <= 16 && pl.KSd <= kDnDepth &&
                        pl.RTd <= 2 * (int)gridDim.x;
-  auto wait_expert = [&](int d) {  // bounded: a timeout sets the status word
+  const unsigned abort0 = s_abort0;
+  auto wait_expert = [&](int d) {  // bounded: a timeout sets the status word; gives up with the launch
     const unsigned need = (unsigned)(g_coff[d + 1] - g_coff[d]) * pl.U8;
     unsigned spins = 0;
     while (__hip_atomic_load(ecnt + d * kCntStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(ctl + kCtlErr, (unsigned)kErrBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((++spins & 63u) == 0u && aborted(ctl, abort0)) break;
+      if (spins > kSpinLimit) {
+        if ((threadIdx.x & 63) == 0) raise_timeout(ctl);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -1212,7 +1224,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     for (int tt = 0; tt < 2; ++tt)  // a row tile past the last reads the zero area
       dn_issue_w(pl, a, zero, g_act, (int)blockIdx.x + tt * (int)gridDim.x, dn_da, 0, pl.I / kBlockK, pf[tt]);
   } else if (!expert_major && !dn_pair) {
-    grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 20));
+    if (!grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 20))) return give_up();
   }
   trace_mark(pl, a.ws, 7);
 
@@ -1232,7 +1244,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + 48 + w] = __builtin_amdgcn_s_memrealtime();
     dn_flush(st, pl, ybuf);
     trace_mark(pl, a.ws, 9);
-    grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 24));
+    if (!grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 24))) return give_up();
     // combine (kimi.py:318,323): expert_sum[t][col] = sum over the token's
     // experts in ascending id order of w * bf16(y), from zero, FP32 adds
     const int K4 = pl.K / 4;
@@ -1302,8 +1314,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   } else
   {
     const int KB = pl.I / kBlockK;
-    float *acc_lds = reinterpret_cast<float *>(scr);  // [8 waves][B][16]
-    float *mine = acc_lds + w * B * 16;
+    // [P pairs][16]: w * bf16(y) of each (token, expert) pair of the row tile;
+    // every pair is written once per row tile, then each token's pairs are
+    // summed from zero in ascending expert order (the order of kimi.py:319-323)
+    float *pv = reinterpret_cast<float *>(scr);
     const int da = D * w / kDecWaves, db = D * (w + 1) / kDecWaves;
     // The wave walks items (expert d, 16-token chunk c, k-steps kc..kc+1) in
     // order with the next item's loads in flight while the current one runs,
@@ -1312,8 +1326,6 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     DnLoad cur, nxt;
     bool prefetched = false;
     for (int rt = blockIdx.x; rt < pl.RTd; rt += gridDim.x) {
-      for (int j = l; j < B * 16; j += 64) mine[j] = 0.f;
-      wave_lds_order();
       int d = da, c = 0, kc = 0;
       if (d < db && !prefetched) dn_issue(pl, a, hbuf, zero, g_act, g_aoff, g_acnt, rt, d, c, kc, KB, cur);
       prefetched = false;
@@ -1341,16 +1353,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) acc = mfma16(av[kk], as_bf16x8(cur.b[j][kk]), acc);
         }
-        if (nkc == 0) {  // (d, c) complete: fold w * bf16(y) into the wave's accumulators
+        if (nkc == 0) {  // (d, c) complete: w * bf16(y) of its pairs
           const int p0 = g_aoff[d], pj = c * 16 + i;
           if (pj < g_acnt[d]) {
-            const int t = g_ptok[p0 + pj];
             const float wt = g_pw[p0 + pj];
-            float *dst = mine + t * 16 + 4 * q;
-#pragma unroll
-            for (int v = 0; v < 4; ++v) dst[v] = __fadd_rn(dst[v], __fmul_rn(round_bf16(acc[v]), wt));
+            *reinterpret_cast<f32x4 *>(pv + (p0 + pj) * 16 + 4 * q) =
+                f32x4{__fmul_rn(round_bf16(acc[0]), wt), __fmul_rn(round_bf16(acc[1]), wt),
+                      __fmul_rn(round_bf16(acc[2]), wt), __fmul_rn(round_bf16(acc[3]), wt)};
           }
-          wave_lds_order();
           acc = f32x4{0.f, 0.f, 0.f, 0.f};
         }
         cur = nxt;
@@ -1360,10 +1370,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       }
       __syncthreads();
       for (int j = tid; j < B * 16; j += kDecThreads) {
-        float sum = acc_lds[j];
-#pragma unroll
-        for (int ww = 1; ww < kDecWaves; ++ww) sum = __fadd_rn(sum, acc_lds[ww * B * 16 + j]);
-        a.out[(size_t)(j >> 4) * pl.K + rt * 16 + (j & 15)] = sum;
+        const int t = j >> 4;
+        float sum = 0.f;
+        for (int sl = 0; sl < k; ++sl) sum = __fadd_rn(sum, pv[g_pof[t * k + sl] * 16 + (j & 15)]);
+        a.out[(size_t)t * pl.K + rt * 16 + (j & 15)] = sum;
       }
       __syncthreads();
     }
@@ -1371,6 +1381,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
 
   // ------------------------------------------------------------------ exit --
   __syncthreads();
+  if (aborted(ctl, abort0)) {  // a wait of this launch gave up (the down-phase waits have no barrier after them)
+    give_up();
+    return;
+  }
   trace_mark(pl, a.ws, 8);
   if (blockIdx.x == 0 && tid == 0) {  // this kernel's code range, for the next launch's warm-up
     crange[0] = pc0;

@@ -352,6 +352,20 @@ __device__ __forceinline__ float lane_f32(float v, int src) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
 }
 
+// Forced routes of token t (kimi.py:311-313), read by lanes l < k: *id gets
+// the lane's expert id. Returns (wave-uniform) whether the row is valid: every
+// id in [0, E) and the k ids distinct (kimi.py:364-367). An invalid row must
+// not be used: its ids would index the expert tensors and the LDS lists.
+__device__ __forceinline__ bool forced_route(const int64_t *routes, int t, int k, int E, int *id) {
+  const int l = threadIdx.x & 63;
+  const int64_t r = l < k ? routes[(size_t)t * k + l] : 0;
+  bool bad = l < k && (r < 0 || r >= E);
+  const int mine = (int)r;
+  for (int j = 0; j < k; ++j) bad |= l < k && j < l && (int)lane_u32((uint32_t)mine, j) == mine;
+  *id = mine;
+  return __ballot(bad) == 0;
+}
+
 // One DPP step of a 64-bit wave maximum: max(v, v of the DPP source lane).
 template <int Ctrl, int RowMask>
 __device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {

@@ -101,11 +101,17 @@ __global__ __launch_bounds__(kThreads) void k_topk(Plan pl, const float *__restr
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // chosen set in selection order (or the forced routes, in their order)
+  // chosen set in selection order (or the forced routes, in their order, when
+  // the row is valid; an invalid row keeps its own top-k and sets the status word)
+  int fid = 0;
+  const bool forced = routes && forced_route(routes, t, k, E, &fid);
+  if (routes && !forced && l == 0)
+    __hip_atomic_fetch_or(reinterpret_cast<unsigned *>(ws + pl.o_ctl) + kCtlErr, (unsigned)kErrRoutes,
+                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   int my_e = -1;
   float my_score = 0.f, my_key = 0.f;
   if (l < k) {
-    my_e = routes ? (int)routes[(size_t)t * k + l] : s_sel[wave][l];
+    my_e = forced ? fid : s_sel[wave][l];
     my_score = s_score[wave][my_e];
     my_key = s_key[wave][my_e];
   }

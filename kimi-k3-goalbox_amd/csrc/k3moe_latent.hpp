@@ -214,7 +214,7 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
   const uint32_t part_bytes = (uint32_t)((long)SP * pl.RT * B * 64);
   const __amdgpu_buffer_rsrc_t rp0 = make_rsrc(a.ws + pl.o_part0, part_bytes);
   const __amdgpu_buffer_rsrc_t rp1 = make_rsrc(a.ws + (OUT ? pl.o_part1 : pl.o_part0), part_bytes);
-  BarrierBase bb{0u, 0u};
+  BarrierBase bb{0u, 0u, 0u};
   if (OUT && !local && tid == 0) bb = barrier_base(ctl);
   // the group counter before this launch: no member can have added a whole kLatGrpTotal yet
   const unsigned gbase =
@@ -371,7 +371,10 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
                  *reinterpret_cast<const uint32_t *>(a.x + (long)t * pl.S + k));
     }
     mark(48);
-    grid_barrier(ctl, bb, 1);
+    if (!grid_barrier(ctl, bb, 1)) {  // a wait of this launch gave up: the rows are incomplete
+      poison_share<true>(a.ya, (long)B * pl.h);
+      return;
+    }
     mark(49);
     stage();
     wait_vm<0>();
@@ -446,16 +449,19 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
   mark(45);
 
   // the group's barrier: every member's partial stores are complete
+  __shared__ int s_gave_up;
   wait_vmem();
   __syncthreads();
   if (tid == 0) {
+    s_gave_up = 0;
     __hip_atomic_fetch_add(gcnt, kLatGrpTotal >> lsp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const unsigned target = gbase + kLatGrpTotal;
     unsigned spins = 0;
     while ((int)(__hip_atomic_load(gcnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
       __builtin_amdgcn_s_sleep(1);
       if (++spins > kSpinLimit) {
-        __hip_atomic_store(ctl + kCtlErr, (unsigned)kErrBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        raise_timeout(ctl);
+        s_gave_up = 1;
         break;
       }
     }
@@ -503,6 +509,11 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
         a.yb[(long)t * pl.S + (rt - pl.ntile0) * 8 + r] =
             f32_to_bf16_bits(apply_act(pl.act, round_bf16(sa), round_bf16(sb)));
     }
+  }
+  if (s_gave_up) {  // the group's partials were incomplete: NaN in this workgroup's share of the outputs
+    __syncthreads();
+    poison_share<true>(a.ya, (long)B * (OUT ? pl.h : pl.lh));
+    if (!OUT) poison_share<true>(a.yb, (long)B * pl.S);
   }
   mark(47);
 }

@@ -36,10 +36,17 @@ constexpr int kDnStage = 128;        // decode down: y rows staged per wave (32 
 constexpr int kRedundantTokens = 1;    // decode: route every token in every workgroup up to this batch
 constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert) keys
 
-// Control block (uint32 words): the sticky error word and the decode kernel's
-// code range (words 4-7) in the first 128-byte line, the top barrier counter
-// in the second, then kBarGroups group counters kCtlStride words (128 B) apart.
+// Control block (uint32 words): the sticky status word, the abort counter and
+// the decode kernel's code range (words 4-7) in the first 128-byte line, the
+// top barrier counter in the second, then kBarGroups group counters kCtlStride
+// words (128 B) apart.
+//   status (kCtlErr): OR of kErr* bits of every step since the workspace init
+//   abort (kCtlAbort): grows by one whenever a workgroup gives up waiting; a
+//     launch reads it at its start and its barriers stop waiting early only
+//     when it moves during that launch (a timeout of an earlier launch leaves
+//     the status set but does not shorten later launches' waits)
 constexpr int kCtlErr = 2;
+constexpr int kCtlAbort = 3;
 constexpr int kCtlCode = 4;  // 2 x uint64: the decode kernel's code range (start, end) of its last launch
 constexpr int kCtlTop = 32;
 constexpr int kBarGroups = 16, kCtlGroup = 64, kCtlStride = 32;
@@ -56,7 +63,8 @@ constexpr int kZeroBytes = 64 * 1024;
 constexpr int kLatCntBytes = 16384;
 constexpr int kInitBytes = 4096 + kZeroBytes + kLatCntBytes;  // control block (page-padded), zero area, counters
 constexpr int kTraceSlots = 56;    // phase timestamps per workgroup when tracing
-constexpr int kErrBarrierTimeout = 1;
+constexpr int kErrBarrierTimeout = 1;  // a wait timed out: that step's outputs are invalid
+constexpr int kErrRoutes = 2;          // forced routes out of range or repeated in a row: those rows used their own top-k
 
 enum Path { kPathGeneral = 0, kPathDecode = 1 };
 
@@ -99,8 +107,9 @@ inline int decode_lds(Plan &p) {
   const int routed = 8 * p.P;                                       // ids + weights per pair
   const int topk = routed + 4 * (3 * nt * p.E + kDecWaves * kMaxTopk) + 8 * kDecWaves * 32 + 8;  // keys, scores, picks, offers
   const int group = routed + 4 * (4 * p.E + 32);                    // counts, offsets, bitmaps, wave sums
-  int down = (p.B <= 16 ? 2 : 1) * kDecWaves * p.B * 16 * 4;       // per-wave combine accumulators (2 row tiles up to 16 tokens)
-  if (down < kDecWaves * kDnStage * 36) down = kDecWaves * kDnStage * 36;  // or per-wave y stages
+  int down = (p.B <= 16 ? 2 : 1) * kDecWaves * p.B * 16 * 4;       // paired down: per-wave accumulators (2 row tiles)
+  if (down < kDecWaves * kDnStage * 36) down = kDecWaves * kDnStage * 36;  // expert-major down: per-wave y stages
+  if (down < p.P * 16 * 4) down = p.P * 16 * 4;                     // row-tile down: one 16-row slice per pair
   int scr = topk;
   if (group > scr) scr = group;
   if (down > scr) scr = down;

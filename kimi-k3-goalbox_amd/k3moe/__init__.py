@@ -14,7 +14,7 @@ include/k3moe.h). There is no CPU fallback.
 """
 
 from .moe import (moe_layer, moe_step, mxfp4_decode, new_workspace, workspace_bytes,  # noqa: F401
-                  workspace_status)
+                  workspace_layout, workspace_status)
 from .configs import ALL as CONFIGS, MoEConfig  # noqa: F401
 from .latent import latent_block, latent_in, latent_moe_layer, latent_out  # noqa: F401
 

@@ -37,9 +37,18 @@ class LatentDims(ctypes.Structure):
                 ('shared', ctypes.c_int32), ('activation', ctypes.c_int32)]
 
 
+class Layout(ctypes.Structure):
+    """Mirror of k3moe_layout in include/k3moe.h (byte offsets of the grouping lists)."""
+    _fields_ = [(n, ctypes.c_int64) for n in ('active_count', 'active', 'offsets', 'counts', 'pair_token',
+                                               'pair_weight', 'pair_of', 'pair_h', 'pair_y')]
+
+
+# bits of the workspace status word (include/k3moe.h K3MOE_STATUS_*)
+STATUS_TIMEOUT, STATUS_ROUTES = 1, 2
+
 EXPORTS = ('k3moe_workspace_bytes', 'k3moe_workspace_init', 'k3moe_workspace_status', 'k3moe_moe_step',
            'k3moe_mxfp4_decode', 'k3moe_last_error', 'k3moe_version', 'k3moe_latent_workspace_bytes',
-           'k3moe_latent_in', 'k3moe_latent_out')
+           'k3moe_latent_in', 'k3moe_latent_out', 'k3moe_workspace_layout')
 
 _lib = None
 
@@ -67,6 +76,8 @@ def load(path: str | None = None):
     lib.k3moe_workspace_status.restype = ctypes.c_int
     lib.k3moe_moe_step.argtypes = [ctypes.POINTER(Dims)] + [p]*15 + [p, sz, p]
     lib.k3moe_moe_step.restype = ctypes.c_int
+    lib.k3moe_workspace_layout.argtypes = [ctypes.POINTER(Dims), ctypes.POINTER(Layout)]
+    lib.k3moe_workspace_layout.restype = ctypes.c_int
     lib.k3moe_mxfp4_decode.argtypes = [p, p, i64, i32, p, p]
     lib.k3moe_mxfp4_decode.restype = ctypes.c_int
     lib.k3moe_latent_workspace_bytes.argtypes = [ctypes.POINTER(LatentDims), ctypes.POINTER(sz)]

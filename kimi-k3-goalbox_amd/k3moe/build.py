@@ -2,7 +2,11 @@
 
 The library is plain `extern "C"` HIP code loaded with ctypes, so it does not
 depend on torch's headers or ABI. Packed FP32 instructions are disabled for
-the device code (-target-feature -packed-fp32-ops).
+the device code (-target-feature -packed-fp32-ops). Floating-point contraction
+is off (-ffp-contract=off): every product and sum rounds where the source
+writes it, as torch's separate operations do (the combine's w x bf16(y) is
+rounded before it is added, kimi.py:323); HIP's default would fuse them into
+one FMA with a single rounding (its __fmul_rn / __fadd_rn are plain operators).
 """
 
 from __future__ import annotations
@@ -31,7 +35,7 @@ def hipcc() -> str:
 
 
 def command(out: str = OUT) -> list[str]:
-    return [hipcc(), f'--offload-arch={ARCH}', '-O3', '-std=c++17', '-fPIC', '-shared',
+    return [hipcc(), f'--offload-arch={ARCH}', '-O3', '-std=c++17', '-fPIC', '-shared', '-ffp-contract=off',
             '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
             '-Wno-unused-command-line-argument',
             '-I', os.path.join(REPO, 'include'),

@@ -102,8 +102,18 @@ def new_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return ws
 
 
+def workspace_layout(dims: Dims) -> dict:
+    """Byte offsets of the general path's grouping lists in the workspace (k3moe_workspace_layout)."""
+    lay = _native.Layout()
+    check(_native.load().k3moe_workspace_layout(ctypes.byref(dims), ctypes.byref(lay)), 'k3moe_workspace_layout')
+    return {n: int(getattr(lay, n)) for n, _ in _native.Layout._fields_}
+
+
 def workspace_status(ws: torch.Tensor) -> int:
-    """Sticky status word of a workspace (0 = every step completed normally). Synchronises."""
+    """Sticky status word of a workspace: 0 = every step since its init completed normally, else
+    bits STATUS_TIMEOUT (a wait timed out: that step's output holds NaN; re-initialise the
+    workspace) and STATUS_ROUTES (a forced-route row was invalid and used its own top-k).
+    Synchronises; the steps themselves never do."""
     st = ctypes.c_int32(-1)
     with torch.cuda.device(ws.device):
         stream = torch.cuda.current_stream(ws.device).cuda_stream

@@ -24,6 +24,10 @@ brute forces written per token and per output row with their own RMS and SiTU
 formulas, chained with moe_ref.moe_step_f64 for the whole block; the RMS
 epsilon against the closed form of a constant vector; planted mistakes (gate
 and up swapped, the norm weight dropped, the mean taken over tokens) fail.
+The BF16 mode against ``latent_in_bf16_f64`` and ``latent_out_bf16_f64``, the
+same brute forces rounded to bf16 where the chain casts, chained with
+moe_ref.moe_step_bf16_f64; planted moved or dropped casts (unrounded
+projections, the norm weight applied in FP32, the expert sum not cast) fail.
 """
 
 from __future__ import annotations
@@ -110,3 +114,40 @@ def latent_in_f64(normalized, latent_down, shared_gate, shared_up):
             g, u = float(np.dot(wg[j], x[t])), float(np.dot(wu[j], x[t]))
             sh[t, j] = 4.0*np.tanh(g/4.0)/(1.0 + np.exp(-g))*25.0*np.tanh(u/25.0)
     return lat, sh
+
+
+def latent_in_bf16_f64(normalized, latent_down, shared_gate, shared_up):
+    """Float64 brute force of latent_in's BF16 mode, per token, rounded to bf16 where kimi.py:317, 326 cast.
+
+    latent = bf16(x . latent_down row); shared_h = bf16(situ(bf16(x . gate row), bf16(x . up row)))
+    with its own SiTU formula (moe_ref.bf16_round_f64: nearest bf16, ties to even).
+    """
+    from .moe_ref import bf16_round_f64 as r16
+    x = normalized.double().numpy()
+    wl, wg, wu = (m.double().numpy() for m in (latent_down, shared_gate, shared_up))
+    lat = np.stack([r16(wl @ x[t]) for t in range(x.shape[0])])
+    sh = []
+    for t in range(x.shape[0]):
+        g, u = r16(wg @ x[t]), r16(wu @ x[t])
+        sh.append(r16(4.0*np.tanh(g/4.0)/(1.0 + np.exp(-g))*25.0*np.tanh(u/25.0)))
+    return lat, np.stack(sh)
+
+
+def latent_out_bf16_f64(expert_sum, latent_norm, latent_up, shared_h, shared_down) -> np.ndarray:
+    """Float64 brute force of latent_out's BF16 mode, per token (kimi.py:325-328, common.py:13-21).
+
+    e = bf16(expert_sum); en = bf16(bf16(e / sqrt(mean(e^2) + 1e-5)) * w_norm);
+    routed = bf16(latent_up . en); shared = bf16(shared_down . shared_h);
+    out = bf16(routed + shared): each rounding is where the BF16 chain casts.
+    """
+    from .moe_ref import bf16_round_f64 as r16
+    e = r16(expert_sum.double().numpy())
+    wn = latent_norm.double().numpy()
+    wu, wd = latent_up.double().numpy(), shared_down.double().numpy()
+    sh = shared_h.double().numpy()
+    out = []
+    for t in range(e.shape[0]):
+        inv = 1.0/np.sqrt(np.mean(e[t]*e[t]) + RMS_EPS)
+        en = r16(r16(e[t]*inv)*wn)
+        out.append(r16(r16(wu @ en) + r16(wd @ sh[t])))
+    return np.stack(out)

@@ -23,7 +23,10 @@ Independent pins (tests/test_oracle.py): the decode is checked bit for bit
 against the C restatement in mxfp4_ref.c (bit construction from the OCP MX
 E2M1/E8M0 definition) and against the closed form; the FP32 chain is checked
 against ``moe_step_f64``, a float64 brute force written per token rather than
-per expert, with a closed-form decode and its own activation formulas.
+per expert, with a closed-form decode and its own activation formulas; the
+BF16 chain against ``moe_step_bf16_f64``, the same brute force rounded to
+bf16 (nearest, ties to even, ``bf16_round_f64``) exactly where kimi.py:322
+casts, with planted dropped casts (through ``_expert_out``) that must fail it.
 """
 
 from __future__ import annotations
@@ -136,7 +139,8 @@ def route(x: torch.Tensor, router: torch.Tensor, bias: torch.Tensor | None, topk
 
 def moe_step(x, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales,
              down_blocks, down_scales, *, topk: int, gating: str = 'sigmoid_bias',
-             activation: str = 'situ', fp32: bool = False, routes=None, latent=None) -> dict:
+             activation: str = 'situ', fp32: bool = False, routes=None, latent=None,
+             pair_out: bool = False) -> dict:
     """One MoE step on the CPU, restating kimi.py:307-324 (without the TP all-reduce).
 
     fp32=False is the BF16 serving oracle, fp32=True the FP32 truth
@@ -144,7 +148,9 @@ def moe_step(x, router, router_bias, gate_blocks, gate_scales, up_blocks, up_sca
     router input (kimi.py:317); by default the experts read `x`.
     Returns expert_sum fp32 [B, K], expert_ids int64 [B, k] sorted,
     route_weights fp32 [B, k] aligned with expert_ids, and route_shortfall
-    fp32 [B] when routes are forced.
+    fp32 [B] when routes are forced; with pair_out, also 'pair_out' fp32
+    [B, k, K]: each (token, expert) output (the down projection after its
+    cast), in expert_ids order.
     """
     act = torch.float32 if fp32 else torch.bfloat16
     cast = lambda t: t.to(act)                                              # kimi.py:240
@@ -154,19 +160,32 @@ def moe_step(x, router, router_bias, gate_blocks, gate_scales, up_blocks, up_sca
     inp = cast(latent if latent is not None else x)
     B, K = inp.shape
     expert_sum = torch.zeros(B, K, dtype=torch.float32)                     # kimi.py:318
+    pairs = torch.zeros(B, indices.shape[1], K, dtype=torch.float32) if pair_out else None
     for expert in indices.unique().tolist():                                # kimi.py:319
         rows, slots = (indices == expert).nonzero(as_tuple=True)            # kimi.py:320
         wg = unpack_mxfp4(gate_blocks[expert], gate_scales[expert]).to(act) # kimi.py:321
         wu = unpack_mxfp4(up_blocks[expert], up_scales[expert]).to(act)
         wd = unpack_mxfp4(down_blocks[expert], down_scales[expert]).to(act)
-        hidden = cast(fn(inp[rows] @ wg.T, inp[rows] @ wu.T))                # kimi.py:322
-        out = cast(hidden @ wd.T)
+        out = _expert_out(inp[rows], wg, wu, wd, fn, cast)                  # kimi.py:322
         expert_sum.index_add_(0, rows, out.float()*weights[rows, slots, None])  # kimi.py:323
+        if pairs is not None:
+            pairs[rows, slots] = out.float()
     result = {'expert_sum': expert_sum, 'expert_ids': r['expert_ids'],
               'route_weights': r['route_weights']}
     if routes is not None:
         result['route_shortfall'] = r['route_shortfall']
+    if pairs is not None:   # per (token, slot) expert output, aligned with expert_ids
+        order = indices.sort(-1).indices
+        result['pair_out'] = pairs.gather(1, order[..., None].expand(-1, -1, K))
     return result
+
+
+def _expert_out(rows_inp, wg, wu, wd, fn, cast):
+    """One expert's output rows, with the casts of kimi.py:322:
+    cast(cast(act(inp @ wg.T, inp @ wu.T)) @ wd.T), where each matmul of
+    activation-dtype operands returns the activation dtype."""
+    hidden = cast(fn(rows_inp @ wg.T, rows_inp @ wu.T))
+    return cast(hidden @ wd.T)
 
 
 # ------------------------------------------------------------ float64 pin --
@@ -216,6 +235,58 @@ def moe_step_f64(x, router, router_bias, gate_blocks, gate_scales, up_blocks, up
             else:
                 a = g/(1.0 + np.exp(-g))*u
             out[b] += weights[b, slot]*(wd @ a)
+    return out
+
+
+def bf16_round_f64(v) -> np.ndarray:
+    """Round float64 values to the nearest bfloat16 value, ties to even, returned as float64.
+
+    bfloat16 keeps 8 significant bits: with v = m 2**e, 0.5 <= |m| < 1
+    (frexp), the result is rint(m 2**8) 2**(e-8); numpy's rint rounds half to
+    even. Valid for the normal bf16 range (|v| >= 2**-126), which the
+    projections here stay in; zeros, infinities and NaN pass through.
+    """
+    v = np.asarray(v, dtype=np.float64)
+    m, e = np.frexp(v)
+    with np.errstate(invalid='ignore'):
+        r = np.ldexp(np.rint(np.ldexp(m, 8)), e - 8)
+    return np.where(np.isfinite(v), r, v)
+
+
+def moe_step_bf16_f64(x, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales,
+                      down_blocks, down_scales, *, routes, weights, activation='situ', latent=None):
+    """Float64 brute force of the BF16 serving chain for given routes and weights.
+
+    Written per token like moe_step_f64, with a closed-form decode, and rounded
+    to bf16 (bf16_round_f64) exactly where kimi.py:322 casts in BF16 mode:
+    the gate and up projections, the activation, the down projection. The
+    combine is a float64 sum of weight x bf16 output (kimi.py:323). It differs
+    from the BF16 oracle only by FP32-versus-float64 arithmetic inside the dot
+    products and the activation, which flips a bf16 rounding rarely; a dropped
+    or added cast moves every value by about a rounding step.
+    Returns expert_sum float64 [B, K].
+    """
+    inp = (latent if latent is not None else x).double().numpy()
+    routes = routes.numpy()
+    weights = weights.double().numpy()
+    B, K = inp.shape
+    out = np.zeros((B, K))
+    cache = {}
+    for b in range(B):
+        for slot in range(routes.shape[1]):
+            e = int(routes[b, slot])
+            if e not in cache:
+                cache[e] = tuple(_decode_f64(blk[e].numpy(), scl[e].numpy()) for blk, scl in
+                                 ((gate_blocks, gate_scales), (up_blocks, up_scales), (down_blocks, down_scales)))
+            wg, wu, wd = cache[e]
+            g = bf16_round_f64(wg @ inp[b])
+            u = bf16_round_f64(wu @ inp[b])
+            if activation == 'situ':
+                a = 4.0*np.tanh(g/4.0)*(1.0/(1.0 + np.exp(-g)))*25.0*np.tanh(u/25.0)
+            else:
+                a = g/(1.0 + np.exp(-g))*u
+            y = bf16_round_f64(wd @ bf16_round_f64(a))
+            out[b] += weights[b, slot]*y
     return out
 
 

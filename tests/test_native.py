@@ -137,3 +137,19 @@ def test_latent_rejects_host_tensors():
         latent.latent_in(x, w, w, w)
     with pytest.raises(NotImplementedError):
         latent.latent_block(x, {}, topk=2, fp32=True)
+
+
+def test_integration_ctypes_snippet_matches_the_binding():
+    """The ctypes declaration documented for other callers has the argument counts _native.py uses."""
+    doc = open(os.path.join(os.path.dirname(HEADER), '..', 'INTEGRATION.md')).read()
+    lib = _native.load()
+    for name, want in (('k3moe_moe_step', lib.k3moe_moe_step.argtypes),
+                       ('k3moe_latent_in', lib.k3moe_latent_in.argtypes)):
+        m = re.search(rf'lib\.{name}\.argtypes = \[ctypes\.POINTER\(\w+\)\] \+ \[ctypes\.c_void_p\] \* (\d+) \+', doc)
+        assert m, name
+        assert 1 + int(m.group(1)) + 3 == len(want), name
+    # and the header's pointer count for the step: 15 device pointers between dims and the workspace
+    text = open(HEADER).read()
+    decl = re.search(r'int k3moe_moe_step\((.*?)\);', text, flags=re.S).group(1)
+    params = [p.strip() for p in decl.split(',')]
+    assert len(params) == 1 + 15 + 3

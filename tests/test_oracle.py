@@ -8,6 +8,9 @@ The oracle is trusted only after these checks:
   * the FP32 expert chain == an independent float64 brute force (per token,
     closed-form decode) to FP32 rounding, on several seeds and both
     activations / gatings; a planted mistake fails it;
+  * the BF16 expert chain (and the latent block's BF16 mode) == float64 brute
+    forces rounded to bf16 at exactly the reference's casts, to ~1e-7; each
+    planted dropped cast moves it by 5e-4 or more and fails;
   * band grader, shortfall and no-mutation rules behave as the reference's
     own unit tests require (megabench/tests/test_kimi.py:67-109).
 """
@@ -135,6 +138,78 @@ def test_fp32_chain_matches_float64_brute_force(seed, activation):
     bf = moe_ref.moe_step(*args, topk=cfg.topk, activation=activation)
     err = moe_ref.rel_l2(bf['expert_sum'], ref)
     assert 1e-4 < err < 2e-2          # the BF16 oracle is visibly coarser than FP32, but close
+
+
+BF16_CASES = [dict(), dict(E=16, k=4, h=256, I=128, B=5)]
+
+
+@pytest.mark.parametrize('seed', [0, 1, 2])
+@pytest.mark.parametrize('gating', ['sigmoid_bias', 'softmax'])
+@pytest.mark.parametrize('activation', ['situ', 'silu'])
+@pytest.mark.parametrize('shape', BF16_CASES, ids=['tiny', 'e16'])
+def test_bf16_chain_matches_bf16_float64_brute_force(seed, gating, activation, shape):
+    """The BF16 oracle equals a float64 brute force that rounds to bf16 at kimi.py:322's casts.
+
+    They differ only by FP32 versus float64 arithmetic inside the sums, which
+    flips a rounding rarely (measured 3-5e-8 rel-L2); a missing cast moves the
+    result by 1.5e-3 or more (test_bf16_planted_dropped_casts_fail).
+    """
+    cfg, inp = tiny_inputs(seed, gating=gating, **shape)
+    args = tuple(inp[k] for k in ('x', 'router', 'router_bias', 'gate_blocks', 'gate_scales', 'up_blocks',
+                                  'up_scales', 'down_blocks', 'down_scales'))
+    r = moe_ref.moe_step(*args, topk=cfg.topk, gating=gating, activation=activation)
+    ref = moe_ref.moe_step_bf16_f64(*args, routes=r['expert_ids'], weights=r['route_weights'],
+                                    activation=activation)
+    assert moe_ref.rel_l2(r['expert_sum'], ref) <= 1e-5
+
+
+# plausible mistakes in the BF16 chain: one of kimi.py:322's casts dropped
+BF16_PLANTS = {
+    'gate/up not rounded': lambda x, wg, wu, wd, fn, cast: cast(cast(fn(x.float() @ wg.float().T,
+                                                                        x.float() @ wu.float().T)) @ wd.T),
+    'activation not rounded': lambda x, wg, wu, wd, fn, cast: cast(fn(x @ wg.T, x @ wu.T) @ wd.float().T),
+    'down not rounded': lambda x, wg, wu, wd, fn, cast: cast(fn(x @ wg.T, x @ wu.T)).float() @ wd.float().T,
+}
+
+
+@pytest.mark.parametrize('plant', sorted(BF16_PLANTS))
+@pytest.mark.parametrize('activation', ['situ', 'silu'])
+def test_bf16_planted_dropped_casts_fail(monkeypatch, plant, activation):
+    cfg, inp = tiny_inputs(1, E=16, k=4, h=256, I=128, B=5)
+    args = tuple(inp[k] for k in ('x', 'router', 'router_bias', 'gate_blocks', 'gate_scales', 'up_blocks',
+                                  'up_scales', 'down_blocks', 'down_scales'))
+    r = moe_ref.moe_step(*args, topk=cfg.topk, activation=activation)
+    ref = moe_ref.moe_step_bf16_f64(*args, routes=r['expert_ids'], weights=r['route_weights'],
+                                    activation=activation)
+    monkeypatch.setattr(moe_ref, '_expert_out', BF16_PLANTS[plant])
+    bad = moe_ref.moe_step(*args, topk=cfg.topk, activation=activation, routes=r['expert_ids'])
+    assert moe_ref.rel_l2(bad['expert_sum'], ref) >= 1e-3
+
+
+def test_bf16_round_f64_ties_and_torch():
+    """Nearest bf16, ties to even, against hand values and torch's fp32 -> bf16 cast."""
+    r = moe_ref.bf16_round_f64
+    step = 2.0**-7                                                    # bf16 spacing in [1, 2)
+    assert list(r(np.array([1 + step/2, 1 + 3*step/2, -(1 + step/2), 1 + step/2 + 2.0**-30]))) == \
+        [1.0, 1 + 2*step, -1.0, 1 + step]
+    assert list(r(np.array([0.0, -0.0, np.inf]))) == [0.0, 0.0, np.inf] and np.isnan(r(np.nan))
+    g = torch.Generator().manual_seed(0)
+    v = (torch.randn(20000, generator=g)*torch.exp(4*torch.randn(20000, generator=g))).float()
+    assert np.array_equal(r(v.double().numpy()), v.bfloat16().double().numpy())
+
+
+def test_pair_out_recombines_to_expert_sum():
+    cfg, inp = tiny_inputs(4, E=16, k=4, h=128, I=64, B=6)
+    args = tuple(inp[k] for k in ('x', 'router', 'router_bias', 'gate_blocks', 'gate_scales', 'up_blocks',
+                                  'up_scales', 'down_blocks', 'down_scales'))
+    r = moe_ref.moe_step(*args, topk=cfg.topk, pair_out=True)
+    assert r['pair_out'].shape == (6, 4, 128)
+    # pair outputs are bf16 values; the weighted sum over ascending ids is the combine
+    assert torch.equal(r['pair_out'], r['pair_out'].bfloat16().float())
+    acc = torch.zeros(6, 128)
+    for j in range(4):
+        acc += r['pair_out'][:, j]*r['route_weights'][:, j, None]
+    assert moe_ref.rel_l2(acc, r['expert_sum']) < 1e-6
 
 
 def test_planted_mistake_fails_brute_force():
@@ -338,3 +413,68 @@ def test_latent_block_chains_float64_pieces(seed):
     assert moe_ref.rel_l2(r['output'], out64) < 1e-5
     bf = latent_ref.latent_block(w['x'], w, topk=cfg.topk, routes=r['expert_ids'])
     assert bf['output'].dtype == torch.bfloat16 and 1e-4 < moe_ref.rel_l2(bf['output'], out64) < 3e-2
+
+
+@pytest.mark.parametrize('seed', [0, 1, 2])
+@pytest.mark.parametrize('B,h,lh,S', [(3, 64, 32, 16), (5, 256, 128, 64)])
+def test_latent_bf16_matches_bf16_float64_brute_force(seed, B, h, lh, S):
+    """latent_in / latent_out in BF16 mode against float64 brute forces rounded at the chain's casts."""
+    from oracle import latent_ref
+    from k3moe import synthetic
+    _, w = latent_case(seed, B=B, h=h, lh=lh, S=S)
+    args = (w['x'], w['latent_down'], w['shared_gate'], w['shared_up'])
+    lat64, sh64 = latent_ref.latent_in_bf16_f64(*args)
+    lat, sh = latent_ref.latent_in(*args)
+    assert moe_ref.rel_l2(lat, lat64) <= 1e-5 and moe_ref.rel_l2(sh, sh64) <= 1e-5
+    es = synthetic.randn(seed, 'expert_sum', (B, lh), 0.3, dtype=torch.float32)
+    shb = synthetic.randn(seed, 'shared_h', (B, S), 0.5)
+    want = latent_ref.latent_out_bf16_f64(es, w['latent_norm'], w['latent_up'], shb, w['shared_down'])
+    got = latent_ref.latent_out(es, w['latent_norm'], w['latent_up'], shb, w['shared_down'])
+    assert got.dtype == torch.bfloat16 and moe_ref.rel_l2(got, want) <= 1e-5
+
+
+def test_latent_bf16_planted_mistakes_fail(monkeypatch):
+    """Dropped or moved casts of the BF16 latent chain move it well away from the brute force."""
+    from oracle import latent_ref
+    from k3moe import synthetic
+    _, w = latent_case(1, B=5, h=256, lh=128, S=64)
+    args = (w['x'], w['latent_down'], w['shared_gate'], w['shared_up'])
+    lat64, sh64 = latent_ref.latent_in_bf16_f64(*args)
+    es = synthetic.randn(1, 'expert_sum', (5, 128), 0.3, dtype=torch.float32)
+    shb = synthetic.randn(1, 'shared_h', (5, 64), 0.5)
+    want = latent_ref.latent_out_bf16_f64(es, w['latent_norm'], w['latent_up'], shb, w['shared_down'])
+    out_args = (es, w['latent_norm'], w['latent_up'], shb, w['shared_down'])
+    project, rms = latent_ref.project, latent_ref.rms
+    # projections accumulate without rounding to bf16
+    monkeypatch.setattr(latent_ref, 'project', lambda W, x, act: x.to(act).float() @ W.to(act).float().T)
+    bl, bs = latent_ref.latent_in(*args)
+    assert moe_ref.rel_l2(bl.float(), lat64) >= 5e-4 and moe_ref.rel_l2(bs.float(), sh64) >= 5e-4
+    assert moe_ref.rel_l2(latent_ref.latent_out(*out_args).float(), want) >= 5e-4
+    monkeypatch.setattr(latent_ref, 'project', project)
+    plants = {
+        # the norm weight applied in FP32 before the cast (the common.py weight_in_fp32 variant)
+        'weight in fp32': lambda x, wt, eps: (x.float()*torch.rsqrt(x.float().square().mean(-1, keepdim=True) + eps)
+                                              * wt.float()).to(x.dtype),
+        # the expert sum normalised without its bf16 cast
+        'sum not cast': lambda x, wt, eps: rms(es, wt, eps).to(x.dtype),
+    }
+    for name, fn in plants.items():
+        monkeypatch.setattr(latent_ref, 'rms', fn)
+        assert moe_ref.rel_l2(latent_ref.latent_out(*out_args), want) >= 5e-4, name
+    monkeypatch.setattr(latent_ref, 'rms', rms)
+
+
+@pytest.mark.parametrize('seed', [0, 2])
+def test_latent_block_bf16_chains_bf16_pieces(seed):
+    """The whole BF16 block against latent_in_bf16_f64 -> moe_step_bf16_f64 -> latent_out_bf16_f64."""
+    from oracle import latent_ref
+    cfg, w = latent_case(seed)
+    r = latent_ref.latent_block(w['x'], w, topk=cfg.topk)
+    lat64, sh64 = latent_ref.latent_in_bf16_f64(w['x'], w['latent_down'], w['shared_gate'], w['shared_up'])
+    es64 = moe_ref.moe_step_bf16_f64(w['x'], w['router'], w['router_bias'], w['gate_blocks'], w['gate_scales'],
+                                     w['up_blocks'], w['up_scales'], w['down_blocks'], w['down_scales'],
+                                     routes=r['expert_ids'], weights=r['route_weights'],
+                                     latent=torch.from_numpy(lat64))
+    out64 = latent_ref.latent_out_bf16_f64(torch.from_numpy(es64), w['latent_norm'], w['latent_up'],
+                                           torch.from_numpy(sh64), w['shared_down'])
+    assert moe_ref.rel_l2(r['output'], out64) <= 1e-5
