@@ -120,6 +120,27 @@ int k3moe_moe_step(const k3moe_dims *dims,
                    float *shortfall,
                    void *workspace, size_t workspace_bytes, void *stream);
 
+/* k3moe_moe_step without a workspace argument, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc. No counterpart in the reference. The
+ * workspace is a 16 MiB array in the library's device memory, one per GPU,
+ * held until the process ends (every step of the persistent decode path fits:
+ * tokens <= 64; a step that needs more, such as a prefill chunk, fails with
+ * K3MOE_EWORKSPACE and a message). The first call on a device looks its
+ * address up and zeroes its control block with a kernel on `stream`; no call
+ * allocates or frees memory. All calls on one GPU share the array, so calls
+ * that may overlap on one GPU (other streams, other threads) race. Arguments,
+ * outputs, numerics and errors are those of k3moe_moe_step. */
+int k3moe_moe_step_noalloc(const k3moe_dims *dims,
+                           const void *x, const void *latent,
+                           const void *router, const float *router_bias,
+                           const uint8_t *gate_blocks, const uint8_t *gate_scales,
+                           const uint8_t *up_blocks, const uint8_t *up_scales,
+                           const uint8_t *down_blocks, const uint8_t *down_scales,
+                           const int64_t *routes,
+                           float *expert_sum, int64_t *expert_ids, float *route_weights,
+                           float *shortfall, void *stream);
+
 /* Where a step of the multi-kernel path leaves its token grouping
  * (kimi.py:319-320: `indices.unique()` and the `(indices == e).nonzero()`
  * lists) in the workspace, as byte offsets from its base. For tests and tools

@@ -10,6 +10,8 @@
 // synchronisation and no device allocation.
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
+
+#include <mutex>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -23,6 +25,13 @@
 #include "k3moe_xgemm.hpp"
 
 using namespace k3moe;
+
+// The allocation-free entry point's workspace (k3moe_moe_step_noalloc): one
+// copy per GPU the library runs on, held until the process ends. Its address
+// on a device comes from hipGetSymbolAddress with that device current (the
+// name is only a host-side stand-in); every call on a GPU shares it.
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
 
 namespace {
 
@@ -221,6 +230,33 @@ int latent_launch(const k3moe_latent_dims *dims, int out, const LatArgs &a, size
 __global__ void k_zero_words(uint32_t *p, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0u;
+}
+
+// The device address of `scratch` on the current device, looked up once per
+// device; the first lookup also zeroes its control block, zero area and
+// counters with a kernel on `st` (stream-ordered before the step that follows).
+std::mutex g_scratch_mu;
+void *g_scratch[64];
+
+int scratch_address(void **out, hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return fail(K3MOE_EHIP, "hipGetDevice failed: %s", hipGetErrorString(hipGetLastError()));
+  if (dev < 0 || dev >= 64) return fail(K3MOE_EINVAL, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void *ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr)
+      return fail(K3MOE_EHIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev, hipGetErrorString(err));
+    hipLaunchKernelGGL(k_zero_words, dim3(cdiv(kInitBytes / 4, 256)), dim3(256), 0, st, reinterpret_cast<uint32_t *>(ptr),
+                       kInitBytes / 4);
+    const int rc = launch_check("scratch init");
+    if (rc) return rc;
+    g_scratch[dev] = ptr;
+  }
+  *out = g_scratch[dev];
+  return K3MOE_OK;
 }
 
 }  // namespace
@@ -426,6 +462,29 @@ int k3moe_mxfp4_decode(const uint8_t *blocks, const uint8_t *scales, int64_t n_b
   hipLaunchKernelGGL(k_decode, dim3((unsigned)grid), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), blocks,
                      scales, n_blocks, out_dtype, out);
   return launch_check("decode");
+}
+
+int k3moe_moe_step_noalloc(const k3moe_dims *dims, const void *x, const void *latent, const void *router,
+                           const float *router_bias, const uint8_t *gate_blocks, const uint8_t *gate_scales,
+                           const uint8_t *up_blocks, const uint8_t *up_scales, const uint8_t *down_blocks,
+                           const uint8_t *down_scales, const int64_t *routes, float *expert_sum, int64_t *expert_ids,
+                           float *route_weights, float *shortfall, void *stream) {
+  g_err[0] = 0;
+  int rc = check_dims(dims);
+  if (rc) return rc;
+  Plan p;
+  make_plan(*dims, device_cus(), p, trace_enabled());
+  if (p.total > kScratchBytes)
+    return fail(K3MOE_EWORKSPACE,
+                "this step needs a %zu-byte workspace; the allocation-free entry point's scratch holds %zu "
+                "(tokens %d, experts %d, topk %d, latent %d, inter %d): use k3moe_moe_step with a workspace",
+                p.total, kScratchBytes, dims->tokens, dims->experts, dims->topk, dims->latent, dims->inter);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  void *ws = nullptr;
+  if ((rc = scratch_address(&ws, st))) return rc;
+  return k3moe_moe_step(dims, x, latent, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales,
+                        down_blocks, down_scales, routes, expert_sum, expert_ids, route_weights, shortfall, ws,
+                        kScratchBytes, stream);
 }
 
 }  // extern "C"

@@ -48,7 +48,8 @@ STATUS_TIMEOUT, STATUS_ROUTES = 1, 2
 
 EXPORTS = ('k3moe_workspace_bytes', 'k3moe_workspace_init', 'k3moe_workspace_status', 'k3moe_moe_step',
            'k3moe_mxfp4_decode', 'k3moe_last_error', 'k3moe_version', 'k3moe_latent_workspace_bytes',
-           'k3moe_latent_in', 'k3moe_latent_out', 'k3moe_workspace_layout')
+           'k3moe_latent_in', 'k3moe_latent_out', 'k3moe_workspace_layout',
+           'k3moe_moe_step_noalloc')
 
 _lib = None
 
@@ -76,6 +77,8 @@ def load(path: str | None = None):
     lib.k3moe_workspace_status.restype = ctypes.c_int
     lib.k3moe_moe_step.argtypes = [ctypes.POINTER(Dims)] + [p]*15 + [p, sz, p]
     lib.k3moe_moe_step.restype = ctypes.c_int
+    lib.k3moe_moe_step_noalloc.argtypes = [ctypes.POINTER(Dims)] + [p]*15 + [p]
+    lib.k3moe_moe_step_noalloc.restype = ctypes.c_int
     lib.k3moe_workspace_layout.argtypes = [ctypes.POINTER(Dims), ctypes.POINTER(Layout)]
     lib.k3moe_workspace_layout.restype = ctypes.c_int
     lib.k3moe_mxfp4_decode.argtypes = [p, p, i64, i32, p, p]
