@@ -106,6 +106,31 @@ def read_trace(cfg, device):
     while G*2 <= min(torch.cuda.get_device_properties(device).multi_processor_count, 1024):
         G *= 2
     full = full[:G]
+    if int(full[0, 55].item()) == 0x5349:   # the single-token kernel's rows
+        names = ('router', 'poll_partials', 'gating', 'select', 'weights_ids', 'gate_up', 'poll_h', 'down_combine')
+        t0 = full[:, 0].min()
+        out = {'kernel': 'single', 'workgroups': G, 'start_spread_us': round(float((full[:, 0].max() - t0)*0.01), 2)}
+        prev = full[:, 0]
+        for n, name in enumerate(names):
+            cur = full[:, n + 1]
+            ok = cur > 0
+            if not bool(ok.any()):
+                continue
+            out[name] = {'median_us': round(float(((cur[ok] - prev[ok])*0.01).median()), 2),
+                         'grid_done_at_us': round(float((cur[ok].max() - t0)*0.01), 2),
+                         'median_done_at_us': round(float((cur[ok].median() - t0)*0.01), 2)}
+            prev = torch.where(ok, cur, prev)
+        out['total_us'] = round(float((full[:, 8].max() - t0)*0.01), 2)
+
+        def span(a, b):   # median over workgroups of slot b - slot a, where both were written in order
+            x, y = full[:, a], full[:, b]
+            ok = (x > 0) & (y >= x)
+            return round(float(((y[ok] - x[ok])*0.01).median()), 2) if bool(ok.any()) else None
+        out['sub_phases_med_us'] = {'poll_first_round_trip': span(1, 10), 'gu_issue': span(5, 9),
+                                    'gu_data_and_mfma_wave0': span(9, 12), 'gu_reduce': span(12, 13),
+                                    'gu_epilogue_store': span(13, 14), 'gu_tail': span(14, 6)}
+        out['poll_rounds_median'] = float(full[:, 11].median())
+        return out
     raw = full[:, :9]
     dump = os.environ.get('K3MOE_TRACE_DUMP')
     if dump:

@@ -46,12 +46,17 @@ extern "C" {
  * once per 128 tokens of an expert) when the experts average at least 16
  * tokens and hidden/latent and inter are multiples of 128, and as per-16-token
  * streams otherwise; GROUPED and STREAMED force one of the two (GROUPED fails
- * with K3MOE_EINVAL when the widths are not multiples of 128). */
+ * with K3MOE_EINVAL when the widths are not multiples of 128). A single token
+ * runs on its own persistent kernel when its shape fits (SINGLE below); AUTO
+ * picks it then, DECODE forces the general persistent kernel. */
 #define K3MOE_PATH_AUTO 0
 #define K3MOE_PATH_GENERAL 1
 #define K3MOE_PATH_DECODE 2
 #define K3MOE_PATH_GROUPED 3
 #define K3MOE_PATH_STREAMED 4
+#define K3MOE_PATH_SINGLE 5 /* the single-token kernel (fails with K3MOE_EINVAL when the
+                             * shape does not fit it: one token, topk <= 8, experts <= 512,
+                             * latent a multiple of 512 up to 8192, inter <= 256) */
 
 /* Element type codes. */
 #define K3MOE_DTYPE_BF16 0
@@ -171,9 +176,10 @@ typedef struct k3moe_layout {
 
 int k3moe_workspace_layout(const k3moe_dims *dims, k3moe_layout *layout);
 
-/* Zero the workspace's first 86016 bytes (the control block with the barrier
+/* Zero the workspace's first 610304 bytes (the control block with the barrier
  * counters and the sticky status word, a zero area the kernels read in place
- * of inactive data, and the latent block's row-tile counters) with a small
+ * of inactive data, the latent block's row-tile counters and the single-token
+ * kernel's tagged exchange area) with a small
  * kernel on `stream`. A workspace must be
  * initialised once before its first step; each step leaves the counters at
  * zero, so one workspace serves any number of consecutive steps on one

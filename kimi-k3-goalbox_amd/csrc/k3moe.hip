@@ -22,6 +22,7 @@
 #include "k3moe_general.hpp"
 #include "k3moe_latent.hpp"
 #include "k3moe_plan.hpp"
+#include "k3moe_single.hpp"
 #include "k3moe_xgemm.hpp"
 
 using namespace k3moe;
@@ -64,7 +65,7 @@ int check_dims(const k3moe_dims *d) {
   if (d->activation != K3MOE_ACT_SITU && d->activation != K3MOE_ACT_SILU)
     return fail(K3MOE_EINVAL, "unknown activation %d", d->activation);
   if (d->x_dtype != K3MOE_DTYPE_BF16) return fail(K3MOE_EINVAL, "x_dtype must be bf16 (%d)", K3MOE_DTYPE_BF16);
-  if (d->path < K3MOE_PATH_AUTO || d->path > K3MOE_PATH_STREAMED) return fail(K3MOE_EINVAL, "unknown path %d", d->path);
+  if (d->path < K3MOE_PATH_AUTO || d->path > K3MOE_PATH_SINGLE) return fail(K3MOE_EINVAL, "unknown path %d", d->path);
   if (d->path == K3MOE_PATH_GROUPED && (d->latent % 128 || d->inter % 128))
     return fail(K3MOE_EINVAL, "the grouped GEMM path needs latent (%d) and inter (%d) multiples of 128", d->latent,
                 d->inter);
@@ -341,6 +342,11 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
   if (dims->path == K3MOE_PATH_DECODE && p.path != kPathDecode)
     return fail(K3MOE_EINVAL, "the persistent decode path needs tokens <= %d and tokens*topk <= %d", kDecMaxTokens,
                 kDecMaxPairs);
+  if (dims->path == K3MOE_PATH_SINGLE && !p.single)
+    return fail(K3MOE_EINVAL,
+                "the single-token kernel needs tokens == 1, topk <= 8, experts <= 512, latent a multiple of 512 "
+                "up to 8192, inter <= 256 (got tokens %d, topk %d, experts %d, latent %d, inter %d)",
+                dims->tokens, dims->topk, dims->experts, dims->latent, dims->inter);
   if (!workspace || workspace_bytes < p.total)
     return fail(K3MOE_EWORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
                 p.total);
@@ -365,6 +371,10 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
     a.out_w = route_weights;
     a.out_short = shortfall;
     a.ws = ws;
+    if (p.single) {
+      hipLaunchKernelGGL(k_moe_single, dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
+      return launch_check("single-token step");
+    }
     int slot = 0;
     const DecodeKernel fn = decode_kernel(p, slot);
     if ((rc = allow_lds(fn, slot, p.lds_total))) return rc;

@@ -716,6 +716,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   const uint8_t *zero = reinterpret_cast<const uint8_t *>(a.ws + pl.o_zero);  // kZeroBytes of zeros
   const int B = pl.B, E = pl.E, k = pl.k;
   trace_mark(pl, a.ws, 0);
+  // The gating bias of experts tid and tid + 512: a token's one-logit-per-thread
+  // gather uses exactly these, and loading them now keeps a cold HBM round trip
+  // out of the top-k phase.
+  float bias_pre[2] = {0.f, 0.f};
+  if (a.bias) {
+    if (tid < pl.E) bias_pre[0] = a.bias[tid];
+    if (tid + kDecThreads < pl.E) bias_pre[1] = a.bias[tid + kDecThreads];
+  }
   // this launch's barrier targets (thread 0 arrives for the workgroup)
   const BarrierBase bb = tid == 0 ? barrier_base(ctl) : BarrierBase{0u, 0u, 0u};
   __shared__ unsigned s_abort0;  // the abort counter at the start, for every thread's bounded waits
@@ -916,7 +924,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
 #pragma unroll
             for (int sp = 1; sp < kDecMaxSplits; ++sp)
               if (sp < pl.Srw) logit += ps[j][sp];
-            gate(f, logit, a.bias ? a.bias[f % E] : 0.f);
+            const float bv = !a.bias ? 0.f : (nt == 1 && j < 2) ? bias_pre[j] : a.bias[f % E];
+            gate(f, logit, bv);
           }
         }
       }

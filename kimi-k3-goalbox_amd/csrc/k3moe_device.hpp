@@ -231,6 +231,11 @@ __device__ __forceinline__ uint64_t program_counter() {
   return pc;
 }
 
+// Device-coherent 8-byte load (sc1).
+__device__ __forceinline__ u32x2 bload8_dev(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kCpolDevice));
+}
+
 // Device-coherent 16-byte load (sc1): sees device-coherent stores of other
 // workgroups without an L2 invalidate.
 __device__ __forceinline__ u32x4 bload16_dev(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -292,6 +297,24 @@ __device__ __forceinline__ float act_silu(float g, float u) {
 
 __device__ __forceinline__ float apply_act(int act, float g, float u) {
   return act == 0 ? act_situ(g, u) : act_silu(g, u);
+}
+
+// apply_act for row l & 7 of a wave, lanes 0-7 returning it, with its
+// transcendental factors spread over lanes: lane l computes factor l >> 3 of
+// row l & 7 (0: sigmoid(g), 1: tanh(g/4), 2: tanh(u/25)) and lanes 0-7 combine
+// them with the same operations in the same order as act_situ / act_silu, so
+// the result is the same bit for bit. g, u: row (l & 7)'s bf16-rounded gate and
+// up values in every lane. Every lane must call it.
+__device__ __forceinline__ float act_parts(int act, float g, float u) {
+  const int l = __lane_id(), f = l >> 3;
+  float part = 0.f;
+  if (f == 0) part = 1.0f / (1.0f + expf(-g));
+  else if (f == 1) part = tanhf(g / 4.0f);
+  else if (f == 2) part = tanhf(u / 25.0f);
+  const float sig = __shfl(part, l & 7, kWave), tg = __shfl(part, 8 + (l & 7), kWave),
+              tu = __shfl(part, 16 + (l & 7), kWave);
+  if (act == 0) return __fmul_rn(__fmul_rn(__fmul_rn(4.0f, tg), sig), __fmul_rn(25.0f, tu));
+  return __fmul_rn(__fmul_rn(g, sig), u);
 }
 
 // ----------------------------------------------------------- wave helpers --

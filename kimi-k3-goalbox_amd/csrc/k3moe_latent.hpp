@@ -132,8 +132,9 @@ inline const char *latent_plan(const k3moe_latent_dims &d, int n_cus, int out, L
   if ((p.G / p.SP) * kLatGrpStride * 4 > kLatCntBytes) return "too many workgroup groups for the counter area";
   long o = 0;
   auto take = [&](long bytes) { long at = o; o = (long)align256((size_t)(o + bytes)); return at; };
-  take(kInitBytes - kLatCntBytes);
+  take(kOffLatCnt);
   p.o_cnt = take(kLatCntBytes);
+  take(kTagBytes);
   const long part = (long)p.SP * p.RT * p.B * 16 * 4;
   p.o_part0 = take(part);
   p.o_part1 = out ? take(part) : 0;

@@ -47,6 +47,12 @@ constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert
 //     the status set but does not shorten later launches' waits)
 constexpr int kCtlErr = 2;
 constexpr int kCtlAbort = 3;
+constexpr int kCtlCodeSingle = 8;  // 2 x uint64: the single-token kernel's code range of its last launch
+// Launch counters of the single-token kernel (k3moe_single.hpp): each of its
+// workgroups adds one, on counter blockIdx % kEpochCounters, when it leaves;
+// the sum, divided by the grid size, counts its earlier launches on this
+// workspace. kCtlEpochStride words (64 bytes) apart.
+constexpr int kCtlEpoch = 640, kEpochCounters = 16, kCtlEpochStride = 16;
 constexpr int kCtlCode = 4;  // 2 x uint64: the decode kernel's code range (start, end) of its last launch
 constexpr int kCtlTop = 32;
 constexpr int kBarGroups = 16, kCtlGroup = 64, kCtlStride = 32;
@@ -61,7 +67,14 @@ constexpr int kZeroBytes = 64 * 1024;
 // k3moe_latent.hpp): zero between launches; the launch that completes a tile
 // puts its counter back to zero.
 constexpr int kLatCntBytes = 16384;
-constexpr int kInitBytes = 4096 + kZeroBytes + kLatCntBytes;  // control block (page-padded), zero area, counters
+constexpr int kOffLatCnt = 4096 + kZeroBytes;
+// Then the single-token kernel's tagged exchange area: 8-byte slots {payload,
+// tag}, where the tag identifies the launch that wrote the payload (zero never
+// does, so a zeroed area holds no valid slot). Only that kernel writes it.
+constexpr int kTagBytes = 512 * 1024;
+constexpr int kTagCopies = 8;  // router partials: one copy per XCD (workgroup b reads copy b mod 8)
+constexpr int kOffTag = kOffLatCnt + kLatCntBytes;
+constexpr int kInitBytes = kOffTag + kTagBytes;  // control block (page-padded), zero area, counters, tags
 constexpr int kTraceSlots = 56;    // phase timestamps per workgroup when tracing
 constexpr int kErrBarrierTimeout = 1;  // a wait timed out: that step's outputs are invalid
 constexpr int kErrRoutes = 2;          // forced routes out of range or repeated in a row: those rows used their own top-k
@@ -86,6 +99,7 @@ struct Plan {
   int NX;      // gate/up: activation rows staged in LDS per round (also the chunk size in tokens)
   int xpitch;  // staged row pitch in elements (K + 8: rows start in different banks)
   int trace;      // 1: the decode kernel records phase timestamps at o_trace
+  int single;     // 1: the single-token kernel runs the step (k3moe_single.hpp)
   int redundant;  // 1: every workgroup routes every token (no barrier before grouping)
   int xgemm;      // general path: 1 = grouped-GEMM expert kernels, 0 = per-16-token streams
   // workspace byte offsets
@@ -96,7 +110,7 @@ struct Plan {
 __host__ __device__ inline int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
-inline int align16(int v) { return (v + 15) & ~15; }
+__host__ __device__ inline int align16(int v) { return (v + 15) & ~15; }
 
 // Decode-path LDS layout for plan p; returns the total bytes.
 inline int decode_lds(Plan &p) {
@@ -123,6 +137,23 @@ inline int decode_lds(Plan &p) {
   if (p.NX < 1) return 1 << 30;  // no decode path
   p.lds_total = p.lds_red + p.lds_grp + p.lds_scr;
   return p.lds_total;
+}
+
+// The single-token kernel (k3moe_single.hpp) takes the step when it fits:
+// one token, top-k <= 8 of at most 512 experts (its top-k is the 8-wave
+// cooperative selection), the expert width K a multiple of 512 (whole
+// 512-column gate/up super-steps, at most kSingleMaxSS per wave) and at most
+// 8192 (its staged row), I <= 256 (the down projection's two k-steps), at most
+// two 16-row output tiles per workgroup, and its tagged partials and
+// intermediates fitting the tag area. Its dynamic LDS: the keys (3 E words),
+// the staged row (2 K bytes) and fixed scratch.
+constexpr int kSingleMaxSS = 2;  // gate/up super-steps of 512 columns per wave: ceil(K / 4096)
+inline int single_lds(const Plan &p) { return align16(3 * 4 * p.E) + 2 * p.K + 8192; }
+inline void single_plan(const k3moe_dims &d, Plan &p) {
+  const bool tags_fit = (long)kTagCopies * p.E * 8 * 8 + (long)p.k * (p.I / 2) * 8 <= kTagBytes;
+  p.single = (d.path == K3MOE_PATH_AUTO || d.path == K3MOE_PATH_SINGLE) && p.B == 1 && p.k <= 8 && p.E <= 512 &&
+             p.K % 512 == 0 && p.K <= kSingleMaxSS * kDecWaves * 512 && p.I <= 256 && p.I % 32 == 0 && p.h % 128 == 0 &&
+             p.RTd <= 2 * p.G && p.k * (p.I / 8) <= 4 * p.G && tags_fit && p.Srw <= kDecMaxSplits;
 }
 
 // n_cus: compute units of the device (the persistent grid size); trace: reserve
@@ -159,8 +190,8 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   if (srw_cap < 1) srw_cap = 1;
   p.Srw = srw_cap;
   p.path = kPathGeneral;
-  if ((d.path == K3MOE_PATH_AUTO || d.path == K3MOE_PATH_DECODE) && p.B <= kDecMaxTokens && p.P <= kDecMaxPairs &&
-      decode_lds(p) <= kDecMaxLds - kDecStaticLds)
+  if ((d.path == K3MOE_PATH_AUTO || d.path == K3MOE_PATH_DECODE || d.path == K3MOE_PATH_SINGLE) &&
+      p.B <= kDecMaxTokens && p.P <= kDecMaxPairs && decode_lds(p) <= kDecMaxLds - kDecStaticLds)
     p.path = kPathDecode;
   // general path expert kernels: grouped GEMMs when the experts average at
   // least kXMinPairsPerExpert tokens (and the widths allow 128-k steps)
@@ -189,6 +220,7 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   p.o_ctl = take(4096);
   p.o_zero = take(kZeroBytes);
   take(kLatCntBytes);  // the latent block's counters, kept by MoE steps on a shared workspace
+  take(kTagBytes);     // the single-token kernel's tagged exchange area
   p.o_logit = take((size_t)logit_splits * p.B * p.Epad * 4);
   p.o_ids = take((size_t)p.P * 4);
   p.o_w = take((size_t)p.P * 4);
@@ -206,6 +238,11 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   // pair outputs: the general path, and the decode path's expert-major down (I = 256, 384, 512)
   p.o_y = take((general || p.I == 256 || p.I == 384 || p.I == 512) ? (size_t)p.P * p.K * 2 : 0);
   p.trace = trace && p.path == kPathDecode;
+  single_plan(d, p);
+  if (p.single) {
+    p.path = kPathDecode;
+    p.lds_total = single_lds(p);
+  }
   p.o_ecnt = take((size_t)p.Dmax * kCntStride * 4);  // decode: gate/up units done per active expert
   p.o_trace = p.trace ? take((size_t)1024 * kTraceSlots * 8) : 0;  // last area of the workspace
   p.total = o;

@@ -20,7 +20,7 @@ K3MOE_OK = 0
 GATING = {'sigmoid_bias': 0, 'softmax': 1}
 ACTIVATION = {'situ': 0, 'silu': 1}
 DTYPE_BF16, DTYPE_F32 = 0, 1
-PATH = {'auto': 0, 'general': 1, 'decode': 2, 'grouped': 3, 'streamed': 4}
+PATH = {'auto': 0, 'general': 1, 'decode': 2, 'grouped': 3, 'streamed': 4, 'single': 5}
 
 
 class Dims(ctypes.Structure):

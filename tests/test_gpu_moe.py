@@ -30,7 +30,7 @@ def decode_ok(cfg):
     return cfg.tokens <= 64 and cfg.tokens*cfg.topk <= 1024
 
 
-def near_oracle_sum(got, oracle, steps=2, min_same=0.95):
+def near_oracle_sum(got, oracle, steps=2, min_same=0.75):
     """expert_sum element by element next to the BF16 oracle.
 
     Both sum w * bf16(y) over a token's experts in ascending order in FP32 from
@@ -41,8 +41,11 @@ def near_oracle_sum(got, oracle, steps=2, min_same=0.95):
     sum_j w_j steps ulp(y_j), plus 1e-6 of the row scale for outputs near
     zero. And the oracle's pair outputs recombined with the GPU's weights in
     that order must equal the GPU's sum bitwise for most elements (every
-    element whose pair outputs all have the oracle's rounding); returns that
-    fraction.
+    element whose pair outputs all have the oracle's rounding; one flipped bf16
+    rounding of an activation moves about a sixteenth of its expert's outputs by
+    a step, and at one token every output sums every chosen expert); returns
+    that fraction. The combine's own arithmetic is checked exactly by
+    test_general_grouping_lists_match_oracle.
     """
     g, o = got['expert_sum'].double(), oracle['expert_sum'].double()
     y, w = oracle['pair_out'].double(), oracle['route_weights'].double()
@@ -209,6 +212,121 @@ def test_moe_small_geometries(gpu, cfg, seed, path):
     run_and_check(cfg, synthetic.moe_layer_inputs(cfg, seed, scale_mode='kimi'), gpu, path=path)
 
 
+# one token on the single-token kernel: top-k <= 8 of <= 512 experts, K a multiple of 1024
+SINGLE = [
+    MoEConfig('single-e64-k8', 64, 8, 1024, 256, 1),
+    MoEConfig('single-e40-k5-i96', 40, 5, 2048, 96, 1),
+    MoEConfig('single-e512-softmax-silu', 512, 8, 1024, 128, 1, gating='softmax', activation='silu'),
+    MoEConfig('single-k1', 16, 1, 1024, 64, 1),
+    MoEConfig('single-k8192', 32, 4, 8192, 32, 1),
+    MoEConfig('single-latent', 64, 8, 512, 256, 1, latent=1024),
+]
+
+
+@pytest.mark.parametrize('cfg', SINGLE, ids=lambda c: c.name)
+@pytest.mark.parametrize('seed', [0, 1])
+@pytest.mark.parametrize('path', ['single', 'decode'])
+def test_moe_single_token_geometries(gpu, cfg, seed, path):
+    say(f'case: {cfg.name} seed={seed} path={path}')
+    run_and_check(cfg, synthetic.moe_layer_inputs(cfg, seed, scale_mode='kimi'), gpu, path=path)
+
+
+def test_single_and_decode_kernels_agree_tp8_b1(gpu):
+    """The same router arithmetic (splits and wave order): identical expert ids and weights;
+    gate/up sums in another order, so expert_sum agrees to the oracle's rounding steps."""
+    cfg = configs.TP8_B1
+    say(f'case: {cfg.name} seed=11, single-token kernel vs general persistent kernel')
+    g = to_dev(synthetic.moe_layer_inputs(cfg, 11), gpu)
+    outs = {}
+    for path in ('single', 'decode'):
+        outs[path] = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, path=path)
+        torch.cuda.synchronize(gpu)
+    a, b = outs['single'], outs['decode']
+    assert torch.equal(a['expert_ids'], b['expert_ids'])
+    assert torch.equal(a['route_weights'], b['route_weights'])
+    assert moe_ref.rel_l2(a['expert_sum'].cpu(), b['expert_sum'].cpu()) < 2e-3
+
+
+def test_single_token_tags_across_launches(gpu):
+    """Consecutive single-token launches on one workspace, alternating inputs and interleaved with
+    a general persistent step (b8) and a latent-width change: each launch's outputs equal a fresh
+    workspace's, so no launch reads another launch's tagged partials or intermediates."""
+    from k3moe.moe import dims_for, workspace_bytes
+    cfg = configs.TP8_B1
+    say(f'case: {cfg.name} seeds 1-2 alternating on one workspace, with b8 and a wider step between')
+    ins = [to_dev(synthetic.moe_layer_inputs(cfg, sd), gpu) for sd in (1, 2)]
+    wide = MoEConfig('single-e64-k8', 64, 8, 1024, 256, 1)
+    g_wide = to_dev(synthetic.moe_layer_inputs(wide, 3), gpu)
+    g8 = to_dev(synthetic.moe_layer_inputs(configs.TP8_B8, 4), gpu)
+    need = max(workspace_bytes(dims_for(g['x'], g['router'], g['gate_blocks'], g['down_blocks'], c.topk, c.gating,
+                                        c.activation)) for g, c in ((ins[0], cfg), (g8, configs.TP8_B8)))
+    fresh = []
+    for g, c in ((ins[0], cfg), (ins[1], cfg), (g_wide, wide), (g8, configs.TP8_B8)):
+        fresh.append(k3moe.moe_step(*synthetic.step_args(g), topk=c.topk, workspace=k3moe.new_workspace(need, gpu)))
+    ws = k3moe.new_workspace(need, gpu)
+    order = [0, 1, 0, 2, 1, 3, 0, 1, 2, 0]
+    plan = [(ins[0], cfg), (ins[1], cfg), (g_wide, wide), (g8, configs.TP8_B8)]
+    for n, idx in enumerate(order):
+        g, c = plan[idx]
+        got = k3moe.moe_step(*synthetic.step_args(g), topk=c.topk, workspace=ws)
+        torch.cuda.synchronize(gpu)
+        for key in ('expert_sum', 'expert_ids', 'route_weights'):
+            assert torch.equal(got[key], fresh[idx][key]), (n, idx, key)
+    assert k3moe.workspace_status(ws) == 0
+
+
+def test_single_token_from_a_large_launch_count(gpu):
+    """The tag comes from the launch counters' sum: preset them to a large, consistent count
+    (as after 2**24 - 3 launches) and run across the tag's wrap-around point."""
+    cfg = configs.TP8_B1
+    say(f'case: {cfg.name} seed=5, launch counters preset near the 32-bit wrap')
+    g = to_dev(synthetic.moe_layer_inputs(cfg, 5), gpu)
+    ref = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, workspace=k3moe.new_workspace(1 << 22, gpu))
+    ws = k3moe.new_workspace(1 << 22, gpu)
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    G = 1
+    while G * 2 <= min(cus, 1024):
+        G *= 2
+    launches = (1 << 32) // G - 3
+    ctl = ws[:4096].view(torch.int32)
+    per = [0] * 16                                   # counter g gets the workgroups b with b % 16 == g
+    for b in range(G):
+        per[b % 16] += 1
+    for gi in range(16):
+        v = (per[gi] * launches) & 0xFFFFFFFF
+        ctl[640 + 16 * gi] = v - (1 << 32) if v >= 1 << 31 else v
+    torch.cuda.synchronize(gpu)
+    for step in range(6):
+        got = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, workspace=ws)
+        torch.cuda.synchronize(gpu)
+        for key in ('expert_sum', 'expert_ids', 'route_weights'):
+            assert torch.equal(got[key], ref[key]), (step, key)
+    assert k3moe.workspace_status(ws) == 0
+
+
+def test_single_token_invalid_forced_routes(gpu):
+    """Through the C ABI, one token's forced routes with a repeated id: its own top-k, status 2."""
+    from k3moe.moe import dims_for, workspace_bytes
+    cfg = MoEConfig('single-bad-routes', 64, 8, 1024, 256, 1)
+    say(f'case: {cfg.name} seed=13 path=single, a repeated forced id through the C ABI')
+    g = to_dev(synthetic.moe_layer_inputs(cfg, 13, scale_mode='kimi'), gpu)
+    free = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, path='single')
+    torch.cuda.synchronize(gpu)
+    routes = free['expert_ids'].clone()
+    routes[0, 5] = routes[0, 2]
+    dims = dims_for(g['x'], g['router'], g['gate_blocks'], g['down_blocks'], cfg.topk, cfg.gating, cfg.activation,
+                    None, 'single')
+    ws = k3moe.new_workspace(workspace_bytes(dims), gpu)
+    outs = {'expert_sum': torch.full((1, cfg.hidden), float('nan'), device=gpu),
+            'expert_ids': torch.full((1, cfg.topk), -1, dtype=torch.int64, device=gpu),
+            'route_weights': torch.zeros(1, cfg.topk, device=gpu), 'route_shortfall': torch.full((1,), -1.0, device=gpu)}
+    raw_step(dims, g, routes.contiguous(), outs, ws)
+    torch.cuda.synchronize(gpu)
+    assert k3moe.workspace_status(ws) == 2
+    for key in ('expert_sum', 'expert_ids', 'route_weights'):
+        assert torch.equal(outs[key], free[key]), key
+
+
 @pytest.mark.parametrize('seed', [0, 1, 2])
 def test_moe_cpu_plumbing(gpu, seed):
     cfg = configs.CPU_PLUMBING
@@ -217,8 +335,10 @@ def test_moe_cpu_plumbing(gpu, seed):
 
 
 @pytest.mark.parametrize('cfg', [configs.TP8_B1, configs.TP8_B8], ids=lambda c: c.name)
-@pytest.mark.parametrize('path', ['general', 'decode'])
+@pytest.mark.parametrize('path', ['general', 'decode', 'single'])
 def test_moe_tp8_rank(gpu, cfg, path):
+    if path == 'single' and cfg.tokens != 1:
+        pytest.skip('the single-token kernel takes one token')
     say(f'case: {cfg.name} seed=0 path={path}')
     run_and_check(cfg, synthetic.moe_layer_inputs(cfg, 0), gpu, path=path)
 
@@ -448,11 +568,11 @@ def test_prefill_b4096_sampled_rows(gpu):
 
 # ---- status word, forced-route validation on the device, grouping lists ----
 
-@pytest.mark.parametrize('path', ['decode', 'general'])
+@pytest.mark.parametrize('path', ['decode', 'general', 'single'])
 def test_old_status_does_not_shorten_waits(gpu, path):
     """A status word and abort counter left set by an earlier step must not let a later
     launch skip its waits: the outputs equal a clean workspace's, the status stays set."""
-    cfg = configs.TP8_B8
+    cfg = configs.TP8_B1 if path == 'single' else configs.TP8_B8
     say(f'case: {cfg.name} seed=8 path={path}, status word 1 and abort counter 5 preset')
     g = to_dev(synthetic.moe_layer_inputs(cfg, 8), gpu)
     from k3moe.moe import dims_for, workspace_bytes
@@ -571,3 +691,13 @@ def test_general_grouping_lists_match_oracle(gpu, cfg):
     w = got['route_weights'].cpu().numpy()
     pw = raw[lay['pair_weight']:lay['pair_weight'] + 4*P].view(np.float32)
     assert np.array_equal(pw.view(np.uint32), w[prow, pslot].view(np.uint32))
+    # the combine (kimi.py:318,323): the step's own pair outputs y times the weights, FP32 products
+    # and sums from zero in ascending expert order, reproduce expert_sum bit for bit
+    K = cfg.width
+    y = torch.from_numpy(raw[lay['pair_y']:lay['pair_y'] + 2*P*K].copy()).view(torch.bfloat16).view(P, K).float()
+    wt = got['route_weights'].cpu()
+    re = torch.zeros(B, K)
+    for j in range(k):
+        p_of = torch.from_numpy(pof.reshape(B, k)[:, j].astype(np.int64))
+        re = re + y[p_of]*wt[:, j, None]
+    assert torch.equal(re, got['expert_sum'].cpu())

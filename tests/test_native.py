@@ -153,3 +153,15 @@ def test_integration_ctypes_snippet_matches_the_binding():
     decl = re.search(r'int k3moe_moe_step\((.*?)\);', text, flags=re.S).group(1)
     params = [p.strip() for p in decl.split(',')]
     assert len(params) == 1 + 15 + 3
+
+
+def test_init_size_agrees_across_header_library_and_python():
+    """k3moe_workspace_init's zeroed prefix: the library's size (from its size check, which fails
+    before anything is launched), the header's documented number and moe.INIT_BYTES agree."""
+    lib = _native.load()
+    rc = lib.k3moe_workspace_init(ctypes.c_void_p(256), ctypes.c_size_t(16), None)
+    assert rc == -2
+    n = int(re.search(r'at least (\d+) bytes', lib.k3moe_last_error().decode()).group(1))
+    assert n == moe.INIT_BYTES
+    text = open(HEADER).read()
+    assert int(re.search(r"Zero the workspace's first (\d+) bytes", text).group(1)) == n
