@@ -171,6 +171,10 @@ def read_trace(cfg, device):
     sub(28, 29, 'group_scan')
     sub(29, 5, 'group_place')
     sub(5, 32, 'gu_round_table')
+    sub(5, 45, 'gu_rt_to_first_barrier')
+    sub(45, 46, 'gu_rt_lds_reads')
+    sub(46, 47, 'gu_rt_table')
+    sub(47, 32, 'gu_rt_second_barrier')
     sub(32, 33, 'gu_stage_x')
     sub(33, 34, 'gu_stream_wave0')
     sub(34, 35, 'gu_wait_all_waves')

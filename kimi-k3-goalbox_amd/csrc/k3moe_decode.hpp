@@ -65,15 +65,26 @@ struct DecodeArgs {
 // while it is behind the workgroup's mean. The branch is wave-uniform:
 // s_setprio ignores the exec mask.
 __device__ __forceinline__ void balance_waves(int *prog, int done, int total) {
-  const int w = threadIdx.x >> 6;
+  const int w = wave_id();
   const int mine = total > 0 ? done * 4096 / total : 4096;
   if ((threadIdx.x & 63) == 0) __hip_atomic_store(prog + w, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  const u32x4 p0 = *reinterpret_cast<const volatile u32x4 *>(prog);
-  const u32x4 p1 = *reinterpret_cast<const volatile u32x4 *>(prog + 4);
-  const int sum = (int)(p0[0] + p0[1] + p0[2] + p0[3] + p1[0] + p1[1] + p1[2] + p1[3]);
+  // relaxed atomic loads: read afresh each call, and (unlike volatile ones,
+  // which keep a generic address) compiled as LDS reads, which wait for
+  // nothing but LDS; a flat read would wait for the wave's weight loads
+  int sum = 0;
+#pragma unroll
+  for (int j = 0; j < kDecWaves; ++j) sum += __hip_atomic_load(prog + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   if (__builtin_amdgcn_readfirstlane(mine * kDecWaves < sum ? 1 : 0)) __builtin_amdgcn_s_setprio(2);
   else __builtin_amdgcn_s_setprio(0);
+}
+
+// The first 8-byte aligned address at or after p (an LDS pointer), derived from
+// p by pointer arithmetic so that it stays an LDS pointer for the compiler (an
+// integer round trip would make its accesses flat ones, which also wait for
+// the wave's global loads).
+__device__ __forceinline__ uint64_t *lds_align8(int *p) {
+  char *c = reinterpret_cast<char *>(p);
+  return reinterpret_cast<uint64_t *>(c + ((8 - (reinterpret_cast<uintptr_t>(c) & 7)) & 7));
 }
 
 // Trace slots of workgroup blockIdx.x starting at `slot`, or null when not tracing.
@@ -158,10 +169,19 @@ __device__ __forceinline__ void gu_issue(GuSS<W> &B, const uint8_t *const (&wr)[
   }
 }
 
-// acc[u] += tile u over super-step ss; xrow: this lane's staged token row (LDS)
+// acc[u] += tile u over super-step ss; xrow: this lane's staged token row (LDS).
+// The scale words enter here through an empty asm: loads issued early (before
+// the round table, or a super-step ahead) would otherwise have their scale
+// conversion hoisted next to them, and the wave would wait there for them.
 template <int W, bool AL>
 __device__ __forceinline__ void gu_compute(const GuSS<W> &B, const uint16_t *xrow, int ss, int KB, f32x4 (&acc)[W]) {
   const int q = (threadIdx.x & 63) >> 4;
+  u32x4 sc[W];
+#pragma unroll
+  for (int u = 0; u < W; ++u) {
+    sc[u] = B.s[u];
+    asm volatile("" : "+v"(sc[u]));
+  }
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     if (!AL && 16 * ss + 4 * t >= KB) break;  // wave-uniform: nothing left in this super-step
@@ -174,7 +194,7 @@ __device__ __forceinline__ void gu_compute(const GuSS<W> &B, const uint16_t *xro
 #pragma unroll
     for (int u = 0; u < W; ++u) {
       bf16x8 av[4];
-      convert_block_fast(B.a[u][t], (B.s[u][t] >> (8 * q)) & 0xFFu, av);
+      convert_block_fast(B.a[u][t], (sc[u][t] >> (8 * q)) & 0xFFu, av);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) acc[u] = mfma16(av[kk], as_bf16x8(b[kk]), acc[u]);
     }
@@ -230,7 +250,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
                                       const int *g_ptok,
                                       uint16_t *xs, GuChunk *tab, int *s_round, int *s_rowtok, int *s_prog, int D,
                                       uint16_t *hbuf, const u32x4 (&xpre)[2], bool xpre_ok) {
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i = l & 15;
+  const int tid = threadIdx.x, w = wave_id(), l = tid & 63, i = l & 15;
   const int KB = pl.K / kBlockK, NSS = (KB + 15) / 16, K8 = pl.K / 8;
   const int GPC = pl.U8 / W;  // groups per chunk
   const int NG = g_coff[D] * GPC;
@@ -269,6 +289,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
     // LDS-only barriers in the round (no vector-memory wait): the previous round is
     // done with the table, the staged rows and the partial tiles
     ring_barrier();
+    if (g0 == ga) trace_mark(pl, a.ws, 45);
     if (w == 0) {
       // lane j < 16 takes chunk ci0 + j; the round is the prefix of chunks whose rows fit
       const int ci = ci0 + l;
@@ -281,6 +302,9 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
         pbase = g_aoff[lo] + c * pl.NX;
         n = min(pl.NX, g_acnt[lo] - c * pl.NX);
       }
+      if (g0 == ga && pl.o_trace && l == 0)
+        reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + 46] =
+            __builtin_amdgcn_s_memrealtime() + (uint64_t)(n & 0);
       const int pre = wave_incl_scan(n);  // inclusive prefix of the token counts (lanes >= 16 add 0)
       const bool fits = in && pre <= pl.NX;
       const int nch = __popcll(__ballot(fits));  // >= 1: one chunk never exceeds NX rows
@@ -295,6 +319,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
         s_round[0] = nch;
         s_round[1] = rows;
       }
+      if (g0 == ga) trace_mark(pl, a.ws, 47);
     }
     ring_barrier();
     if (g0 == ga) trace_mark(pl, a.ws, 32);
@@ -373,14 +398,20 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
       f32x4 acc[W];
 #pragma unroll
       for (int u = 0; u < W; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // step(pos): issue super-step pos + 1 (always: past the range end the
+      // range's last super-step again, an L2 hit), then compute pos if it is in
+      // the range. An issue under a condition would make the compiler's wait for
+      // pos's data cover the loads just issued (vmcnt(0) at the join), and the
+      // stream would run one super-step deep.
       auto step = [&](GuSS<W> &cur, GuSS<W> &nxt, int pos) {
         if (pos + 1 < e) {
           if (++iss == NSS) {
             iss = 0;
             rows_of(++ig, iwr, isr);
           }
-          gu_issue<W, AL>(nxt, iwr, isr, iss, KB);
         }
+        gu_issue<W, AL>(nxt, iwr, isr, iss, KB);
+        if (pos >= e) return;  // wave-uniform: the odd step past an odd range
         gu_compute<W, AL>(cur, xrow, css, KB, acc);
         balance_waves(s_prog, pos + 1 - s, e - s);
         if (++css == NSS || pos + 1 == e) {
@@ -401,7 +432,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
       };
       for (int pos = s; pos < e; pos += 2) {
         step(B0, B1, pos);
-        if (pos + 1 < e) step(B1, B0, pos + 1);
+        step(B1, B0, pos + 1);
       }
     }
     __builtin_amdgcn_s_setprio(0);
@@ -469,13 +500,13 @@ __device__ __forceinline__ void dnc_issue(DnTileBatch<KSD> &bt, const Plan &pl, 
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const bool ok = rt0 + t < rt1;  // wave-uniform
-    uint32_t sc = 0u;
-    if (ok) {
-      if constexpr (KSD == 2) sc = *reinterpret_cast<const uint16_t *>(srow + t * sstride);
-      else if constexpr (KSD == 4) sc = *reinterpret_cast<const uint32_t *>(srow + t * sstride);
-      else sc = (uint32_t)srow[t * sstride] | ((uint32_t)srow[t * sstride + 1] << 8) |
-                ((uint32_t)srow[t * sstride + 2] << 16);
-    }
+    // unconditional loads (a tile past the last reads the zero area): a load
+    // under a condition is joined by a copy that waits for it at once
+    const uint8_t *sp = ok ? srow + t * sstride : zero;
+    uint32_t sc;
+    if constexpr (KSD == 2) sc = *reinterpret_cast<const uint16_t *>(sp);
+    else if constexpr (KSD == 4) sc = *reinterpret_cast<const uint32_t *>(sp);
+    else sc = (uint32_t)sp[0] | ((uint32_t)sp[1] << 8) | ((uint32_t)sp[2] << 16);
 #pragma unroll
     for (int ks = 0; ks < KSD; ++ks) {
       bt.a[t][ks] = load16(ok ? wrow + t * tstride + ks * 16 : zero);
@@ -520,7 +551,9 @@ __device__ __forceinline__ void dnc_compute(const DnTileBatch<KSD> &bt, const Pl
 #pragma unroll
     for (int ks = 0; ks < KSD; ++ks) {
       bf16x8 av[4];
-      convert_block_fast(bt.a[t][ks], bt.s[t][ks], av);
+      uint32_t sc = bt.s[t][ks];
+      asm volatile("" : "+v"(sc));  // no conversion hoisted next to the (early) load
+      convert_block_fast(bt.a[t][ks], sc, av);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) acc = mfma16(av[kk], as_bf16x8(hb[ks][kk]), acc);
     }
@@ -568,15 +601,15 @@ __device__ __forceinline__ void dn_expert_major(const Plan &pl, const DecodeArgs
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) hb[ks][kk] = bload16_dev(hrs, ho + kk * 16);  // device-coherent
       }
+      // the next batch is always issued (tiles at or past rt1 read the zero
+      // area): an issue under a condition would make the wait for the current
+      // batch cover it (vmcnt(0) at the join)
       for (int rt = rt0; rt < rt1; rt += 2 * T) {
         const int o1 = rt + T - rt0, o2 = rt + 2 * T - rt0;
-        if (rt + T < rt1) dnc_issue<KSD>(b1, pl, wrow + o1 * tstride, srow + o1 * sstride, zero, rt + T, rt1);
+        dnc_issue<KSD>(b1, pl, wrow + o1 * tstride, srow + o1 * sstride, zero, rt + T, rt1);
         dnc_compute<KSD>(b0, pl, hb, st, ybuf, rt, rt1, p0 + c * 16, ncol);
-        if (rt + T < rt1) {
-          if (rt + 2 * T < rt1)
-            dnc_issue<KSD>(b0, pl, wrow + o2 * tstride, srow + o2 * sstride, zero, rt + 2 * T, rt1);
-          dnc_compute<KSD>(b1, pl, hb, st, ybuf, rt + T, rt1, p0 + c * 16, ncol);
-        }
+        dnc_issue<KSD>(b0, pl, wrow + o2 * tstride, srow + o2 * sstride, zero, rt + 2 * T, rt1);
+        if (rt + T < rt1) dnc_compute<KSD>(b1, pl, hb, st, ybuf, rt + T, rt1, p0 + c * 16, ncol);
       }
     }
     t += rt1 - rt0;
@@ -587,9 +620,21 @@ __device__ __forceinline__ void dn_expert_major(const Plan &pl, const DecodeArgs
 // scales) and B (the activated h of the item's 16-token chunk).
 struct DnLoad {
   u32x4 w[kDnDepth];
-  uint32_t s[kDnDepth];
+  uint32_t s[kDnDepth];   // the aligned dword holding the scale byte
+  uint32_t sh[kDnDepth];  // the byte's bit offset in it
   u32x4 b[kDnDepth][4];
 };
+
+// Scale byte j of a down item. The byte is loaded as its aligned dword (a
+// dword never crosses a page, so the load stays in mapped memory) and taken
+// apart here, at its use: a byte load's value is zero-extended where the
+// compiler places it, which can be a loop latch ahead of the next issue, and
+// that wait would then hold up the next item's loads.
+__device__ __forceinline__ uint32_t dn_scale(const DnLoad &L, int j) {
+  uint32_t v = L.s[j];
+  asm volatile("" : "+v"(v));
+  return (v >> L.sh[j]) & 0xffu;
+}
 
 // Weights and scales of a down item (they do not depend on h): exactly
 // 2 kDnDepth loads per lane, k-steps past I and row tiles past the last read
@@ -604,13 +649,17 @@ __device__ __forceinline__ void dn_issue_w(const Plan &pl, const DecodeArgs &a, 
     const int kb = (kc + j) * 4 + q;
     const bool ok = rt_ok && kc + j < pl.KSd && kb < KB;
     L.w[j] = load16(ok ? a.dblk + (row * KB + kb) * 16 : zero);
-    L.s[j] = *(ok ? a.dscl + row * KB + kb : zero);
+    const uint8_t *sp = ok ? a.dscl + row * KB + kb : zero;
+    const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(sp) & 3u;
+    L.s[j] = *reinterpret_cast<const uint32_t *>(sp - mis);  // (pointer arithmetic keeps it a global load)
+    L.sh[j] = mis * 8u;
   }
 }
 
 // The activated h rows (B operand) of a down item: token chunk c of active expert d.
-__device__ __forceinline__ void dn_issue_h(const Plan &pl, const uint16_t *hbuf, const int *g_aoff,
-                                           const int *g_acnt, int d, int c, int kc, int KB, DnLoad &L) {
+__device__ __forceinline__ void dn_issue_h(const Plan &pl, const uint16_t *hbuf, const uint8_t *zero,
+                                           const int *g_aoff, const int *g_acnt, int d, int c, int kc, int KB,
+                                           DnLoad &L) {
   const int l = threadIdx.x & 63, i = l & 15, q = l >> 4;
   const int p0 = g_aoff[d], n = g_acnt[d];
   const int pj = c * 16 + i;
@@ -620,9 +669,11 @@ __device__ __forceinline__ void dn_issue_h(const Plan &pl, const uint16_t *hbuf,
   for (int j = 0; j < kDnDepth; ++j) {
     const int kb = (kc + j) * 4 + q;
     const bool ok = kc + j < pl.KSd && kb < KB;
+    // out-of-range lanes read the zero area rather than skip the load: a
+    // skipped load is joined by a copy that waits for it at once
+    const uint8_t *src = (ok && tok_ok) ? reinterpret_cast<const uint8_t *>(hr + kb * kBlockK) : zero;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      L.b[j][kk] = (ok && tok_ok) ? load16(hr + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
+    for (int kk = 0; kk < 4; ++kk) L.b[j][kk] = load16(src + kk * 16);
   }
 }
 
@@ -648,7 +699,7 @@ __device__ __forceinline__ void dn_issue(const Plan &pl, const DecodeArgs &a, co
                                          const uint8_t *zero, const int *g_act, const int *g_aoff,
                                          const int *g_acnt, int rt, int d, int c, int kc, int KB, DnLoad &L) {
   dn_issue_w(pl, a, zero, g_act, rt, d, kc, KB, L);
-  dn_issue_h(pl, hbuf, g_aoff, g_acnt, d, c, kc, KB, L);
+  dn_issue_h(pl, hbuf, zero, g_aoff, g_acnt, d, c, kc, KB, L);
 }
 
 static_assert(sizeof(Plan) % alignof(DecodeArgs) == 0, "DecodeArgs follows Plan in the argument segment");
@@ -706,7 +757,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   __shared__ int s_round[2], s_rowtok[16];
   __shared__ __attribute__((aligned(16))) int s_prog[kDecWaves];
 
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int tid = threadIdx.x, w = wave_id(), l = tid & 63;
   const int i = l & 15, q = l >> 4;
   unsigned *ctl = reinterpret_cast<unsigned *>(a.ws + pl.o_ctl);
   float *part = reinterpret_cast<float *>(a.ws + pl.o_logit);
@@ -750,7 +801,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     if (c0 == pc0 && c1 > pc0 && c1 - pc0 < (1u << 20)) {
       const uint64_t lo = pc0 & ~(uint64_t)1023;
       const uint64_t addr = lo + (uint64_t)((blockIdx.x >> 3) + 32 * w) * 1024 + l * 16;
-      if (addr + 16 <= c1) code_probe = *reinterpret_cast<const volatile u32x4 *>(addr);
+      // one unconditional global load (a conditional one would be joined by a
+      // copy that waits for it at once); out of range, the kernel's own first bytes
+      const uint64_t at = addr + 16 <= c1 ? addr : (pc0 & ~(uint64_t)15);
+      code_probe = *reinterpret_cast<const __attribute__((address_space(1))) u32x4 *>(at);
     }
   };
 
@@ -943,8 +997,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       const bool coop2 = nt == 1 && !coop && E <= 2 * kDecWaves * 64 && k <= 32;
       for (int tg = 0; tg < nt; tg += kDecWaves) {
         if (coop2) {
-          uint64_t *cand = reinterpret_cast<uint64_t *>(
-              (reinterpret_cast<uintptr_t>(sel + kDecWaves * kMaxTopk) + 7) & ~(uintptr_t)7);  // [8][32]
+          uint64_t *cand = lds_align8(sel + kDecWaves * kMaxTopk);  // [8][32]
           const int e0 = w * 64 + l, e1 = (w + kDecWaves) * 64 + l;
           uint64_t v0 = e0 < E ? ((uint64_t)kyl[e0] << 32) | (uint32_t)~e0 : 0ull;
           uint64_t v1 = e1 < E ? ((uint64_t)kyl[e1] << 32) | (uint32_t)~e1 : 0ull;
@@ -965,8 +1018,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
           }
         }
         if (coop) {
-          uint64_t *cand = reinterpret_cast<uint64_t *>(
-              (reinterpret_cast<uintptr_t>(sel + kDecWaves * kMaxTopk) + 7) & ~(uintptr_t)7);  // [8 k]
+          uint64_t *cand = lds_align8(sel + kDecWaves * kMaxTopk);  // [8 k]
           const int e = w * 64 + l;
           uint64_t v = e < E ? ((uint64_t)kyl[e] << 32) | (uint32_t)~e : 0ull;
           v = wave_top8_desc(v);
@@ -1291,7 +1343,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
         for (int j = 0; j < kDnDepth; ++j) {
           if (j >= pl.KSd) break;
           bf16x8 av[4];
-          convert_block_fast(pf[tt].w[j], pf[tt].s[j], av);
+          convert_block_fast(pf[tt].w[j], dn_scale(pf[tt], j), av);  // the weights were loaded before the wait
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) acc[tt] = mfma16(av[kk], as_bf16x8(pf[0].b[j][kk]), acc[tt]);
         }
@@ -1332,50 +1384,65 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     // order with the next item's loads in flight while the current one runs,
     // across row tiles too (the next row tile's first item is issued before
     // the current one's reduction).
-    DnLoad cur, nxt;
-    bool prefetched = false;
-    for (int rt = blockIdx.x; rt < pl.RTd; rt += gridDim.x) {
-      int d = da, c = 0, kc = 0;
-      if (d < db && !prefetched) dn_issue(pl, a, hbuf, zero, g_act, g_aoff, g_acnt, rt, d, c, kc, KB, cur);
-      prefetched = false;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      while (d < db) {
-        int nd = d, nc = c, nkc = kc + kDnDepth;
-        if (nkc >= pl.KSd) {
-          nkc = 0;
-          if (++nc * 16 >= g_acnt[d]) {
-            nc = 0;
-            ++nd;
-          }
+    // Two load buffers in turn (a copy of the next item's registers into the
+    // current one would wait for its loads). The wave's item list of a row
+    // tile is padded to an even length n2 with a filler (k-step KSd:
+    // zero-area reads), so a tile starts with its first item in L0 and the
+    // loop over item pairs has one exit: a path that re-enters the loop from
+    // an exit test makes the compiler wait on the buffer being reissued.
+    // `item` runs item `it` (loaded in X) and issues item it + 1 into Y: the
+    // wave's next item, the filler, the next row tile's first item, or an
+    // empty one. Every k-step is computed, those past KSd on zero-area
+    // operands that add zero: a load left unread keeps its register busy.
+    const int ksi = (pl.KSd + kDnDepth - 1) / kDnDepth;
+    int n = 0;
+    for (int d = da; d < db; ++d) n += (g_acnt[d] + 15) / 16 * ksi;
+    n = __builtin_amdgcn_readfirstlane(n);
+    const int n2 = (n + 1) & ~1;
+    DnLoad L0, L1;
+    auto item = [&](DnLoad &X, DnLoad &Y, int rt, int it, int &d, int &c, int &kc, f32x4 &acc) {
+      int nd = d, nc = c, nkc = kc + kDnDepth;
+      if (nkc >= pl.KSd) {
+        nkc = 0;
+        if (++nc * 16 >= g_acnt[d]) {
+          nc = 0;
+          ++nd;
         }
-        if (nd < db) {
-          dn_issue(pl, a, hbuf, zero, g_act, g_aoff, g_acnt, rt, nd, nc, nkc, KB, nxt);
-        } else if (rt + (int)gridDim.x < pl.RTd) {
-          dn_issue(pl, a, hbuf, zero, g_act, g_aoff, g_acnt, rt + gridDim.x, da, 0, 0, KB, nxt);
-          prefetched = true;
-        }
+      }
+      const bool more = it + 1 < n, filler = !more && it + 1 < n2;
+      const bool next_rt = !more && !filler && rt + (int)gridDim.x < pl.RTd;
+      dn_issue(pl, a, hbuf, zero, g_act, g_aoff, g_acnt, next_rt ? rt + (int)gridDim.x : rt, more ? nd : da,
+               more ? nc : 0, more ? nkc : (next_rt ? 0 : pl.KSd), KB, Y);
 #pragma unroll
-        for (int j = 0; j < kDnDepth; ++j) {
-          if (kc + j >= pl.KSd) break;
-          bf16x8 av[4];
-          convert_block_fast(cur.w[j], cur.s[j], av);
+      for (int j = 0; j < kDnDepth; ++j) {
+        bf16x8 av[4];
+        convert_block_fast(X.w[j], dn_scale(X, j), av);
 #pragma unroll
-          for (int kk = 0; kk < 4; ++kk) acc = mfma16(av[kk], as_bf16x8(cur.b[j][kk]), acc);
+        for (int kk = 0; kk < 4; ++kk) acc = mfma16(av[kk], as_bf16x8(X.b[j][kk]), acc);
+      }
+      if (it < n && nkc == 0) {  // (d, c) complete: w * bf16(y) of its pairs
+        const int p0 = g_aoff[d], pj = c * 16 + i;
+        if (pj < g_acnt[d]) {
+          const float wt = g_pw[p0 + pj];
+          *reinterpret_cast<f32x4 *>(pv + (p0 + pj) * 16 + 4 * q) =
+              f32x4{__fmul_rn(round_bf16(acc[0]), wt), __fmul_rn(round_bf16(acc[1]), wt),
+                    __fmul_rn(round_bf16(acc[2]), wt), __fmul_rn(round_bf16(acc[3]), wt)};
         }
-        if (nkc == 0) {  // (d, c) complete: w * bf16(y) of its pairs
-          const int p0 = g_aoff[d], pj = c * 16 + i;
-          if (pj < g_acnt[d]) {
-            const float wt = g_pw[p0 + pj];
-            *reinterpret_cast<f32x4 *>(pv + (p0 + pj) * 16 + 4 * q) =
-                f32x4{__fmul_rn(round_bf16(acc[0]), wt), __fmul_rn(round_bf16(acc[1]), wt),
-                      __fmul_rn(round_bf16(acc[2]), wt), __fmul_rn(round_bf16(acc[3]), wt)};
-          }
-          acc = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-        cur = nxt;
+        acc = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      if (more) {
         d = nd;
         c = nc;
         kc = nkc;
+      }
+    };
+    if (n > 0) dn_issue(pl, a, hbuf, zero, g_act, g_aoff, g_acnt, blockIdx.x, da, 0, 0, KB, L0);
+    for (int rt = blockIdx.x; rt < pl.RTd; rt += gridDim.x) {
+      int d = da, c = 0, kc = 0;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int it = 0; it < n2; it += 2) {
+        item(L0, L1, rt, it, d, c, kc, acc);
+        item(L1, L0, rt, it + 1, d, c, kc, acc);
       }
       __syncthreads();
       for (int j = tid; j < B * 16; j += kDecThreads) {

@@ -28,6 +28,11 @@ constexpr int kBlockK = 32;  // MXFP4 block (quantization.py:10)
 constexpr int kStepK = 128;  // k covered by one k-step of a wave
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
+// The wave's index in the workgroup, as a value the compiler knows to be
+// wave-uniform: loops and branches on it then use scalar control flow rather
+// than exec-mask loops (whose merged paths also make the wait counts of the
+// loads in them conservative).
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); }
 
 // ---------------------------------------------------------------- bf16 bits --
 

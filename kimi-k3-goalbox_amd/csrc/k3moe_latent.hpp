@@ -199,7 +199,7 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
   float *red = reinterpret_cast<float *>(lds + pl.lds_x);          // [parts][TT][8 waves][256]
   __shared__ float s_wsum[kLatWaves];
 
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int tid = threadIdx.x, w = wave_id(), l = tid & 63;
   const int i = l & 15, q = l >> 4;
   const int B = pl.B, TT = pl.TT, SP = pl.SP;
   const int lsp = __builtin_ctz(SP), lstep = __builtin_ctz(gridDim.x) - lsp;  // SP and the grid are powers of two

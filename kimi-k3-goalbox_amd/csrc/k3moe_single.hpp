@@ -94,7 +94,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   __shared__ uint32_t s_tag, s_abort0;
   __shared__ int s_fail;
 
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i = l & 15, q = l >> 4;
+  const int tid = threadIdx.x, w = wave_id(), l = tid & 63, i = l & 15, q = l >> 4;
   unsigned *ctl = reinterpret_cast<unsigned *>(a.ws + pl.o_ctl);
   char *tag_area = a.ws + kOffTag;
   const __amdgpu_buffer_rsrc_t tagr = make_rsrc(tag_area, kTagBytes);
@@ -163,7 +163,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     if (c0 == pc0 && c1 > pc0 && c1 - pc0 < (1u << 20)) {
       const uint64_t lo = pc0 & ~(uint64_t)1023;
       const uint64_t addr = lo + (uint64_t)((blockIdx.x >> 3) + 32 * w) * 1024 + l * 16;
-      if (addr + 16 <= c1) code_probe = *reinterpret_cast<const volatile u32x4 *>(addr);
+      const uint64_t at = addr + 16 <= c1 ? addr : (pc0 & ~(uint64_t)15);  // unconditional (see k_moe_decode)
+      code_probe = *reinterpret_cast<const __attribute__((address_space(1))) u32x4 *>(at);
     }
   };
 
@@ -466,14 +467,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
                               : u32x4{0, 0, 0, 0};
     }
     const float wt = sh.wts[w];
-    // The down scale bytes enter here, after the h poll: the compiler would
-    // otherwise convert them right where they are loaded and wait there for
-    // the loads, which are meant to arrive while h is exchanged.
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-      for (int jj = 0; jj < kDnDepth; ++jj) asm volatile("" : "+v"(pf[tt].s[jj]));
-    }
+    // The down scale bytes are taken apart only here, after the h poll
+    // (dn_scale): the compiler would otherwise convert them right where they
+    // are loaded and wait there for the loads, which are meant to arrive
+    // while h is exchanged.
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -481,7 +478,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
       for (int jj = 0; jj < kDnDepth; ++jj) {
         if (jj >= pl.KSd) break;
         bf16x8 av[4];
-        convert_block_fast(pf[tt].w[jj], pf[tt].s[jj], av);
+        convert_block_fast(pf[tt].w[jj], dn_scale(pf[tt], jj), av);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) acc = mfma16(av[kk], as_bf16x8(hb[jj][kk]), acc);
       }
