@@ -61,6 +61,7 @@ extern "C" {
 /* Element type codes. */
 #define K3MOE_DTYPE_BF16 0
 #define K3MOE_DTYPE_F32 1
+#define K3MOE_DTYPE_F16 2 /* accepted by k3moe_mxfp4_encode only */
 
 /* Geometry and options of one MoE step.
  *   tokens   B: rows of x (and of latent)
@@ -264,6 +265,19 @@ int k3moe_latent_out(const k3moe_latent_dims *dims, const float *expert_sum, con
  * bit-exact including -0.0, subnormal results and NaN for scale 255. */
 int k3moe_mxfp4_decode(const uint8_t *blocks, const uint8_t *scales, int64_t n_blocks,
                        int32_t out_dtype, void *out, void *stream);
+
+/* MXFP4 encode, pack_mxfp4 (megabench/tasks/quantization.py:13-37): n_blocks
+ * groups of 32 consecutive values of in_dtype (K3MOE_DTYPE_F32, _BF16 or
+ * _F16; in 16-byte aligned for f32, 8-byte for the others) -> n_blocks blocks
+ * of 16 bytes (byte j: element 2j in the low nibble, 2j+1 in the high one;
+ * blocks 2-byte aligned) and n_blocks E8M0 scale bytes. Bit for bit with the
+ * reference's torch CPU chain: block exponent ceil(log2(max|x|/6)) with the
+ * fp32 logarithm rounded to nearest (clamped to [-126, 127]), fp32 products
+ * x 2^-e, round to nearest with ties to the even code; a block holding a NaN
+ * gets scale byte 127, code 7 for its NaN and infinite elements and 0 for
+ * the rest (torch's result on x86). */
+int k3moe_mxfp4_encode(const void *in, int32_t in_dtype, int64_t n_blocks, uint8_t *blocks,
+                       uint8_t *scales, void *stream);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char *k3moe_last_error(void);

@@ -17,6 +17,7 @@
 #include <string.h>
 
 #include "k3moe.h"
+#include "k3moe_codec.hpp"
 #include "k3moe_decode.hpp"
 #include "k3moe_device.hpp"
 #include "k3moe_general.hpp"
@@ -472,6 +473,24 @@ int k3moe_mxfp4_decode(const uint8_t *blocks, const uint8_t *scales, int64_t n_b
   hipLaunchKernelGGL(k_decode, dim3((unsigned)grid), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), blocks,
                      scales, n_blocks, out_dtype, out);
   return launch_check("decode");
+}
+
+int k3moe_mxfp4_encode(const void *in, int32_t in_dtype, int64_t n_blocks, uint8_t *blocks, uint8_t *scales,
+                       void *stream) {
+  g_err[0] = 0;
+  if (n_blocks < 0) return fail(K3MOE_EINVAL, "n_blocks must be >= 0");
+  if (in_dtype != K3MOE_DTYPE_F32 && in_dtype != K3MOE_DTYPE_BF16 && in_dtype != K3MOE_DTYPE_F16)
+    return fail(K3MOE_EINVAL, "in_dtype must be f32, bf16 or f16, got %d", in_dtype);
+  if (n_blocks == 0) return K3MOE_OK;
+  if (!in || !blocks || !scales) return fail(K3MOE_EINVAL, "a required pointer is NULL");
+  const uintptr_t align = in_dtype == K3MOE_DTYPE_F32 ? 16 : 8;
+  if (reinterpret_cast<uintptr_t>(in) % align || reinterpret_cast<uintptr_t>(blocks) % 2)
+    return fail(K3MOE_EINVAL, "in must be %d-byte aligned and blocks 2-byte aligned", (int)align);
+  long grid = (long)((n_blocks + kEncThreads / 8 - 1) / (kEncThreads / 8));
+  if (grid > 16384) grid = 16384;
+  hipLaunchKernelGGL(k_encode, dim3((unsigned)grid), dim3(kEncThreads), 0, reinterpret_cast<hipStream_t>(stream), in,
+                     in_dtype, n_blocks, blocks, scales);
+  return launch_check("encode");
 }
 
 int k3moe_moe_step_noalloc(const k3moe_dims *dims, const void *x, const void *latent, const void *router,

@@ -19,7 +19,7 @@ LIB_PATH = os.path.join(HERE, 'libk3moe.so')
 K3MOE_OK = 0
 GATING = {'sigmoid_bias': 0, 'softmax': 1}
 ACTIVATION = {'situ': 0, 'silu': 1}
-DTYPE_BF16, DTYPE_F32 = 0, 1
+DTYPE_BF16, DTYPE_F32, DTYPE_F16 = 0, 1, 2
 PATH = {'auto': 0, 'general': 1, 'decode': 2, 'grouped': 3, 'streamed': 4, 'single': 5}
 
 
@@ -49,7 +49,7 @@ STATUS_TIMEOUT, STATUS_ROUTES = 1, 2
 EXPORTS = ('k3moe_workspace_bytes', 'k3moe_workspace_init', 'k3moe_workspace_status', 'k3moe_moe_step',
            'k3moe_mxfp4_decode', 'k3moe_last_error', 'k3moe_version', 'k3moe_latent_workspace_bytes',
            'k3moe_latent_in', 'k3moe_latent_out', 'k3moe_workspace_layout',
-           'k3moe_moe_step_noalloc')
+           'k3moe_moe_step_noalloc', 'k3moe_mxfp4_encode')
 
 _lib = None
 
@@ -83,6 +83,8 @@ def load(path: str | None = None):
     lib.k3moe_workspace_layout.restype = ctypes.c_int
     lib.k3moe_mxfp4_decode.argtypes = [p, p, i64, i32, p, p]
     lib.k3moe_mxfp4_decode.restype = ctypes.c_int
+    lib.k3moe_mxfp4_encode.argtypes = [p, i32, i64, p, p, p]
+    lib.k3moe_mxfp4_encode.restype = ctypes.c_int
     lib.k3moe_latent_workspace_bytes.argtypes = [ctypes.POINTER(LatentDims), ctypes.POINTER(sz)]
     lib.k3moe_latent_workspace_bytes.restype = ctypes.c_int
     lib.k3moe_latent_in.argtypes = [ctypes.POINTER(LatentDims)] + [p]*6 + [p, sz, p]

@@ -274,3 +274,35 @@ def mxfp4_decode(blocks: torch.Tensor, scales: torch.Tensor, dtype: torch.dtype 
                                                _dev_ptr(out), ctypes.c_void_p(stream))
         check(rc, 'k3moe_mxfp4_decode')
     return out
+
+
+_ENCODE_DTYPES = {torch.float32: 'DTYPE_F32', torch.bfloat16: 'DTYPE_BF16', torch.float16: 'DTYPE_F16'}
+
+
+def pack_mxfp4(matrix: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """pack_mxfp4 (quantization.py:13-37) on the GPU: groups of 32 along the last axis -> E2M1 + E8M0.
+
+    matrix [..., K] on a ROCm GPU (float32, bfloat16 or float16 read as they are; any other dtype
+    is first cast to float32, as the reference's ``matrix.float()``) -> packed u8 [..., K/32, 16]
+    (low nibble = even element), scales u8 [..., K/32], bit for bit with the reference's torch CPU
+    chain. Raises ValueError when K is not a multiple of 32, as the reference does.
+    """
+    if not isinstance(matrix, torch.Tensor):
+        raise ValueError('matrix must be a tensor')
+    if matrix.dim() == 0 or matrix.shape[-1] % MX_BLOCK:
+        raise ValueError('MXFP4 block axis must be divisible by 32')
+    if matrix.device.type != 'cuda':
+        raise ValueError('matrix must be on a ROCm GPU')
+    if matrix.dtype not in _ENCODE_DTYPES:
+        matrix = matrix.float()
+    src = matrix.contiguous()
+    lead, n = tuple(matrix.shape[:-1]), matrix.shape[-1] // MX_BLOCK
+    packed = torch.empty(*lead, n, MX_BLOCK // 2, dtype=torch.uint8, device=matrix.device)
+    scales = torch.empty(*lead, n, dtype=torch.uint8, device=matrix.device)
+    code = getattr(_native, _ENCODE_DTYPES[src.dtype])
+    with torch.cuda.device(matrix.device):
+        stream = torch.cuda.current_stream(matrix.device).cuda_stream
+        rc = _native.load().k3moe_mxfp4_encode(_dev_ptr(src), code, scales.numel(), _dev_ptr(packed),
+                                               _dev_ptr(scales), ctypes.c_void_p(stream))
+        check(rc, 'k3moe_mxfp4_encode')
+    return packed, scales
