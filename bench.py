@@ -502,22 +502,28 @@ def cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
-MFMA_BF16_DENSE_TFLOPS = 2500.0  # MI355X dense bf16 MFMA peak (the instruction type the GEMMs use)
+# MI355X dense MFMA peaks. The prefill step's grouped GEMMs run the scaled FP4 MFMA
+# (v_mfma_scale_f32_16x16x128_f8f6f4) at the FP8 rate, 5.0 PFLOP/s dense, twice per product (the
+# activations are two E4M3 terms): 2.5 PFLOP/s of useful FLOPs, the bf16 MFMA peak.
+MFMA_FP8_DENSE_TFLOPS = 5000.0
+MFMA_USEFUL_TFLOPS = MFMA_FP8_DENSE_TFLOPS / 2
 
 
 def roofline_entry(head, cfg, layers, measured, workload):
     """The roofline object of the JSON line: HBM for the decode-sized steps (one persistent kernel),
-    bf16 MFMA for the prefill step (grouped GEMMs; its HBM rate is given beside it)."""
+    MFMA for the prefill step (grouped GEMMs on the scaled FP4 MFMA; its HBM rate is given beside it)."""
     if workload == 'kimi-latent':
         return {'bound': 'hbm', 'kernel': 'k3moe::k_latent<0> + k3moe::k_moe_decode + k3moe::k_latent<1> '
                                           '(the whole block; per-kernel rates in per_batch stages)',
                 'achieved': head['hbm_GBps'], 'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac'],
                 'traffic': None}
     if workload == 'prefill':
-        return {'bound': 'mfma', 'kernel': 'k3moe::k_xgemm<gate/up> + k3moe::k_xgemm<down> (grouped GEMMs) '
-                                           'with the router, top-k, grouping and combine kernels',
-                'achieved': head['tflops'], 'peak': MFMA_BF16_DENSE_TFLOPS, 'unit': 'TFLOP/s',
-                'frac': round(head['tflops'] / MFMA_BF16_DENSE_TFLOPS, 4), 'traffic': None,
+        return {'bound': 'mfma', 'kernel': 'k3moe::k_fgemm<gate/up> + k3moe::k_fgemm<down> (grouped GEMMs on '
+                                           'v_mfma_scale_f32_16x16x128_f8f6f4: MXFP4 weights, two-term E4M3 '
+                                           'activations) with the router, top-k, grouping, split and combine kernels',
+                'achieved': head['tflops'], 'peak': MFMA_USEFUL_TFLOPS, 'unit': 'TFLOP/s',
+                'peak_note': 'useful FLOPs: FP8-rate MFMA (5.0 PFLOP/s dense) run twice per product',
+                'frac': round(head['tflops'] / MFMA_USEFUL_TFLOPS, 4), 'traffic': None,
                 'hbm': {'achieved': head['hbm_GBps'], 'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac']}}
     return {'bound': 'hbm', 'kernel': 'k3moe::k_moe_decode (the whole step, one launch)',
             'achieved': head['hbm_GBps'], 'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac'],

@@ -46,7 +46,11 @@ extern "C" {
  * once per 128 tokens of an expert) when the experts average at least 16
  * tokens and hidden/latent and inter are multiples of 128, and as per-16-token
  * streams otherwise; GROUPED and STREAMED force one of the two (GROUPED fails
- * with K3MOE_EINVAL when the widths are not multiples of 128). A single token
+ * with K3MOE_EINVAL when the widths are not multiples of 128). The grouped
+ * GEMMs run on the scaled FP4 MFMA (MXFP4 weights as stored, activations as
+ * two E4M3 terms with E8M0 block scales, which represent the bf16 values) when
+ * latent is a multiple of 512 and inter of 256, and on bf16 MFMA after an
+ * in-register decode otherwise; GROUPED_BF16 forces the latter. A single token
  * runs on its own persistent kernel when its shape fits (SINGLE below); AUTO
  * picks it then, DECODE forces the general persistent kernel. */
 #define K3MOE_PATH_AUTO 0
@@ -57,6 +61,7 @@ extern "C" {
 #define K3MOE_PATH_SINGLE 5 /* the single-token kernel (fails with K3MOE_EINVAL when the
                              * shape does not fit it: one token, topk <= 8, experts <= 512,
                              * latent a multiple of 512 up to 8192, inter <= 256) */
+#define K3MOE_PATH_GROUPED_BF16 6 /* grouped GEMMs on bf16 MFMA (same conditions as GROUPED) */
 
 /* Element type codes. */
 #define K3MOE_DTYPE_BF16 0
@@ -161,6 +166,11 @@ int k3moe_moe_step_noalloc(const k3moe_dims *dims,
  *   pair_of       int32 [B k]    pair of (token t, slot j), slots in expert_ids order
  *   pair_h        bf16  [B k, I] each pair's activation output, cast(act(gate, up))
  *   pair_y        bf16  [B k, K] each pair's down projection, cast(h @ down.T)
+ *   input_split   the FP4-MFMA grouped GEMMs' expert inputs as two E4M3 terms:
+ *                 hi u8 [B, K], lo u8 [B, K], then their E8M0 block scales
+ *                 hi u8 [B, K/32], lo u8 [B, K/32] (-1 on other paths)
+ *   h_split       h in the same form: [B k, I] twice, then [B k, I/32] twice
+ *                 (-1 on other paths; pair_h is then -1 too: h is kept only split)
  * The persistent decode path keeps its grouping in LDS; for dims that select
  * it this returns K3MOE_EINVAL. */
 typedef struct k3moe_layout {
@@ -173,6 +183,8 @@ typedef struct k3moe_layout {
     int64_t pair_of;
     int64_t pair_h;
     int64_t pair_y;
+    int64_t input_split;
+    int64_t h_split;
 } k3moe_layout;
 
 int k3moe_workspace_layout(const k3moe_dims *dims, k3moe_layout *layout);

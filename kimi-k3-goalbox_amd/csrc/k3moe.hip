@@ -20,6 +20,7 @@
 #include "k3moe_codec.hpp"
 #include "k3moe_decode.hpp"
 #include "k3moe_device.hpp"
+#include "k3moe_fgemm.hpp"
 #include "k3moe_general.hpp"
 #include "k3moe_latent.hpp"
 #include "k3moe_plan.hpp"
@@ -66,8 +67,9 @@ int check_dims(const k3moe_dims *d) {
   if (d->activation != K3MOE_ACT_SITU && d->activation != K3MOE_ACT_SILU)
     return fail(K3MOE_EINVAL, "unknown activation %d", d->activation);
   if (d->x_dtype != K3MOE_DTYPE_BF16) return fail(K3MOE_EINVAL, "x_dtype must be bf16 (%d)", K3MOE_DTYPE_BF16);
-  if (d->path < K3MOE_PATH_AUTO || d->path > K3MOE_PATH_SINGLE) return fail(K3MOE_EINVAL, "unknown path %d", d->path);
-  if (d->path == K3MOE_PATH_GROUPED && (d->latent % 128 || d->inter % 128))
+  if (d->path < K3MOE_PATH_AUTO || d->path > K3MOE_PATH_GROUPED_BF16)
+    return fail(K3MOE_EINVAL, "unknown path %d", d->path);
+  if ((d->path == K3MOE_PATH_GROUPED || d->path == K3MOE_PATH_GROUPED_BF16) && (d->latent % 128 || d->inter % 128))
     return fail(K3MOE_EINVAL, "the grouped GEMM path needs latent (%d) and inter (%d) multiples of 128", d->latent,
                 d->inter);
   if ((long)d->tokens * d->topk > (1L << 30)) return fail(K3MOE_EINVAL, "tokens*topk too large");
@@ -150,6 +152,13 @@ int allow_xgemm_lds() {
   static int granted_gu = 0, granted_dn = 0;
   int rc = grant_lds(reinterpret_cast<const void *>(&k_xgemm<true>), kXLds, granted_gu, "gate/up GEMM");
   if (!rc) rc = grant_lds(reinterpret_cast<const void *>(&k_xgemm<false>), kXLds, granted_dn, "down GEMM");
+  return rc;
+}
+
+int allow_fgemm_lds() {
+  static int granted_gu = 0, granted_dn = 0;
+  int rc = grant_lds(reinterpret_cast<const void *>(&k_fgemm<true>), kFLds, granted_gu, "FP4 gate/up GEMM");
+  if (!rc) rc = grant_lds(reinterpret_cast<const void *>(&k_fgemm<false>), kFLds, granted_dn, "FP4 down GEMM");
   return rc;
 }
 
@@ -296,8 +305,11 @@ int k3moe_workspace_layout(const k3moe_dims *dims, k3moe_layout *layout) {
   layout->pair_token = (int64_t)p.o_ptok;
   layout->pair_weight = (int64_t)p.o_pw;
   layout->pair_of = (int64_t)p.o_pof;
-  layout->pair_h = (int64_t)p.o_h;
+  const bool split = p.fgemm && p.xgemm;
+  layout->pair_h = split ? -1 : (int64_t)p.o_h;
   layout->pair_y = (int64_t)p.o_y;
+  layout->input_split = split ? (int64_t)p.o_xq : -1;
+  layout->h_split = split ? (int64_t)p.o_hq : -1;
   return K3MOE_OK;
 }
 
@@ -383,16 +395,40 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
     return launch_check("decode step");
   }
 
-  const int nr = p.RTr * p.TTr * p.Sr;
-  hipLaunchKernelGGL(k_router, dim3(cdiv(nr, kWavesPerBlock)), dim3(kThreads), 0, st, p,
-                     reinterpret_cast<const uint16_t *>(x), reinterpret_cast<const uint16_t *>(router), ws);
+  const int nr = cdiv(p.B, kRM) * cdiv(p.E, kRExperts) * p.Sr;
+  hipLaunchKernelGGL(k_router, dim3(nr), dim3(kRWaves * 64), 0, st, p, reinterpret_cast<const uint16_t *>(x),
+                     reinterpret_cast<const uint16_t *>(router), ws);
   if ((rc = launch_check("router"))) return rc;
   hipLaunchKernelGGL(k_topk, dim3(cdiv(p.B, kWavesPerBlock)), dim3(kThreads), 0, st, p, router_bias, routes, ws,
                      expert_ids, route_weights, shortfall);
   if ((rc = launch_check("topk"))) return rc;
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, st, p, ws);
-  if ((rc = launch_check("group"))) return rc;
-  if (p.xgemm) {  // many tokens per expert: grouped GEMMs, weights read once per 128 tokens
+  const int nch = cdiv(p.B, kGroupChunk);
+  hipLaunchKernelGGL(k_group_count, dim3(nch), dim3(256), 0, st, p, ws);
+  if ((rc = launch_check("group count"))) return rc;
+  hipLaunchKernelGGL(k_group_scan, dim3(1), dim3(1024), 0, st, p, ws);
+  if ((rc = launch_check("group scan"))) return rc;
+  hipLaunchKernelGGL(k_group_place, dim3(nch), dim3(256), 0, st, p, ws);
+  if ((rc = launch_check("group place"))) return rc;
+  if (p.fgemm) {  // many tokens per expert: grouped GEMMs on the scaled FP4 MFMA
+    if ((rc = allow_fgemm_lds())) return rc;
+    uint8_t *xq = reinterpret_cast<uint8_t *>(ws + p.o_xq);
+    const long nxb = (long)p.B * (p.K / kBlockK);
+    MxAct ax{xq, xq + (size_t)p.B * p.K, xq + (size_t)2 * p.B * p.K, xq + (size_t)2 * p.B * p.K + nxb, p.K};
+    long qg = (nxb + 31) / 32;
+    if (qg > 8192) qg = 8192;
+    hipLaunchKernelGGL(k_quant, dim3((unsigned)qg), dim3(256), 0, st, xin, nxb, const_cast<uint8_t *>(ax.hi),
+                       const_cast<uint8_t *>(ax.lo), const_cast<uint8_t *>(ax.shi), const_cast<uint8_t *>(ax.slo));
+    if ((rc = launch_check("activation split"))) return rc;
+    hipLaunchKernelGGL(k_fgemm<true>, dim3(p.G), dim3(kFThreads), kFLds, st, p, ax, gate_blocks, gate_scales, up_blocks,
+                       up_scales, ws);
+    if ((rc = launch_check("FP4 gate/up GEMM"))) return rc;
+    const uint8_t *hq = reinterpret_cast<const uint8_t *>(ws + p.o_hq);
+    const size_t nh = (size_t)p.P * p.I;
+    MxAct ah{hq, hq + nh, hq + 2 * nh, hq + 2 * nh + (size_t)p.P * (p.I / kBlockK), p.I};
+    hipLaunchKernelGGL(k_fgemm<false>, dim3(p.G), dim3(kFThreads), kFLds, st, p, ah, down_blocks, down_scales, nullptr,
+                       nullptr, ws);
+    if ((rc = launch_check("FP4 down GEMM"))) return rc;
+  } else if (p.xgemm) {  // grouped GEMMs on bf16 MFMA, weights decoded in registers
     if ((rc = allow_xgemm_lds())) return rc;
     hipLaunchKernelGGL(k_xgemm<true>, dim3(p.G), dim3(kXThreads), kXLds, st, p, xin, gate_blocks, gate_scales,
                        up_blocks, up_scales, ws);
@@ -410,7 +446,7 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
                        ws);
     if ((rc = launch_check("down"))) return rc;
   }
-  const long nc = (long)p.B * (p.K / 4);
+  const long nc = (long)p.B * (p.K / 8);
   hipLaunchKernelGGL(k_combine, dim3(cdiv(nc, 256)), dim3(256), 0, st, p, ws, expert_sum);
   return launch_check("combine");
 }

@@ -2,7 +2,7 @@
 //
 //   k_router   router logits x . router^T on MFMA, split over k      (kimi.py:308)
 //   k_topk     FP32 gating + top-k + renormalised weights, 1 wave/token (kimi.py:308-316)
-//   k_group    expert histogram, active-expert list, token->expert pairs (kimi.py:319-320)
+//   k_group_*  expert histogram, active-expert list, token->expert pairs (kimi.py:319-320)
 //   k_gateup   gate and up projections of every active expert, FP4 dequant in
 //              registers, MFMA, activation epilogue -> bf16 h          (kimi.py:321-322)
 //   k_down     down projection of every active expert -> bf16 y       (kimi.py:322)
@@ -23,40 +23,118 @@ __device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib)
   return ia < ib;
 }
 
-// Router logits: partial[s][t][e] = sum over k-split s of x[t] . router[e].
-// Wave item = (k split, router row tile, token tile).
-__global__ __launch_bounds__(kThreads) void k_router(Plan pl, const uint16_t *__restrict__ x,
-                                                      const uint16_t *__restrict__ router, char *ws) {
-  const int wave = threadIdx.x / kWave, l = threadIdx.x % kWave;
-  const int item = blockIdx.x * kWavesPerBlock + wave;
-  if (item >= pl.RTr * pl.TTr * pl.Sr) return;
-  const int s = item % pl.Sr;
-  const int rest = item / pl.Sr;
-  const int rt = rest % pl.RTr, tt = rest / pl.RTr;
+// Router logits (kimi.py:308): partial[s][t][e] = sum over k-split s of
+// x[t] . router[e], fp32 accumulation (bf16 MFMA 16x16x32).
+// Workgroup tile = (kRM tokens, kRExperts experts, k split s): the tile's
+// token rows move through a ring of kRRing LDS slots (direct-to-LDS loads two
+// 128-k steps ahead; the 16-byte chunk c of row j at position c ^ (j & 15), so
+// the B reads of 16 lanes hit distinct banks), and each of the 4 waves streams
+// its kRTiles 16-expert row tiles from L2 / HBM straight to registers one step
+// ahead. The router (a few MB) is re-read once per token tile; x once.
+// Rows past E read the zero area; tokens past B stage zero rows.
+constexpr int kRM = 64;                         // tokens per workgroup tile
+constexpr int kRWaves = 4;
+constexpr int kRTiles = 6;                      // expert row tiles per wave
+constexpr int kRExperts = kRWaves * kRTiles * 16;  // 384 experts per workgroup tile
+constexpr int kRRing = 3;
+constexpr int kRSlot = kRM * 256;               // 64 token rows x 128 bf16
+constexpr int kRLds = kRRing * kRSlot;          // 49152 bytes
+
+__global__ __launch_bounds__(kRWaves * 64, 1) void k_router(Plan pl, const uint16_t *__restrict__ x,
+                                                            const uint16_t *__restrict__ router, char *ws) {
+  __shared__ __attribute__((aligned(16))) char lds[kRLds];
+  const int tid = threadIdx.x, l = tid & 63, i = l & 15, q = l >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int TT = cdiv(pl.B, kRM), EG = cdiv(pl.E, kRExperts);
+  const int tt = blockIdx.x % TT, eg = (blockIdx.x / TT) % EG, s = blockIdx.x / (TT * EG);
   const int ks0 = (int)((long)s * pl.KSr / pl.Sr), ks1 = (int)((long)(s + 1) * pl.KSr / pl.Sr);
-  const int i = l & 15, q = l >> 4;
-  const int row = rt * 16 + i, tok = tt * 16 + i;
-  const bool row_ok = row < pl.E, tok_ok = tok < pl.B;
-  const uint16_t *arow = router + (size_t)(row_ok ? row : 0) * pl.h;
-  const uint16_t *brow = x + (size_t)(tok_ok ? tok : 0) * pl.h;
   const int KB = pl.h / kBlockK;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int ks = ks0; ks < ks1; ++ks) {
-    const int kb = ks * 4 + q;
-    const bool ok = kb < KB;
-    u32x4 a[4], b[4];
+  const uint8_t *zero = reinterpret_cast<const uint8_t *>(ws + pl.o_zero);
+  // this wave's row tiles: experts eg * 384 + 96 w + 16 r + i
+  const int e0 = eg * kRExperts + w * kRTiles * 16;
+  const uint16_t *arow[kRTiles];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      a[kk] = (ok && row_ok) ? load16(arow + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
-      b[kk] = (ok && tok_ok) ? load16(brow + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) acc = mfma16(as_bf16x8(a[kk]), as_bf16x8(b[kk]), acc);
+  for (int r = 0; r < kRTiles; ++r) {
+    const int row = e0 + 16 * r + i;
+    arow[r] = row < pl.E ? router + (size_t)row * pl.h : nullptr;
   }
-  if (tok_ok) {
-    // lane holds rows (experts) rt*16 + 4q + v of token column i
-    float *dst = reinterpret_cast<float *>(ws + pl.o_logit) + ((size_t)s * pl.B + tok) * pl.Epad + rt * 16 + 4 * q;
-    *reinterpret_cast<f32x4 *>(dst) = acc;
+  // staging: wave w loads token rows 16 w .. 16 w + 15; lane L of load u covers
+  // row 16 w + 4 u + L / 16 at position L % 16
+  const uint16_t *xrow[4];
+  int xc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int r = 16 * w + 4 * u + (l >> 4), t = tt * kRM + r;
+    xc[u] = (l & 15) ^ (r & 15);
+    xrow[u] = t < pl.B ? x + (size_t)t * pl.h : nullptr;
+  }
+  auto issue_x = [&](int ks) {
+    char *base = lds + ((ks - ks0) % kRRing) * kRSlot;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = ks * 128 + 8 * xc[u];
+      const void *src = (xrow[u] && k < pl.h) ? (const void *)(xrow[u] + k) : (const void *)(zero + 16 * (l & 15));
+      load_lds<16>(src, base + (16 * w + 4 * u) * 256);
+    }
+  };
+  u32x4 av[2][kRTiles][4];
+  auto issue_a = [&](int ks, int sl) {
+    const int kb = ks * 4 + q;
+#pragma unroll
+    for (int r = 0; r < kRTiles; ++r)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        av[sl][r][kk] = (arow[r] && kb < KB) ? load16(arow[r] + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
+  };
+  f32x4 acc[kRTiles][kRM / 16];
+#pragma unroll
+  for (int r = 0; r < kRTiles; ++r)
+#pragma unroll
+    for (int t = 0; t < kRM / 16; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int NS = ks1 - ks0;
+  if (NS > 0) {
+    issue_x(ks0);
+    issue_a(ks0, 0);
+    if (NS > 1) issue_x(ks0 + 1);
+  }
+  static_assert(kRRing == 3, "the waits below follow this issue order");
+  // per step and wave the issue order is a(ks + 1) (4 kRTiles loads), then x(ks + 2) (4 loads)
+  for (int j0 = 0; j0 < NS; j0 += 2) {
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int j = j0 + sub, ks = ks0 + j;
+      if (j < NS) {
+        if (j + 1 < NS) wait_vm<4>(); else wait_vm<0>();
+        ring_barrier();  // everyone's x rows of step ks have landed; step ks - 1's slot is free
+        if (j + 1 < NS) issue_a(ks + 1, sub ^ 1);
+        if (j + 2 < NS) issue_x(ks + 2);
+        const char *base = lds + (j % kRRing) * kRSlot;
+#pragma unroll
+        for (int t = 0; t < kRM / 16; ++t) {
+          const int row = 16 * t + i;
+          u32x4 b[4];
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk)
+            b[kk] = *reinterpret_cast<const u32x4 *>(base + row * 256 + (((4 * q + kk) ^ (row & 15)) * 16));
+#pragma unroll
+          for (int r = 0; r < kRTiles; ++r)
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) acc[r][t] = mfma16(as_bf16x8(av[sub][r][kk]), as_bf16x8(b[kk]), acc[r][t]);
+        }
+      }
+    }
+  }
+  // lane (token column i, q) holds experts e0 + 16 r + 4q .. + 3
+  float *part = reinterpret_cast<float *>(ws + pl.o_logit);
+#pragma unroll
+  for (int t = 0; t < kRM / 16; ++t) {
+    const int tok = tt * kRM + 16 * t + i;
+    if (tok >= pl.B) continue;
+#pragma unroll
+    for (int r = 0; r < kRTiles; ++r) {
+      if (e0 + 16 * r >= pl.Epad) break;  // wave-uniform
+      *reinterpret_cast<f32x4 *>(part + ((size_t)s * pl.B + tok) * pl.Epad + e0 + 16 * r + 4 * q) = acc[r][t];
+    }
   }
 }
 
@@ -75,12 +153,12 @@ __global__ __launch_bounds__(kThreads) void k_topk(Plan pl, const float *__restr
   const float *part = reinterpret_cast<const float *>(ws + pl.o_logit);
   const int E = pl.E, k = pl.k;
   for (int e = l; e < E; e += kWave) {
-    float ps[4];
+    float ps[kMaxRouterSplits];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) ps[s] = s < pl.Sr ? part[((size_t)s * pl.B + t) * pl.Epad + e] : 0.f;
+    for (int s = 0; s < kMaxRouterSplits; ++s) ps[s] = s < pl.Sr ? part[((size_t)s * pl.B + t) * pl.Epad + e] : 0.f;
     float logit = ps[0];
 #pragma unroll
-    for (int s = 1; s < 4; ++s)
+    for (int s = 1; s < kMaxRouterSplits; ++s)
       if (s < pl.Sr) logit += ps[s];
     float score, kv;
     if (pl.gating == K3MOE_GATING_SIGMOID_BIAS) {
@@ -146,36 +224,52 @@ __global__ __launch_bounds__(kThreads) void k_topk(Plan pl, const float *__restr
   }
 }
 
-// Grouping by expert (kimi.py:319-320), one workgroup of 1024 threads:
-// histogram, active-expert list in ascending order, and pairs grouped by
-// expert with ascending token order inside an expert (placement by per-chunk
-// token bitmaps, so the layout is deterministic). Also clears the gate/up
-// split-k arrival counters for this step.
-__global__ __launch_bounds__(1024) void k_group(Plan pl, char *ws) {
+// Grouping by expert (kimi.py:319-320) in three kernels over chunks of
+// kGroupChunk tokens: the active experts ascending, each expert's pairs in a
+// contiguous range with its tokens ascending (the order of `nonzero`), so the
+// layout is deterministic.
+//   k_group_count  one workgroup per chunk: the chunk's expert histogram
+//                  (LDS atomics) -> cnt[chunk][e]
+//   k_group_scan   one workgroup: per expert the chunks' counts summed in
+//                  chunk order (exclusive prefix per chunk), then a scan over
+//                  the experts of the totals and of the active flags; writes
+//                  the active list, offsets and counts, and turns cnt into the
+//                  absolute first position of each (chunk, expert) run; clears
+//                  the gate/up split arrival counters for this step
+//   k_group_place  one workgroup per chunk: a pair's rank among its expert's
+//                  pairs in the chunk, from per-expert token bitmaps (popcounts
+//                  of the bits below it), gives its position
+__global__ __launch_bounds__(256) void k_group_count(Plan pl, char *ws) {
   __shared__ int s_cnt[kMaxExperts];
+  const int tid = threadIdx.x, c = blockIdx.x;
+  const int *ids = reinterpret_cast<const int *>(ws + pl.o_ids);
+  for (int e = tid; e < pl.E; e += 256) s_cnt[e] = 0;
+  __syncthreads();
+  const int p0 = c * kGroupChunk * pl.k, p1 = min(pl.P, (c + 1) * kGroupChunk * pl.k);
+  for (int p = p0 + tid; p < p1; p += 256) atomicAdd(&s_cnt[ids[p]], 1);
+  __syncthreads();
+  int *cnt = reinterpret_cast<int *>(ws + pl.o_gchunk) + (size_t)c * pl.E;
+  for (int e = tid; e < pl.E; e += 256) cnt[e] = s_cnt[e];
+}
+
+__global__ __launch_bounds__(1024) void k_group_scan(Plan pl, char *ws) {
   __shared__ int s_off[kMaxExperts];
   __shared__ int s_act[kMaxExperts];
-  __shared__ int s_cur[kMaxExperts];
-  __shared__ uint32_t s_bits[kMaxExperts * (kGroupChunk / 32)];
-  const int tid = threadIdx.x, nt = blockDim.x;
-  const int E = pl.E, k = pl.k;
-  const int *ids = reinterpret_cast<const int *>(ws + pl.o_ids);
-  const float *wts = reinterpret_cast<const float *>(ws + pl.o_w);
-  int *active = reinterpret_cast<int *>(ws + pl.o_active);
-  int *aoff = reinterpret_cast<int *>(ws + pl.o_aoff);
-  int *acnt = reinterpret_cast<int *>(ws + pl.o_acnt);
-  int *ptok = reinterpret_cast<int *>(ws + pl.o_ptok);
-  float *pw = reinterpret_cast<float *>(ws + pl.o_pw);
-  int *pof = reinterpret_cast<int *>(ws + pl.o_pof);
-  for (int e = tid; e < E; e += nt) s_cnt[e] = 0;
-  __syncthreads();
-  for (int p = tid; p < pl.P; p += nt) atomicAdd(&s_cnt[ids[p]], 1);
-  __syncthreads();
-  // inclusive Hillis-Steele scans of counts (s_off) and active flags (s_act);
+  const int tid = threadIdx.x, E = pl.E;
+  const int nch = cdiv(pl.B, kGroupChunk);
+  int *cnt = reinterpret_cast<int *>(ws + pl.o_gchunk);
+  // per expert: chunk counts -> exclusive prefixes (relative to the expert's first pair)
+  int total = 0;
+  if (tid < E)
+    for (int c = 0; c < nch; ++c) {
+      const int v = cnt[(size_t)c * E + tid];
+      cnt[(size_t)c * E + tid] = total;
+      total += v;
+    }
+  // inclusive Hillis-Steele scans of the totals (s_off) and active flags (s_act);
   // the block has exactly kMaxExperts threads, one per expert slot
-  const int c = tid < E ? s_cnt[tid] : 0;
-  s_off[tid] = c;
-  s_act[tid] = c > 0 ? 1 : 0;
+  s_off[tid] = total;
+  s_act[tid] = total > 0 ? 1 : 0;
   __syncthreads();
   for (int d = 1; d < kMaxExperts; d <<= 1) {
     const int vo = tid >= d ? s_off[tid - d] : 0;
@@ -186,50 +280,53 @@ __global__ __launch_bounds__(1024) void k_group(Plan pl, char *ws) {
     __syncthreads();
   }
   if (tid == kMaxExperts - 1) *reinterpret_cast<int *>(ws + pl.o_nact) = s_act[tid];
-  if (tid < E && c > 0) {
+  const int first = s_off[tid] - total;
+  if (tid < E && total > 0) {
     const int d = s_act[tid] - 1;  // exclusive index of this active expert
-    active[d] = tid;
-    aoff[d] = s_off[tid] - c;
-    acnt[d] = c;
+    reinterpret_cast<int *>(ws + pl.o_active)[d] = tid;
+    reinterpret_cast<int *>(ws + pl.o_aoff)[d] = first;
+    reinterpret_cast<int *>(ws + pl.o_acnt)[d] = total;
   }
-  if (tid < E) s_cur[tid] = s_off[tid] - c;
-  __syncthreads();
-  // stable placement, kGroupChunk tokens at a time
-  constexpr int W = kGroupChunk / 32;
-  for (int c0 = 0; c0 < pl.B; c0 += kGroupChunk) {
-    for (int i = tid; i < E * W; i += nt) s_bits[i] = 0;
-    __syncthreads();
-    const int n = min(kGroupChunk, pl.B - c0) * k;
-    for (int i = tid; i < n; i += nt) {
-      const int tl = i / k, t = c0 + tl;
-      const int e = ids[(size_t)t * k + (i % k)];
-      atomicOr(&s_bits[e * W + tl / 32], 1u << (tl % 32));
-    }
-    __syncthreads();
-    for (int i = tid; i < n; i += nt) {
-      const int tl = i / k, t = c0 + tl, slot = i % k;
-      const int e = ids[(size_t)t * k + slot];
-      int rank = 0;
-      for (int w = 0; w < W; ++w) {
-        const uint32_t bits = s_bits[e * W + w];
-        if (w < tl / 32) rank += __popc(bits);
-        else if (w == tl / 32) rank += __popc(bits & ((1u << (tl % 32)) - 1u));
-      }
-      const int pos = s_cur[e] + rank;
-      ptok[pos] = t;
-      pw[pos] = wts[(size_t)t * k + slot];
-      pof[(size_t)t * k + slot] = pos;
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += nt) {
-      int add = 0;
-      for (int w = 0; w < W; ++w) add += __popc(s_bits[e * W + w]);
-      s_cur[e] += add;
-    }
-    __syncthreads();
-  }
+  if (tid < E)
+    for (int c = 0; c < nch; ++c) cnt[(size_t)c * E + tid] += first;
   int *gcnt = reinterpret_cast<int *>(ws + pl.o_gcnt);
-  for (int i = tid; i < pl.Dmax * pl.RTg; i += nt) gcnt[i] = 0;
+  for (int i = tid; i < pl.Dmax * pl.RTg; i += 1024) gcnt[i] = 0;
+}
+
+__global__ __launch_bounds__(256) void k_group_place(Plan pl, char *ws) {
+  constexpr int W = kGroupChunk / 32;
+  __shared__ uint32_t s_bits[kMaxExperts * W];
+  const int tid = threadIdx.x, c = blockIdx.x, E = pl.E, k = pl.k;
+  const int *ids = reinterpret_cast<const int *>(ws + pl.o_ids);
+  const float *wts = reinterpret_cast<const float *>(ws + pl.o_w);
+  const int *pos0 = reinterpret_cast<const int *>(ws + pl.o_gchunk) + (size_t)c * E;
+  int *ptok = reinterpret_cast<int *>(ws + pl.o_ptok);
+  float *pw = reinterpret_cast<float *>(ws + pl.o_pw);
+  int *pof = reinterpret_cast<int *>(ws + pl.o_pof);
+  for (int i = tid; i < E * W; i += 256) s_bits[i] = 0;
+  __syncthreads();
+  const int c0 = c * kGroupChunk, n = min(kGroupChunk, pl.B - c0) * k;
+  for (int i = tid; i < n; i += 256) {
+    const int tl = i / k;
+    const int e = ids[(size_t)c0 * k + i];
+    atomicOr(&s_bits[e * W + tl / 32], 1u << (tl % 32));
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += 256) {
+    const int tl = i / k, t = c0 + tl;
+    const int e = ids[(size_t)c0 * k + i];
+    int rank = 0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const uint32_t bits = s_bits[e * W + w];
+      if (w < tl / 32) rank += __popc(bits);
+      else if (w == tl / 32) rank += __popc(bits & ((1u << (tl % 32)) - 1u));
+    }
+    const int pos = pos0[e] + rank;
+    ptok[pos] = t;
+    pw[pos] = wts[(size_t)c0 * k + i];
+    pof[(size_t)c0 * k + i] = pos;
+  }
 }
 
 // Gate/up epilogue for one lane: rows r0 .. r0+3 of token pair p.
@@ -395,26 +492,30 @@ __global__ __launch_bounds__(kThreads) void k_down(Plan pl, const uint8_t *__res
 
 // Weighted combine (kimi.py:318,323): expert_sum[t] = sum over the token's
 // experts in ascending id order of float(y) * w, each product rounded to
-// FP32 before the FP32 add, starting from zero.
+// FP32 before the FP32 add, starting from zero. One thread per 8 columns
+// (16-byte y loads, two 16-byte stores); K % 8 == 0.
 __global__ __launch_bounds__(256) void k_combine(Plan pl, char *ws, float *__restrict__ out) {
-  const int K4 = pl.K / 4;
+  const int K8 = pl.K / 8;
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (long)pl.B * K4) return;
-  const int t = (int)(idx / K4), c = (int)(idx % K4) * 4;
+  if (idx >= (long)pl.B * K8) return;
+  const int t = (int)(idx / K8), c = (int)(idx % K8) * 8;
   const int *pof = reinterpret_cast<const int *>(ws + pl.o_pof);
   const float *wts = reinterpret_cast<const float *>(ws + pl.o_w);
   const uint16_t *ybuf = reinterpret_cast<const uint16_t *>(ws + pl.o_y);
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < pl.k; ++s) {
     const int p = pof[(size_t)t * pl.k + s];
     const float w = wts[(size_t)t * pl.k + s];
-    const u32x2 yv = *reinterpret_cast<const u32x2 *>(ybuf + (size_t)p * pl.K + c);
-    acc[0] = __fadd_rn(acc[0], __fmul_rn(bf16_bits_to_f32(yv[0] & 0xFFFFu), w));
-    acc[1] = __fadd_rn(acc[1], __fmul_rn(bf16_bits_to_f32(yv[0] >> 16), w));
-    acc[2] = __fadd_rn(acc[2], __fmul_rn(bf16_bits_to_f32(yv[1] & 0xFFFFu), w));
-    acc[3] = __fadd_rn(acc[3], __fmul_rn(bf16_bits_to_f32(yv[1] >> 16), w));
+    const u32x4 yv = *reinterpret_cast<const u32x4 *>(ybuf + (size_t)p * pl.K + c);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      acc[2 * v] = __fadd_rn(acc[2 * v], __fmul_rn(bf16_bits_to_f32(yv[v] & 0xFFFFu), w));
+      acc[2 * v + 1] = __fadd_rn(acc[2 * v + 1], __fmul_rn(bf16_bits_to_f32(yv[v] >> 16), w));
+    }
   }
-  *reinterpret_cast<f32x4 *>(out + (size_t)t * pl.K + c) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+  float *o = out + (size_t)t * pl.K + c;
+  *reinterpret_cast<f32x4 *>(o) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+  *reinterpret_cast<f32x4 *>(o + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
 }
 
 // Exact MXFP4 decode, one thread per block byte (quantization.py:40-51).

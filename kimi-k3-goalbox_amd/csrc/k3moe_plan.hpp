@@ -23,6 +23,7 @@ constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopk = 32;
 constexpr int kGroupChunk = 128;   // tokens per placement chunk in k_group
 constexpr int kXMinPairsPerExpert = 16;  // general path: grouped GEMMs from this many token-expert pairs per expert
+constexpr int kMaxRouterSplits = 8;      // general path: router k-splits (partials summed by the top-k kernel)
 
 constexpr int kDecWaves = 8;       // decode path: waves per workgroup
 constexpr int kDecThreads = kDecWaves * 64;
@@ -102,9 +103,10 @@ struct Plan {
   int single;     // 1: the single-token kernel runs the step (k3moe_single.hpp)
   int redundant;  // 1: every workgroup routes every token (no barrier before grouping)
   int xgemm;      // general path: 1 = grouped-GEMM expert kernels, 0 = per-16-token streams
+  int fgemm;      // grouped GEMMs on the scaled FP4 MFMA with two-term E4M3 activations (k3moe_fgemm.hpp)
   // workspace byte offsets
   size_t o_ctl, o_zero, o_logit, o_ids, o_w, o_nact, o_active, o_aoff, o_acnt, o_ptok, o_pw, o_pof, o_gpart, o_gcnt,
-      o_h, o_y, o_ecnt, o_trace, total;
+      o_gchunk, o_h, o_y, o_xq, o_hq, o_ecnt, o_trace, total;
 };
 
 __host__ __device__ inline int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
@@ -196,16 +198,20 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   // general path expert kernels: grouped GEMMs when the experts average at
   // least kXMinPairsPerExpert tokens (and the widths allow 128-k steps)
   const bool widths = p.K % 128 == 0 && p.I % 128 == 0;
-  p.xgemm = d.path == K3MOE_PATH_GROUPED ||
+  p.xgemm = d.path == K3MOE_PATH_GROUPED || d.path == K3MOE_PATH_GROUPED_BF16 ||
             (d.path != K3MOE_PATH_STREAMED && widths && (long)p.P >= (long)kXMinPairsPerExpert * p.E);
+  // the FP4-MFMA grouped GEMMs take whole row blocks (I % 128 for gate/up, K % 256 for down)
+  // and whole 128-k steps
+  p.fgemm = p.xgemm && d.path != K3MOE_PATH_GROUPED_BF16 && p.K % 256 == 0 && p.I % 128 == 0;
   p.Srw = (int)(p.G / p.RTr);  // decode router units: (row tile, split), every token tile
   if (p.Srw > srw_cap) p.Srw = srw_cap;
   if (p.Srw < 1) p.Srw = 1;
   decode_lds(p);
 
-  // general path splits: router about 1024 waves (at most 4 splits), gate/up about 2048 waves
-  p.Sr = cdiv(1024, base);
-  if (p.Sr > 4) p.Sr = 4;
+  // general path splits: router tiles of 64 tokens x 384 experts, at least 256 workgroups
+  // (at most 8 splits), gate/up about 2048 waves
+  p.Sr = cdiv(256, (long)cdiv(p.B, 64) * cdiv(p.E, 384));
+  if (p.Sr > kMaxRouterSplits) p.Sr = kMaxRouterSplits;
   if (p.Sr > p.KSr) p.Sr = p.KSr;
   if (p.Sr < 1) p.Sr = 1;
   base = (long)p.Dmax * p.RTg;
@@ -234,7 +240,13 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   const bool general = p.path == kPathGeneral;
   p.o_gpart = take(general && p.Sg > 1 ? (size_t)p.Sg * p.P * 2 * p.I * 4 : 0);
   p.o_gcnt = take(general ? (size_t)p.Dmax * p.RTg * 4 : 0);
-  p.o_h = take((size_t)p.P * p.I * 2);
+  p.o_gchunk = take(general ? (size_t)cdiv(p.B, kGroupChunk) * p.E * 4 : 0);  // grouping: per-chunk counts
+  const bool fg = general && p.fgemm;
+  p.o_h = take(fg ? 0 : (size_t)p.P * p.I * 2);
+  // two-term E4M3 activations of the FP4-MFMA GEMMs: expert inputs [B, K] and h [P, I]
+  // (hi, lo, then the hi and lo block scales)
+  p.o_xq = take(fg ? (size_t)p.B * p.K * 2 + (size_t)p.B * (p.K / 32) * 2 : 0);
+  p.o_hq = take(fg ? (size_t)p.P * p.I * 2 + (size_t)p.P * (p.I / 32) * 2 : 0);
   // pair outputs: the general path, and the decode path's expert-major down (I = 256, 384, 512)
   p.o_y = take((general || p.I == 256 || p.I == 384 || p.I == 512) ? (size_t)p.P * p.K * 2 : 0);
   p.trace = trace && p.path == kPathDecode;

@@ -20,7 +20,7 @@ K3MOE_OK = 0
 GATING = {'sigmoid_bias': 0, 'softmax': 1}
 ACTIVATION = {'situ': 0, 'silu': 1}
 DTYPE_BF16, DTYPE_F32, DTYPE_F16 = 0, 1, 2
-PATH = {'auto': 0, 'general': 1, 'decode': 2, 'grouped': 3, 'streamed': 4, 'single': 5}
+PATH = {'auto': 0, 'general': 1, 'decode': 2, 'grouped': 3, 'streamed': 4, 'single': 5, 'grouped_bf16': 6}
 
 
 class Dims(ctypes.Structure):
@@ -40,7 +40,8 @@ class LatentDims(ctypes.Structure):
 class Layout(ctypes.Structure):
     """Mirror of k3moe_layout in include/k3moe.h (byte offsets of the grouping lists)."""
     _fields_ = [(n, ctypes.c_int64) for n in ('active_count', 'active', 'offsets', 'counts', 'pair_token',
-                                               'pair_weight', 'pair_of', 'pair_h', 'pair_y')]
+                                               'pair_weight', 'pair_of', 'pair_h', 'pair_y', 'input_split',
+                                               'h_split')]
 
 
 # bits of the workspace status word (include/k3moe.h K3MOE_STATUS_*)
