@@ -7,7 +7,8 @@ Default workload: one TP8 rank's expert shard (E=384, top-8, h=7168, I=256)
 at batch 1 (the headline line), with batches 8 and 64 reported beside it, and
 (unless --no-extra) 8 stacked batch-64 layers of that shard with fresh weights
 per layer, and the unsharded prefill chunk (I=2048, 4096 tokens), both with
-inputs made on the device.
+inputs made on the device, and the MXFP4 encoder on a TP8 rank's gate weights
+(the "codec" object).
 
 Self-check: the last timed run's outputs are checked against the CPU oracle
 (expert sets exact or FP64-certified near-ties, the band ratio of kimi.py's
@@ -509,6 +510,41 @@ MFMA_FP8_DENSE_TFLOPS = 5000.0
 MFMA_USEFUL_TFLOPS = MFMA_FP8_DENSE_TFLOPS / 2
 
 
+def measure_encode(device, steps, warmup, check):
+    """MXFP4 encoder (k3moe.pack_mxfp4, quantization.py:13-37) on a TP8 rank's gate weights in bf16,
+    [384, 256, 7168] made on the device: us per call (HIP events), algorithmic bytes (bf16 in, packed
+    blocks and scales out) and GB/s; the first call's expert 0 and 383 are checked bit for bit against
+    the oracle's encoder."""
+    import torch
+    import k3moe
+    g = torch.Generator(device=device).manual_seed(11)
+    w = (torch.randn(384, 256, 7168, generator=g, device=device)*0.02).to(torch.bfloat16)
+    n = w.numel()
+    nbytes = 2*n + n//2 + n//32
+    out = k3moe.pack_mxfp4(w)
+    ok = None
+    if check:
+        from oracle import pack_ref
+        ok = all(torch.equal(out[0][e].cpu(), ref[0]) and torch.equal(out[1][e].cpu(), ref[1])
+                 for e in (0, 383) for ref in [pack_ref.pack_mxfp4(w[e].cpu())])
+    for _ in range(warmup):
+        k3moe.pack_mxfp4(w)
+    torch.cuda.synchronize(device)
+    times = []
+    for _ in range(steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        k3moe.pack_mxfp4(w)
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1)*1000.0)
+    us = statistics.mean(times)
+    del w, out
+    return {'kernel': 'k3moe::k_encode', 'shape': [384, 256, 7168], 'dtype_in': 'bf16', 'us': round(us, 2),
+            'us_p50': round(statistics.median(times), 2), 'algorithmic_bytes': nbytes,
+            'hbm_GBps': round(nbytes/us/1e3, 1), 'hbm_frac': round(nbytes/us/1e3/8000.0, 4), 'oracle_exact': ok}
+
+
 def roofline_entry(head, cfg, layers, measured, workload):
     """The roofline object of the JSON line: HBM for the decode-sized steps (one persistent kernel),
     MFMA for the prefill step (grouped GEMMs on the scaled FP4 MFMA; its HBM rate is given beside it)."""
@@ -525,7 +561,8 @@ def roofline_entry(head, cfg, layers, measured, workload):
                 'peak_note': 'useful FLOPs: FP8-rate MFMA (5.0 PFLOP/s dense) run twice per product',
                 'frac': round(head['tflops'] / MFMA_USEFUL_TFLOPS, 4), 'traffic': None,
                 'hbm': {'achieved': head['hbm_GBps'], 'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac']}}
-    return {'bound': 'hbm', 'kernel': 'k3moe::k_moe_decode (the whole step, one launch)',
+    kernel = 'k3moe::k_moe_single' if cfg.tokens == 1 else 'k3moe::k_moe_decode'
+    return {'bound': 'hbm', 'kernel': kernel + ' (the whole step, one launch)',
             'achieved': head['hbm_GBps'], 'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac'],
             'traffic': measured.get(cfg.name, {}).get('traffic_bytes') if layers == 1 else None,
             'traffic_source': TRAFFIC_FILE if measured else None}
@@ -660,6 +697,14 @@ def main():
         if 'check' in r and not r['check']['ok']:
             failures.append(f'{name}: timed outputs fail the oracle check {r["check"]}')
 
+    codec = None
+    if args.workload == 'tp8' and not args.no_extra:
+        log('bench: MXFP4 encoder')
+        codec = measure_encode(device, args.steps, args.warmup, not args.no_check)
+        log(f'bench: encoder {codec}')
+        if codec['oracle_exact'] is False:
+            failures.append(f'encoder output differs from the oracle {codec}')
+        torch.cuda.empty_cache()
     ms_step = head['us_per_layer']*head_layers/1000.0
     line = {
         'metric': METRIC,
@@ -687,6 +732,8 @@ def main():
         'roofline': roofline_entry(head, head_cfg, head_layers, measured, args.workload),
         'cpu_baseline': cpu,
     }
+    if codec is not None:
+        line['codec'] = codec
     print(json.dumps(line), flush=True)
     if failures:
         for f in failures:

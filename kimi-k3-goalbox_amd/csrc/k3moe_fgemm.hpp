@@ -203,7 +203,7 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
     __syncthreads();
   }
   const int J = s_gstart[nact];
-  const int Kd = a.width;                  // reduction length, a multiple of 512
+  const int Kd = a.width;                  // reduction length, a multiple of 128
   const int KB = Kd / kBlockK, KS = Kd / 128;
   const int Nout = GU ? pl.I : pl.K;
   const int RPB = GU ? 256 : 512;          // output rows per unit

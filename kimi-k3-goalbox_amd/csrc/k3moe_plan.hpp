@@ -200,9 +200,9 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   const bool widths = p.K % 128 == 0 && p.I % 128 == 0;
   p.xgemm = d.path == K3MOE_PATH_GROUPED || d.path == K3MOE_PATH_GROUPED_BF16 ||
             (d.path != K3MOE_PATH_STREAMED && widths && (long)p.P >= (long)kXMinPairsPerExpert * p.E);
-  // the FP4-MFMA grouped GEMMs take whole row blocks (I % 128 for gate/up, K % 256 for down)
+  // the FP4-MFMA grouped GEMMs take whole units of output rows: 256 of I for gate/up, 512 of K for down
   // and whole 128-k steps
-  p.fgemm = p.xgemm && d.path != K3MOE_PATH_GROUPED_BF16 && p.K % 256 == 0 && p.I % 128 == 0;
+  p.fgemm = p.xgemm && d.path != K3MOE_PATH_GROUPED_BF16 && p.K % 512 == 0 && p.I % 256 == 0;
   p.Srw = (int)(p.G / p.RTr);  // decode router units: (row tile, split), every token tile
   if (p.Srw > srw_cap) p.Srw = srw_cap;
   if (p.Srw < 1) p.Srw = 1;

@@ -19,8 +19,13 @@ import json
 import sqlite3
 import statistics
 
-STEP_KERNEL = 'k_moe_decode'
+STEP_KERNELS = ('k_moe_single', 'k_moe_decode')  # the one-launch step kernels (one token; up to 64)
 COPY_KERNEL = 'copyBuffer'
+
+
+def _like(names) -> tuple[str, tuple]:
+    names = (names,) if isinstance(names, str) else tuple(names)
+    return '(' + ' or '.join(['name like ?'] * len(names)) + ')', tuple(f'%{n}%' for n in names)
 
 
 def _runs(rows):
@@ -33,10 +38,10 @@ def _runs(rows):
     return out
 
 
-def kernel_durations(db: str, name: str = STEP_KERNEL) -> list[dict]:
+def kernel_durations(db: str, name=STEP_KERNELS) -> list[dict]:
     con = sqlite3.connect(db)
-    rows = con.execute('select lds_size, duration from kernels where name like ? order by start',
-                       (f'%{name}%',)).fetchall()
+    cond, args = _like(name)
+    rows = con.execute(f'select lds_size, duration from kernels where {cond} order by start', args).fetchall()
     out = []
     for lds, vals in _runs(rows):
         us = [v[0] / 1e3 for v in vals]
@@ -54,12 +59,14 @@ def top_kernels(db: str, n: int = 6) -> list[dict]:
              'total_us': round(r[3] / 1e3, 1)} for r in rows]
 
 
-def counter_kib(db: str, counter: str, name: str) -> list[tuple[int, int, float]]:
+def counter_kib(db: str, counter: str, name) -> list[tuple[int, int, float]]:
     """(lds size, grid size, summed counter value in KiB) per dispatch of kernels matching `name`."""
     con = sqlite3.connect(db)
+    cond, args = _like(name)
+    cond = cond.replace('name like', 'kernel_name like')
     rows = con.execute('select lds_block_size, grid_size, sum(value) from counters_collection '
-                       'where counter_name = ? and kernel_name like ? group by dispatch_id order by start',
-                       (counter, f'%{name}%')).fetchall()
+                       f'where counter_name = ? and {cond} group by dispatch_id order by start',
+                       (counter,) + args).fetchall()
     return [(r[0], r[1], float(r[2])) for r in rows]
 
 
@@ -70,7 +77,7 @@ def calibration(db: str, counter: str, copy_bytes: int) -> float:
 
 
 def step_counter(db: str, counter: str) -> list[dict]:
-    rows = [(lds, v) for lds, _, v in counter_kib(db, counter, STEP_KERNEL)]
+    rows = [(lds, v) for lds, _, v in counter_kib(db, counter, STEP_KERNELS)]
     return [{'lds_bytes': lds, 'dispatches': len(vals), 'kib_per_dispatch': round(statistics.median([v[0] for v in vals]), 1)}
             for lds, vals in _runs(rows)]
 

@@ -536,6 +536,16 @@ def test_grouped_gemm_experts_over_128_tokens(gpu, path):
     run_and_check(cfg, synthetic.moe_layer_inputs(cfg, 7), gpu, routes=routes, rows=rows, path=path)
 
 
+@pytest.mark.parametrize('width,inter', [(768, 384), (1536, 640)])
+def test_grouped_gemm_widths_off_the_fp4_units(gpu, width, inter):
+    """Grouped widths that are multiples of 128 but not of the FP4 GEMMs' output units (512 of the
+    latent, 256 of inter) run the bf16-MFMA grouped GEMMs; every output column is checked."""
+    cfg = MoEConfig(f'grouped-b512-{width}-{inter}', 32, 4, width, inter, 512, gating='softmax')
+    say(f'case: {cfg.name} seed=8 path=grouped (oracle on 6 sampled rows)')
+    rows = torch.tensor([0, 1, 200, 300, 510, 511])
+    run_and_check(cfg, synthetic.moe_layer_inputs(cfg, 8), gpu, rows=rows, path='grouped')
+
+
 # ---- the stacked-layer and prefill configurations at full size ----
 
 def test_stacked_layers_tp8_b64(gpu):

@@ -165,3 +165,17 @@ def test_init_size_agrees_across_header_library_and_python():
     assert n == moe.INIT_BYTES
     text = open(HEADER).read()
     assert int(re.search(r"Zero the workspace's first (\d+) bytes", text).group(1)) == n
+
+
+@pytest.mark.parametrize('K,I,fp4', [(1024, 512, True), (512, 256, True), (7168, 2048, True), (768, 384, False),
+                                     (1024, 384, False), (768, 512, False), (1024, 128, False)])
+def test_fp4_grouped_gemms_only_for_whole_output_units(K, I, fp4):
+    """The FP4-MFMA grouped GEMMs write 256 columns of I (gate/up) or 512 of the latent (down) per
+    work unit, so the plan takes them only when both widths are whole multiples; other grouped
+    shapes run the bf16-MFMA GEMMs (no activation split in the workspace, h kept in bf16)."""
+    d = _native.Dims(tokens=512, experts=32, topk=4, hidden=K, latent=K, inter=I, gating=0, activation=0,
+                     x_dtype=0, path=_native.PATH['grouped'])
+    lay = moe.workspace_layout(d)
+    assert (lay['input_split'] >= 0) == fp4
+    assert (lay['h_split'] >= 0) == fp4
+    assert (lay['pair_h'] == -1) == fp4
