@@ -85,7 +85,7 @@ def measured_traffic() -> dict:
         return json.load(fh).get('workloads', {})
 
 
-PHASES = ('router', 'barrier1', 'topk', 'barrier2', 'group', 'gate_up', 'barrier3', 'down_combine')
+PHASES = ('router', 'router_tail', 'topk', 'pairs_poll', 'group', 'gate_up', 'gate_up_done', 'down_combine')
 
 
 def read_trace(cfg, device):
@@ -171,6 +171,12 @@ def read_trace(cfg, device):
     sub(4, 28, 'group_count')
     sub(28, 29, 'group_scan')
     sub(29, 5, 'group_place')
+    sub(5, 12, 'gu_entry')
+    sub(12, 13, 'gu_pre_issue')
+    sub(13, 45, 'gu_to_round_barrier')
+    sub(35, 14, 'gu_cut_sums')
+    sub(14, 15, 'gu_more_rounds')
+    sub(15, 6, 'gu_exit')
     sub(5, 32, 'gu_round_table')
     sub(5, 45, 'gu_rt_to_first_barrier')
     sub(45, 46, 'gu_rt_lds_reads')
@@ -192,7 +198,7 @@ def read_trace(cfg, device):
         rel = (ends[okw] - full[okw, 7:8])*0.01
         out['dn_stream_end_by_wave_med_us'] = [round(float(rel[:, j].median()), 1) for j in range(8)]
         out['dn_stream_end_max_us'] = round(float(rel.max()), 1)
-    for n in range(4):   # inside each grid barrier: release+add, spin, acquire
+    for n in (2, 3):   # inside grid barriers 3 (row-tile down) and 4 (before the combine): release+add, spin, acquire
         if float(full[:, 13 + 4*n].max()) <= 0:
             continue
         b = full[:, 12 + 4*n: 16 + 4*n]

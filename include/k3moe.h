@@ -189,10 +189,10 @@ typedef struct k3moe_layout {
 
 int k3moe_workspace_layout(const k3moe_dims *dims, k3moe_layout *layout);
 
-/* Zero the workspace's first 610304 bytes (the control block with the barrier
- * counters and the sticky status word, a zero area the kernels read in place
- * of inactive data, the latent block's row-tile counters and the single-token
- * kernel's tagged exchange area) with a small
+/* Zero the workspace's first 2183168 bytes (the control block with the barrier
+ * and launch counters and the sticky status word, a zero area the kernels read
+ * in place of inactive data, the latent block's row-tile counters and the
+ * persistent kernels' tagged exchange area) with a small
  * kernel on `stream`. A workspace must be
  * initialised once before its first step; each step leaves the counters at
  * zero, so one workspace serves any number of consecutive steps on one

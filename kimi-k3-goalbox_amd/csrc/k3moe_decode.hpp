@@ -267,6 +267,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
   // holds); otherwise they are issued again.
   GuSS<W> B0, B1;
   int s_pre = -1;
+  trace_mark(pl, a.ws, 12);
   if (ga < gb) {
     const int work = (gb - ga) * NSS;
     const int s = wave_share(work, w), e = wave_share(work, w + 1);
@@ -284,6 +285,7 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
       s_pre = s;
     }
   }
+  trace_mark(pl, a.ws, 13);
   for (int g0 = ga; g0 < gb;) {
     const int ci0 = g0 / GPC;
     // LDS-only barriers in the round (no vector-memory wait): the previous round is
@@ -470,8 +472,10 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
         finish(gl, sum);
       }
     }
+    if (g0 == ga) trace_mark(pl, a.ws, 14);
     g0 = g1;
   }
+  trace_mark(pl, a.ws, 15);
 }
 
 // ---------------------------------------------------- down, expert-major --
@@ -756,13 +760,40 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   __shared__ GuChunk s_tab[16];
   __shared__ int s_round[2], s_rowtok[16];
   __shared__ __attribute__((aligned(16))) int s_prog[kDecWaves];
+  __shared__ uint32_t s_tag;
+  __shared__ int s_fail;
 
   const int tid = threadIdx.x, w = wave_id(), l = tid & 63;
   const int i = l & 15, q = l >> 4;
   unsigned *ctl = reinterpret_cast<unsigned *>(a.ws + pl.o_ctl);
-  float *part = reinterpret_cast<float *>(a.ws + pl.o_logit);
-  int *ws_ids = reinterpret_cast<int *>(a.ws + pl.o_ids);
-  float *ws_w = reinterpret_cast<float *>(a.ws + pl.o_w);
+  // Workgroups hand the router partials, the routed pairs and the gate/up
+  // completions to each other through tagged 8-byte slots {payload, tag} in
+  // the tag area; the tag numbers the launch (launches so far on this
+  // workspace + 1, from the launch counters every workgroup of the decode and
+  // single-token kernels adds to when it leaves), so a reader polls the data
+  // itself until it carries this launch's tag, and no slot needs clearing.
+  const __amdgpu_buffer_rsrc_t tagr = make_rsrc(a.ws + kOffTag, kTagBytes);
+  uint32_t launches = 0u;  // wave 0, lane g < kEpochCounters: launch counter g
+  if (w == 0 && l < kEpochCounters)
+    launches = __hip_atomic_load(ctl + kCtlEpoch + l * kCtlEpochStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  bool tag_made = false;
+  auto make_tag = [&]() {  // wave 0, once, after the router's loads are issued
+    if (tag_made || w != 0) return;
+    tag_made = true;
+    uint32_t sum = 0u;
+#pragma unroll
+    for (int g = 0; g < kEpochCounters; ++g) sum += lane_u32(launches, g);
+    if (l == 0) {
+      s_tag = (sum >> __builtin_ctz(gridDim.x)) + 1u;
+      s_fail = 0;
+    }
+  };
+  // this workgroup's count on its launch counter: once, on every way out
+  auto leave = [&]() {
+    if (tid == 0)
+      __hip_atomic_fetch_add(ctl + kCtlEpoch + (blockIdx.x % kEpochCounters) * kCtlEpochStride, 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  };
   uint16_t *hbuf = reinterpret_cast<uint16_t *>(a.ws + pl.o_h);
   const uint8_t *zero = reinterpret_cast<const uint8_t *>(a.ws + pl.o_zero);  // kZeroBytes of zeros
   const int B = pl.B, E = pl.E, k = pl.k;
@@ -841,6 +872,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
           for (int kk = 0; kk < 4; ++kk) vb[tt][kk] = tok_ok ? load16(brow + kk * 8) : u32x4{0, 0, 0, 0};
         }
         warm_code();
+        make_tag();
 #pragma unroll
         for (int tt = 0; tt < kDecMaxTokens / 16; ++tt) {
           if (tt < pl.TTr) {
@@ -849,35 +881,37 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
           }
         }
       }
+      make_tag();
       if (u == (int)blockIdx.x) trace_mark(pl, a.ws, 31);
 #pragma unroll
       for (int tt = 0; tt < kDecMaxTokens / 16; ++tt)
         if (tt < pl.TTr) *reinterpret_cast<f32x4 *>(red + (tt * kDecWaves + w) * 256 + l * 4) = acc[tt];
       __syncthreads();
+      // partial s of logit (t, e): slot kTagDecPart + ((t Srw + s) Epad + e) 8
       for (int j = tid; j < pl.TTr * 256; j += kDecThreads) {
         const int tt = j >> 8, ln = (j >> 2) & 63, v = j & 3;
         const int r = 4 * (ln >> 4) + v, c = ln & 15;
         const int t = tt * 16 + c, e = rt * 16 + r;
         if (t < B)
-          st_dev32(make_rsrc(part, (uint32_t)(pl.Srw * B * pl.Epad * 4)), (uint32_t)(((size_t)s * B + t) * pl.Epad + e) * 4,
-                   __float_as_uint(red_sum(red + tt * kDecWaves * 256, j & 255)));
+          st_dev64(tagr, (uint32_t)(kTagDecPart + (((size_t)t * pl.Srw + s) * pl.Epad + e) * 8),
+                   u32x2{__float_as_uint(red_sum(red + tt * kDecWaves * 256, j & 255)), s_tag});
       }
       __syncthreads();
     }
   }
   warm_code();  // workgroups without router work
-  unsigned *ecnt = reinterpret_cast<unsigned *>(a.ws + pl.o_ecnt);  // gate/up units done per active expert
-  {
-    const __amdgpu_buffer_rsrc_t er = make_rsrc(ecnt, (uint32_t)pl.Dmax * kCntStride * 4);
-    for (int j = blockIdx.x * kDecThreads + tid; j < pl.Dmax; j += gridDim.x * kDecThreads)
-      st_dev32(er, j * kCntStride * 4, 0u);
-  }
+  make_tag();
   trace_mark(pl, a.ws, 1);
   asm volatile("" ::"v"(code_probe));  // the warm-up loads complete here
-  unsigned nbar = 0;  // barriers of this launch passed so far
+  __syncthreads();  // s_tag, s_fail, s_abort0
+  const uint32_t tag = s_tag;
+  const unsigned abort0 = s_abort0;
+  unsigned nbar = 0;  // grid barriers of this launch passed so far
   // a wait of this launch gave up: NaN in this workgroup's share of the output, and leave
-  auto give_up = [&]() { poison_share<false>(a.out, (long)B * pl.K); };
-  if (!grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 12))) return give_up();
+  auto give_up = [&]() {
+    poison_share<false>(a.out, (long)B * pl.K);
+    leave();
+  };
   trace_mark(pl, a.ws, 2);
   // A single token's expert-input row is known from the start: its loads are
   // issued here and arrive during the top-k and grouping phases; gate/up then
@@ -894,9 +928,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   }
 
   // -------------------------------------------------------- T: top-k/gating --
-  // Small batches: every workgroup routes every token itself (no barrier, the
-  // grouping reads its own LDS). Larger batches: token t is routed by
-  // workgroup t mod G and the results meet in the workspace after barrier 2.
+  // One token: every workgroup routes it itself (the grouping reads its own
+  // LDS). More tokens: token t is routed by workgroup t, which publishes its
+  // (id, weight) pairs in tagged slots that every workgroup polls.
   const bool redundant = pl.redundant;
   int *rid = reinterpret_cast<int *>(scr);     // [P] expert ids, ascending per token
   float *rw = reinterpret_cast<float *>(rid + pl.P);  // [P] weights aligned with rid
@@ -908,12 +942,6 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     float *scl = kyf + nt * E;                           // [nt][E] scores (sigmoid or logits)
     int *sel = reinterpret_cast<int *>(scl + nt * E);    // [8 waves][kMaxTopk]
     for (int t0 = redundant ? 0 : blockIdx.x; t0 < B; t0 += redundant ? B : gridDim.x) {
-      // logits of (t0 + f / E, f % E): partials summed in split order. With
-      // E % 4 == 0 and more logits than threads a thread takes 4 consecutive
-      // experts of a token per item group (one 16-byte load per split;
-      // partial rows are 64-byte aligned) and two groups at a time, every load
-      // in flight together; otherwise one logit per thread (the gating math
-      // spread over the most threads).
       auto gate = [&](int f, float logit, float bias) {
         float score, key;
         if (pl.gating == K3MOE_GATING_SIGMOID_BIAS) {
@@ -927,63 +955,53 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
         kyf[f] = key;
         kyl[f] = ordered_key(key);
       };
-      if ((E & 3) == 0 && nt * E > kDecThreads) {
-        const int NG4 = nt * E / 4;
-        for (int g0 = tid; g0 < NG4; g0 += 2 * kDecThreads) {
-          f32x4 ps[2][kDecMaxSplits];
-          float bv[2][4];
+      // logits of token t0: thread e polls the partial slots of experts e and
+      // e + 512 (every split's 8-byte load per round) until each carries this
+      // launch's tag, then sums them in split order
+      {
+        const int e0 = tid, e1 = tid + kDecThreads;
+        const int n0 = e0 < E ? pl.Srw : 0, n1 = e1 < E ? pl.Srw : 0;
+        const uint32_t pbase = (uint32_t)(kTagDecPart + (size_t)t0 * pl.Srw * pl.Epad * 8);
+        const uint32_t sstride = (uint32_t)pl.Epad * 8;
+        u32x2 v0[kDecMaxSplits], v1[kDecMaxSplits];
+        bool ok = true;
+        unsigned spins = 0;
+        for (;;) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int g = g0 + j * kDecThreads;
-            const bool ok = g < NG4;
-            const int f = 4 * (ok ? g : 0), t = t0 + f / E, e = f % E;
-#pragma unroll
-            for (int sp = 0; sp < kDecMaxSplits; ++sp)
-              ps[j][sp] = (ok && sp < pl.Srw)
-                              ? *reinterpret_cast<const f32x4 *>(part + ((size_t)sp * B + t) * pl.Epad + e)
-                              : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int v = 0; v < 4; ++v) bv[j][v] = (ok && a.bias) ? a.bias[e + v] : 0.f;
+          for (int sp = 0; sp < kDecMaxSplits; ++sp) {
+            v0[sp] = sp < n0 ? bload8_dev(tagr, pbase + sp * sstride + e0 * 8) : u32x2{0u, tag};
+            v1[sp] = sp < n1 ? bload8_dev(tagr, pbase + sp * sstride + e1 * 8) : u32x2{0u, tag};
           }
+          bool ready = true;
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int g = g0 + j * kDecThreads;
-            if (g >= NG4) break;
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              float logit = ps[j][0][v];
-#pragma unroll
-              for (int sp = 1; sp < kDecMaxSplits; ++sp)
-                if (sp < pl.Srw) logit += ps[j][sp][v];
-              gate(4 * g + v, logit, bv[j][v]);
-            }
+          for (int sp = 0; sp < kDecMaxSplits; ++sp) ready = ready && v0[sp][1] == tag && v1[sp][1] == tag;
+          if (spins == 0 && w == 0) trace_mark(pl, a.ws, 44);
+          if (__ballot(!ready) == 0) break;
+          ++spins;
+          if ((spins & 63u) == 0u && aborted(ctl, abort0)) {
+            ok = false;
+            break;
           }
+          if (spins > kSpinLimit) {
+            if (l == 0) raise_timeout(ctl);
+            ok = false;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
         }
-      } else {
-        for (int f0 = tid; f0 < nt * E; f0 += 4 * kDecThreads) {
-          float ps[4][kDecMaxSplits];
+        if (!ok) s_fail = 1;
+        float lg0 = __uint_as_float(v0[0][0]), lg1 = __uint_as_float(v1[0][0]);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int f = f0 + j * kDecThreads;
-            const int t = t0 + f / E, e = f % E;
-#pragma unroll
-            for (int sp = 0; sp < kDecMaxSplits; ++sp)
-              ps[j][sp] = (f < nt * E && sp < pl.Srw) ? part[((size_t)sp * B + t) * pl.Epad + e] : 0.f;
+        for (int sp = 1; sp < kDecMaxSplits; ++sp)
+          if (sp < pl.Srw) {
+            lg0 += __uint_as_float(v0[sp][0]);
+            lg1 += __uint_as_float(v1[sp][0]);
           }
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int f = f0 + j * kDecThreads;
-            if (f >= nt * E) break;
-            float logit = ps[j][0];
-#pragma unroll
-            for (int sp = 1; sp < kDecMaxSplits; ++sp)
-              if (sp < pl.Srw) logit += ps[j][sp];
-            const float bv = !a.bias ? 0.f : (nt == 1 && j < 2) ? bias_pre[j] : a.bias[f % E];
-            gate(f, logit, bv);
-          }
-        }
+        if (n0) gate(e0, lg0, bias_pre[0]);
+        if (n1) gate(e1, lg1, bias_pre[1]);
       }
       __syncthreads();
+      if (s_fail) return give_up();
       trace_mark(pl, a.ws, 10);
       // One token per pass: the 8 waves share its selection. With E <= 512
       // and k <= 8, wave w selects the 8 best of experts 64 w .. 64 w + 63 as
@@ -1082,9 +1100,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
           if (redundant) {
             rid[o] = my_e;
             rw[o] = wt;
-          } else {
-            st_dev32(make_rsrc(ws_ids, (uint32_t)pl.P * 4), (uint32_t)o * 4, (uint32_t)my_e);
-            st_dev32(make_rsrc(ws_w, (uint32_t)pl.P * 4), (uint32_t)o * 4, __float_as_uint(wt));
+          } else {  // pair slot o: {id, tag, weight, tag}
+            st_dev128(tagr, (uint32_t)(kTagDecPairs + o * 16), u32x4{(uint32_t)my_e, tag, __float_as_uint(wt), tag});
           }
         }
       }
@@ -1094,26 +1111,42 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   }
   trace_mark(pl, a.ws, 3);
   if (!redundant) {
-    if (!grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 16))) return give_up();
-    for (int p0 = tid; p0 < pl.P; p0 += 4 * kDecThreads) {
-      int iv[4];
-      float wv[4];
+    // every pair's slot (pairs tid and tid + 512), polled until both halves carry this launch's tag
+    u32x4 pv[2];
+    bool ok = true;
+    unsigned spins = 0;
+    for (;;) {
+      bool ready = true;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int p = p0 + j * kDecThreads;
-        iv[j] = p < pl.P ? ws_ids[p] : 0;
-        wv[j] = p < pl.P ? ws_w[p] : 0.f;
+      for (int j = 0; j < 2; ++j) {
+        const int p = tid + j * kDecThreads;
+        pv[j] = p < pl.P ? bload16_dev(tagr, (uint32_t)(kTagDecPairs + p * 16)) : u32x4{0u, tag, 0u, tag};
+        ready = ready && pv[j][1] == tag && pv[j][3] == tag;
       }
+      if (__ballot(!ready) == 0) break;
+      ++spins;
+      if ((spins & 63u) == 0u && aborted(ctl, abort0)) {
+        ok = false;
+        break;
+      }
+      if (spins > kSpinLimit) {
+        if (l == 0) raise_timeout(ctl);
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ok) s_fail = 1;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int p = p0 + j * kDecThreads;
-        if (p < pl.P) {
-          rid[p] = iv[j];
-          rw[p] = wv[j];
-        }
+    for (int j = 0; j < 2; ++j) {
+      const int p = tid + j * kDecThreads;
+      if (p < pl.P) {
+        rid[p] = (int)pv[j][0];
+        rw[p] = __uint_as_float(pv[j][2]);
       }
     }
     __syncthreads();
+    if (s_fail) return give_up();
   }
   trace_mark(pl, a.ws, 4);
 
@@ -1231,13 +1264,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   }
   trace_mark(pl, a.ws, 6);
   // Expert-major down reads an expert's h only after its gate/up units are
-  // done: instead of a grid barrier, each workgroup counts the gate/up units it
-  // finished per expert (after its h stores have completed), and a down wave
-  // waits for its expert's count. Each count has a 128-byte line of its own:
-  // increments of one line are serialised where they are performed. The
-  // paired row-tile path below (at most one expert per wave) waits the same
-  // way; the general row-tile path needs every expert in every workgroup and
-  // keeps the barrier.
+  // done: instead of a grid barrier, each workgroup that finished gate/up
+  // units of active expert d (after its h stores have completed) writes the
+  // tagged slot d + b (b: the workgroup; unique, since a later expert's
+  // workgroups never come before an earlier one's), and a down wave polls the
+  // slots of the workgroups whose gate/up range holds a group of its expert.
+  // The paired row-tile path below (at most one expert per wave) waits the
+  // same way; the general row-tile path needs every expert in every workgroup
+  // and keeps the barrier.
   const bool expert_major = KSD > 0 && D > kDnExpertMajorMin && pl.o_y;
   // Paired row-tile down: at most one active expert per wave, one token
   // chunk per expert, I <= 256 and at most two row tiles per workgroup (small
@@ -1247,17 +1281,31 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   const int dn_da = D * w / kDecWaves, dn_db = D * (w + 1) / kDecWaves;
   const bool dn_pair = !expert_major && D <= kDecWaves && B <= 16 && pl.KSd <= kDnDepth &&
                        pl.RTd <= 2 * (int)gridDim.x;
-  const unsigned abort0 = s_abort0;
+  // gate/up groups (as in the gate/up phase): W units each, NG in all; workgroup
+  // b's range is [NG b / G, NG (b + 1) / G)
+  const int gu_w = gu_pairs(g_coff[D] * pl.U8) ? 2 : 1;
+  const int ngu = g_coff[D] * (pl.U8 / gu_w);
+  // the workgroup whose range holds group x: the largest b with NG b / G <= x
+  auto wg_of = [&](unsigned x) { return (int)(((x + 1u) * gridDim.x - 1u) / (unsigned)ngu); };
   auto wait_expert = [&](int d) {  // bounded: a timeout sets the status word; gives up with the launch
-    const unsigned need = (unsigned)(g_coff[d + 1] - g_coff[d]) * pl.U8;
+    const unsigned gpc = (unsigned)(pl.U8 / gu_w);
+    const int b0 = wg_of((unsigned)g_coff[d] * gpc), b1 = wg_of((unsigned)g_coff[d + 1] * gpc - 1u);
     unsigned spins = 0;
-    while (__hip_atomic_load(ecnt + d * kCntStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
-      if ((++spins & 63u) == 0u && aborted(ctl, abort0)) break;
-      if (spins > kSpinLimit) {
-        if ((threadIdx.x & 63) == 0) raise_timeout(ctl);
-        break;
+    for (int bs = b0; bs <= b1; bs += 64) {
+      const int b = bs + l;
+      // workgroups in [b0, b1] with an empty range (fewer groups than workgroups) write no slot
+      const bool need = b <= b1 && grid_share(ngu, b) < grid_share(ngu, b + 1);
+      for (;;) {
+        const u32x2 v = need ? bload8_dev(tagr, (uint32_t)(kTagDecDone + (d + b) * 8)) : u32x2{0u, tag};
+        if (__ballot(v[1] != tag) == 0) break;
+        ++spins;
+        if ((spins & 63u) == 0u && aborted(ctl, abort0)) return;
+        if (spins > kSpinLimit) {
+          if (l == 0) raise_timeout(ctl);
+          return;
+        }
+        __builtin_amdgcn_s_sleep(1);
       }
-      __builtin_amdgcn_s_sleep(1);
     }
     // the h loads after the wait stay after it (the hardware issues in
     // order; this keeps the compiler from hoisting them)
@@ -1266,17 +1314,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   if (expert_major || dn_pair) {
     wait_vmem();
     __syncthreads();
-    const int W = gu_pairs(g_coff[D] * pl.U8) ? 2 : 1;  // as in the gate/up phase
-    const int NG = g_coff[D] * (pl.U8 / W);
-    const int ga = grid_share(NG, blockIdx.x), gb = grid_share(NG, blockIdx.x + 1);
+    const int ga = grid_share(ngu, blockIdx.x), gb = grid_share(ngu, blockIdx.x + 1);
     if (ga < gb) {
-      const int ua = ga * W, ub = gb * W;  // this workgroup's units, chunk-major (chunk * U8 + unit)
+      const int ua = ga * gu_w, ub = gb * gu_w;  // this workgroup's units, chunk-major (chunk * U8 + unit)
       const int d0 = g_cexp[ua / pl.U8], d1 = g_cexp[(ub - 1) / pl.U8];
-      for (int d = d0 + tid; d <= d1; d += kDecThreads) {
-        const int n = min(ub, g_coff[d + 1] * pl.U8) - max(ua, g_coff[d] * pl.U8);
-        if (n > 0)
-          __hip_atomic_fetch_add(ecnt + d * kCntStride, (unsigned)n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      for (int d = d0 + tid; d <= d1; d += kDecThreads)
+        st_dev64(tagr, (uint32_t)(kTagDecDone + (d + (int)blockIdx.x) * 8), u32x2{0u, tag});
     }
   }
   DnLoad pf[2];
@@ -1466,6 +1509,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     crange[0] = pc0;
     crange[1] = program_counter();
   }
+  leave();
 }
 
 }  // namespace k3moe

@@ -49,16 +49,16 @@ constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert
 constexpr int kCtlErr = 2;
 constexpr int kCtlAbort = 3;
 constexpr int kCtlCodeSingle = 8;  // 2 x uint64: the single-token kernel's code range of its last launch
-// Launch counters of the single-token kernel (k3moe_single.hpp): each of its
-// workgroups adds one, on counter blockIdx % kEpochCounters, when it leaves;
-// the sum, divided by the grid size, counts its earlier launches on this
-// workspace. kCtlEpochStride words (64 bytes) apart.
+// Launch counters of the single-token and decode kernels (k3moe_single.hpp,
+// k3moe_decode.hpp): each of their workgroups adds one, on counter blockIdx %
+// kEpochCounters, when it leaves; the sum, divided by the grid size (the same
+// for both), counts their earlier launches on this workspace.
+// kCtlEpochStride words (64 bytes) apart.
 constexpr int kCtlEpoch = 640, kEpochCounters = 16, kCtlEpochStride = 16;
 constexpr int kCtlCode = 4;  // 2 x uint64: the decode kernel's code range (start, end) of its last launch
 constexpr int kCtlTop = 32;
 constexpr int kBarGroups = 16, kCtlGroup = 64, kCtlStride = 32;
 constexpr int kCtlBytes = 4 * (kCtlGroup + kBarGroups * kCtlStride);  // 2304
-constexpr int kCntStride = 32;  // 32-bit words between per-expert counters: one 128-byte line each
 // A zero area follows the control block: loads of inactive lanes and of k-steps
 // past a range read it instead of branching. Zeroed with the control block by
 // the workspace init and never written by a step. Holds any row offset used
@@ -69,11 +69,19 @@ constexpr int kZeroBytes = 64 * 1024;
 // puts its counter back to zero.
 constexpr int kLatCntBytes = 16384;
 constexpr int kOffLatCnt = 4096 + kZeroBytes;
-// Then the single-token kernel's tagged exchange area: 8-byte slots {payload,
+// Then the persistent kernels' tagged exchange area: 8-byte slots {payload,
 // tag}, where the tag identifies the launch that wrote the payload (zero never
-// does, so a zeroed area holds no valid slot). Only that kernel writes it.
-constexpr int kTagBytes = 512 * 1024;
-constexpr int kTagCopies = 8;  // router partials: one copy per XCD (workgroup b reads copy b mod 8)
+// does, so a zeroed area holds no valid slot). Only the single-token and decode
+// kernels write it; both number their launches on the same counters, so a slot
+// left by any earlier launch never carries the current tag.
+constexpr int kTagBytes = 2 * 1024 * 1024;
+constexpr int kTagCopies = 8;  // single-token router partials: one copy per XCD (workgroup b reads copy b mod 8)
+// The decode kernel's regions: the routed pairs (16-byte slots {id, tag,
+// weight, tag}), the gate/up completion slots (slot d + b: active expert d,
+// workgroup b), then the router partials ([B][Srw][Epad] slots).
+constexpr int kTagDecPairs = 0;
+constexpr int kTagDecDone = kTagDecPairs + kDecMaxPairs * 16;
+constexpr int kTagDecPart = kTagDecDone + (kMaxExperts + 1024) * 8;
 constexpr int kOffTag = kOffLatCnt + kLatCntBytes;
 constexpr int kInitBytes = kOffTag + kTagBytes;  // control block (page-padded), zero area, counters, tags
 constexpr int kTraceSlots = 56;    // phase timestamps per workgroup when tracing
@@ -106,7 +114,7 @@ struct Plan {
   int fgemm;      // grouped GEMMs on the scaled FP4 MFMA with two-term E4M3 activations (k3moe_fgemm.hpp)
   // workspace byte offsets
   size_t o_ctl, o_zero, o_logit, o_ids, o_w, o_nact, o_active, o_aoff, o_acnt, o_ptok, o_pw, o_pof, o_gpart, o_gcnt,
-      o_gchunk, o_h, o_y, o_xq, o_hq, o_ecnt, o_trace, total;
+      o_gchunk, o_h, o_y, o_xq, o_hq, o_trace, total;
 };
 
 __host__ __device__ inline int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
@@ -190,10 +198,14 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   int srw_cap = p.KSr / kDecWaves;
   if (srw_cap > kDecMaxSplits) srw_cap = kDecMaxSplits;
   if (srw_cap < 1) srw_cap = 1;
+  // the decode kernel's router partials, [B][Srw][Epad] tagged slots, fit the tag area
+  const long part_room = kTagBytes - kTagDecPart;
+  while (srw_cap > 1 && (long)srw_cap * p.B * p.Epad * 8 > part_room) --srw_cap;
   p.Srw = srw_cap;
   p.path = kPathGeneral;
   if ((d.path == K3MOE_PATH_AUTO || d.path == K3MOE_PATH_DECODE || d.path == K3MOE_PATH_SINGLE) &&
-      p.B <= kDecMaxTokens && p.P <= kDecMaxPairs && decode_lds(p) <= kDecMaxLds - kDecStaticLds)
+      p.B <= kDecMaxTokens && p.P <= kDecMaxPairs && (long)p.B * p.Epad * 8 <= part_room &&
+      decode_lds(p) <= kDecMaxLds - kDecStaticLds)
     p.path = kPathDecode;
   // general path expert kernels: grouped GEMMs when the experts average at
   // least kXMinPairsPerExpert tokens (and the widths allow 128-k steps)
@@ -218,7 +230,7 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   p.Sg = cdiv(2048, base);
   if (p.Sg > p.KSg) p.Sg = p.KSg;
   if (p.Sg < 1) p.Sg = 1;
-  const int logit_splits = p.path == kPathDecode ? srw_cap : p.Sr;
+  const int logit_splits = p.path == kPathDecode ? 0 : p.Sr;  // decode: partials in the tag area
   if (p.path == kPathDecode) p.Sr = p.Srw;
 
   size_t o = 0;
@@ -226,7 +238,7 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   p.o_ctl = take(4096);
   p.o_zero = take(kZeroBytes);
   take(kLatCntBytes);  // the latent block's counters, kept by MoE steps on a shared workspace
-  take(kTagBytes);     // the single-token kernel's tagged exchange area
+  take(kTagBytes);     // the persistent kernels' tagged exchange area
   p.o_logit = take((size_t)logit_splits * p.B * p.Epad * 4);
   p.o_ids = take((size_t)p.P * 4);
   p.o_w = take((size_t)p.P * 4);
@@ -255,7 +267,6 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
     p.path = kPathDecode;
     p.lds_total = single_lds(p);
   }
-  p.o_ecnt = take((size_t)p.Dmax * kCntStride * 4);  // decode: gate/up units done per active expert
   p.o_trace = p.trace ? take((size_t)1024 * kTraceSlots * 8) : 0;  // last area of the workspace
   p.total = o;
 }

@@ -19,7 +19,7 @@ from . import _native
 from ._native import ACTIVATION, GATING, Dims, check
 
 MX_BLOCK = 32
-INIT_BYTES = 4096 + 65536 + 16384 + 524288  # control block, zero area, latent-block counters and tag area (k3moe_workspace_init)
+INIT_BYTES = 4096 + 65536 + 16384 + 2097152  # control block, zero area, latent-block counters and tag area (k3moe_workspace_init)
 
 
 def _dev_ptr(t: torch.Tensor | None):

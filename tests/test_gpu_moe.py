@@ -276,14 +276,19 @@ def test_single_token_tags_across_launches(gpu):
     assert k3moe.workspace_status(ws) == 0
 
 
-def test_single_token_from_a_large_launch_count(gpu):
-    """The tag comes from the launch counters' sum: preset them to a large, consistent count
-    (as after 2**24 - 3 launches) and run across the tag's wrap-around point."""
-    cfg = configs.TP8_B1
-    say(f'case: {cfg.name} seed=5, launch counters preset near the 32-bit wrap')
+@pytest.mark.parametrize('cfg,path', [(configs.TP8_B1, 'single'), (configs.TP8_B1, 'decode'),
+                                      (configs.TP8_B8, 'decode')], ids=['b1-single', 'b1-decode', 'b8-decode'])
+def test_tags_from_a_large_launch_count(gpu, cfg, path):
+    """The tag of the single-token and decode kernels comes from the launch counters' sum: preset
+    them to a large, consistent count (as after 2**32 / G - 3 launches) and run across the tag's
+    wrap-around point."""
+    from k3moe.moe import dims_for, workspace_bytes
+    say(f'case: {cfg.name} seed=5 path={path}, launch counters preset near the 32-bit wrap')
     g = to_dev(synthetic.moe_layer_inputs(cfg, 5), gpu)
-    ref = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, workspace=k3moe.new_workspace(1 << 22, gpu))
-    ws = k3moe.new_workspace(1 << 22, gpu)
+    need = workspace_bytes(dims_for(g['x'], g['router'], g['gate_blocks'], g['down_blocks'], cfg.topk, cfg.gating,
+                                    cfg.activation, None, path))
+    ref = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, path=path, workspace=k3moe.new_workspace(need, gpu))
+    ws = k3moe.new_workspace(need, gpu)
     cus = torch.cuda.get_device_properties(gpu).multi_processor_count
     G = 1
     while G * 2 <= min(cus, 1024):
@@ -298,7 +303,7 @@ def test_single_token_from_a_large_launch_count(gpu):
         ctl[640 + 16 * gi] = v - (1 << 32) if v >= 1 << 31 else v
     torch.cuda.synchronize(gpu)
     for step in range(6):
-        got = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, workspace=ws)
+        got = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, path=path, workspace=ws)
         torch.cuda.synchronize(gpu)
         for key in ('expert_sum', 'expert_ids', 'route_weights'):
             assert torch.equal(got[key], ref[key]), (step, key)
@@ -451,13 +456,14 @@ def test_submission_build_run_matches_moe_step(gpu):
         assert torch.equal(got3[k], want[k]), k
 
 
-@pytest.mark.parametrize('cfg', [configs.TP8_B1, configs.TP8_B8], ids=lambda c: c.name)
+@pytest.mark.parametrize('cfg', [configs.TP8_B8, configs.TP8_B64], ids=lambda c: c.name)
 def test_decode_barrier_counters_wrap(gpu, cfg):
     """The persistent kernel's barrier counters are never reset; they grow by
     whole barriers and wrap at 2**32. Preset them (consistently) two barriers
-    before the wrap and run steps across it: results equal a fresh workspace's
-    and no barrier times out. A wrong target would only hit the barrier's
-    bounded wait, which sets the status word."""
+    before the wrap and run steps across it (these batches run the expert-major
+    down, one grid barrier before the combine): results equal a fresh
+    workspace's and no barrier times out. A wrong target would only hit the
+    barrier's bounded wait, which sets the status word."""
     say(f'case: {cfg.name} seed=5, barrier counters preset 2 barriers before the 32-bit wrap')
     g = to_dev(synthetic.moe_layer_inputs(cfg, 5), gpu)
     from k3moe.moe import dims_for, workspace_bytes
