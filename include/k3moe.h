@@ -280,9 +280,9 @@ int k3moe_mxfp4_decode(const uint8_t *blocks, const uint8_t *scales, int64_t n_b
 
 /* MXFP4 encode, pack_mxfp4 (megabench/tasks/quantization.py:13-37): n_blocks
  * groups of 32 consecutive values of in_dtype (K3MOE_DTYPE_F32, _BF16 or
- * _F16; in 16-byte aligned for f32, 8-byte for the others) -> n_blocks blocks
- * of 16 bytes (byte j: element 2j in the low nibble, 2j+1 in the high one;
- * blocks 2-byte aligned) and n_blocks E8M0 scale bytes. Bit for bit with the
+ * _F16; in 16-byte aligned) -> n_blocks blocks of 16 bytes (byte j: element
+ * 2j in the low nibble, 2j+1 in the high one; blocks 4-byte aligned) and
+ * n_blocks E8M0 scale bytes. Bit for bit with the
  * reference's torch CPU chain: block exponent ceil(log2(max|x|/6)) with the
  * fp32 logarithm rounded to nearest (clamped to [-126, 127]), fp32 products
  * x 2^-e, round to nearest with ties to the even code; a block holding a NaN

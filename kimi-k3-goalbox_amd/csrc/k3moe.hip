@@ -519,10 +519,9 @@ int k3moe_mxfp4_encode(const void *in, int32_t in_dtype, int64_t n_blocks, uint8
     return fail(K3MOE_EINVAL, "in_dtype must be f32, bf16 or f16, got %d", in_dtype);
   if (n_blocks == 0) return K3MOE_OK;
   if (!in || !blocks || !scales) return fail(K3MOE_EINVAL, "a required pointer is NULL");
-  const uintptr_t align = in_dtype == K3MOE_DTYPE_F32 ? 16 : 8;
-  if (reinterpret_cast<uintptr_t>(in) % align || reinterpret_cast<uintptr_t>(blocks) % 2)
-    return fail(K3MOE_EINVAL, "in must be %d-byte aligned and blocks 2-byte aligned", (int)align);
-  long grid = (long)((n_blocks + kEncThreads / 8 - 1) / (kEncThreads / 8));
+  if (reinterpret_cast<uintptr_t>(in) % 16 || reinterpret_cast<uintptr_t>(blocks) % 4)
+    return fail(K3MOE_EINVAL, "in must be 16-byte aligned and blocks 4-byte aligned");
+  long grid = (long)((n_blocks + kEncThreads / 4 - 1) / (kEncThreads / 4));
   if (grid > 16384) grid = 16384;
   hipLaunchKernelGGL(k_encode, dim3((unsigned)grid), dim3(kEncThreads), 0, reinterpret_cast<hipStream_t>(stream), in,
                      in_dtype, n_blocks, blocks, scales);

@@ -21,10 +21,11 @@
 // int32 as INT_MIN, so the scale byte wraps to 127 and ldexp scales by
 // 2^INT_MIN = 0 (NaN and infinite elements then take code 7, finite ones 0).
 //
-// Layout: 8 lanes per block, lane s of the group holding elements 4s .. 4s+3
-// (one 16-byte load of fp32, 8 bytes of bf16 / fp16), so a wave reads 8
-// consecutive blocks with contiguous loads and writes their 128 packed bytes
-// with contiguous 2-byte stores; the block maximum is three xor-shuffles.
+// Layout: 4 lanes per block, lane s of the group holding elements 8s .. 8s+7
+// (one 16-byte load of bf16 / fp16, two of fp32), so a wave reads 16
+// consecutive blocks with contiguous 16-byte loads and writes their 256 packed
+// bytes with contiguous 4-byte stores and their 16 scale bytes with one byte
+// store per block; the block maximum is two xor-shuffles.
 // HBM-bound: per block 32 input values in, 17 bytes out.
 #pragma once
 
@@ -66,26 +67,35 @@ __device__ __forceinline__ float pow2_neg(int e) {
 // in_dtype: K3MOE_DTYPE_F32 / _BF16 / _F16 (values converted to fp32 exactly)
 __global__ __launch_bounds__(kEncThreads) void k_encode(const void *__restrict__ in, int in_dtype, int64_t n_blocks,
                                                         uint8_t *__restrict__ blocks, uint8_t *__restrict__ scales) {
-  const int s = threadIdx.x & 7;
-  const int64_t stride = (int64_t)gridDim.x * (kEncThreads / 8);
-  for (int64_t blk = (int64_t)blockIdx.x * (kEncThreads / 8) + (threadIdx.x >> 3); blk < n_blocks; blk += stride) {
-    float v[4];
+  const int s = threadIdx.x & 3;
+  const int64_t stride = (int64_t)gridDim.x * (kEncThreads / 4);
+  for (int64_t blk = (int64_t)blockIdx.x * (kEncThreads / 4) + (threadIdx.x >> 2); blk < n_blocks; blk += stride) {
+    float v[8];
     if (in_dtype == 1) {  // fp32
-      const u32x4 w = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const float *>(in) + blk * 32 + 4 * s);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] = __uint_as_float(w[t]);
-    } else {
-      const u32x2 w = *reinterpret_cast<const u32x2 *>(reinterpret_cast<const uint16_t *>(in) + blk * 32 + 4 * s);
+      const float *src = reinterpret_cast<const float *>(in) + blk * 32 + 8 * s;
+      const u32x4 w0 = *reinterpret_cast<const u32x4 *>(src), w1 = *reinterpret_cast<const u32x4 *>(src + 4);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
+        v[t] = __uint_as_float(w0[t]);
+        v[4 + t] = __uint_as_float(w1[t]);
+      }
+    } else {
+      const u32x4 w = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint16_t *>(in) + blk * 32 + 8 * s);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
         const uint32_t h = (w[t >> 1] >> (16 * (t & 1))) & 0xFFFFu;
         v[t] = in_dtype == 0 ? __uint_as_float(h << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)h);
       }
     }
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    int nan = (v[0] != v[0]) | (v[1] != v[1]) | (v[2] != v[2]) | (v[3] != v[3]);
+    float amax = 0.f;
+    int nan = 0;
 #pragma unroll
-    for (int m = 1; m < 8; m <<= 1) {
+    for (int t = 0; t < 8; ++t) {
+      amax = fmaxf(amax, fabsf(v[t]));
+      nan |= v[t] != v[t];
+    }
+#pragma unroll
+    for (int m = 1; m < 4; m <<= 1) {
       amax = fmaxf(amax, shfl_xor(amax, m));
       nan |= shfl_xor(nan, m);
     }
@@ -99,11 +109,10 @@ __global__ __launch_bounds__(kEncThreads) void k_encode(const void *__restrict__
       sbyte = (uint32_t)(e + 127);
       step = pow2_neg(e);
     }
-    uint32_t c[4];
+    uint32_t packed = 0u;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) c[t] = e2m1_code(__fmul_rn(v[t], step));
-    const uint16_t packed = (uint16_t)(c[0] | (c[1] << 4) | (c[2] << 8) | (c[3] << 12));
-    *reinterpret_cast<uint16_t *>(blocks + blk * 16 + 2 * s) = packed;
+    for (int t = 0; t < 8; ++t) packed |= e2m1_code(__fmul_rn(v[t], step)) << (4 * t);
+    *reinterpret_cast<uint32_t *>(blocks + blk * 16 + 4 * s) = packed;
     if (s == 0) scales[blk] = (uint8_t)sbyte;
   }
 }

@@ -296,6 +296,8 @@ def pack_mxfp4(matrix: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     if matrix.dtype not in _ENCODE_DTYPES:
         matrix = matrix.float()
     src = matrix.contiguous()
+    if src.data_ptr() % 16:  # a view starting inside a 16-byte word: the encoder reads 16-byte words
+        src = src.clone()
     lead, n = tuple(matrix.shape[:-1]), matrix.shape[-1] // MX_BLOCK
     packed = torch.empty(*lead, n, MX_BLOCK // 2, dtype=torch.uint8, device=matrix.device)
     scales = torch.empty(*lead, n, dtype=torch.uint8, device=matrix.device)

@@ -85,6 +85,12 @@ def test_encode_empty_and_ragged(gpu):
     p, s = k3moe.pack_mxfp4(x)
     q, t = pack_ref.pack_mxfp4(x.cpu())
     assert torch.equal(p.cpu(), q) and torch.equal(s.cpu(), t)
+    # a contiguous view that starts 8 bytes into its storage
+    base = torch.randn(8 + 4*64, device=gpu).to(torch.bfloat16)
+    xv = base[4:4 + 4*64].view(4, 64)
+    p, s = k3moe.pack_mxfp4(xv)
+    q, t = pack_ref.pack_mxfp4(xv.cpu())
+    assert torch.equal(p.cpu(), q) and torch.equal(s.cpu(), t)
     xi = torch.randint(-40, 40, (4, 64), device=gpu, dtype=torch.int32)
     p, s = k3moe.pack_mxfp4(xi)
     q, t = pack_ref.pack_mxfp4(xi.cpu())
