@@ -22,23 +22,24 @@
 //     byte is the one of block q (k 32q .. 32q + 31), whatever lane holds it.
 //   D (16 x 16 fp32): lane (column j, q) holds rows 4q .. 4q + 3.
 //
-// Unit = (group j, row block nb) as in the bf16 grouped GEMMs: a group is up
-// to kFM = 112 of one active expert's token-expert pairs; a row block is
-// gate/up: 256 rows of I (gate rows and the same up rows), down: 512 rows of
-// the hidden dimension. Four waves (one per SIMD, so each may hold 512
-// registers): wave w owns 8 weight row tiles (gate/up: gate rows 64w .. 64w +
-// 63 and the same up rows, so the activation is applied in registers; down:
-// rows 128w .. 128w + 127) for every 16-token tile of the unit, up to 8 x 7 fp32
-// accumulator tiles (in AGPRs).
-// The unit's weights and activation rows (two terms) move through two LDS
-// slots, filled by direct-to-LDS loads one k-step ahead (the compiler's own
-// waits for loads into registers fall back to waiting for everything across
-// the loop), one barrier per k-step. LDS slot: activation hi then lo, 128 rows
-// x 128 bytes each, the 16-byte chunk c of row r at position c ^ ((r >> 1) & 7)
-// (the B reads of 16 lanes then cover all 64 banks once); the activation scale
-// dwords (blocks 4ks .. 4ks + 3) of each wave's 32 rows (hi at +0, lo at +128
-// of the wave's 256-byte piece); the weight tiles in A-operand lane order; the
-// weight scale dwords of each wave's 128 rows.
+// Unit = (group j, row block nb): a group is up to kFM = 96 of one active
+// expert's token-expert pairs; a row block is gate/up: 128 rows of I (gate
+// rows and the same up rows), down: 256 rows of the hidden dimension. Eight
+// waves, two per SIMD: waves 0-3 run the MFMAs, waves 4-7 issue the loads. A
+// vector-memory issue that waits for room in full memory queues then holds up
+// only its loader wave; with one wave doing both, it held up the MFMAs of its
+// SIMD too. MFMA wave w owns 4 weight row tiles (gate/up: gate rows 32w ..
+// 32w + 31 and the same up rows, so the activation is applied in registers;
+// down: rows 64w .. 64w + 63) for every 16-token tile of the unit, up to 4 x 6
+// fp32 accumulator tiles; loader wave 4 + w fills the LDS pieces MFMA wave w
+// reads. The unit's weights, activation rows (two terms) and scales move
+// through kFRing LDS slots, filled by direct-to-LDS loads two k-steps ahead,
+// one barrier per k-step. LDS slot: activation hi then lo, 96 rows x 128
+// bytes each, the 16-byte chunk c of row r at position c ^ ((r >> 1) & 7) (the
+// B reads of 16 lanes then cover all 64 banks once); the activation scale
+// dwords (blocks 4ks .. 4ks + 3) of each loader's 24 rows (hi at +0, lo at
+// +128 of its 256-byte piece); the weight tiles in A-operand lane order; the
+// weight scale dwords of each MFMA wave's 64 rows.
 //
 // Gate/up epilogue: h = act(bf16(gate), bf16(up)) in bf16 (kimi.py:322), split
 // into two E4M3 terms per 32 columns of I (two gate tiles are one block) and
@@ -52,18 +53,21 @@ namespace k3moe {
 
 typedef __attribute__((ext_vector_type(8))) int i32x8;
 
-constexpr int kFM = 112;                                  // tokens per unit (at most 7 tiles of 16)
-constexpr int kFWaves = 4;                                // one wave per SIMD, 512 registers each
-constexpr int kFThreads = kFWaves * 64;
-constexpr int kFTiles = 8;                                // weight row tiles per wave
-constexpr int kFRing = 2;                                 // k-step slots in LDS
-constexpr int kFSlotX = 128 * 128;                        // one term's rows of a k-step (128 rows)
-constexpr int kFOffXS = 2 * kFSlotX;                      // activation scale pieces (256 B per wave)
-constexpr int kFOffW = kFOffXS + kFWaves * 256;           // weight tiles (1 KiB each, 8 per wave)
-constexpr int kFOffWS = kFOffW + kFWaves * kFTiles * 1024;  // weight scale pieces (512 B per wave)
-constexpr int kFSlot = kFOffWS + kFWaves * 512;           // 68608 bytes
-constexpr int kFLds = kFRing * kFSlot;                    // 137216 bytes
-constexpr int kFAhead = kFRing - 1;                       // k-steps of loads in flight beyond the current one
+constexpr int kFM = 96;                                   // tokens per unit (at most 6 tiles of 16)
+constexpr int kFWaves = 4;                                // MFMA waves (one per SIMD) and as many loaders
+constexpr int kFThreads = 2 * kFWaves * 64;
+constexpr int kFTiles = 4;                                // weight row tiles per MFMA wave
+constexpr int kFRing = 3;                                 // k-step slots in LDS
+constexpr int kFSlotX = kFM * 128;                        // one term's rows of a k-step (96 rows)
+constexpr int kFOffXS = 2 * kFSlotX;                      // activation scale pieces (256 B per loader)
+constexpr int kFOffW = kFOffXS + kFWaves * 256;           // weight tiles (1 KiB each, kFTiles per wave)
+constexpr int kFOffWS = kFOffW + kFWaves * kFTiles * 1024;  // weight scale pieces (256 B per wave)
+constexpr int kFSlot = kFOffWS + kFWaves * 256;           // 43008 bytes
+constexpr int kFLds = kFRing * kFSlot;                    // 129024 bytes
+constexpr int kFAhead = kFRing - 1;                       // k-steps of loads issued ahead of the current one
+constexpr int kFRowsL = kFM / kFWaves;                    // activation rows a loader stages (24)
+constexpr int kFLoads = 2 * kFRowsL / 8 + 1 + kFTiles + 1;  // a loader's loads per k-step (rows, their scales, tiles, theirs)
+static_assert(kFRowsL % 8 == 0, "8-row activation loads");
 
 // ------------------------------------------------------ two-term MXFP8 --
 
@@ -167,10 +171,12 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
                                                        const uint8_t *__restrict__ scl1, char *ws) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   __shared__ int s_gstart[kMaxExperts + 1];  // first group of each active expert
-  __shared__ int s_wsum[kFWaves];
-  __shared__ int s_row[128];                 // activation row of each staged row (-1: none)
+  __shared__ int s_wsum[2 * kFWaves];
+  __shared__ int s_row[kFM];                 // activation row of each staged row (-1: none)
   const int tid = threadIdx.x, l = tid & 63, i = l & 15, q = l >> 4;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool loader = wv >= kFWaves;
+  const int w = wv & (kFWaves - 1);  // the MFMA wave (or the one this loader feeds)
   const int nact = *reinterpret_cast<const int *>(ws + pl.o_nact);
   const int *active = reinterpret_cast<const int *>(ws + pl.o_active);
   const int *aoff = reinterpret_cast<const int *>(ws + pl.o_aoff);
@@ -178,26 +184,26 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
   const int *ptok = reinterpret_cast<const int *>(ws + pl.o_ptok);
   const uint8_t *zero = reinterpret_cast<const uint8_t *>(ws + pl.o_zero);
 
-  // groups per active expert, exclusive prefix (four experts per thread)
+  // groups per active expert, exclusive prefix (two experts per thread)
   {
-    int t4[4], sum = 0;
+    int t2[2], sum = 0;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int dd = 4 * tid + u;
-      t4[u] = dd < nact ? (acnt[dd] + kFM - 1) / kFM : 0;
-      sum += t4[u];
+    for (int u = 0; u < 2; ++u) {
+      const int dd = 2 * tid + u;
+      t2[u] = dd < nact ? (acnt[dd] + kFM - 1) / kFM : 0;
+      sum += t2[u];
     }
     const int incl = wave_incl_scan(sum);
-    if (l == 63) s_wsum[w] = incl;
+    if (l == 63) s_wsum[wv] = incl;
     __syncthreads();
     int base = 0;
-    for (int ww = 0; ww < w; ++ww) base += s_wsum[ww];
+    for (int ww = 0; ww < wv; ++ww) base += s_wsum[ww];
     int excl = base + incl - sum;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int dd = 4 * tid + u;
+    for (int u = 0; u < 2; ++u) {
+      const int dd = 2 * tid + u;
       if (dd < nact) s_gstart[dd] = excl;
-      excl += t4[u];
+      excl += t2[u];
     }
     if (tid == kFThreads - 1) s_gstart[nact] = base + incl;
     __syncthreads();
@@ -206,7 +212,7 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
   const int Kd = a.width;                  // reduction length, a multiple of 128
   const int KB = Kd / kBlockK, KS = Kd / 128;
   const int Nout = GU ? pl.I : pl.K;
-  const int RPB = GU ? 256 : 512;          // output rows per unit
+  const int RPB = GU ? 128 : 256;          // output rows per unit
   const int NB = Nout / RPB;
   const int xcds = gridDim.x < 8 ? (int)gridDim.x : 8;
   const int xcd = blockIdx.x % xcds, nslot = gridDim.x / xcds, slot = blockIdx.x / xcds;
@@ -229,62 +235,57 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
     const int d = lo_, mt = (int)j - s_gstart[d];
     const int e = active[d], p0 = aoff[d] + mt * kFM;
     const int m = min(kFM, acnt[d] - mt * kFM), T = (m + 15) / 16;
-    wait_vm<0>();     // the previous unit's stores are done (the waits below count loads only)
+    wait_vm<0>();     // the previous unit's loads and stores are done
     __syncthreads();  // the previous unit is done with the ring and s_row
-    for (int r = tid; r < 128; r += kFThreads) s_row[r] = r < m ? (GU ? ptok[p0 + r] : p0 + r) : -1;
+    if (tid < kFM) s_row[tid] = tid < m ? (GU ? ptok[p0 + tid] : p0 + tid) : -1;
     __syncthreads();
 
-    // this wave's 8 weight row tiles: gate/up: gate rows 64w + 16r (r < 4),
-    // then the same up rows; down: rows 128w + 16r. Weight load r: lane (i, q)
-    // takes block 4 ks + q of its row (16 bytes), landing at the tile's 1 KiB
-    // in lane order, i.e. in the A-operand layout; scale load h: lane L takes
-    // the dword of blocks 4 ks .. 4 ks + 3 of row L % 16 of tile 4 h + L / 16.
-    // Addresses: a per-lane byte offset from a wave-uniform base, tiles a
-    // wave-uniform stride apart.
-    const size_t wrow = (size_t)e * Nout + nb * RPB + (GU ? 64 : 128) * w;
-    const uint8_t *const wg = blk0 + (wrow * KB + q) * 16;                       // gate (down) tiles
-    const uint8_t *const wu = (GU ? blk1 : blk0) + (wrow * KB + q) * 16 + (GU ? 0 : 64 * KB * 16);
-    const uint32_t wlane = (uint32_t)i * KB * 16;                                // row i of a tile
-    const size_t wtile = (size_t)16 * KB * 16;                                   // tile stride
-    const uint8_t *const sg = scl0 + wrow * KB, *const su = (GU ? scl1 : scl0) + wrow * KB + (GU ? 0 : 64 * KB);
-    const uint32_t slane = (uint32_t)(16 * (l >> 4) + (l & 15)) * KB;            // tile L/16, row L%16
-    // this wave's activation rows 32 w .. 32 w + 31: lane L of load u (u < 4: hi,
-    // u >= 4: lo, the same rows) covers row 32 w + 8 (u & 3) + L / 8 at chunk
-    // position L % 8; scale load: lanes 0-31 the hi scale dwords of the rows,
-    // lanes 32-63 the lo ones. Loads whose rows all lie past the unit's tokens
-    // are not issued: the slot keeps stale bytes there, which reach only
-    // accumulator columns of tokens that are not stored. Lanes of an issued
-    // load whose row has no token read the zero area.
-    uint32_t aoffs[4];
-    bool arow[4];
+    // Loader 4 + w: MFMA wave w's 4 weight row tiles (gate/up: gate rows 32w +
+    // 16r, r < 2, then the same up rows; down: rows 64w + 16r). Weight load r:
+    // lane (i, q) takes block 4 ks + q of its row (16 bytes), landing at the
+    // tile's 1 KiB in lane order, i.e. in the A-operand layout; scale load:
+    // lane L takes the dword of blocks 4 ks .. 4 ks + 3 of row L % 16 of tile
+    // L / 16. Activation rows 24 w .. 24 w + 23: lane L of load u (u < 3: hi,
+    // u >= 3: lo, the same rows) covers row 24 w + 8 (u % 3) + L / 8 at chunk
+    // position L % 8; scale load (lane L lands at +4 L of the loader's
+    // 256-byte piece): lanes 0-23 the hi scale dwords of the rows, lanes
+    // 32-55 the lo ones (at +128), the other lanes read the zero area. Every load is issued (rows without a token read
+    // the zero area), so that every k-step issues kFLoads of them.
+    const size_t wrow = (size_t)e * Nout + nb * RPB + (GU ? 32 : 64) * w;
+    const uint32_t wlane = (uint32_t)i * KB * 16 + q * 16;                 // row i of a tile, block q
+    const size_t wtile = (size_t)16 * KB * 16;                             // tile stride
+    auto tile_ptr = [&](int r) {                                           // tile r's first row, lane's block
+      return GU ? (r < 2 ? blk0 : blk1) + (wrow + 16 * (r & 1)) * KB * 16 + wlane
+                : blk0 + wrow * KB * 16 + r * wtile + wlane;
+    };
+    const int st = l >> 4, sr = l & 15;                                    // scale load: tile, row
+    const uint8_t *const sptr = GU ? (st < 2 ? scl0 : scl1) + (wrow + 16 * (st & 1) + sr) * KB
+                                   : scl0 + (wrow + 16 * st + sr) * KB;
+    constexpr int kNR = kFRowsL / 8;  // 8-row loads per term
+    uint32_t aoffs[kNR];
+    bool arow[kNR];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int r = 32 * w + 8 * u + (l >> 3);
+    for (int u = 0; u < kNR; ++u) {
+      const int r = kFRowsL * w + 8 * u + (l >> 3);
       const int c = (l & 7) ^ ((r >> 1) & 7);
       const int ar = s_row[r];
       arow[u] = ar >= 0;
       aoffs[u] = ar >= 0 ? (uint32_t)ar * (uint32_t)Kd + (uint32_t)c * 16 : (uint32_t)(l & 7) * 16;
     }
-    const int sar = s_row[32 * w + (l & 31)];
+    const int sar = (l & 31) < kFRowsL ? s_row[kFRowsL * w + (l & 31)] : -1;
     const bool srow = sar >= 0;
     const uint32_t soff = srow ? (uint32_t)sar * (uint32_t)KB : 0u;
     const uint8_t *const sbase = l < 32 ? a.shi : a.slo;
-    int fill = 0;
-    auto issue = [&](int ks) {
-      char *base = lds + fill * kFSlot;
-      fill ^= 1;
+    auto issue = [&](int ks) {  // a loader's loads of step ks into slot ks % kFRing
+      char *base = lds + (ks % kFRing) * kFSlot;
 #pragma unroll
-      for (int r = 0; r < kFTiles; ++r)
-        load_lds<16>((r < 4 ? wg + r * wtile : wu + (r - 4) * wtile) + wlane + ks * 64,
-                     base + kFOffW + (kFTiles * w + r) * 1024);
-      load_lds<4>(sg + slane + 4 * ks, base + kFOffWS + w * 512);
-      load_lds<4>(su + slane + 4 * ks, base + kFOffWS + w * 512 + 256);
+      for (int r = 0; r < kFTiles; ++r) load_lds<16>(tile_ptr(r) + ks * 64, base + kFOffW + (kFTiles * w + r) * 1024);
+      load_lds<4>(sptr + 4 * ks, base + kFOffWS + w * 256);
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (32 * w + 8 * (u & 3) < m)  // wave-uniform
-          load_lds<16>(arow[u & 3] ? (u < 4 ? a.hi : a.lo) + aoffs[u & 3] + ks * 128 : zero + aoffs[u & 3],
-                       base + (u >= 4 ? kFSlotX : 0) + (32 * w + 8 * (u & 3)) * 128);
-      if (32 * w < m) load_lds<4>(srow ? sbase + soff + 4 * ks : zero, base + kFOffXS + w * 256);
+      for (int u = 0; u < 2 * kNR; ++u)
+        load_lds<16>(arow[u % kNR] ? (u < kNR ? a.hi : a.lo) + aoffs[u % kNR] + ks * 128 : zero + aoffs[u % kNR],
+                     base + (u >= kNR ? kFSlotX : 0) + (kFRowsL * w + 8 * (u % kNR)) * 128);
+      load_lds<4>(srow ? sbase + soff + 4 * ks : zero, base + kFOffXS + w * 256);
     };
 
     // The k-loop and the epilogue for NT token tiles (a compile-time count: the
@@ -292,41 +293,45 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
     // control flow depends on the count inside the loop).
     auto run = [&](auto nt) {
       constexpr int NT = decltype(nt)::value;
+      if (loader) {
+        // k-steps ahead: at the barrier of step ks the loads of ks have landed and
+        // the MFMA waves are done with step ks - 1, whose slot takes step ks + 2
+        static_assert(kFAhead == 2, "two k-steps ahead");
+        issue(0);
+        if (1 < KS) issue(1);
+        for (int ks = 0; ks < KS; ++ks) {
+          if (ks + 1 < KS) wait_vm<kFLoads>();  // step ks landed (step ks + 1's loads may be in flight)
+          else wait_vm<0>();
+          ring_barrier();
+          if (ks + 2 < KS) issue(ks + 2);
+        }
+        return;
+      }
       f32x4 acc[kFTiles][NT];
 #pragma unroll
       for (int r = 0; r < kFTiles; ++r)
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-      static_assert(kFRing == 2 && kFAhead == 1, "one k-step of loads in flight");
-      issue(0);
-      int slot_rd = 0;
       for (int ks = 0; ks < KS; ++ks) {
-        wait_vm<0>();    // this wave's loads of step ks have landed (none later are in flight)
-        ring_barrier();  // everyone's have, and everyone is done with step ks - 1's slot
-        if (ks + 1 < KS) issue(ks + 1);
-        const char *base = lds + slot_rd * kFSlot;
-        slot_rd ^= 1;
+        ring_barrier();  // the loaders' loads of step ks have landed
+        const char *base = lds + (ks % kFRing) * kFSlot;
         u32x4 wa[kFTiles];
         uint32_t sa[kFTiles];
 #pragma unroll
         for (int r = 0; r < kFTiles; ++r) {
           wa[r] = *reinterpret_cast<const u32x4 *>(base + kFOffW + (kFTiles * w + r) * 1024 + 16 * l);
-          sa[r] = *reinterpret_cast<const uint8_t *>(base + kFOffWS + w * 512 + 4 * (16 * r + i) + q);
+          sa[r] = *reinterpret_cast<const uint8_t *>(base + kFOffWS + w * 256 + 4 * (16 * r + i) + q);
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          // one token tile's operand reads at a time: hoisting every tile's reads
-          // would not fit beside the accumulators
-          __builtin_amdgcn_sched_barrier(0);
           const int row = 16 * t + i, sw = (row >> 1) & 7;
           const char *hr = base + row * 128, *lr = hr + kFSlotX;
           const u32x4 h0 = *reinterpret_cast<const u32x4 *>(hr + ((q ^ sw) * 16));
           const u32x4 h1 = *reinterpret_cast<const u32x4 *>(hr + (((4 + q) ^ sw) * 16));
           const u32x4 l0 = *reinterpret_cast<const u32x4 *>(lr + ((q ^ sw) * 16));
           const u32x4 l1 = *reinterpret_cast<const u32x4 *>(lr + (((4 + q) ^ sw) * 16));
-          // rows 16t .. 16t + 15 were staged by wave t / 2, at row 16 (t & 1) + i of its piece
-          const char *sp = base + kFOffXS + (t >> 1) * 256 + 4 * (16 * (t & 1) + i) + q;
+          // row 16t + i was staged by loader row / 24, at row row % 24 of its piece
+          const char *sp = base + kFOffXS + (row / kFRowsL) * 256 + 4 * (row % kFRowsL) + q;
           const uint32_t sbh = *reinterpret_cast<const uint8_t *>(sp);
           const uint32_t sbl = *reinterpret_cast<const uint8_t *>(sp + 128);
           const i32x8 bh = {(int)h0[0], (int)h0[1], (int)h0[2], (int)h0[3],
@@ -339,6 +344,7 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
           for (int r = 0; r < kFTiles; ++r) acc[r][t] = mfma_fp4x8(wa[r], bl, sa[r], sbl, acc[r][t]);
         }
       }
+      // (no barrier here: loaders and MFMA waves pass exactly KS barriers per unit)
 
       // epilogue: lane (token column i, q) holds rows 4q .. 4q + 3 of each tile
 #pragma unroll
@@ -347,51 +353,47 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
         const bool ok = jrow < m;
         const size_t p = (size_t)(p0 + (ok ? jrow : 0));
         if constexpr (GU) {
-          // two 32-column blocks of I per token: gate tiles 2b, 2b + 1 with up tiles 4 + 2b, 5 + 2b
+          // one 32-column block of I per token: gate tiles 0, 1 with up tiles 2, 3
+          float h[2][4];
 #pragma unroll
-          for (int b = 0; b < 2; ++b) {
-            float h[2][4];
+          for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-            for (int s = 0; s < 2; ++s)
+            for (int vv = 0; vv < 4; ++vv)
+              h[s2][vv] = round_bf16(apply_act(pl.act, round_bf16(acc[s2][t][vv]), round_bf16(acc[2 + s2][t][vv])));
+          float m8 = 0.f;
 #pragma unroll
-              for (int vv = 0; vv < 4; ++vv)
-                h[s][vv] = round_bf16(apply_act(pl.act, round_bf16(acc[2 * b + s][t][vv]),
-                                                round_bf16(acc[4 + 2 * b + s][t][vv])));
-            float m8 = 0.f;
+          for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-            for (int s = 0; s < 2; ++s)
+            for (int vv = 0; vv < 4; ++vv) m8 = fmaxf(m8, fabsf(h[s2][vv]));
+          const uint32_t sh = mx8_scale(group_amax<16, 32>(m8));
+          const float ih = mx8_inv(sh), vh = mx8_val(sh);
+          uint32_t hw[2], lw[2];
+          float rr[2][4];
 #pragma unroll
-              for (int vv = 0; vv < 4; ++vv) m8 = fmaxf(m8, fabsf(h[s][vv]));
-            const uint32_t sh = mx8_scale(group_amax<16, 32>(m8));
-            const float ih = mx8_inv(sh), vh = mx8_val(sh);
-            uint32_t hw[2], lw[2];
-            float rr[2][4];
+          for (int s2 = 0; s2 < 2; ++s2) {
+            hw[s2] = e4m3x4(h[s2][0] * ih, h[s2][1] * ih, h[s2][2] * ih, h[s2][3] * ih);
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-              hw[s] = e4m3x4(h[s][0] * ih, h[s][1] * ih, h[s][2] * ih, h[s][3] * ih);
+            for (int vv = 0; vv < 4; ++vv) rr[s2][vv] = __fsub_rn(h[s2][vv], __fmul_rn(e4m3_f32(hw[s2], vv), vh));
+          }
+          float mr = 0.f;
 #pragma unroll
-              for (int vv = 0; vv < 4; ++vv) rr[s][vv] = __fsub_rn(h[s][vv], __fmul_rn(e4m3_f32(hw[s], vv), vh));
+          for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) mr = fmaxf(mr, fabsf(rr[s2][vv]));
+          const uint32_t sl = mx8_scale(group_amax<16, 32>(mr));
+          const float il = mx8_inv(sl);
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) lw[s2] = e4m3x4(rr[s2][0] * il, rr[s2][1] * il, rr[s2][2] * il, rr[s2][3] * il);
+          if (ok) {
+            const int c0 = nb * RPB + 32 * w;  // the block's first column of I
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+              *reinterpret_cast<uint32_t *>(hq_hi + p * pl.I + c0 + 16 * s2 + 4 * q) = hw[s2];
+              *reinterpret_cast<uint32_t *>(hq_lo + p * pl.I + c0 + 16 * s2 + 4 * q) = lw[s2];
             }
-            float mr = 0.f;
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
-#pragma unroll
-              for (int vv = 0; vv < 4; ++vv) mr = fmaxf(mr, fabsf(rr[s][vv]));
-            const uint32_t sl = mx8_scale(group_amax<16, 32>(mr));
-            const float il = mx8_inv(sl);
-#pragma unroll
-            for (int s = 0; s < 2; ++s) lw[s] = e4m3x4(rr[s][0] * il, rr[s][1] * il, rr[s][2] * il, rr[s][3] * il);
-            if (ok) {
-              const int c0 = nb * RPB + 64 * w + 32 * b;  // the block's first column of I
-#pragma unroll
-              for (int s = 0; s < 2; ++s) {
-                *reinterpret_cast<uint32_t *>(hq_hi + p * pl.I + c0 + 16 * s + 4 * q) = hw[s];
-                *reinterpret_cast<uint32_t *>(hq_lo + p * pl.I + c0 + 16 * s + 4 * q) = lw[s];
-              }
-              if (q == 0) {
-                hq_shi[p * (pl.I / kBlockK) + c0 / kBlockK] = (uint8_t)sh;
-                hq_slo[p * (pl.I / kBlockK) + c0 / kBlockK] = (uint8_t)sl;
-              }
+            if (q == 0) {
+              hq_shi[p * (pl.I / kBlockK) + c0 / kBlockK] = (uint8_t)sh;
+              hq_slo[p * (pl.I / kBlockK) + c0 / kBlockK] = (uint8_t)sl;
             }
           }
         } else {
@@ -401,21 +403,20 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
               const f32x4 a4 = acc[r][t];
               const u32x2 packed = {(uint32_t)f32_to_bf16_bits(a4[0]) | ((uint32_t)f32_to_bf16_bits(a4[1]) << 16),
                                     (uint32_t)f32_to_bf16_bits(a4[2]) | ((uint32_t)f32_to_bf16_bits(a4[3]) << 16)};
-              *reinterpret_cast<u32x2 *>(ybuf + p * pl.K + nb * RPB + 128 * w + 16 * r + 4 * q) = packed;
+              *reinterpret_cast<u32x2 *>(ybuf + p * pl.K + nb * RPB + 64 * w + 16 * r + 4 * q) = packed;
             }
           }
         }
       }
     };
-    static_assert(kFM <= 112, "at most 7 token tiles: 8 x 7 accumulator tiles leave AGPRs to spare");
-    switch (T) {  // 1 .. 7 (m in 1 .. kFM)
+    static_assert(kFM == 96, "at most 6 token tiles");
+    switch (T) {  // 1 .. 6 (m in 1 .. kFM)
       case 1: run(IntC<1>{}); break;
       case 2: run(IntC<2>{}); break;
       case 3: run(IntC<3>{}); break;
       case 4: run(IntC<4>{}); break;
       case 5: run(IntC<5>{}); break;
-      case 6: run(IntC<6>{}); break;
-      default: run(IntC<7>{}); break;
+      default: run(IntC<6>{}); break;
     }
   }
 }
