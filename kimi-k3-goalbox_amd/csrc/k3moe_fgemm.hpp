@@ -38,8 +38,11 @@
 // bytes each, the 16-byte chunk c of row r at position c ^ ((r >> 1) & 7) (the
 // B reads of 16 lanes then cover all 64 banks once); the activation scale
 // dwords (blocks 4ks .. 4ks + 3) of each loader's 24 rows (hi at +0, lo at
-// +128 of its 256-byte piece); the weight tiles in A-operand lane order; the
-// weight scale dwords of each MFMA wave's 64 rows.
+// +128 of its 256-byte piece); the weight tiles in A-operand lane order. The
+// weight scales go through two further LDS buffers in chunks of 16 k-steps
+// (64 bytes of each of the unit's weight rows): a scale row of a unit's 256
+// weight rows is then read from memory in whole 64-byte pieces rather than 4
+// bytes per k-step, whose 128-byte lines were fetched about ten times each.
 //
 // Gate/up epilogue: h = act(bf16(gate), bf16(up)) in bf16 (kimi.py:322), split
 // into two E4M3 terms per 32 columns of I (two gate tiles are one block) and
@@ -61,12 +64,14 @@ constexpr int kFRing = 3;                                 // k-step slots in LDS
 constexpr int kFSlotX = kFM * 128;                        // one term's rows of a k-step (96 rows)
 constexpr int kFOffXS = 2 * kFSlotX;                      // activation scale pieces (256 B per loader)
 constexpr int kFOffW = kFOffXS + kFWaves * 256;           // weight tiles (1 KiB each, kFTiles per wave)
-constexpr int kFOffWS = kFOffW + kFWaves * kFTiles * 1024;  // weight scale pieces (256 B per wave)
-constexpr int kFSlot = kFOffWS + kFWaves * 256;           // 43008 bytes
-constexpr int kFLds = kFRing * kFSlot;                    // 129024 bytes
+constexpr int kFSlot = kFOffW + kFWaves * kFTiles * 1024;  // 41984 bytes
+constexpr int kFScSteps = 16;                             // k-steps per weight-scale chunk (64 bytes of a row)
+constexpr int kFScBuf = kFWaves * kFTiles * 16 * 64;      // one chunk of the unit's 256 weight rows (16 KiB)
+constexpr int kFOffSc = kFRing * kFSlot;                  // the two chunk buffers
+constexpr int kFLds = kFOffSc + 2 * kFScBuf;              // 158720 bytes
 constexpr int kFAhead = kFRing - 1;                       // k-steps of loads issued ahead of the current one
 constexpr int kFRowsL = kFM / kFWaves;                    // activation rows a loader stages (24)
-constexpr int kFLoads = 2 * kFRowsL / 8 + 1 + kFTiles + 1;  // a loader's loads per k-step (rows, their scales, tiles, theirs)
+constexpr int kFLoads = 2 * kFRowsL / 8 + 1 + kFTiles;    // a loader's loads per k-step (rows, their scales, tiles)
 static_assert(kFRowsL % 8 == 0, "8-row activation loads");
 
 // ------------------------------------------------------ two-term MXFP8 --
@@ -149,6 +154,9 @@ __device__ __forceinline__ f32x4 mfma_fp4x8(const u32x4 &a, const i32x8 &b, uint
   const i32x8 a8 = {(int)a[0], (int)a[1], (int)a[2], (int)a[3], 0, 0, 0, 0};
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, b, c, 4, 0, 0, (int)sa, 0, (int)sb);
 }
+
+// s_waitcnt with lgkmcnt(0) and the other counters at their maxima (no wait on them)
+constexpr int kLgkmZero = 0xC07F;
 
 template <int N>
 struct IntC {
@@ -243,14 +251,16 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
     // Loader 4 + w: MFMA wave w's 4 weight row tiles (gate/up: gate rows 32w +
     // 16r, r < 2, then the same up rows; down: rows 64w + 16r). Weight load r:
     // lane (i, q) takes block 4 ks + q of its row (16 bytes), landing at the
-    // tile's 1 KiB in lane order, i.e. in the A-operand layout; scale load:
-    // lane L takes the dword of blocks 4 ks .. 4 ks + 3 of row L % 16 of tile
-    // L / 16. Activation rows 24 w .. 24 w + 23: lane L of load u (u < 3: hi,
-    // u >= 3: lo, the same rows) covers row 24 w + 8 (u % 3) + L / 8 at chunk
-    // position L % 8; scale load (lane L lands at +4 L of the loader's
-    // 256-byte piece): lanes 0-23 the hi scale dwords of the rows, lanes
-    // 32-55 the lo ones (at +128), the other lanes read the zero area. Every load is issued (rows without a token read
-    // the zero area), so that every k-step issues kFLoads of them.
+    // tile's 1 KiB in lane order, i.e. in the A-operand layout. Activation rows:
+    // the 8-row blocks w, w + 4, w + 8; lane L of load u (u < 3: hi, u >= 3:
+    // lo, the same rows) covers row 8 (w + 4 (u % 3)) + L / 8 at chunk position
+    // L % 8. Scale load (lane L lands at +4 L of the loader's 256-byte piece):
+    // lanes 0-23 the hi scale dwords of rows 4 L + w, lanes 32-55 the lo ones
+    // (at +128), the other lanes read the zero area; a token tile's scale
+    // addresses then differ from the next tile's by a constant. Every load is
+    // issued (rows without a
+    // token read the zero area), so that every k-step issues kFLoads of them
+    // (and kFTiles more with a weight-scale chunk).
     const size_t wrow = (size_t)e * Nout + nb * RPB + (GU ? 32 : 64) * w;
     const uint32_t wlane = (uint32_t)i * KB * 16 + q * 16;                 // row i of a tile, block q
     const size_t wtile = (size_t)16 * KB * 16;                             // tile stride
@@ -258,33 +268,48 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
       return GU ? (r < 2 ? blk0 : blk1) + (wrow + 16 * (r & 1)) * KB * 16 + wlane
                 : blk0 + wrow * KB * 16 + r * wtile + wlane;
     };
-    const int st = l >> 4, sr = l & 15;                                    // scale load: tile, row
-    const uint8_t *const sptr = GU ? (st < 2 ? scl0 : scl1) + (wrow + 16 * (st & 1) + sr) * KB
-                                   : scl0 + (wrow + 16 * st + sr) * KB;
+    // weight-scale chunk c, tile r: lane L takes bytes 64c + 16 (L % 4) .. + 15
+    // of row L / 4 (the zero area past the row's end), landing at +16 L
+    const int sci = l >> 2, scp = 16 * (l & 3);
+    auto scale_ptr = [&](int r, int c) -> const uint8_t * {
+      if (64 * c + scp >= KB) return zero;
+      return GU ? (r < 2 ? scl0 : scl1) + (wrow + 16 * (r & 1) + sci) * KB + 64 * c + scp
+                : scl0 + (wrow + 16 * r + sci) * KB + 64 * c + scp;
+    };
+    const int NSC = (KS + kFScSteps - 1) / kFScSteps;  // scale chunks of the unit
+    // chunk c lands with the loads of step sc_step(c): 0 for the first, 2 steps
+    // after the first step of chunk c - 1 for the others (its buffer held chunk
+    // c - 2, whose last step is done once that step's barrier has passed)
+    auto chunk_at = [&](int s) { return s == 0 || (s >= 2 && (s - 2) % kFScSteps == 0 && (s - 2) / kFScSteps + 1 < NSC); };
     constexpr int kNR = kFRowsL / 8;  // 8-row loads per term
     uint32_t aoffs[kNR];
     bool arow[kNR];
 #pragma unroll
     for (int u = 0; u < kNR; ++u) {
-      const int r = kFRowsL * w + 8 * u + (l >> 3);
+      const int r = 8 * (w + kFWaves * u) + (l >> 3);
       const int c = (l & 7) ^ ((r >> 1) & 7);
       const int ar = s_row[r];
       arow[u] = ar >= 0;
       aoffs[u] = ar >= 0 ? (uint32_t)ar * (uint32_t)Kd + (uint32_t)c * 16 : (uint32_t)(l & 7) * 16;
     }
-    const int sar = (l & 31) < kFRowsL ? s_row[kFRowsL * w + (l & 31)] : -1;
+    const int sar = (l & 31) < kFRowsL ? s_row[kFWaves * (l & 31) + w] : -1;
     const bool srow = sar >= 0;
     const uint32_t soff = srow ? (uint32_t)sar * (uint32_t)KB : 0u;
     const uint8_t *const sbase = l < 32 ? a.shi : a.slo;
     auto issue = [&](int ks) {  // a loader's loads of step ks into slot ks % kFRing
       char *base = lds + (ks % kFRing) * kFSlot;
+      if (chunk_at(ks)) {
+        const int c = ks == 0 ? 0 : (ks - 2) / kFScSteps + 1;
+#pragma unroll
+        for (int r = 0; r < kFTiles; ++r)
+          load_lds<16>(scale_ptr(r, c), lds + kFOffSc + (c & 1) * kFScBuf + (kFTiles * w + r) * 1024);
+      }
 #pragma unroll
       for (int r = 0; r < kFTiles; ++r) load_lds<16>(tile_ptr(r) + ks * 64, base + kFOffW + (kFTiles * w + r) * 1024);
-      load_lds<4>(sptr + 4 * ks, base + kFOffWS + w * 256);
 #pragma unroll
       for (int u = 0; u < 2 * kNR; ++u)
         load_lds<16>(arow[u % kNR] ? (u < kNR ? a.hi : a.lo) + aoffs[u % kNR] + ks * 128 : zero + aoffs[u % kNR],
-                     base + (u >= kNR ? kFSlotX : 0) + (kFRowsL * w + 8 * (u % kNR)) * 128);
+                     base + (u >= kNR ? kFSlotX : 0) + 8 * (w + kFWaves * (u % kNR)) * 128);
       load_lds<4>(srow ? sbase + soff + 4 * ks : zero, base + kFOffXS + w * 256);
     };
 
@@ -300,8 +325,10 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
         issue(0);
         if (1 < KS) issue(1);
         for (int ks = 0; ks < KS; ++ks) {
-          if (ks + 1 < KS) wait_vm<kFLoads>();  // step ks landed (step ks + 1's loads may be in flight)
-          else wait_vm<0>();
+          // step ks landed (step ks + 1's loads may be in flight)
+          if (ks + 1 >= KS) wait_vm<0>();
+          else if (chunk_at(ks + 1)) wait_vm<kFLoads + kFTiles>();
+          else wait_vm<kFLoads>();
           ring_barrier();
           if (ks + 2 < KS) issue(ks + 2);
         }
@@ -315,33 +342,61 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
       for (int ks = 0; ks < KS; ++ks) {
         ring_barrier();  // the loaders' loads of step ks have landed
         const char *base = lds + (ks % kFRing) * kFSlot;
+        const char *scb = lds + kFOffSc + ((ks / kFScSteps) & 1) * kFScBuf + kFTiles * w * 1024 + 64 * i +
+                          4 * (ks % kFScSteps) + q;
         u32x4 wa[kFTiles];
         uint32_t sa[kFTiles];
 #pragma unroll
         for (int r = 0; r < kFTiles; ++r) {
           wa[r] = *reinterpret_cast<const u32x4 *>(base + kFOffW + (kFTiles * w + r) * 1024 + 16 * l);
-          sa[r] = *reinterpret_cast<const uint8_t *>(base + kFOffWS + w * 256 + 4 * (16 * r + i) + q);
+          sa[r] = *reinterpret_cast<const uint8_t *>(scb + r * 1024);
         }
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
+        // token tile t's B operands (both terms) and scales; the reads of tile
+        // t + 2 go out after the MFMAs of tile t, so that the MFMAs of tile
+        // t + 1 cover their latency (with one MFMA wave per SIMD nothing else does)
+        struct BTile {
+          i32x8 h, l;
+          uint32_t sh, sl;
+        };
+        auto read_b = [&](int t) {
           const int row = 16 * t + i, sw = (row >> 1) & 7;
           const char *hr = base + row * 128, *lr = hr + kFSlotX;
           const u32x4 h0 = *reinterpret_cast<const u32x4 *>(hr + ((q ^ sw) * 16));
           const u32x4 h1 = *reinterpret_cast<const u32x4 *>(hr + (((4 + q) ^ sw) * 16));
           const u32x4 l0 = *reinterpret_cast<const u32x4 *>(lr + ((q ^ sw) * 16));
           const u32x4 l1 = *reinterpret_cast<const u32x4 *>(lr + (((4 + q) ^ sw) * 16));
-          // row 16t + i was staged by loader row / 24, at row row % 24 of its piece
-          const char *sp = base + kFOffXS + (row / kFRowsL) * 256 + 4 * (row % kFRowsL) + q;
-          const uint32_t sbh = *reinterpret_cast<const uint8_t *>(sp);
-          const uint32_t sbl = *reinterpret_cast<const uint8_t *>(sp + 128);
-          const i32x8 bh = {(int)h0[0], (int)h0[1], (int)h0[2], (int)h0[3],
-                            (int)h1[0], (int)h1[1], (int)h1[2], (int)h1[3]};
-          const i32x8 bl = {(int)l0[0], (int)l0[1], (int)l0[2], (int)l0[3],
-                            (int)l1[0], (int)l1[1], (int)l1[2], (int)l1[3]};
+          // the scales of row 16t + i are in the piece of loader row % 4, at row / 4
+          const char *sp = base + kFOffXS + (row % kFWaves) * 256 + 4 * (row / kFWaves) + q;
+          BTile bt;
+          bt.sh = *reinterpret_cast<const uint8_t *>(sp);
+          bt.sl = *reinterpret_cast<const uint8_t *>(sp + 128);
+          bt.h = i32x8{(int)h0[0], (int)h0[1], (int)h0[2], (int)h0[3], (int)h1[0], (int)h1[1], (int)h1[2], (int)h1[3]};
+          bt.l = i32x8{(int)l0[0], (int)l0[1], (int)l0[2], (int)l0[3], (int)l1[0], (int)l1[1], (int)l1[2], (int)l1[3]};
+          return bt;
+        };
+        auto mfma_hi = [&](const BTile &b, int t) {
 #pragma unroll
-          for (int r = 0; r < kFTiles; ++r) acc[r][t] = mfma_fp4x8(wa[r], bh, sa[r], sbh, acc[r][t]);
+          for (int r = 0; r < kFTiles; ++r) acc[r][t] = mfma_fp4x8(wa[r], b.h, sa[r], b.sh, acc[r][t]);
+        };
+        auto mfma_lo = [&](const BTile &b, int t) {
 #pragma unroll
-          for (int r = 0; r < kFTiles; ++r) acc[r][t] = mfma_fp4x8(wa[r], bl, sa[r], sbl, acc[r][t]);
+          for (int r = 0; r < kFTiles; ++r) acc[r][t] = mfma_fp4x8(wa[r], b.l, sa[r], b.sl, acc[r][t]);
+        };
+        // Tile t + 1's reads go out just before the MFMAs of tile t, which cover
+        // their latency, after an explicit wait for tile t's: every wait is then
+        // for everything outstanding, which is what the compiler can count.
+        BTile bb[2];
+        bb[0] = read_b(0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          __builtin_amdgcn_s_waitcnt(kLgkmZero);  // tile t's operands (and at t = 0 the weights) are in
+          __builtin_amdgcn_sched_barrier(0);
+          if (t + 1 < NT) bb[(t + 1) & 1] = read_b(t + 1);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma_hi(bb[t & 1], t);
+          mfma_lo(bb[t & 1], t);
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
       // (no barrier here: loaders and MFMA waves pass exactly KS barriers per unit)
