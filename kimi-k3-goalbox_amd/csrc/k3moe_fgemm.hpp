@@ -71,7 +71,6 @@ constexpr int kFOffSc = kFRing * kFSlot;                  // the two chunk buffe
 constexpr int kFLds = kFOffSc + 2 * kFScBuf;              // 158720 bytes
 constexpr int kFAhead = kFRing - 1;                       // k-steps of loads issued ahead of the current one
 constexpr int kFRowsL = kFM / kFWaves;                    // activation rows a loader stages (24)
-constexpr int kFLoads = 2 * kFRowsL / 8 + 1 + kFTiles;    // a loader's loads per k-step (rows, their scales, tiles)
 static_assert(kFRowsL % 8 == 0, "8-row activation loads");
 
 // ------------------------------------------------------ two-term MXFP8 --
@@ -252,15 +251,15 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
     // 16r, r < 2, then the same up rows; down: rows 64w + 16r). Weight load r:
     // lane (i, q) takes block 4 ks + q of its row (16 bytes), landing at the
     // tile's 1 KiB in lane order, i.e. in the A-operand layout. Activation rows:
-    // the 8-row blocks w, w + 4, w + 8; lane L of load u (u < 3: hi, u >= 3:
-    // lo, the same rows) covers row 8 (w + 4 (u % 3)) + L / 8 at chunk position
-    // L % 8. Scale load (lane L lands at +4 L of the loader's 256-byte piece):
-    // lanes 0-23 the hi scale dwords of rows 4 L + w, lanes 32-55 the lo ones
-    // (at +128), the other lanes read the zero area; a token tile's scale
-    // addresses then differ from the next tile's by a constant. Every load is
-    // issued (rows without a
-    // token read the zero area), so that every k-step issues kFLoads of them
-    // (and kFTiles more with a weight-scale chunk).
+    // the 8-row blocks w + 4u, u < NR (NR = 3 for 6 token tiles); lane L of load
+    // u (u < NR: hi, u >= NR: lo, the same rows) covers row 8 (w + 4 (u % NR)) +
+    // L / 8 at chunk position L % 8. Scale load (lane L lands at +4 L of the
+    // loader's 256-byte piece): lanes 0-23 the hi scale dwords of rows 4 L + w,
+    // lanes 32-55 the lo ones (at +128), the other lanes read the zero area; a
+    // token tile's scale addresses then differ from the next tile's by a
+    // constant. Every load is issued (rows without a token read the zero area),
+    // so that every k-step of a unit issues the same number of them (and kFTiles
+    // more with a weight-scale chunk).
     const size_t wrow = (size_t)e * Nout + nb * RPB + (GU ? 32 : 64) * w;
     const uint32_t wlane = (uint32_t)i * KB * 16 + q * 16;                 // row i of a tile, block q
     const size_t wtile = (size_t)16 * KB * 16;                             // tile stride
@@ -296,7 +295,10 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
     const bool srow = sar >= 0;
     const uint32_t soff = srow ? (uint32_t)sar * (uint32_t)KB : 0u;
     const uint8_t *const sbase = l < 32 ? a.shi : a.slo;
-    auto issue = [&](int ks) {  // a loader's loads of step ks into slot ks % kFRing
+    // a loader's loads of step ks into slot ks % kFRing, with NR 8-row activation
+    // blocks per term (blocks w + 4u, u < NR: those of a unit's token tiles)
+    auto issue = [&](int ks, auto nr) {
+      constexpr int NR = decltype(nr)::value;
       char *base = lds + (ks % kFRing) * kFSlot;
       if (chunk_at(ks)) {
         const int c = ks == 0 ? 0 : (ks - 2) / kFScSteps + 1;
@@ -307,9 +309,9 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
 #pragma unroll
       for (int r = 0; r < kFTiles; ++r) load_lds<16>(tile_ptr(r) + ks * 64, base + kFOffW + (kFTiles * w + r) * 1024);
 #pragma unroll
-      for (int u = 0; u < 2 * kNR; ++u)
-        load_lds<16>(arow[u % kNR] ? (u < kNR ? a.hi : a.lo) + aoffs[u % kNR] + ks * 128 : zero + aoffs[u % kNR],
-                     base + (u >= kNR ? kFSlotX : 0) + 8 * (w + kFWaves * (u % kNR)) * 128);
+      for (int u = 0; u < 2 * NR; ++u)
+        load_lds<16>(arow[u % NR] ? (u < NR ? a.hi : a.lo) + aoffs[u % NR] + ks * 128 : zero + aoffs[u % NR],
+                     base + (u >= NR ? kFSlotX : 0) + 8 * (w + kFWaves * (u % NR)) * 128);
       load_lds<4>(srow ? sbase + soff + 4 * ks : zero, base + kFOffXS + w * 256);
     };
 
@@ -322,15 +324,20 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
         // k-steps ahead: at the barrier of step ks the loads of ks have landed and
         // the MFMA waves are done with step ks - 1, whose slot takes step ks + 2
         static_assert(kFAhead == 2, "two k-steps ahead");
-        issue(0);
-        if (1 < KS) issue(1);
+        // the 8-row blocks of NT token tiles, spread evenly over the 4 loaders
+        // (a loader's blocks past them read the zero area, so that all count alike)
+        constexpr int NR = (NT + 1) / 2;
+        constexpr int kLoads = 2 * NR + 1 + kFTiles;
+        const IntC<NR> nr{};
+        issue(0, nr);
+        if (1 < KS) issue(1, nr);
         for (int ks = 0; ks < KS; ++ks) {
           // step ks landed (step ks + 1's loads may be in flight)
           if (ks + 1 >= KS) wait_vm<0>();
-          else if (chunk_at(ks + 1)) wait_vm<kFLoads + kFTiles>();
-          else wait_vm<kFLoads>();
+          else if (chunk_at(ks + 1)) wait_vm<kLoads + kFTiles>();
+          else wait_vm<kLoads>();
           ring_barrier();
-          if (ks + 2 < KS) issue(ks + 2);
+          if (ks + 2 < KS) issue(ks + 2, nr);
         }
         return;
       }

@@ -485,14 +485,15 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
       const int it = tid + c * kLatThreads;
       const int t = it >> 4, r = it & 15;
       const bool ok = t < B && (!pair || r < 8);
+      // (only the splits that wrote a part: <1>'s part 1 lives in the last few)
       float va[kLatMaxSplits], vb[kLatMaxSplits];
 #pragma unroll
       for (int ss = 0; ss < kLatMaxSplits; ++ss) {
         va[ss] = vb[ss] = 0.f;
         if (ss < SP) {
           const uint32_t o = (uint32_t)((((long)ss * pl.RT + rt) * B + t) * 64 + r * 4);
-          va[ss] = bload4_dev(rp0, ok ? o : kOffNone);
-          vb[ss] = bload4_dev(OUT ? rp1 : rp0, ok && (OUT || pair) ? o + (OUT ? 0 : 32) : kOffNone);
+          va[ss] = bload4_dev(rp0, ok && ss < last0 ? o : kOffNone);
+          vb[ss] = bload4_dev(OUT ? rp1 : rp0, ok && (OUT ? ss >= s0 : pair) ? o + (OUT ? 0 : 32) : kOffNone);
         }
       }
       if (!ok) continue;
