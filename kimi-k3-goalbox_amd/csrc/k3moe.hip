@@ -195,11 +195,14 @@ int latent_plans(const k3moe_latent_dims *d, int n_cus, LatPlan &pin, LatPlan &p
   return K3MOE_OK;
 }
 
-int allow_latent_lds(int out, int bytes) {
-  static int granted[2] = {0, 0};
+int allow_latent_lds(int out, int sk, int bytes) {
+  static int granted[2][2] = {{0, 0}, {0, 0}};
   if (bytes <= 65536) return K3MOE_OK;
-  const void *fn = out ? reinterpret_cast<const void *>(&k_latent<1>) : reinterpret_cast<const void *>(&k_latent<0>);
-  return grant_lds(fn, kLatMaxLds, granted[out], "latent block");
+  const void *fn = sk ? (out ? reinterpret_cast<const void *>(&k_latent_sk<1>)
+                             : reinterpret_cast<const void *>(&k_latent_sk<0>))
+                      : (out ? reinterpret_cast<const void *>(&k_latent<1>)
+                             : reinterpret_cast<const void *>(&k_latent<0>));
+  return grant_lds(fn, kLatMaxLds, granted[sk][out], "latent block");
 }
 
 int latent_launch(const k3moe_latent_dims *dims, int out, const LatArgs &a, size_t workspace_bytes, void *stream) {
@@ -230,8 +233,10 @@ int latent_launch(const k3moe_latent_dims *dims, int out, const LatArgs &a, size
       ac.esum = a.esum + b0 * lh;
       ac.ya = a.ya + b0 * h;
     }
-    if ((rc = allow_latent_lds(out, p.lds_total))) return rc;
-    if (out) hipLaunchKernelGGL(k_latent<1>, dim3(p.G), dim3(kLatThreads), p.lds_total, st, p, ac);
+    if ((rc = allow_latent_lds(out, p.sk, p.lds_total))) return rc;
+    if (p.sk && out) hipLaunchKernelGGL(k_latent_sk<1>, dim3(p.G), dim3(kLatThreads), p.lds_total, st, p, ac);
+    else if (p.sk) hipLaunchKernelGGL(k_latent_sk<0>, dim3(p.G), dim3(kLatThreads), p.lds_total, st, p, ac);
+    else if (out) hipLaunchKernelGGL(k_latent<1>, dim3(p.G), dim3(kLatThreads), p.lds_total, st, p, ac);
     else hipLaunchKernelGGL(k_latent<0>, dim3(p.G), dim3(kLatThreads), p.lds_total, st, p, ac);
     if ((rc = launch_check(out ? "latent_out" : "latent_in"))) return rc;
   }

@@ -59,6 +59,14 @@ constexpr int kLatLocalNorm = 8;   // k_latent<1>: up to this many tokens every 
 constexpr int kLatNormChunks = 16; // ... from 16-byte chunks, 64 lanes x 16 x 4 = latent widths up to 4096
 constexpr float kLatRmsEps = 1e-5f;  // kimi.py:325
 constexpr int kLatGrpStride = 16;    // words between group counters (64 bytes)
+// streamed kernels (k_latent_sk)
+constexpr int kSkAhead = 4;             // activation steps loaded ahead of the current one
+constexpr int kSkSlots = kSkAhead + 1;  // activation ring slots, one 128-k step of 64 tokens (16 KiB) each
+constexpr int kSkSlotBytes = kLatMaxTokens * kStepK * 2;
+constexpr int kSkWAhead = 11;           // weight steps loaded ahead (HBM latency)
+constexpr int kSkWSlots = kSkWAhead + 1;  // weight ring slots, one row tile's 128-k step (4 KiB) each
+constexpr int kSkWSlotBytes = 16 * kStepK * 2;
+constexpr int kSkCntWord = 2048;        // first counter word (per row tile and token tile) in the latent counter area
 constexpr unsigned kLatGrpTotal = 1024;  // a group counter grows by this much per launch, whatever SP is
 
 struct LatPlan {
@@ -75,6 +83,7 @@ struct LatPlan {
   int lds_x, lds_total;
   int ntile0;  // k_latent<0>: latent_down row tiles (the shared pair tiles follow)
   int local_norm;  // k_latent<1>: every workgroup normalises the expert sum (no grid barrier)
+  int sk;          // 1: the streamed kernel k_latent_sk (no k-splits; G workgroups share the (tile, k-step) items)
   long o_cnt, o_part0, o_part1, o_en, o_trace, total;
 };
 
@@ -111,6 +120,42 @@ inline const char *latent_plan(const k3moe_latent_dims &d, int n_cus, int out, L
   p.local_norm = out && p.B <= kLatLocalNorm && p.lh <= 64 * 4 * kLatNormChunks;
 
   const int parts = out ? 2 : 1;
+  // Past the batches that normalise locally, the streamed kernel: the staged
+  // one's split partials would move 8 SP B / K of the weights' bytes (0.5 at
+  // 64 tokens), the streamed one's move a row tile's partial at most once per
+  // workgroup. Its grid is at most the row tile count (each workgroup's run of
+  // (tile, k-step) items then spans a whole tile's worth, so a tile is cut at
+  // most once). Only <1> takes it (measured at 64 tokens on a TP8 rank's
+  // geometry: 51 us against the staged kernel's 66, while <0> ran 77 us against
+  // 42), and only with the full grid: its grid barrier counts arrivals in
+  // groups, and every launch on a workspace that uses one must use the same
+  // grid size for the counts of earlier launches to round off.
+  p.sk = 0;
+  if (p.B > kLatLocalNorm) {
+    int g = 1;
+    while (g * 2 <= p.G && g * 2 <= p.RT) g *= 2;
+    if (out && g == p.G && g >= p.B && p.RT * 4 <= kLatCntBytes / 4 - kSkCntWord) {
+      p.sk = 1;
+      p.G = g;
+      p.SP = 1;
+      p.J = 0;
+      p.kwmax = 0;
+      p.xpitch = 0;
+      p.lds_x = kSkSlots * kSkSlotBytes + kSkWSlots * kSkWSlotBytes;
+      p.lds_total = p.lds_x;
+      long o = 0;
+      auto take = [&](long bytes) { long at = o; o = (long)align256((size_t)(o + bytes)); return at; };
+      take(kOffLatCnt);
+      p.o_cnt = take(kLatCntBytes);
+      take(kTagBytes);
+      p.o_part0 = take((long)p.RT * 2 * parts * 4 * 1024);  // [tile][segment][part][token tile] 16 x 16 fp32
+      p.o_part1 = 0;
+      p.o_en = out ? take((long)p.B * (p.lh + p.S) * 2) : 0;
+      p.o_trace = 0;
+      p.total = o;
+      return nullptr;
+    }
+  }
   const int red = parts * p.TT * kLatWaves * 1024;
   p.SP = 0;
   for (int sp = 4; sp <= kLatMaxSplits && !p.SP; sp *= 2) {
@@ -127,9 +172,14 @@ inline const char *latent_plan(const k3moe_latent_dims &d, int n_cus, int out, L
   p.xpitch = p.kwmax * kStepK + 8;
   p.lds_x = p.B * p.xpitch * 2;
   p.lds_total = p.lds_x + red;
+  // the group counters stay below the streamed kernels' counters (kSkCntWord
+  // on): only a single-step <0> has more groups (k_latent<1> has at least two
+  // steps, so SP >= 2), and <0> has no grid barrier, so its grid may shrink
+  if (!out || p.local_norm)
+    while (p.G > p.SP && (p.G / p.SP) * kLatGrpStride > kSkCntWord) p.G /= 2;
   p.J = cdiv(p.RT, p.G / p.SP);
   if (p.J > kLatMaxUnits) return "too many row tiles per workgroup";
-  if ((p.G / p.SP) * kLatGrpStride * 4 > kLatCntBytes) return "too many workgroup groups for the counter area";
+  if ((p.G / p.SP) * kLatGrpStride > kSkCntWord) return "too many workgroup groups for the counter area";
   long o = 0;
   auto take = [&](long bytes) { long at = o; o = (long)align256((size_t)(o + bytes)); return at; };
   take(kOffLatCnt);
@@ -518,6 +568,298 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
     if (!OUT) poison_share<true>(a.yb, (long)B * pl.S);
   }
   mark(47);
+}
+
+
+// ---------------------------------------------------------------- streamed --
+// k_latent_sk<OUT>: the same outputs for batches past kLatLocalNorm tokens,
+// without k-splits. The (row tile, 128-k step) items, tile-major, are cut
+// into G equal runs, one per workgroup; a run covers at least one tile's worth
+// of steps, so a tile is either whole in one run or cut once, into segments 0
+// and 1 of two neighbouring runs. Eight waves:
+//   - waves 4-7 load each step's operands into two LDS rings by direct-to-LDS
+//     loads: the row tile's weights (16 rows x 256 bytes) kSkWAhead steps
+//     ahead (the HBM stream) and the activation rows (all tokens) kSkAhead
+//     steps ahead (read from L2); in both, 16-byte chunk c of row r sits at
+//     position c ^ (r & 15) of its 256-byte row, so the operand reads of 16
+//     rows cover all 64 banks; one barrier per step;
+//   - wave tt < 4 multiplies token tile tt: four 16x16x32 MFMAs per step, MFMA
+//     c taking k 32q + 8c .. + 7 of both operands in lane (row or token i, q)
+//     (the same permutation of the step's 128 k in A and B).
+// At the end of a segment the wave writes its tile's outputs, or, for a cut
+// tile, its fp32 partial (device-coherent), and after its run it counts
+// itself in on the (tile, token tile) counter; the second of the two finishes
+// the tile: segment 0's sum plus segment 1's, each in step order, so the
+// result does not depend on which arrives last. It then clears the counter.
+// k_latent<1> first normalises the expert sums into the workspace rows
+// [en | shared_h] (workgroup t for token t) behind a grid barrier.
+
+// Row i's first bf16 of step ks of row tile rt (plus 32 q).
+__device__ __forceinline__ const uint16_t *sk_src(const LatPlan &pl, const LatArgs &a, int rt, int ks, int i, int q) {
+  const long r = (long)rt * 16 + i;
+  const int kq = q * 32;
+  if (!pl.out) {
+    // pair tile p: rows i < 8 are shared_gate row 8 p + i, rows i >= 8 shared_up row 8 p + i - 8
+    const long sr = 8L * (rt - pl.ntile0) + (i & 7);
+    const uint16_t *row = rt < pl.ntile0 ? a.wa + r * pl.h : (i < 8 ? a.wb : a.wc) + sr * pl.h;
+    return row + ks * kStepK + kq;
+  }
+  return ks < pl.KS0 ? a.wa + r * pl.lh + ks * kStepK + kq : a.wb + r * pl.S + (ks - pl.KS0) * kStepK + kq;
+}
+
+template <int OUT>
+__global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, LatArgs a_arg) {
+  const uint64_t kargs = touch_kernargs<sizeof(LatPlan) + sizeof(LatArgs)>();
+  const LatPlan pl = load_const<LatPlan>(kargs);
+  const LatArgs a = lat_args(kargs + sizeof(LatPlan));
+  (void)pl_arg;
+  (void)a_arg;
+  // kSkSlots x [64 tokens][256 B] activation steps, then kSkWSlots x [16 rows][256 B] weight steps
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  char *const wring = lds + kSkSlots * kSkSlotBytes;
+  __shared__ float s_wsum[kLatWaves];
+
+  const int tid = threadIdx.x, w = wave_id(), l = tid & 63;
+  const int i = l & 15, q = l >> 4;
+  const int B = pl.B, KS = pl.KS;
+  const long NI = (long)pl.RT * KS;
+  const long lo = NI * blockIdx.x / gridDim.x, hi = NI * (blockIdx.x + 1) / gridDim.x;
+  const int n = (int)(hi - lo);  // this workgroup's steps
+  const bool loader = w >= 4;
+  const int tt = w & 3;          // compute wave: its token tile; loader: which quarter of the loads
+  unsigned *ctl = reinterpret_cast<unsigned *>(a.ws);
+  const uint16_t *zlane = reinterpret_cast<const uint16_t *>(a.ws + 4096 + l * 64);  // 64 zero bytes
+  const int erow = pl.lh + pl.S;  // <1>: workspace row of a token, [en | shared_h]
+  const int rt_lo = (int)(lo / KS), ks_lo = (int)(lo - (long)rt_lo * KS);  // the run's first item
+  // (tile, step) of consecutive items, advanced one at a time
+  struct Cursor {
+    int rt, ks;
+    __device__ void next(int KS) {
+      if (++ks == KS) {
+        ks = 0;
+        ++rt;
+      }
+    }
+  };
+
+  if (OUT) {
+    BarrierBase bb{0u, 0u, 0u};
+    if (tid == 0) bb = barrier_base(ctl);
+    if ((int)blockIdx.x < B) {  // token t's [en | shared_h] row (as k_latent<1> for larger batches)
+      const int t = blockIdx.x;
+      float ss = 0.f;
+      for (int k = 2 * tid; k < pl.lh; k += 2 * kLatThreads) {
+        const float2 v = *reinterpret_cast<const float2 *>(a.esum + (long)t * pl.lh + k);
+        const float e0 = round_bf16(v.x), e1 = round_bf16(v.y);
+        ss += e0 * e0;
+        ss += e1 * e1;
+      }
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
+      if (l == 0) s_wsum[w] = ss;
+      __syncthreads();
+      float tot = s_wsum[0];
+#pragma unroll
+      for (int v = 1; v < kLatWaves; ++v) tot += s_wsum[v];
+      const float r = 1.0f / __fsqrt_rn(tot / (float)pl.lh + kLatRmsEps);
+      const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.ws + pl.o_en, (uint32_t)(B * erow * 2));
+      for (int k = 2 * tid; k < pl.lh; k += 2 * kLatThreads) {
+        const float2 v = *reinterpret_cast<const float2 *>(a.esum + (long)t * pl.lh + k);
+        const uint32_t wn = *reinterpret_cast<const uint32_t *>(a.norm + k);
+        const float n0 = round_bf16(round_bf16(v.x) * r), n1 = round_bf16(round_bf16(v.y) * r);
+        const uint32_t o0 = f32_to_bf16_bits(n0 * bf16_bits_to_f32(wn & 0xFFFFu));
+        const uint32_t o1 = f32_to_bf16_bits(n1 * bf16_bits_to_f32(wn >> 16));
+        st_dev32(rw, (uint32_t)(((long)t * erow + k) * 2), o0 | (o1 << 16));
+      }
+      for (int k = 2 * tid; k < pl.S; k += 2 * kLatThreads)
+        st_dev32(rw, (uint32_t)(((long)t * erow + pl.lh + k) * 2),
+                 *reinterpret_cast<const uint32_t *>(a.x + (long)t * pl.S + k));
+    }
+    if (!grid_barrier(ctl, bb, 1)) {  // a wait of this launch gave up: the rows are incomplete
+      poison_share<true>(a.ya, (long)B * pl.h);
+      return;
+    }
+  }
+
+  if (loader) {
+    // Waves 4-5 load the weights (two loads of 4 rows, 1 KiB, per step each),
+    // waves 6-7 the activations (eight loads of 4 token rows each; rows past
+    // the batch from the zero area): loads complete in issue order within a
+    // wave, so the weight stream, kSkWAhead steps ahead, does not hold up the
+    // activation loads. Past the run the loads read the zero area, so that
+    // every step issues the same number. A slot is free at the barrier after
+    // its last reader (the step kSkWSlots, or kSkSlots, before).
+    const bool wl = w < 6;
+    const int lw = w & 1;
+    Cursor cur{rt_lo, ks_lo};
+    auto issue_w = [&](int s) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int j = 2 * lw + u;  // rows 4j .. 4j + 3
+        const int r = 4 * j + (l >> 4), p = l & 15, c = p ^ r;
+        const uint16_t *src = s < n ? sk_src(pl, a, cur.rt, cur.ks, r, 0) + c * 8 : zlane;
+        load_lds<16>(src, wring + (s % kSkWSlots) * kSkWSlotBytes + j * 1024);
+      }
+      cur.next(KS);
+    };
+    auto issue_a = [&](int s) {
+      const int ks = cur.ks;
+      cur.next(KS);
+      char *slot = lds + (s % kSkSlots) * kSkSlotBytes;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int g = lw + 2 * u;             // token group: tokens 4g .. 4g + 3
+        const int t = 4 * g + (l >> 4), p = l & 15;
+        const int c = p ^ (t & 15);           // the global 16-byte chunk landing at position p
+        const uint16_t *src = (t >= B || s >= n) ? zlane
+                              : !OUT ? a.x + (long)t * pl.h + ks * kStepK + c * 8
+                                     : reinterpret_cast<const uint16_t *>(a.ws + pl.o_en) + (long)t * erow + ks * kStepK + c * 8;
+        load_lds<16, OUT ? kCpolDevice : 0>(src, slot + g * 1024);  // one instruction for all lanes
+      }
+    };
+    // at the barrier of step s its loads have landed: what may be outstanding
+    // is what this wave issued after them (the later steps' loads)
+    if (wl) {
+      for (int s = 0; s < kSkWAhead; ++s) issue_w(s);
+      for (int s = 0; s < n; ++s) {
+        wait_vm<2 * (kSkWAhead - 1)>();
+        ring_barrier();
+        issue_w(s + kSkWAhead);
+      }
+    } else {
+      for (int s = 0; s < kSkAhead; ++s) issue_a(s);
+      for (int s = 0; s < n; ++s) {
+        wait_vm<8 * (kSkAhead - 1)>();
+        ring_barrier();
+        issue_a(s + kSkAhead);
+      }
+    }
+    wait_vm<0>();  // no load lands after the workgroup is done
+    return;
+  }
+
+  // compute wave tt: token tile tt, token 16 tt + i (B operand lane (i, q))
+  const bool active = tt < pl.TT;
+  const int parts = OUT ? 2 : 1;
+  const __amdgpu_buffer_rsrc_t rpart = make_rsrc(a.ws + pl.o_part0, (uint32_t)((long)pl.RT * 2 * parts * 4 * 1024));
+  unsigned *cnt = reinterpret_cast<unsigned *>(a.ws + pl.o_cnt) + kSkCntWord;
+  const int tok = 16 * tt + i;
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+
+  // the outputs of row tile rt for this token tile from the finished sums
+  auto write_out = [&](int rt, const f32x4 &s0, const f32x4 &s1) {
+    // lane (token i, q): rows 4q .. 4q + 3 of the tile
+    if (OUT) {
+      uint32_t o[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16_bits(round_bf16(s0[v]) + round_bf16(s1[v]));
+      if (tok < B)
+        *reinterpret_cast<u32x2 *>(a.ya + (long)tok * pl.h + rt * 16 + 4 * q) = u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+    } else if (rt < pl.ntile0) {
+      uint32_t o[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16_bits(s0[v]);
+      if (tok < B)
+        *reinterpret_cast<u32x2 *>(a.ya + (long)tok * pl.lh + rt * 16 + 4 * q) = u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+    } else {
+      // pair tile: rows 0-7 shared_gate, rows 8-15 the same shared_up rows; lane
+      // q < 2 holds gate rows 4q .., lane q + 2 (lane + 32) the matching up rows
+      f32x4 up;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) up[v] = shfl_xor(s0[v], 32);
+      uint32_t o[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16_bits(apply_act(pl.act, round_bf16(s0[v]), round_bf16(up[v])));
+      if (q < 2 && tok < B)
+        *reinterpret_cast<u32x2 *>(a.yb + (long)tok * pl.S + (rt - pl.ntile0) * 8 + 4 * q) =
+            u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+    }
+  };
+  auto part_off = [&](int rt, int seg, int p) {
+    return (uint32_t)((((((long)rt * 2 + seg) * parts + p) * 4 + tt) * 256 + l * 4) * 4);
+  };
+  // parts with steps in [k_a, k_b) (<1>: part 0 below KS0, part 1 from it)
+  auto has0 = [&](int k_a) { return !OUT || k_a < pl.KS0; };
+  auto has1 = [&](int k_b) { return OUT && k_b > pl.KS0; };
+  // A cut tile's segment stores its partial now and counts in after the loop
+  // (their wait then comes once):
+  // at most the run's first and last tiles are cut.
+  int cut_rt[2] = {0, 0}, cut_a[2] = {0, 0}, cut_b[2] = {0, 0}, ncut = 0;
+  auto finish = [&](int rt, int k_a, int k_b) {
+    if (k_a == 0 && k_b == KS) {
+      write_out(rt, acc0, acc1);
+      return;
+    }
+    const int seg = k_a == 0 ? 0 : 1;
+    if (has0(k_a)) st_dev128(rpart, part_off(rt, seg, 0), __builtin_bit_cast(u32x4, acc0));
+    if (has1(k_b)) st_dev128(rpart, part_off(rt, seg, 1), __builtin_bit_cast(u32x4, acc1));
+    cut_rt[ncut] = rt;
+    cut_a[ncut] = k_a;
+    cut_b[ncut] = k_b;
+    ++ncut;
+  };
+
+  // operand reads: row (weight row i, or token tok) of a slot, the 16-byte
+  // chunk 4q + c at its swizzled position
+  const int bq = tok * 256;
+  int seg_a = ks_lo;  // first step of the current segment
+  Cursor cc{rt_lo, ks_lo};  // the current item
+  for (int s = 0; s < n; ++s) {
+    ring_barrier();  // the loaders' step s has landed
+    const char *aslot = lds + (s % kSkSlots) * kSkSlotBytes;
+    const char *wslot = wring + (s % kSkWSlots) * kSkWSlotBytes;
+    const int rt = cc.rt, ks = cc.ks;
+    cc.next(KS);
+    if (active) {
+      u32x4 av[4], bv[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        av[c] = *reinterpret_cast<const u32x4 *>(wslot + i * 256 + (((4 * q + c) ^ i) * 16));
+        bv[c] = *reinterpret_cast<const u32x4 *>(aslot + bq + (((4 * q + c) ^ i) * 16));
+      }
+      if (OUT && ks >= pl.KS0) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc1 = mfma16(as_bf16x8(av[c]), as_bf16x8(bv[c]), acc1);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc0 = mfma16(as_bf16x8(av[c]), as_bf16x8(bv[c]), acc0);
+      }
+    }
+    if (ks == KS - 1 || s == n - 1) {  // the segment ends here
+      if (active) finish(rt, seg_a, ks + 1);
+      acc0 = acc1 = f32x4{0.f, 0.f, 0.f, 0.f};
+      seg_a = 0;
+    }
+  }
+
+  // the cut tiles: the second of a tile's two segments to count in sums
+  // segment 0's partial and segment 1's and writes the outputs
+  wait_vmem();  // this wave's partial stores are complete
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    if (c >= ncut) break;
+    const int rt = cut_rt[c];
+    unsigned old = 0;
+    if (l == 0) old = __hip_atomic_fetch_add(cnt + rt * 4 + tt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old == 0) continue;  // the other segment's wave finishes the tile
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // segment 0 holds steps [0, kc), segment 1 [kc, KS)
+    const int kc = cut_a[c] == 0 ? cut_b[c] : cut_a[c];
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    f32x4 s0 = z, s1 = z;
+    if (has0(0)) s0 = __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(rt, 0, 0)));
+    if (has1(kc)) s1 = __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(rt, 0, 1)));
+    const f32x4 t0 = has0(kc) ? __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(rt, 1, 0))) : z;
+    const f32x4 t1 = has1(KS) ? __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(rt, 1, 1))) : z;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      s0[v] += t0[v];
+      s1[v] += t1[v];
+    }
+    write_out(rt, s0, s1);
+    if (l == 0) __hip_atomic_store(cnt + rt * 4 + tt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 }  // namespace k3moe

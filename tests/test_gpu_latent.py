@@ -21,7 +21,8 @@ pytestmark = pytest.mark.gpu
 # reference's batches, and small or ragged shapes (token tiles, splits and row tiles partly filled)
 SHAPES = [(1, 7168, 3584, 768), (8, 7168, 3584, 768), (64, 7168, 3584, 768), (3, 256, 128, 128),
           (17, 512, 256, 128), (33, 1024, 512, 256), (40, 2048, 1024, 384), (1, 128, 128, 128),
-          (100, 1024, 512, 256), (130, 512, 256, 128)]   # more than 64 tokens: launches of 64 rows
+          (100, 1024, 512, 256), (130, 512, 256, 128),   # more than 64 tokens: launches of 64 rows
+          (40, 5120, 2560, 384)]  # latent_out streamed with cut row tiles (320 tiles of 23 steps, 256 runs)
 
 
 def say(*a):
@@ -141,6 +142,25 @@ def test_latent_repeated_launches_are_identical():
     assert int(cnt[:, 1:].abs().sum()) == 0
     used = cnt[:, 0][cnt[:, 0] != 0]
     assert used.numel() > 0 and bool((used == 8*1024).all()), used.unique()
+
+
+def test_latent_out_streamed_counters_return_to_zero():
+    """The streamed latent_out (64 tokens, full grid): repeated launches agree bit for bit and leave
+    every (row tile, token tile) counter at zero for the next launch."""
+    B, h, lh, S = 64, 7168, 3584, 768
+    say(f'latent_out streamed repeat B={B} h={h} lh={lh} S={S}')
+    dev = torch.device('cuda:0')
+    w = {k: v.to(dev) for k, v in block_weights(B, h, lh, S, seed=9).items()}
+    w['shared_h'] = synthetic.randn(9, 'shared_h', (B, S), 0.5, device=dev)
+    ws = k3moe.new_workspace(64 << 20, dev)
+    outs = [k3moe.latent_out(w['expert_sum'], w['latent_norm'], w['latent_up'], w['shared_h'], w['shared_down'],
+                             workspace=ws).clone() for _ in range(3)]
+    torch.cuda.synchronize(dev)
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+    assert k3moe.workspace_status(ws) == 0
+    # the streamed kernels' counters: words 2048 .. 4095 of the latent counter area
+    cnt = ws[4096 + 65536 + 2048 * 4:4096 + 65536 + 16384].view(torch.int32).cpu()
+    assert int(cnt.abs().sum()) == 0
 
 
 def block_case(cfg, seed, shared, shared_fan=None):
