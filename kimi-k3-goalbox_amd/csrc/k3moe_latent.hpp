@@ -60,11 +60,12 @@ constexpr int kLatNormChunks = 16; // ... from 16-byte chunks, 64 lanes x 16 x 4
 constexpr float kLatRmsEps = 1e-5f;  // kimi.py:325
 constexpr int kLatGrpStride = 16;    // words between group counters (64 bytes)
 // streamed kernels (k_latent_sk)
-constexpr int kSkAhead = 4;             // activation steps loaded ahead of the current one
-constexpr int kSkSlots = kSkAhead + 1;  // activation ring slots, one 128-k step of 64 tokens (16 KiB) each
+// (steps go in pairs: one barrier per two 128-k steps)
+constexpr int kSkAPairs = 2;                    // activation step pairs loaded ahead of the current one
+constexpr int kSkSlots = 2 * (kSkAPairs + 1);   // activation ring slots, one step of 64 tokens (16 KiB) each
 constexpr int kSkSlotBytes = kLatMaxTokens * kStepK * 2;
-constexpr int kSkWAhead = 11;           // weight steps loaded ahead (HBM latency)
-constexpr int kSkWSlots = kSkWAhead + 1;  // weight ring slots, one row tile's 128-k step (4 KiB) each
+constexpr int kSkWPairs = 5;                    // weight step pairs loaded ahead (HBM latency)
+constexpr int kSkWSlots = 2 * (kSkWPairs + 1);  // weight ring slots, one row tile's step (4 KiB) each
 constexpr int kSkWSlotBytes = 16 * kStepK * 2;
 constexpr int kSkCntWord = 2048;        // first counter word (per row tile and token tile) in the latent counter area
 constexpr unsigned kLatGrpTotal = 1024;  // a group counter grows by this much per launch, whatever SP is
@@ -141,7 +142,7 @@ inline const char *latent_plan(const k3moe_latent_dims &d, int n_cus, int out, L
       p.J = 0;
       p.kwmax = 0;
       p.xpitch = 0;
-      p.lds_x = kSkSlots * kSkSlotBytes + kSkWSlots * kSkWSlotBytes;
+      p.lds_x = kSkSlots * kSkSlotBytes + kSkWSlots * kSkWSlotBytes;  // 144 KiB
       p.lds_total = p.lds_x;
       long o = 0;
       auto take = [&](long bytes) { long at = o; o = (long)align256((size_t)(o + bytes)); return at; };
@@ -578,19 +579,20 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
 // of steps, so a tile is either whole in one run or cut once, into segments 0
 // and 1 of two neighbouring runs. Eight waves:
 //   - waves 4-7 load each step's operands into two LDS rings by direct-to-LDS
-//     loads: the row tile's weights (16 rows x 256 bytes) kSkWAhead steps
-//     ahead (the HBM stream) and the activation rows (all tokens) kSkAhead
+//     loads: the row tile's weights (16 rows x 256 bytes) 2 kSkWPairs steps
+//     ahead (the HBM stream) and the activation rows (all tokens) 2 kSkAPairs
 //     steps ahead (read from L2); in both, 16-byte chunk c of row r sits at
 //     position c ^ (r & 15) of its 256-byte row, so the operand reads of 16
-//     rows cover all 64 banks; one barrier per step;
+//     rows cover all 64 banks; one barrier per pair of steps;
 //   - wave tt < 4 multiplies token tile tt: four 16x16x32 MFMAs per step, MFMA
 //     c taking k 32q + 8c .. + 7 of both operands in lane (row or token i, q)
 //     (the same permutation of the step's 128 k in A and B).
 // At the end of a segment the wave writes its tile's outputs, or, for a cut
-// tile, its fp32 partial (device-coherent), and after its run it counts
-// itself in on the (tile, token tile) counter; the second of the two finishes
-// the tile: segment 0's sum plus segment 1's, each in step order, so the
-// result does not depend on which arrives last. It then clears the counter.
+// tile, its fp32 partial (device-coherent), and counts itself in on the
+// (tile, token tile) counter; the second of the two finishes the tile:
+// segment 0's sum plus segment 1's, each in step order (and per MFMA c, summed
+// in c order), so the result does not depend on which arrives last. It then
+// clears the counter.
 // k_latent<1> first normalises the expert sums into the workspace rows
 // [en | shared_h] (workgroup t for token t) behind a grid barrier.
 
@@ -685,10 +687,10 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
     // Waves 4-5 load the weights (two loads of 4 rows, 1 KiB, per step each),
     // waves 6-7 the activations (eight loads of 4 token rows each; rows past
     // the batch from the zero area): loads complete in issue order within a
-    // wave, so the weight stream, kSkWAhead steps ahead, does not hold up the
+    // wave, so the weight stream, further ahead, does not hold up the
     // activation loads. Past the run the loads read the zero area, so that
     // every step issues the same number. A slot is free at the barrier after
-    // its last reader (the step kSkWSlots, or kSkSlots, before).
+    // its last reader (the pair of steps a ring's length before).
     const bool wl = w < 6;
     const int lw = w & 1;
     Cursor cur{rt_lo, ks_lo};
@@ -717,21 +719,24 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
         load_lds<16, OUT ? kCpolDevice : 0>(src, slot + g * 1024);  // one instruction for all lanes
       }
     };
-    // at the barrier of step s its loads have landed: what may be outstanding
-    // is what this wave issued after them (the later steps' loads)
+    // at the barrier of pair p its loads have landed: what may be outstanding
+    // is what this wave issued after them (the later pairs' loads)
+    const int np = (n + 1) / 2;
     if (wl) {
-      for (int s = 0; s < kSkWAhead; ++s) issue_w(s);
-      for (int s = 0; s < n; ++s) {
-        wait_vm<2 * (kSkWAhead - 1)>();
+      for (int s = 0; s < 2 * kSkWPairs; ++s) issue_w(s);
+      for (int p = 0; p < np; ++p) {
+        wait_vm<4 * (kSkWPairs - 1)>();
         ring_barrier();
-        issue_w(s + kSkWAhead);
+        issue_w(2 * (p + kSkWPairs));
+        issue_w(2 * (p + kSkWPairs) + 1);
       }
     } else {
-      for (int s = 0; s < kSkAhead; ++s) issue_a(s);
-      for (int s = 0; s < n; ++s) {
-        wait_vm<8 * (kSkAhead - 1)>();
+      for (int s = 0; s < 2 * kSkAPairs; ++s) issue_a(s);
+      for (int p = 0; p < np; ++p) {
+        wait_vm<16 * (kSkAPairs - 1)>();
         ring_barrier();
-        issue_a(s + kSkAhead);
+        issue_a(2 * (p + kSkAPairs));
+        issue_a(2 * (p + kSkAPairs) + 1);
       }
     }
     wait_vm<0>();  // no load lands after the workgroup is done
@@ -744,7 +749,12 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
   const __amdgpu_buffer_rsrc_t rpart = make_rsrc(a.ws + pl.o_part0, (uint32_t)((long)pl.RT * 2 * parts * 4 * 1024));
   unsigned *cnt = reinterpret_cast<unsigned *>(a.ws + pl.o_cnt) + kSkCntWord;
   const int tok = 16 * tt + i;
+  // four accumulators per part (MFMA c of every step), so that a step's four
+  // MFMAs do not wait for each other; summed in c order at the segment's end
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 c0[4], c1[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) c0[c] = c1[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // the outputs of row tile rt for this token tile from the finished sums
   auto write_out = [&](int rt, const f32x4 &s0, const f32x4 &s1) {
@@ -781,10 +791,9 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
   // parts with steps in [k_a, k_b) (<1>: part 0 below KS0, part 1 from it)
   auto has0 = [&](int k_a) { return !OUT || k_a < pl.KS0; };
   auto has1 = [&](int k_b) { return OUT && k_b > pl.KS0; };
-  // A cut tile's segment stores its partial now and counts in after the loop
-  // (their wait then comes once):
-  // at most the run's first and last tiles are cut.
-  int cut_rt[2] = {0, 0}, cut_a[2] = {0, 0}, cut_b[2] = {0, 0}, ncut = 0;
+  // A cut tile's segment stores its partial and counts itself in; the second
+  // of the two sums segment 0's partial and segment 1's and writes the outputs.
+  // (The compute waves have no loads in flight, so the wait is for the stores.)
   auto finish = [&](int rt, int k_a, int k_b) {
     if (k_a == 0 && k_b == KS) {
       write_out(rt, acc0, acc1);
@@ -793,59 +802,14 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
     const int seg = k_a == 0 ? 0 : 1;
     if (has0(k_a)) st_dev128(rpart, part_off(rt, seg, 0), __builtin_bit_cast(u32x4, acc0));
     if (has1(k_b)) st_dev128(rpart, part_off(rt, seg, 1), __builtin_bit_cast(u32x4, acc1));
-    cut_rt[ncut] = rt;
-    cut_a[ncut] = k_a;
-    cut_b[ncut] = k_b;
-    ++ncut;
-  };
-
-  // operand reads: row (weight row i, or token tok) of a slot, the 16-byte
-  // chunk 4q + c at its swizzled position
-  const int bq = tok * 256;
-  int seg_a = ks_lo;  // first step of the current segment
-  Cursor cc{rt_lo, ks_lo};  // the current item
-  for (int s = 0; s < n; ++s) {
-    ring_barrier();  // the loaders' step s has landed
-    const char *aslot = lds + (s % kSkSlots) * kSkSlotBytes;
-    const char *wslot = wring + (s % kSkWSlots) * kSkWSlotBytes;
-    const int rt = cc.rt, ks = cc.ks;
-    cc.next(KS);
-    if (active) {
-      u32x4 av[4], bv[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        av[c] = *reinterpret_cast<const u32x4 *>(wslot + i * 256 + (((4 * q + c) ^ i) * 16));
-        bv[c] = *reinterpret_cast<const u32x4 *>(aslot + bq + (((4 * q + c) ^ i) * 16));
-      }
-      if (OUT && ks >= pl.KS0) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc1 = mfma16(as_bf16x8(av[c]), as_bf16x8(bv[c]), acc1);
-      } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc0 = mfma16(as_bf16x8(av[c]), as_bf16x8(bv[c]), acc0);
-      }
-    }
-    if (ks == KS - 1 || s == n - 1) {  // the segment ends here
-      if (active) finish(rt, seg_a, ks + 1);
-      acc0 = acc1 = f32x4{0.f, 0.f, 0.f, 0.f};
-      seg_a = 0;
-    }
-  }
-
-  // the cut tiles: the second of a tile's two segments to count in sums
-  // segment 0's partial and segment 1's and writes the outputs
-  wait_vmem();  // this wave's partial stores are complete
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    if (c >= ncut) break;
-    const int rt = cut_rt[c];
+    wait_vmem();  // the partial is stored before the count
     unsigned old = 0;
     if (l == 0) old = __hip_atomic_fetch_add(cnt + rt * 4 + tt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = __builtin_amdgcn_readfirstlane(old);
-    if (old == 0) continue;  // the other segment's wave finishes the tile
+    if (old == 0) return;  // the other segment's wave finishes the tile
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     // segment 0 holds steps [0, kc), segment 1 [kc, KS)
-    const int kc = cut_a[c] == 0 ? cut_b[c] : cut_a[c];
+    const int kc = seg ? k_a : k_b;
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     f32x4 s0 = z, s1 = z;
     if (has0(0)) s0 = __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(rt, 0, 0)));
@@ -859,6 +823,50 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
     }
     write_out(rt, s0, s1);
     if (l == 0) __hip_atomic_store(cnt + rt * 4 + tt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+
+  // operand reads: row (weight row i, or token tok) of a slot, the 16-byte
+  // chunk 4q + c at its swizzled position
+  const int bq = tok * 256;
+  int seg_a = ks_lo;  // first step of the current segment
+  Cursor cc{rt_lo, ks_lo};  // the current item
+  for (int s2 = 0; s2 < n; s2 += 2) {
+    ring_barrier();  // the loaders' steps s2, s2 + 1 have landed
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int s = s2 + h;
+      if (s >= n) break;
+      const char *aslot = lds + (s % kSkSlots) * kSkSlotBytes;
+      const char *wslot = wring + (s % kSkWSlots) * kSkWSlotBytes;
+      const int rt = cc.rt, ks = cc.ks;
+      cc.next(KS);
+      if (active) {
+        u32x4 av[4], bv[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          av[c] = *reinterpret_cast<const u32x4 *>(wslot + i * 256 + (((4 * q + c) ^ i) * 16));
+          bv[c] = *reinterpret_cast<const u32x4 *>(aslot + bq + (((4 * q + c) ^ i) * 16));
+        }
+        if (OUT && ks >= pl.KS0) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) c1[c] = mfma16(as_bf16x8(av[c]), as_bf16x8(bv[c]), c1[c]);
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) c0[c] = mfma16(as_bf16x8(av[c]), as_bf16x8(bv[c]), c0[c]);
+        }
+      }
+      if (ks == KS - 1 || s == n - 1) {  // the segment ends here
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          acc0[v] = ((c0[0][v] + c0[1][v]) + c0[2][v]) + c0[3][v];
+          acc1[v] = ((c1[0][v] + c1[1][v]) + c1[2][v]) + c1[3][v];
+        }
+        if (active) finish(rt, seg_a, ks + 1);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) c0[c] = c1[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        seg_a = 0;
+      }
+    }
   }
 }
 
