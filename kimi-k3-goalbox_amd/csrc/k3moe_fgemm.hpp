@@ -179,7 +179,7 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
   extern __shared__ __attribute__((aligned(16))) char lds[];
   __shared__ int s_gstart[kMaxExperts + 1];  // first group of each active expert
   __shared__ int s_wsum[2 * kFWaves];
-  __shared__ int s_row[kFM];                 // activation row of each staged row (-1: none)
+  __shared__ int s_row[2][kFM];              // per unit parity: activation row of each staged row (-1: none)
   const int tid = threadIdx.x, l = tid & 63, i = l & 15, q = l >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool loader = wv >= kFWaves;
@@ -230,90 +230,125 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
   uint8_t *const hq_slo = hq_shi + (size_t)pl.P * (pl.I / kBlockK);
   uint16_t *const ybuf = reinterpret_cast<uint16_t *>(ws + pl.o_y);
 
-  for (long v = slot;; v += nslot) {
+  // The unit of number v: group j, row block nb, expert e, pairs p0 .. p0 + m - 1.
+  struct UnitP {
+    int e, p0, m, nb;
+  };
+  auto unit_of = [&](long v, UnitP &U) -> bool {
     const long j = xcd + (long)xcds * (v / NB);
-    if (j >= J) break;
-    const int nb = (int)(v % NB);
+    if (j >= J) return false;
+    U.nb = (int)(v % NB);
     int lo_ = 0, hi_ = nact - 1;  // the group's expert: largest d with s_gstart[d] <= j
     while (lo_ < hi_) {
       const int mid = (lo_ + hi_ + 1) >> 1;
       if (s_gstart[mid] <= j) lo_ = mid; else hi_ = mid - 1;
     }
     const int d = lo_, mt = (int)j - s_gstart[d];
-    const int e = active[d], p0 = aoff[d] + mt * kFM;
-    const int m = min(kFM, acnt[d] - mt * kFM), T = (m + 15) / 16;
-    wait_vm<0>();     // the previous unit's loads and stores are done
-    __syncthreads();  // the previous unit is done with the ring and s_row
-    if (tid < kFM) s_row[tid] = tid < m ? (GU ? ptok[p0 + tid] : p0 + tid) : -1;
-    __syncthreads();
+    U.e = active[d];
+    U.p0 = aoff[d] + mt * kFM;
+    U.m = min(kFM, acnt[d] - mt * kFM);
+    return true;
+  };
+  // a unit's staged rows, written one unit ahead (threads 0 .. kFM - 1, in the
+  // MFMA waves) into the buffer of its parity, read by the loaders
+  auto fill_rows = [&](const UnitP &U, int buf) {
+    if (tid < kFM) s_row[buf][tid] = tid < U.m ? (GU ? ptok[U.p0 + tid] : U.p0 + tid) : -1;
+  };
 
-    // Loader 4 + w: MFMA wave w's 4 weight row tiles (gate/up: gate rows 32w +
-    // 16r, r < 2, then the same up rows; down: rows 64w + 16r). Weight load r:
-    // lane (i, q) takes block 4 ks + q of its row (16 bytes), landing at the
-    // tile's 1 KiB in lane order, i.e. in the A-operand layout. Activation rows:
-    // the 8-row blocks w + 4u, u < NR (NR = 3 for 6 token tiles); lane L of load
-    // u (u < NR: hi, u >= NR: lo, the same rows) covers row 8 (w + 4 (u % NR)) +
-    // L / 8 at chunk position L % 8. Scale load (lane L lands at +4 L of the
-    // loader's 256-byte piece): lanes 0-23 the hi scale dwords of rows 4 L + w,
-    // lanes 32-55 the lo ones (at +128), the other lanes read the zero area; a
-    // token tile's scale addresses then differ from the next tile's by a
-    // constant. Every load is issued (rows without a token read the zero area),
-    // so that every k-step of a unit issues the same number of them (and kFTiles
-    // more with a weight-scale chunk).
-    const size_t wrow = (size_t)e * Nout + nb * RPB + (GU ? 32 : 64) * w;
-    const uint32_t wlane = (uint32_t)i * KB * 16 + q * 16;                 // row i of a tile, block q
-    const size_t wtile = (size_t)16 * KB * 16;                             // tile stride
-    auto tile_ptr = [&](int r) {                                           // tile r's first row, lane's block
-      return GU ? (r < 2 ? blk0 : blk1) + (wrow + 16 * (r & 1)) * KB * 16 + wlane
-                : blk0 + wrow * KB * 16 + r * wtile + wlane;
-    };
-    // weight-scale chunk c, tile r: lane L takes bytes 64c + 16 (L % 4) .. + 15
-    // of row L / 4 (the zero area past the row's end), landing at +16 L
-    const int sci = l >> 2, scp = 16 * (l & 3);
-    auto scale_ptr = [&](int r, int c) -> const uint8_t * {
-      if (64 * c + scp >= KB) return zero;
-      return GU ? (r < 2 ? scl0 : scl1) + (wrow + 16 * (r & 1) + sci) * KB + 64 * c + scp
-                : scl0 + (wrow + 16 * r + sci) * KB + 64 * c + scp;
-    };
-    const int NSC = (KS + kFScSteps - 1) / kFScSteps;  // scale chunks of the unit
-    // chunk c lands with the loads of step sc_step(c): 0 for the first, 2 steps
-    // after the first step of chunk c - 1 for the others (its buffer held chunk
-    // c - 2, whose last step is done once that step's barrier has passed)
-    auto chunk_at = [&](int s) { return s == 0 || (s >= 2 && (s - 2) % kFScSteps == 0 && (s - 2) / kFScSteps + 1 < NSC); };
-    constexpr int kNR = kFRowsL / 8;  // 8-row loads per term
+  // Loader 4 + w: MFMA wave w's 4 weight row tiles (gate/up: gate rows 32w +
+  // 16r, r < 2, then the same up rows; down: rows 64w + 16r). Weight load r:
+  // lane (i, q) takes block 4 ks + q of its row (16 bytes), landing at the
+  // tile's 1 KiB in lane order, i.e. in the A-operand layout. Activation rows:
+  // the 8-row blocks w + 4u, u < 3; lane L of load u (u < 3: hi, u >= 3: lo,
+  // the same rows) covers row 8 (w + 4 (u % 3)) + L / 8 at chunk position L %
+  // 8. Scale load (lane L lands at +4 L of the loader's 256-byte piece): lanes
+  // 0-23 the hi scale dwords of rows 4 L + w, lanes 32-55 the lo ones (at
+  // +128), the other lanes read the zero area; a token tile's scale addresses
+  // then differ from the next tile's by a constant. Every load is issued (rows
+  // without a token read the zero area), so that every k-step issues the same
+  // number of them (and kFTiles more with a weight-scale chunk).
+  const uint32_t wlane = (uint32_t)i * KB * 16 + q * 16;                 // row i of a tile, block q
+  const size_t wtile = (size_t)16 * KB * 16;                             // tile stride
+  const int sci = l >> 2, scp = 16 * (l & 3);
+  const uint8_t *const sbase = l < 32 ? a.shi : a.slo;
+  const int NSC = (KS + kFScSteps - 1) / kFScSteps;  // scale chunks of a unit
+  // chunk c lands with the loads of step sc_step(c): 0 for the first, 2 steps
+  // after the first step of chunk c - 1 for the others (its buffer held chunk
+  // c - 2, whose last step is done once that step's barrier has passed)
+  auto chunk_at = [&](int s) { return s == 0 || (s >= 2 && (s - 2) % kFScSteps == 0 && (s - 2) / kFScSteps + 1 < NSC); };
+  constexpr int kNR = kFRowsL / 8;                  // 8-row loads per term
+  constexpr int kLoads = 2 * kNR + 1 + kFTiles;     // a loader's loads per step (and kFTiles more with a chunk)
+  struct LoadP {  // one unit's load addresses for this lane
+    size_t wrow;
     uint32_t aoffs[kNR];
     bool arow[kNR];
+    bool srow;
+    uint32_t soff;
+  };
+  auto load_params = [&](const UnitP &U, int buf) {
+    LoadP P;
+    P.wrow = (size_t)U.e * Nout + U.nb * RPB + (GU ? 32 : 64) * w;
 #pragma unroll
     for (int u = 0; u < kNR; ++u) {
       const int r = 8 * (w + kFWaves * u) + (l >> 3);
       const int c = (l & 7) ^ ((r >> 1) & 7);
-      const int ar = s_row[r];
-      arow[u] = ar >= 0;
-      aoffs[u] = ar >= 0 ? (uint32_t)ar * (uint32_t)Kd + (uint32_t)c * 16 : (uint32_t)(l & 7) * 16;
+      const int ar = s_row[buf][r];
+      P.arow[u] = ar >= 0;
+      P.aoffs[u] = ar >= 0 ? (uint32_t)ar * (uint32_t)Kd + (uint32_t)c * 16 : (uint32_t)(l & 7) * 16;
     }
-    const int sar = (l & 31) < kFRowsL ? s_row[kFWaves * (l & 31) + w] : -1;
-    const bool srow = sar >= 0;
-    const uint32_t soff = srow ? (uint32_t)sar * (uint32_t)KB : 0u;
-    const uint8_t *const sbase = l < 32 ? a.shi : a.slo;
-    // a loader's loads of step ks into slot ks % kFRing, with NR 8-row activation
-    // blocks per term (blocks w + 4u, u < NR: those of a unit's token tiles)
-    auto issue = [&](int ks, auto nr) {
-      constexpr int NR = decltype(nr)::value;
-      char *base = lds + (ks % kFRing) * kFSlot;
-      if (chunk_at(ks)) {
-        const int c = ks == 0 ? 0 : (ks - 2) / kFScSteps + 1;
+    const int sar = (l & 31) < kFRowsL ? s_row[buf][kFWaves * (l & 31) + w] : -1;
+    P.srow = sar >= 0;
+    P.soff = P.srow ? (uint32_t)sar * (uint32_t)KB : 0u;
+    return P;
+  };
+  // The loads of step ks of a unit (P) into ring slot g % kFRing, g the
+  // workgroup's running step count; its weight-scale chunk c (if any) into
+  // buffer (cb0 + c) & 1, cb0 the unit's first chunk number.
+  auto issue = [&](const LoadP &P, int ks, int g, int cb0) {
+    char *base = lds + (g % kFRing) * kFSlot;
+    if (chunk_at(ks)) {
+      const int c = ks == 0 ? 0 : (ks - 2) / kFScSteps + 1;
+      const bool cin = 64 * c + scp < KB;  // lane L: bytes 64c + 16 (L % 4) .. of row L / 4 (zero area past the row)
 #pragma unroll
-        for (int r = 0; r < kFTiles; ++r)
-          load_lds<16>(scale_ptr(r, c), lds + kFOffSc + (c & 1) * kFScBuf + (kFTiles * w + r) * 1024);
+      for (int r = 0; r < kFTiles; ++r) {
+        const uint8_t *sp = GU ? (r < 2 ? scl0 : scl1) + (P.wrow + 16 * (r & 1) + sci) * KB + 64 * c + scp
+                               : scl0 + (P.wrow + 16 * r + sci) * KB + 64 * c + scp;
+        load_lds<16>(cin ? sp : zero, lds + kFOffSc + ((cb0 + c) & 1) * kFScBuf + (kFTiles * w + r) * 1024);
       }
+    }
 #pragma unroll
-      for (int r = 0; r < kFTiles; ++r) load_lds<16>(tile_ptr(r) + ks * 64, base + kFOffW + (kFTiles * w + r) * 1024);
+    for (int r = 0; r < kFTiles; ++r) {
+      const uint8_t *tp = GU ? (r < 2 ? blk0 : blk1) + (P.wrow + 16 * (r & 1)) * KB * 16 + wlane
+                             : blk0 + P.wrow * KB * 16 + r * wtile + wlane;
+      load_lds<16>(tp + ks * 64, base + kFOffW + (kFTiles * w + r) * 1024);
+    }
 #pragma unroll
-      for (int u = 0; u < 2 * NR; ++u)
-        load_lds<16>(arow[u % NR] ? (u < NR ? a.hi : a.lo) + aoffs[u % NR] + ks * 128 : zero + aoffs[u % NR],
-                     base + (u >= NR ? kFSlotX : 0) + 8 * (w + kFWaves * (u % NR)) * 128);
-      load_lds<4>(srow ? sbase + soff + 4 * ks : zero, base + kFOffXS + w * 256);
-    };
+    for (int u = 0; u < 2 * kNR; ++u)
+      load_lds<16>(P.arow[u % kNR] ? (u < kNR ? a.hi : a.lo) + P.aoffs[u % kNR] + ks * 128 : zero + P.aoffs[u % kNR],
+                   base + (u >= kNR ? kFSlotX : 0) + 8 * (w + kFWaves * (u % kNR)) * 128);
+    load_lds<4>(P.srow ? sbase + P.soff + 4 * ks : zero, base + kFOffXS + w * 256);
+  };
+
+  // Units follow each other without a pause in the loads: the loaders issue a
+  // unit's first two steps during the previous unit's last two steps (ring
+  // slots and chunk buffers are numbered over the workgroup's whole run), so
+  // they land while the MFMA waves finish that unit's epilogue.
+  UnitP U, Un;
+  long v = slot;
+  if (!unit_of(v, U)) return;  // (every wave of the workgroup alike)
+  fill_rows(U, 0);
+  __syncthreads();
+  bool have_n = unit_of(v + nslot, Un);
+  if (have_n) fill_rows(Un, 1);
+  LoadP Pc, Pn;
+  if (loader) {
+    Pc = load_params(U, 0);
+    issue(Pc, 0, 0, 0);
+    issue(Pc, 1, 1, 0);
+  }
+  for (int uidx = 0;; ++uidx) {
+    const int p0 = U.p0, m = U.m, nb = U.nb, T = (m + 15) / 16;
+    const int g0 = uidx * KS, cb0 = uidx * NSC;  // the unit's first step and chunk numbers
 
     // The k-loop and the epilogue for NT token tiles (a compile-time count: the
     // accumulators of tiles past the unit's tokens are never touched, and no
@@ -321,23 +356,27 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
     auto run = [&](auto nt) {
       constexpr int NT = decltype(nt)::value;
       if (loader) {
-        // k-steps ahead: at the barrier of step ks the loads of ks have landed and
-        // the MFMA waves are done with step ks - 1, whose slot takes step ks + 2
+        // two steps ahead: at the barrier of step ks the loads of ks have landed
+        // and the MFMA waves are done with step ks - 1, whose slot takes the
+        // running step after next (the next unit's first two at the end)
         static_assert(kFAhead == 2, "two k-steps ahead");
-        // the 8-row blocks of NT token tiles, spread evenly over the 4 loaders
-        // (a loader's blocks past them read the zero area, so that all count alike)
-        constexpr int NR = (NT + 1) / 2;
-        constexpr int kLoads = 2 * NR + 1 + kFTiles;
-        const IntC<NR> nr{};
-        issue(0, nr);
-        if (1 < KS) issue(1, nr);
         for (int ks = 0; ks < KS; ++ks) {
-          // step ks landed (step ks + 1's loads may be in flight)
-          if (ks + 1 >= KS) wait_vm<0>();
-          else if (chunk_at(ks + 1)) wait_vm<kLoads + kFTiles>();
-          else wait_vm<kLoads>();
+          // step ks landed (the loads of the step after it may be in flight)
+          if (ks + 1 < KS) {
+            if (chunk_at(ks + 1)) wait_vm<kLoads + kFTiles>();
+            else wait_vm<kLoads>();
+          } else if (have_n) {
+            wait_vm<kLoads + kFTiles>();  // the next unit's step 0 carries its first chunk
+          } else {
+            wait_vm<0>();
+          }
           ring_barrier();
-          if (ks + 2 < KS) issue(ks + 2, nr);
+          if (ks + 2 < KS) {
+            issue(Pc, ks + 2, g0 + ks + 2, cb0);
+          } else if (have_n) {
+            if (ks + 2 == KS) Pn = load_params(Un, (uidx + 1) & 1);  // written before this unit's first barrier
+            issue(Pn, ks + 2 - KS, g0 + ks + 2, cb0 + NSC);
+          }
         }
         return;
       }
@@ -348,8 +387,8 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
         for (int t = 0; t < NT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
       for (int ks = 0; ks < KS; ++ks) {
         ring_barrier();  // the loaders' loads of step ks have landed
-        const char *base = lds + (ks % kFRing) * kFSlot;
-        const char *scb = lds + kFOffSc + ((ks / kFScSteps) & 1) * kFScBuf + kFTiles * w * 1024 + 64 * i +
+        const char *base = lds + ((g0 + ks) % kFRing) * kFSlot;
+        const char *scb = lds + kFOffSc + ((cb0 + ks / kFScSteps) & 1) * kFScBuf + kFTiles * w * 1024 + 64 * i +
                           4 * (ks % kFScSteps) + q;
         u32x4 wa[kFTiles];
         uint32_t sa[kFTiles];
@@ -480,6 +519,13 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
       case 5: run(IntC<5>{}); break;
       default: run(IntC<6>{}); break;
     }
+    if (!have_n) break;
+    U = Un;
+    if (loader) Pc = Pn;
+    have_n = unit_of(v + (long)(uidx + 2) * nslot, Un);
+    wait_vm<0>();     // the epilogue's stores (MFMA waves), the next unit's first steps (loaders)
+    __syncthreads();  // the loaders are done with the rows of unit uidx, whose buffer takes unit uidx + 2's
+    if (have_n) fill_rows(Un, uidx & 1);
   }
 }
 
