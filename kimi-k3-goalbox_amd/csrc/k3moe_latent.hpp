@@ -596,17 +596,49 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
 // k_latent<1> first normalises the expert sums into the workspace rows
 // [en | shared_h] (workgroup t for token t) behind a grid barrier.
 
-// Row i's first bf16 of step ks of row tile rt (plus 32 q).
-__device__ __forceinline__ const uint16_t *sk_src(const LatPlan &pl, const LatArgs &a, int rt, int ks, int i, int q) {
+// Row i's first bf16 of step ks of row tile rt (plus 32 q); wa, wb, wc: the
+// weight pointers of LatArgs, passed as values (a choice between members of
+// the argument struct by address would keep the struct in scratch memory and
+// put a scratch load, and a wait for every load in flight, before each load).
+__device__ __forceinline__ const uint16_t *sk_src(const LatPlan &pl, const uint16_t *wa, const uint16_t *wb,
+                                                  const uint16_t *wc, int rt, int ks, int i, int q) {
   const long r = (long)rt * 16 + i;
   const int kq = q * 32;
   if (!pl.out) {
     // pair tile p: rows i < 8 are shared_gate row 8 p + i, rows i >= 8 shared_up row 8 p + i - 8
     const long sr = 8L * (rt - pl.ntile0) + (i & 7);
-    const uint16_t *row = rt < pl.ntile0 ? a.wa + r * pl.h : (i < 8 ? a.wb : a.wc) + sr * pl.h;
+    const uint16_t *row = rt < pl.ntile0 ? wa + r * pl.h : (i < 8 ? wb : wc) + sr * pl.h;
     return row + ks * kStepK + kq;
   }
-  return ks < pl.KS0 ? a.wa + r * pl.lh + ks * kStepK + kq : a.wb + r * pl.S + (ks - pl.KS0) * kStepK + kq;
+  return ks < pl.KS0 ? wa + r * pl.lh + ks * kStepK + kq : wb + r * pl.S + (ks - pl.KS0) * kStepK + kq;
+}
+
+// A run's items in processing order: entry 0 the last tile's head [0, ks_end)
+// when that tile is cut, entry 1 the first tile's tail [ks_lo, KS) when that
+// one is, entry 2 the whole tiles between, so that a cut tile's partial is
+// stored early and both segments' counts and the sum come off the run's end.
+// (A run spans at least one tile's steps, so a run within one tile is that
+// whole tile.) The run's bounds are passed as values: choosing between
+// variables by reference would keep them in scratch memory.
+struct SkCursor {
+  int e, rt, r1, ks, k0, k1;  // entry, tile, the entry's last tile, step, the tile's first step and end
+};
+// the first item of entry e, or of the first non-empty entry after it
+__device__ __forceinline__ SkCursor sk_entry(int e, int rt_lo, int ks_lo, int rt_hi, int ks_end, int KS) {
+  const int cut_first = ks_lo > 0, cut_last = rt_hi != rt_lo && ks_end < KS;
+  if (e == 0 && cut_last) return SkCursor{0, rt_hi, rt_hi, 0, 0, ks_end};
+  if (e <= 1 && cut_first) return SkCursor{1, rt_lo, rt_lo, ks_lo, ks_lo, KS};
+  if (e <= 2 && rt_lo + cut_first <= rt_hi - cut_last) return SkCursor{2, rt_lo + cut_first, rt_hi - cut_last, 0, 0, KS};
+  return SkCursor{3, 0, 0, 0, 0, KS};  // past the run (its loads read the zero area)
+}
+__device__ __forceinline__ void sk_next(SkCursor &c, int rt_lo, int ks_lo, int rt_hi, int ks_end, int KS) {
+  if (++c.ks < c.k1) return;
+  if (c.rt < c.r1) {  // entry 2's next whole tile
+    ++c.rt;
+    c.ks = 0;
+  } else if (c.e < 3) {
+    c = sk_entry(c.e + 1, rt_lo, ks_lo, rt_hi, ks_end, KS);
+  }
 }
 
 template <int OUT>
@@ -633,16 +665,27 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
   const uint16_t *zlane = reinterpret_cast<const uint16_t *>(a.ws + 4096 + l * 64);  // 64 zero bytes
   const int erow = pl.lh + pl.S;  // <1>: workspace row of a token, [en | shared_h]
   const int rt_lo = (int)(lo / KS), ks_lo = (int)(lo - (long)rt_lo * KS);  // the run's first item
-  // (tile, step) of consecutive items, advanced one at a time
-  struct Cursor {
-    int rt, ks;
-    __device__ void next(int KS) {
-      if (++ks == KS) {
-        ks = 0;
-        ++rt;
-      }
+  const int rt_hi = (int)((hi - 1) / KS), ks_end = (int)(hi - 1 - (long)rt_hi * KS) + 1;  // its last, + 1
+  auto cur_from = [&](int e) __attribute__((always_inline)) { return sk_entry(e, rt_lo, ks_lo, rt_hi, ks_end, KS); };
+  auto cur_next = [&](SkCursor &c) __attribute__((always_inline)) { sk_next(c, rt_lo, ks_lo, rt_hi, ks_end, KS); };
+  // Waves 4-5 load the weights (two loads of 4 rows, 1 KiB, per step each) from
+  // the kernel's start, ahead of the <1> normalisation's grid barrier.
+  const int lw = w & 1;
+  const uint16_t *const wa = a.wa, *const wb = a.wb, *const wc = a.wc;
+  SkCursor wcur = cur_from(0);
+  auto issue_w = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int j = 2 * lw + u;  // rows 4j .. 4j + 3
+      const int r = 4 * j + (l >> 4), p = l & 15, c = p ^ r;
+      const uint16_t *src = s < n ? sk_src(pl, wa, wb, wc, wcur.rt, wcur.ks, r, 0) + c * 8 : zlane;
+      load_lds<16>(src, wring + (s % kSkWSlots) * kSkWSlotBytes + j * 1024);
     }
+    cur_next(wcur);
   };
+  const bool wl = w == 4 || w == 5;
+  if (wl)
+    for (int s = 0; s < 2 * kSkWPairs; ++s) issue_w(s);
 
   if (OUT) {
     BarrierBase bb{0u, 0u, 0u};
@@ -684,29 +727,16 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
   }
 
   if (loader) {
-    // Waves 4-5 load the weights (two loads of 4 rows, 1 KiB, per step each),
-    // waves 6-7 the activations (eight loads of 4 token rows each; rows past
-    // the batch from the zero area): loads complete in issue order within a
-    // wave, so the weight stream, further ahead, does not hold up the
-    // activation loads. Past the run the loads read the zero area, so that
-    // every step issues the same number. A slot is free at the barrier after
-    // its last reader (the pair of steps a ring's length before).
-    const bool wl = w < 6;
-    const int lw = w & 1;
-    Cursor cur{rt_lo, ks_lo};
-    auto issue_w = [&](int s) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int j = 2 * lw + u;  // rows 4j .. 4j + 3
-        const int r = 4 * j + (l >> 4), p = l & 15, c = p ^ r;
-        const uint16_t *src = s < n ? sk_src(pl, a, cur.rt, cur.ks, r, 0) + c * 8 : zlane;
-        load_lds<16>(src, wring + (s % kSkWSlots) * kSkWSlotBytes + j * 1024);
-      }
-      cur.next(KS);
-    };
-    auto issue_a = [&](int s) {
+    // Waves 4-5 load the weights, waves 6-7 the activations (eight loads of 4
+    // token rows each; rows past the batch from the zero area): loads complete
+    // in issue order within a wave, so the weight stream, further ahead, does
+    // not hold up the activation loads. Past the run the loads read the zero
+    // area, so that every step issues the same number. A slot is free at the
+    // barrier after its last reader (the pair of steps a ring's length before).
+    SkCursor cur = cur_from(0);
+    auto issue_a = [&](int s) __attribute__((always_inline)) {
       const int ks = cur.ks;
-      cur.next(KS);
+      cur_next(cur);
       char *slot = lds + (s % kSkSlots) * kSkSlotBytes;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
@@ -722,8 +752,7 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
     // at the barrier of pair p its loads have landed: what may be outstanding
     // is what this wave issued after them (the later pairs' loads)
     const int np = (n + 1) / 2;
-    if (wl) {
-      for (int s = 0; s < 2 * kSkWPairs; ++s) issue_w(s);
+    if (wl) {  // (the first 2 kSkWPairs steps issued at the start)
       for (int p = 0; p < np; ++p) {
         wait_vm<4 * (kSkWPairs - 1)>();
         ring_barrier();
@@ -757,7 +786,7 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
   for (int c = 0; c < 4; ++c) c0[c] = c1[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // the outputs of row tile rt for this token tile from the finished sums
-  auto write_out = [&](int rt, const f32x4 &s0, const f32x4 &s1) {
+  auto write_out = [&](int rt, const f32x4 &s0, const f32x4 &s1) __attribute__((always_inline)) {
     // lane (token i, q): rows 4q .. 4q + 3 of the tile
     if (OUT) {
       uint32_t o[4];
@@ -785,16 +814,22 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
             u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
     }
   };
-  auto part_off = [&](int rt, int seg, int p) {
+  auto part_off = [&](int rt, int seg, int p) __attribute__((always_inline)) {
     return (uint32_t)((((((long)rt * 2 + seg) * parts + p) * 4 + tt) * 256 + l * 4) * 4);
   };
   // parts with steps in [k_a, k_b) (<1>: part 0 below KS0, part 1 from it)
-  auto has0 = [&](int k_a) { return !OUT || k_a < pl.KS0; };
-  auto has1 = [&](int k_b) { return OUT && k_b > pl.KS0; };
-  // A cut tile's segment stores its partial and counts itself in; the second
-  // of the two sums segment 0's partial and segment 1's and writes the outputs.
-  // (The compute waves have no loads in flight, so the wait is for the stores.)
-  auto finish = [&](int rt, int k_a, int k_b) {
+  auto has0 = [&](int k_a) __attribute__((always_inline)) { return !OUT || k_a < pl.KS0; };
+  auto has1 = [&](int k_b) __attribute__((always_inline)) { return OUT && k_b > pl.KS0; };
+  // A cut tile's segment stores its partial and, a few steps later (the stores
+  // done by then), counts itself in on the (tile, token tile) counter; after
+  // the run, the second of a tile's two counts sums segment 0's partial and
+  // segment 1's and writes the outputs. Cut tiles come first in a run, so a
+  // wave holds at most two, (rt_a, kc_a) then (rt_b, kc_b); kc: segment 0 holds
+  // steps [0, kc), segment 1 [kc, KS). (The compute waves have no loads in
+  // flight, so waiting for the stores waits for nothing else.)
+  int ncut = 0, ncounted = 0, count_at = 0, rt_a = 0, kc_a = 0, rt_b = 0, kc_b = 0;
+  unsigned old_a = 0u, old_b = 0u;
+  auto finish = [&](int rt, int k_a, int k_b, int s) __attribute__((always_inline)) {
     if (k_a == 0 && k_b == KS) {
       write_out(rt, acc0, acc1);
       return;
@@ -802,14 +837,27 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
     const int seg = k_a == 0 ? 0 : 1;
     if (has0(k_a)) st_dev128(rpart, part_off(rt, seg, 0), __builtin_bit_cast(u32x4, acc0));
     if (has1(k_b)) st_dev128(rpart, part_off(rt, seg, 1), __builtin_bit_cast(u32x4, acc1));
-    wait_vmem();  // the partial is stored before the count
-    unsigned old = 0;
-    if (l == 0) old = __hip_atomic_fetch_add(cnt + rt * 4 + tt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __builtin_amdgcn_readfirstlane(old);
-    if (old == 0) return;  // the other segment's wave finishes the tile
+    if (ncut == 0) {
+      rt_a = rt;
+      kc_a = seg ? k_a : k_b;
+    } else {
+      rt_b = rt;
+      kc_b = seg ? k_a : k_b;
+    }
+    ++ncut;
+    count_at = s + 4;
+  };
+  auto count_in = [&]() __attribute__((always_inline)) {
+    wait_vmem();  // the partials are stored before the counts
+    if (l == 0) {
+      if (ncounted == 0) old_a = __hip_atomic_fetch_add(cnt + rt_a * 4 + tt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (ncut == 2) old_b = __hip_atomic_fetch_add(cnt + rt_b * 4 + tt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    ncounted = ncut;
+  };
+  // the second arriver's sum of tile rt's two segments
+  auto sum_cut = [&](int rt, int kc) __attribute__((always_inline)) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // segment 0 holds steps [0, kc), segment 1 [kc, KS)
-    const int kc = seg ? k_a : k_b;
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     f32x4 s0 = z, s1 = z;
     if (has0(0)) s0 = __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(rt, 0, 0)));
@@ -828,18 +876,18 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
   // operand reads: row (weight row i, or token tok) of a slot, the 16-byte
   // chunk 4q + c at its swizzled position
   const int bq = tok * 256;
-  int seg_a = ks_lo;  // first step of the current segment
-  Cursor cc{rt_lo, ks_lo};  // the current item
+  SkCursor cc = cur_from(0);  // the current item
   for (int s2 = 0; s2 < n; s2 += 2) {
     ring_barrier();  // the loaders' steps s2, s2 + 1 have landed
+    if (active && ncounted < ncut && s2 >= count_at) count_in();
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int s = s2 + h;
       if (s >= n) break;
       const char *aslot = lds + (s % kSkSlots) * kSkSlotBytes;
       const char *wslot = wring + (s % kSkWSlots) * kSkWSlotBytes;
-      const int rt = cc.rt, ks = cc.ks;
-      cc.next(KS);
+      const int rt = cc.rt, ks = cc.ks, k0 = cc.k0, k1 = cc.k1;
+      cur_next(cc);
       if (active) {
         u32x4 av[4], bv[4];
 #pragma unroll
@@ -855,19 +903,22 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
           for (int c = 0; c < 4; ++c) c0[c] = mfma16(as_bf16x8(av[c]), as_bf16x8(bv[c]), c0[c]);
         }
       }
-      if (ks == KS - 1 || s == n - 1) {  // the segment ends here
+      if (ks + 1 == k1) {  // the tile's segment ends here
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           acc0[v] = ((c0[0][v] + c0[1][v]) + c0[2][v]) + c0[3][v];
           acc1[v] = ((c1[0][v] + c1[1][v]) + c1[2][v]) + c1[3][v];
         }
-        if (active) finish(rt, seg_a, ks + 1);
+        if (active) finish(rt, k0, k1, s);
 #pragma unroll
         for (int c = 0; c < 4; ++c) c0[c] = c1[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-        seg_a = 0;
       }
     }
   }
+  if (!active) return;
+  if (ncounted < ncut) count_in();
+  if (ncut >= 1 && __builtin_amdgcn_readfirstlane(old_a) != 0u) sum_cut(rt_a, kc_a);
+  if (ncut == 2 && __builtin_amdgcn_readfirstlane(old_b) != 0u) sum_cut(rt_b, kc_b);
 }
 
 }  // namespace k3moe

@@ -61,22 +61,45 @@ def test_fgemm_stream_schedule(KS, nunits):
     fgemm_stream(KS, nunits)
 
 
-def latent_sk_runs(RT, KS, KS0, G, out):
+def sk_order(lo, hi, KS):
+    """k_latent_sk's processing order of a run's (tile, step) items: the last
+    tile's head when that tile is cut, the first tile's tail when that one is,
+    then the whole tiles between; (rt, ks, k0, k1) per item, k0 / k1 the
+    tile's first step and end in the run."""
+    rt_lo, ks_lo = lo // KS, lo % KS
+    rt_hi, ks_end = (hi - 1) // KS, (hi - 1) % KS + 1
+    cut_first, cut_last = ks_lo > 0, rt_hi != rt_lo and ks_end < KS
+    entries = []
+    if cut_last:
+        entries.append((rt_hi, rt_hi, 0, ks_end))
+    if cut_first:
+        entries.append((rt_lo, rt_lo, ks_lo, KS))
+    if rt_lo + cut_first <= rt_hi - cut_last:
+        entries.append((rt_lo + cut_first, rt_hi - cut_last, 0, KS))
+    items = []
+    for r0, r1, k0, k1 in entries:
+        for rt in range(r0, r1 + 1):
+            a = k0 if rt == r0 else 0
+            b = k1 if rt == r1 else KS
+            items += [(rt, ks, a, b) for ks in range(a, b)]
+    return items
+
+
+def latent_sk_runs(RT, KS, KS0, G, out, second_first=False):
     NI = RT * KS
     has0 = lambda ka: (not out) or ka < KS0
     has1 = lambda kb: out and kb > KS0
     parts, result, count = {}, {}, {}
-    order = []
+    counts = []
     for b in range(G):
         lo, hi = NI * b // G, NI * (b + 1) // G
         assert hi - lo >= KS
-        seg_a, acc0, acc1 = lo % KS, set(), set()
-        for s in range(hi - lo):
-            it = lo + s
-            rt, ks = it // KS, it % KS
+        items = sk_order(lo, hi, KS)
+        assert sorted((rt * KS + ks) for rt, ks, _, _ in items) == list(range(lo, hi))
+        acc0, acc1, cuts = set(), set(), []
+        for rt, ks, ka, kb in items:
             (acc1 if out and ks >= KS0 else acc0).add((rt, ks))
-            if ks == KS - 1 or s == hi - lo - 1:
-                ka, kb = seg_a, ks + 1
+            if ks + 1 == kb:
                 if ka == 0 and kb == KS:
                     result[rt] = (frozenset(acc0), frozenset(acc1))
                 else:
@@ -85,13 +108,16 @@ def latent_sk_runs(RT, KS, KS0, G, out):
                         parts[(rt, seg, 0)] = frozenset(acc0)
                     if has1(kb):
                         parts[(rt, seg, 1)] = frozenset(acc1)
-                    order.append((rt, ka, kb))
-                acc0, acc1, seg_a = set(), set(), 0
-    for rt, ka, kb in order:
+                    cuts.append((rt, kb if ka == 0 else ka))
+                acc0, acc1 = set(), set()
+        assert len(cuts) <= 2  # the kernel keeps two
+        counts += cuts
+    # the counts arrive in any order; the second of a tile's two sums both
+    # segments (after every partial is stored)
+    for rt, kc in (reversed(counts) if second_first else counts):
         count[rt] = count.get(rt, 0) + 1
         if count[rt] == 1:
             continue
-        kc = kb if ka == 0 else ka
         s0 = parts[(rt, 0, 0)] | (parts[(rt, 1, 0)] if has0(kc) else frozenset())
         s1 = (parts[(rt, 0, 1)] if has1(kc) else frozenset()) | (parts[(rt, 1, 1)] if has1(KS) else frozenset())
         result[rt] = (s0, s1)
@@ -111,3 +137,13 @@ def latent_sk_runs(RT, KS, KS0, G, out):
 ])
 def test_latent_sk_segments(RT, KS, KS0, G, out):
     latent_sk_runs(RT, KS, KS0, G, out)
+    latent_sk_runs(RT, KS, KS0, G, out, second_first=True)
+
+
+def test_latent_sk_order_puts_cut_segments_first():
+    # run [5, 5 + 20) of 8-step tiles: tile 0 steps 5-7, tile 1, tile 2, tile 3 steps 0-0
+    items = sk_order(5, 25, 8)
+    assert items[0] == (3, 0, 0, 1)
+    assert [it[:2] for it in items[1:4]] == [(0, 5), (0, 6), (0, 7)]
+    assert [it[:2] for it in items[4:]] == [(1, k) for k in range(8)] + [(2, k) for k in range(8)]
+    assert sk_order(16, 24, 8) == [(2, k, 0, 8) for k in range(8)]
