@@ -20,7 +20,10 @@ constexpr unsigned kSpinLimit = 1u << 21;  // bounded barrier wait (about 0.1-1 
 // device-coherent stores (st_dev*), so arriving needs only their completion
 // (every wave waits for its vector memory operations) and a relaxed
 // increment; after the top counter shows every group, an agent-scope acquire
-// invalidates the local L2 for the reads that follow.
+// invalidates the local L2 for the reads that follow, unless the caller reads
+// the barrier's data only with device-coherent loads (acquire = false): the
+// invalidation takes microseconds and empties the XCD's L2 for every
+// workgroup on it.
 struct BarrierBase {
   unsigned top, grp;  // the top counter and this workgroup's group counter before barrier 1
   unsigned abort;     // the abort counter at this workgroup's start
@@ -78,10 +81,11 @@ __device__ __forceinline__ void barrier_arrive(unsigned *ctl, const BarrierBase 
   if (trace) trace[1] = __builtin_amdgcn_s_memrealtime();
 }
 
-// Thread 0: spins until the top counter shows every group, then acquires at
-// agent scope. Bounded: it gives up after kSpinLimit polls (a timeout), or
+// Thread 0: spins until the top counter shows every group, then (acquire)
+// acquires at agent scope. Bounded: it gives up after kSpinLimit polls (a timeout), or
 // when another wait of this launch gave up. Returns false when it gave up.
-__device__ __forceinline__ bool barrier_wait(unsigned *ctl, const BarrierBase &bb, unsigned n, uint64_t *trace) {
+__device__ __forceinline__ bool barrier_wait(unsigned *ctl, const BarrierBase &bb, unsigned n, uint64_t *trace,
+                                             bool acquire = true) {
   const unsigned target = bb.top + n * bar_groups();
   unsigned spins = 0;
   bool ok = true;
@@ -99,7 +103,7 @@ __device__ __forceinline__ bool barrier_wait(unsigned *ctl, const BarrierBase &b
     }
   }
   if (trace) trace[2] = __builtin_amdgcn_s_memrealtime();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (acquire) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (trace) trace[3] = __builtin_amdgcn_s_memrealtime();
   return ok;
 }
@@ -108,13 +112,13 @@ __device__ __forceinline__ bool barrier_wait(unsigned *ctl, const BarrierBase &b
 // data the barrier should publish may be incomplete, so the caller leaves
 // (every later wait of the launch then gives up early too).
 __device__ __forceinline__ bool grid_barrier(unsigned *ctl, const BarrierBase &bb, unsigned n,
-                                             uint64_t *trace = nullptr) {
+                                             uint64_t *trace = nullptr, bool acquire = true) {
   __shared__ int s_ok;
   wait_vmem();  // this wave's device-coherent stores are done (and thread 0's base loads)
   __syncthreads();
   if (threadIdx.x == 0) {
     barrier_arrive(ctl, bb, n, trace);
-    s_ok = barrier_wait(ctl, bb, n, trace) ? 1 : 0;
+    s_ok = barrier_wait(ctl, bb, n, trace, acquire) ? 1 : 0;
   }
   __syncthreads();
   return s_ok != 0;

@@ -1348,17 +1348,20 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + 48 + w] = __builtin_amdgcn_s_memrealtime();
     dn_flush(st, pl, ybuf);
     trace_mark(pl, a.ws, 9);
-    if (!grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 24))) return give_up();
+    // (no acquire: the combine reads y only, with device-coherent loads; an
+    // agent-scope acquire would invalidate the XCD's L2 first)
+    if (!grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 24), false)) return give_up();
     // combine (kimi.py:318,323): expert_sum[t][col] = sum over the token's
     // experts in ascending id order of w * bf16(y), from zero, FP32 adds
     const int K4 = pl.K / 4;
+    const __amdgpu_buffer_rsrc_t yrs = make_rsrc(ybuf, (uint32_t)pl.P * pl.K * 2);
     for (unsigned idx = blockIdx.x * kDecThreads + tid; idx < (unsigned)(B * K4); idx += gridDim.x * kDecThreads) {
       const int t = (int)(idx / (unsigned)K4), c4 = ((int)idx - t * K4) * 4;
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
       for (int sl = 0; sl < k; ++sl) {
         const int p = g_pof[t * k + sl];
         const float wt = g_pw[p];
-        const u32x2 yv = *reinterpret_cast<const u32x2 *>(ybuf + (size_t)p * pl.K + c4);
+        const u32x2 yv = bload8_dev(yrs, (uint32_t)((size_t)p * pl.K + c4) * 2);
         acc[0] = __fadd_rn(acc[0], __fmul_rn(bf16_bits_to_f32(yv[0] & 0xFFFFu), wt));
         acc[1] = __fadd_rn(acc[1], __fmul_rn(bf16_bits_to_f32(yv[0] >> 16), wt));
         acc[2] = __fadd_rn(acc[2], __fmul_rn(bf16_bits_to_f32(yv[1] & 0xFFFFu), wt));

@@ -423,7 +423,8 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
                  *reinterpret_cast<const uint32_t *>(a.x + (long)t * pl.S + k));
     }
     mark(48);
-    if (!grid_barrier(ctl, bb, 1)) {  // a wait of this launch gave up: the rows are incomplete
+    // (no acquire: the rows are read with device-coherent loads)
+    if (!grid_barrier(ctl, bb, 1, nullptr, false)) {  // a wait of this launch gave up: the rows are incomplete
       poison_share<true>(a.ya, (long)B * pl.h);
       return;
     }
@@ -517,7 +518,7 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
         break;
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // no acquire fence: the partials are read with device-coherent loads
   }
   __syncthreads();
   mark(46);
@@ -692,8 +693,26 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
     if (tid == 0) bb = barrier_base(ctl);
     if ((int)blockIdx.x < B) {  // token t's [en | shared_h] row (as k_latent<1> for larger batches)
       const int t = blockIdx.x;
+      // the row's first kHeld float pairs per thread (and their norm weights)
+      // stay in registers between the two passes; sums in ascending k as ever
+      constexpr int kHeld = 4;
+      float2 vh[kHeld];
+      uint32_t wh[kHeld];
+#pragma unroll
+      for (int j = 0; j < kHeld; ++j) {
+        const int k = 2 * tid + j * 2 * kLatThreads;
+        vh[j] = k < pl.lh ? *reinterpret_cast<const float2 *>(a.esum + (long)t * pl.lh + k) : float2{0.f, 0.f};
+        wh[j] = k < pl.lh ? *reinterpret_cast<const uint32_t *>(a.norm + k) : 0u;
+      }
       float ss = 0.f;
-      for (int k = 2 * tid; k < pl.lh; k += 2 * kLatThreads) {
+#pragma unroll
+      for (int j = 0; j < kHeld; ++j) {
+        if (2 * tid + j * 2 * kLatThreads >= pl.lh) break;
+        const float e0 = round_bf16(vh[j].x), e1 = round_bf16(vh[j].y);
+        ss += e0 * e0;
+        ss += e1 * e1;
+      }
+      for (int k = 2 * tid + kHeld * 2 * kLatThreads; k < pl.lh; k += 2 * kLatThreads) {
         const float2 v = *reinterpret_cast<const float2 *>(a.esum + (long)t * pl.lh + k);
         const float e0 = round_bf16(v.x), e1 = round_bf16(v.y);
         ss += e0 * e0;
@@ -708,19 +727,25 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
       for (int v = 1; v < kLatWaves; ++v) tot += s_wsum[v];
       const float r = 1.0f / __fsqrt_rn(tot / (float)pl.lh + kLatRmsEps);
       const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.ws + pl.o_en, (uint32_t)(B * erow * 2));
-      for (int k = 2 * tid; k < pl.lh; k += 2 * kLatThreads) {
-        const float2 v = *reinterpret_cast<const float2 *>(a.esum + (long)t * pl.lh + k);
-        const uint32_t wn = *reinterpret_cast<const uint32_t *>(a.norm + k);
+      auto put = [&](int k, float2 v, uint32_t wn) __attribute__((always_inline)) {
         const float n0 = round_bf16(round_bf16(v.x) * r), n1 = round_bf16(round_bf16(v.y) * r);
         const uint32_t o0 = f32_to_bf16_bits(n0 * bf16_bits_to_f32(wn & 0xFFFFu));
         const uint32_t o1 = f32_to_bf16_bits(n1 * bf16_bits_to_f32(wn >> 16));
         st_dev32(rw, (uint32_t)(((long)t * erow + k) * 2), o0 | (o1 << 16));
+      };
+#pragma unroll
+      for (int j = 0; j < kHeld; ++j) {
+        const int k = 2 * tid + j * 2 * kLatThreads;
+        if (k < pl.lh) put(k, vh[j], wh[j]);
       }
+      for (int k = 2 * tid + kHeld * 2 * kLatThreads; k < pl.lh; k += 2 * kLatThreads)
+        put(k, *reinterpret_cast<const float2 *>(a.esum + (long)t * pl.lh + k), *reinterpret_cast<const uint32_t *>(a.norm + k));
       for (int k = 2 * tid; k < pl.S; k += 2 * kLatThreads)
         st_dev32(rw, (uint32_t)(((long)t * erow + pl.lh + k) * 2),
                  *reinterpret_cast<const uint32_t *>(a.x + (long)t * pl.S + k));
     }
-    if (!grid_barrier(ctl, bb, 1)) {  // a wait of this launch gave up: the rows are incomplete
+    // (no acquire: the rows are read with device-coherent loads)
+    if (!grid_barrier(ctl, bb, 1, nullptr, false)) {  // a wait of this launch gave up: the rows are incomplete
       poison_share<true>(a.ya, (long)B * pl.h);
       return;
     }
@@ -820,15 +845,26 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
   // parts with steps in [k_a, k_b) (<1>: part 0 below KS0, part 1 from it)
   auto has0 = [&](int k_a) __attribute__((always_inline)) { return !OUT || k_a < pl.KS0; };
   auto has1 = [&](int k_b) __attribute__((always_inline)) { return OUT && k_b > pl.KS0; };
-  // A cut tile's segment stores its partial and, a few steps later (the stores
-  // done by then), counts itself in on the (tile, token tile) counter; after
-  // the run, the second of a tile's two counts sums segment 0's partial and
-  // segment 1's and writes the outputs. Cut tiles come first in a run, so a
-  // wave holds at most two, (rt_a, kc_a) then (rt_b, kc_b); kc: segment 0 holds
-  // steps [0, kc), segment 1 [kc, KS). (The compute waves have no loads in
-  // flight, so waiting for the stores waits for nothing else.)
-  int ncut = 0, ncounted = 0, count_at = 0, rt_a = 0, kc_a = 0, rt_b = 0, kc_b = 0;
-  unsigned old_a = 0u, old_b = 0u;
+  // A cut tile's segment stores its fp32 partial; kLagStore steps later (the
+  // stores done by then) it counts itself in on the (tile, token tile) counter;
+  // kLag steps after that the count's answer is back, and the second of the
+  // tile's two counts loads both segments' partials, which
+  // kLagLoad steps later still it sums (segment 0 + segment 1) into the
+  // outputs, then clears the counter: the round trips overlap the step stream.
+  // Cut tiles come first in a run, so a wave holds at most two, in slots ca and
+  // cb. (A compute wave's only loads are these, so waiting for the stores waits
+  // for nothing else.)
+  constexpr int kLagStore = 8, kLag = 8, kLagLoad = 8;
+  struct CutSlot {
+    int st;        // 0 unused, 1 partial stored, 2 counted, 3 partials loading, 4 done
+    int rt, kc;    // the tile; segment 0 holds steps [0, kc), segment 1 [kc, KS)
+    int at;        // the first step at which the next stage may run
+    unsigned old;  // the count's answer (lane 0)
+    f32x4 s0, s1, t0, t1;
+  };
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  CutSlot ca{0, 0, 0, 0, 0u, z4, z4, z4, z4}, cb{0, 0, 0, 0, 0u, z4, z4, z4, z4};
+  int count_at = 0;
   auto finish = [&](int rt, int k_a, int k_b, int s) __attribute__((always_inline)) {
     if (k_a == 0 && k_b == KS) {
       write_out(rt, acc0, acc1);
@@ -837,40 +873,59 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
     const int seg = k_a == 0 ? 0 : 1;
     if (has0(k_a)) st_dev128(rpart, part_off(rt, seg, 0), __builtin_bit_cast(u32x4, acc0));
     if (has1(k_b)) st_dev128(rpart, part_off(rt, seg, 1), __builtin_bit_cast(u32x4, acc1));
-    if (ncut == 0) {
-      rt_a = rt;
-      kc_a = seg ? k_a : k_b;
+    if (ca.st == 0) {
+      ca.st = 1;
+      ca.rt = rt;
+      ca.kc = seg ? k_a : k_b;
     } else {
-      rt_b = rt;
-      kc_b = seg ? k_a : k_b;
+      cb.st = 1;
+      cb.rt = rt;
+      cb.kc = seg ? k_a : k_b;
     }
-    ++ncut;
-    count_at = s + 4;
+    count_at = s + kLagStore;
   };
-  auto count_in = [&]() __attribute__((always_inline)) {
+  auto count_in = [&](int s) __attribute__((always_inline)) {
     wait_vmem();  // the partials are stored before the counts
-    if (l == 0) {
-      if (ncounted == 0) old_a = __hip_atomic_fetch_add(cnt + rt_a * 4 + tt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (ncut == 2) old_b = __hip_atomic_fetch_add(cnt + rt_b * 4 + tt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (ca.st == 1) {
+      if (l == 0) ca.old = __hip_atomic_fetch_add(cnt + ca.rt * 4 + tt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ca.st = 2;
+      ca.at = s + kLag;
     }
-    ncounted = ncut;
+    if (cb.st == 1) {
+      if (l == 0) cb.old = __hip_atomic_fetch_add(cnt + cb.rt * 4 + tt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      cb.st = 2;
+      cb.at = s + kLag;
+    }
   };
-  // the second arriver's sum of tile rt's two segments
-  auto sum_cut = [&](int rt, int kc) __attribute__((always_inline)) {
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    f32x4 s0 = z, s1 = z;
-    if (has0(0)) s0 = __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(rt, 0, 0)));
-    if (has1(kc)) s1 = __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(rt, 0, 1)));
-    const f32x4 t0 = has0(kc) ? __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(rt, 1, 0))) : z;
-    const f32x4 t1 = has1(KS) ? __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(rt, 1, 1))) : z;
+  // the next stage of slot c: the answer (first count: done, the other
+  // segment's wave finishes the tile), or the sum of the loaded partials
+  auto advance = [&](CutSlot &c, int s) __attribute__((always_inline)) {
+    if (c.st == 2) {
+      if (__builtin_amdgcn_readfirstlane(c.old) == 0u) {
+        c.st = 4;
+        return;
+      }
+      // no acquire fence: the partials are read with device-coherent loads,
+      // issued after the answer showed the other segment's count, whose
+      // device-coherent stores had completed before it counted (an agent-scope
+      // acquire would invalidate the XCD's L2, several us mid-stream)
+      if (has0(0)) c.s0 = __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(c.rt, 0, 0)));
+      if (has1(c.kc)) c.s1 = __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(c.rt, 0, 1)));
+      if (has0(c.kc)) c.t0 = __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(c.rt, 1, 0)));
+      if (has1(KS)) c.t1 = __builtin_bit_cast(f32x4, bload16_dev(rpart, part_off(c.rt, 1, 1)));
+      c.st = 3;
+      c.at = s + kLagLoad;
+      return;
+    }
+    f32x4 s0 = c.s0, s1 = c.s1;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      s0[v] += t0[v];
-      s1[v] += t1[v];
+      s0[v] += c.t0[v];
+      s1[v] += c.t1[v];
     }
-    write_out(rt, s0, s1);
-    if (l == 0) __hip_atomic_store(cnt + rt * 4 + tt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    write_out(c.rt, s0, s1);
+    if (l == 0) __hip_atomic_store(cnt + c.rt * 4 + tt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    c.st = 4;
   };
 
   // operand reads: row (weight row i, or token tok) of a slot, the 16-byte
@@ -879,7 +934,11 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
   SkCursor cc = cur_from(0);  // the current item
   for (int s2 = 0; s2 < n; s2 += 2) {
     ring_barrier();  // the loaders' steps s2, s2 + 1 have landed
-    if (active && ncounted < ncut && s2 >= count_at) count_in();
+    if (active) {
+      if ((ca.st == 1 || cb.st == 1) && s2 >= count_at) count_in(s2);
+      if ((ca.st == 2 || ca.st == 3) && s2 >= ca.at) advance(ca, s2);
+      if ((cb.st == 2 || cb.st == 3) && s2 >= cb.at) advance(cb, s2);
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int s = s2 + h;
@@ -916,9 +975,12 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent_sk(LatPlan pl_arg, La
     }
   }
   if (!active) return;
-  if (ncounted < ncut) count_in();
-  if (ncut >= 1 && __builtin_amdgcn_readfirstlane(old_a) != 0u) sum_cut(rt_a, kc_a);
-  if (ncut == 2 && __builtin_amdgcn_readfirstlane(old_b) != 0u) sum_cut(rt_b, kc_b);
+  // what the run's end left: both slots' loads first, then the sums
+  if (ca.st == 1 || cb.st == 1) count_in(n);
+  if (ca.st == 2) advance(ca, n);
+  if (cb.st == 2) advance(cb, n);
+  if (ca.st == 3) advance(ca, n);
+  if (cb.st == 3) advance(cb, n);
 }
 
 }  // namespace k3moe
