@@ -660,6 +660,12 @@ __device__ __forceinline__ void dn_issue_w(const Plan &pl, const DecodeArgs &a, 
   }
 }
 
+// The row-tile down reads h with device-coherent loads, and leaves its grid
+// barrier without an L2 invalidate, when all of h is at most this many bytes;
+// a larger h is read through the L2 (every workgroup reads all of it).
+constexpr long kHDevBytes = 131072;
+__device__ __forceinline__ bool dn_h_dev(const Plan &pl) { return (long)pl.P * pl.I * 2 <= kHDevBytes; }
+
 // The activated h rows (B operand) of a down item: token chunk c of active expert d.
 __device__ __forceinline__ void dn_issue_h(const Plan &pl, const uint16_t *hbuf, const uint8_t *zero,
                                            const int *g_aoff, const int *g_acnt, int d, int c, int kc, int KB,
@@ -668,6 +674,18 @@ __device__ __forceinline__ void dn_issue_h(const Plan &pl, const uint16_t *hbuf,
   const int p0 = g_aoff[d], n = g_acnt[d];
   const int pj = c * 16 + i;
   const bool tok_ok = pj < n;
+  if (dn_h_dev(pl)) {
+    const __amdgpu_buffer_rsrc_t hrs = make_rsrc(hbuf, (uint32_t)pl.P * pl.I * 2);
+#pragma unroll
+    for (int j = 0; j < kDnDepth; ++j) {
+      const int kb = (kc + j) * 4 + q;
+      const bool ok = tok_ok && kc + j < pl.KSd && kb < KB;
+      const uint32_t off = ok ? (uint32_t)(((p0 + pj) * pl.I + kb * kBlockK) * 2) : kOffNone;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) L.b[j][kk] = bload16_dev(hrs, off + kk * 16);
+    }
+    return;
+  }
   const uint16_t *hr = hbuf + (size_t)(p0 + (tok_ok ? pj : 0)) * pl.I;
 #pragma unroll
   for (int j = 0; j < kDnDepth; ++j) {
@@ -1328,7 +1346,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     for (int tt = 0; tt < 2; ++tt)  // a row tile past the last reads the zero area
       dn_issue_w(pl, a, zero, g_act, (int)blockIdx.x + tt * (int)gridDim.x, dn_da, 0, pl.I / kBlockK, pf[tt]);
   } else if (!expert_major && !dn_pair) {
-    if (!grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 20))) return give_up();
+    if (!grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 20), !dn_h_dev(pl))) return give_up();
   }
   trace_mark(pl, a.ws, 7);
 
