@@ -126,16 +126,17 @@ inline const char *latent_plan(const k3moe_latent_dims &d, int n_cus, int out, L
   // 64 tokens), the streamed one's move a row tile's partial at most once per
   // workgroup. Its grid is at most the row tile count (each workgroup's run of
   // (tile, k-step) items then spans a whole tile's worth, so a tile is cut at
-  // most once). Only <1> takes it (measured at 64 tokens on a TP8 rank's
-  // geometry: 51 us against the staged kernel's 66, while <0> ran 77 us against
-  // 42), and only with the full grid: its grid barrier counts arrivals in
-  // groups, and every launch on a workspace that uses one must use the same
-  // grid size for the counts of earlier launches to round off.
+  // most once). Measured at 64 tokens on a TP8 rank's geometry: <1> 36 us
+  // against the staged kernel's 66, <0> 39 us against 45. <1> takes it only
+  // with the full grid (its grid barrier counts arrivals in groups, and every
+  // launch on a workspace that uses one must use the same grid size for the
+  // counts of earlier launches to round off); <0>, which has no grid barrier,
+  // from 64 workgroups on.
   p.sk = 0;
   if (p.B > kLatLocalNorm) {
     int g = 1;
     while (g * 2 <= p.G && g * 2 <= p.RT) g *= 2;
-    if (out && g == p.G && g >= p.B && p.RT * 4 <= kLatCntBytes / 4 - kSkCntWord) {
+    if ((out ? g == p.G && g >= p.B : g >= 64) && p.RT * 4 <= kLatCntBytes / 4 - kSkCntWord) {
       p.sk = 1;
       p.G = g;
       p.SP = 1;

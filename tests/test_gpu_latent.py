@@ -145,8 +145,8 @@ def test_latent_repeated_launches_are_identical():
 
 
 def test_latent_out_streamed_counters_return_to_zero():
-    """The streamed latent_out (64 tokens, full grid): repeated launches agree bit for bit and leave
-    every (row tile, token tile) counter at zero for the next launch."""
+    """The streamed latent_in and latent_out (64 tokens, full grid): repeated launches agree bit for
+    bit and leave every (row tile, token tile) counter at zero for the next launch."""
     B, h, lh, S = 64, 7168, 3584, 768
     say(f'latent_out streamed repeat B={B} h={h} lh={lh} S={S}')
     dev = torch.device('cuda:0')
@@ -155,8 +155,11 @@ def test_latent_out_streamed_counters_return_to_zero():
     ws = k3moe.new_workspace(64 << 20, dev)
     outs = [k3moe.latent_out(w['expert_sum'], w['latent_norm'], w['latent_up'], w['shared_h'], w['shared_down'],
                              workspace=ws).clone() for _ in range(3)]
+    ins = [torch.cat([t.flatten() for t in k3moe.latent_in(w['x'], w['latent_down'], w['shared_gate'],
+                                                           w['shared_up'], workspace=ws)]) for _ in range(3)]
     torch.cuda.synchronize(dev)
     assert all(torch.equal(outs[0], o) for o in outs[1:])
+    assert all(torch.equal(ins[0], o) for o in ins[1:])
     assert k3moe.workspace_status(ws) == 0
     # the streamed kernels' counters: words 2048 .. 4095 of the latent counter area
     cnt = ws[4096 + 65536 + 2048 * 4:4096 + 65536 + 16384].view(torch.int32).cpu()
