@@ -283,6 +283,103 @@ def test_forced_routes_and_shortfall():
     assert not grading.valid_routes(rep, cfg.experts)
 
 
+# Closed-form shortfall cases (kimi.py:311-313: kth-best biased score minus the
+# lowest biased score among the forced routes, clamped at zero; the softmax
+# variant's shortfall works on the raw logits). Token b's logits are the
+# bf16-exact column b of the router, reached through a one-hot x row, so every
+# score below is a textbook value: sigmoid(0) = 0.5, sigmoid(2) =
+# 0.8807970779778823, sigmoid(-2) = 0.11920292202211755; biases are binary
+# fractions. Each expected value is written out by hand.
+SIG2, SIGM2 = 0.8807970779778823, 0.11920292202211755
+
+SHORTFALL_CASES = [
+    # (gating, k, per-token logits [E], bias [E], forced routes, expected shortfall)
+    # the forced set takes the lowest biased expert: 1.125 - 0.5
+    ('sigmoid_bias', 3, [0]*8, [0, .125, .25, .375, .5, .625, .75, .875], [0, 3, 7], 0.625),
+    # the forced set is the top-k itself, in another order
+    ('sigmoid_bias', 3, [0]*8, [0, .125, .25, .375, .5, .625, .75, .875], [6, 5, 7], 0.0),
+    # a repeated forced id can sit above the kth best (1.25 > 1.125): the clamp gives 0
+    # (the oracle accepts such a row as kimi.py does; the GPU path reports it as invalid)
+    ('sigmoid_bias', 3, [0]*8, [0, .125, .25, .375, .5, .625, .75, .875], [7, 7, 6], 0.0),
+    # one forced expert ties the kth best exactly (experts 1-3 all at 0.75)
+    ('sigmoid_bias', 2, [0]*8, [0, .25, .25, .25, 0, 0, 0, 0], [1, 3], 0.0),
+    # a known gap below a tie: kth best 0.75, forced min 0.5
+    ('sigmoid_bias', 2, [0]*8, [0, .25, .25, .25, 0, 0, 0, 0], [0, 3], 0.25),
+    # the bias reorders the sigmoid scores: biased = [s(2), .5, s(-2)+.5, .5, .5, .5, .5, .5]
+    # top-2 = {0, 2}, kth = s(-2) + 0.5; forced {1, 3} have 0.5
+    ('sigmoid_bias', 2, [2, 0, -2, 0, 0, 0, 0, 0], [0, 0, .5, 0, 0, 0, 0, 0], [1, 3], SIGM2),
+    # forced onto the unbiased-best expert with a low biased score: kth = 0.5 + 0.25 (experts 4, 5),
+    # forced {2, 4}: expert 2 has s(-2) + 0 -> shortfall 0.75 - s(-2)
+    ('sigmoid_bias', 2, [2, 0, -2, 0, 0, 0, 0, 0], [-.5, 0, 0, 0, .25, .25, 0, 0], [2, 4], 0.75 - SIGM2),
+    # the top score is forced with a much lower one: kth = s(2) - .5 vs. 0.5 + .375 ...
+    # biased = [s(2) - .5, .5, s(-2), .875, .5, .5, .5, .5]: top-2 = {3, 1}; kth 0.5; forced {0, 3}
+    ('sigmoid_bias', 2, [2, 0, -2, 0, 0, 0, 0, 0], [-.5, 0, 0, .375, 0, 0, 0, 0], [0, 3], 0.5 - (SIG2 - .5)),
+    # softmax variant: shortfall on the logits; kth best 2, forced min -1
+    ('softmax', 2, [3, 1, 2, -1, .5, 0, -2, .25], None, [1, 3], 3.0),
+    ('softmax', 2, [3, 1, 2, -1, .5, 0, -2, .25], None, [2, 0], 0.0),
+    ('softmax', 3, [3, 1, 2, -1, .5, 0, -2, .25], None, [0, 4, 2], 0.5),
+]
+
+
+def _shortfall_mismatches(route_fn):
+    """Run every case through route_fn one token at a time and as one batch per
+    (gating, k, bias); return the cases whose shortfall misses its hand value."""
+    bad = []
+    for i, (gating, k, logits, bias, forced, want) in enumerate(SHORTFALL_CASES):
+        E = len(logits)
+        router = torch.tensor(logits, dtype=torch.bfloat16)[:, None]          # [E, h=1]
+        assert router.float().flatten().tolist() == [float(v) for v in logits]
+        x = torch.ones(1, 1, dtype=torch.bfloat16)
+        b = torch.tensor(bias, dtype=torch.float32) if bias is not None else None
+        r = route_fn(x, router, b, k, gating, torch.tensor([forced]))
+        got = float(r['route_shortfall'][0])
+        if not abs(got - want) <= 1e-6:
+            bad.append((i, got, want))
+    # rows of one batch must not mix: token t reads column t of the router
+    groups = {}
+    for gating, k, logits, bias, forced, want in SHORTFALL_CASES:
+        groups.setdefault((gating, k, tuple(bias) if bias else None), []).append((logits, forced, want))
+    for (gating, k, bias), rows in groups.items():
+        B = len(rows)
+        router = torch.tensor([r[0] for r in rows], dtype=torch.bfloat16).T.contiguous()   # [E, B]
+        x = torch.eye(B, dtype=torch.bfloat16)
+        b = torch.tensor(bias, dtype=torch.float32) if bias is not None else None
+        r = route_fn(x, router, b, k, gating, torch.tensor([r[1] for r in rows]))
+        for t, (_, _, want) in enumerate(rows):
+            got = float(r['route_shortfall'][t])
+            if not abs(got - want) <= 1e-6:
+                bad.append((gating, k, t, got, want))
+    return bad
+
+
+def _planted_route(old: str, new: str):
+    """moe_ref.route with one source edit applied to its shortfall lines."""
+    import inspect
+    import textwrap
+    src = textwrap.dedent(inspect.getsource(moe_ref.route))
+    lines = [ln.replace(old, new) if ('route_shortfall' in ln or 'kth =' in ln) else ln
+             for ln in src.splitlines()]
+    mutated = '\n'.join(lines)
+    assert mutated != src, f'planted edit {old!r} -> {new!r} changed nothing'
+    ns = dict(vars(moe_ref))
+    exec(compile(mutated, '<planted route>', 'exec'), ns)
+    return ns['route']
+
+
+def test_route_shortfall_closed_form():
+    assert _shortfall_mismatches(moe_ref.route) == []
+
+
+@pytest.mark.parametrize('old,new', [
+    ('.min(-1)', '.max(-1)'),                      # the best forced score instead of the worst
+    ('biased.gather', 'scores.gather'),            # unbiased sigmoid scores
+    ('[:, -1]', '[:, 0]'),                         # the best score instead of the kth best
+    ('.clamp_min(0)', ''),                         # no clamp at zero
+])
+def test_route_shortfall_planted_mistakes_fail(old, new):
+    assert _shortfall_mismatches(_planted_route(old, new)) != []
+
+
 def test_oracle_does_not_mutate_inputs():
     cfg, inp = tiny_inputs(17)
     before = grading.snapshot(inp)
