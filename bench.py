@@ -8,7 +8,8 @@ at batch 1 (the headline line), with batches 8 and 64 reported beside it, and
 (unless --no-extra) 8 stacked batch-64 layers of that shard with fresh weights
 per layer, and the unsharded prefill chunk (I=2048, 4096 tokens), both with
 inputs made on the device, and the MXFP4 encoder on a TP8 rank's gate weights
-(the "codec" object).
+(the "codec" object), and the latent MoE block of the reference's own Kimi K3
+TP8 rank at batches 1, 8 and 64 (see workload kimi-latent).
 
 Self-check: the last timed run's outputs are checked against the CPU oracle
 (expert sets exact or FP64-certified near-ties, the band ratio of kimi.py's
@@ -264,12 +265,15 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, 
         graph.replay()
     torch.cuda.synchronize(device)
     run = graph.replay
+    host_us = []
     if launch == 'stream':
         calls = [(synthetic.step_args(inp), dict(kw, latent=inp.get('latent'), out=o)) for (inp, _), o in zip(data, outs)]
 
         def run():
             for a, k_ in calls:
+                t = time.perf_counter()
                 k3moe.moe_step(*a, **k_)
+                host_us.append((time.perf_counter() - t)*1e6)
         for i in range(warmup):
             if cold:
                 torch.sum(flush, 0, out=sink)
@@ -287,6 +291,16 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, 
     torch.cuda.synchronize(device)
     wall = time.perf_counter() - t0
     ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    host_us = host_us[-steps*layers:]
+    # the host side of one moe_step call alone (Python checks, the C ABI call and its launch),
+    # back to back with no flush between calls: it bounds a drop-in loop of consecutive layers
+    host_loop_us = None
+    if launch == 'stream':
+        t = time.perf_counter()
+        for _ in range(50):
+            run()
+        host_loop_us = (time.perf_counter() - t)*1e6/(50*layers)
+        torch.cuda.synchronize(device)
     # the last timed run's outputs, for the oracle checks
     timed = [{k: v.cpu() for k, v in o.items()} for o in outs]
     # the step's workspace status: 0 unless a wait timed out or a forced-route row was invalid
@@ -306,11 +320,14 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, 
     trace = read_trace(cfg, device) if os.environ.get('K3MOE_TRACE') == '1' and layers == 1 else None
     del graph, outs, flush
     return {'ms': ms, 'wall_s': wall, 'distinct': distinct, 'bytes': nbytes, 'flops': flops,
+            'host_us': host_us, 'host_loop_us': host_loop_us,
             'graph_matches_eager': same, 'host_inputs': [h for _, h in data], 'trace': trace,
             'timed': timed, 'status': status, 'device_inputs': [d for d, _ in data]}
 
 
 KIMI_SHARED, KIMI_SHARED_FAN = 768, 6144  # shared-expert width of a TP8 rank (3072 x 2 / 8), unsharded fan-in
+# token rows of the latent block the oracle check covers, per batch (every row up to 8 tokens)
+LATENT_ROWS = {1: None, 8: None, 64: [0, 21, 42, 63]}
 
 
 def measure_latent(cfg, *, seed, steps, warmup, cold, device):
@@ -355,16 +372,48 @@ def measure_latent(cfg, *, seed, steps, warmup, cold, device):
     torch.cuda.synchronize(device)
     block_ms = [e[0].elapsed_time(e[-1]) for e in ev]
     stage_ms = {name: [e[j].elapsed_time(e[j + 1]) for e in ev] for j, (name, _) in enumerate(stages)}
+    timed = {'latent': lat.cpu(), 'shared_h': sh.cpu(), 'output': out.cpu(),
+             **{k: v.cpu() for k, v in moe_out.items()}}
     same = torch.equal(out, k3moe.latent_block(x, w, **kw)['output'])
     B, h, lh, S = cfg.tokens, cfg.hidden, cfg.latent, KIMI_SHARED
     nbytes = {'latent_in': traffic.latent_in_bytes(B=B, h=h, lh=lh, S=S),
               'moe_step': traffic.step_bytes(B=B, E=cfg.experts, k=cfg.topk, h=h, I=cfg.inter, distinct=distinct,
                                              K=lh),
               'latent_out': traffic.latent_out_bytes(B=B, h=h, lh=lh, S=S)}
-    host = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in w.items()}
+    host = host_view(w)
     del flush
     return {'ms': block_ms, 'stage_ms': stage_ms, 'distinct': distinct, 'bytes': sum(nbytes.values()),
-            'stage_bytes': nbytes, 'repeat_matches': same, 'host': host}
+            'stage_bytes': nbytes, 'repeat_matches': same, 'host': host, 'timed': timed}
+
+
+def latent_check(cfg, got, host, rows=None) -> dict:
+    """The latent block's timed outputs against its CPU restatement (oracle/latent_ref.py, the chain of
+    kimi.py:317-328) on token rows `rows` (every row when None; each token's block is independent of
+    the others): expert sets exact or FP64-certified, and the band ratio of the block output, the
+    experts' latent input and expert_sum <= 1."""
+    import torch
+    from oracle import grading, latent_ref, moe_ref
+    ref_in = dict(host)
+    if rows is not None:
+        rows = torch.as_tensor(rows)
+        ref_in['x'] = host['x'][rows]
+        got = {k: v[rows] for k, v in got.items()}
+    bf = latent_ref.latent_block(ref_in['x'], ref_in, topk=cfg.topk, gating=cfg.gating)
+    sets = grading.route_sets(got['expert_ids'], bf['expert_ids'], ref_in['x'], ref_in['router'],
+                              ref_in['router_bias'], cfg.topk, cfg.gating)
+    truth_o = latent_ref.latent_block(ref_in['x'], ref_in, topk=cfg.topk, gating=cfg.gating, fp32=True,
+                                      routes=bf['expert_ids'])
+    truth_c = truth_o if sets['exact'] else latent_ref.latent_block(
+        ref_in['x'], ref_in, topk=cfg.topk, gating=cfg.gating, fp32=True, routes=got['expert_ids'])
+    ratios = {}
+    for name in ('latent', 'expert_sum', 'output'):
+        cand = moe_ref.rel_l2(got[name], truth_c[name])
+        orc = moe_ref.rel_l2(bf[name], truth_o[name])
+        ratios[name] = round(cand/(grading.BAND*orc + grading.FLOOR), 4)
+    finite = bool(torch.isfinite(got['output'].float()).all())
+    return {'rows': 'all' if rows is None else [int(r) for r in rows], 'sets_exact': sets['exact'],
+            'sets_certified': sets['certified'], 'band_ratio': ratios, 'finite': finite,
+            'ok': bool(sets['ok'] and finite and max(ratios.values()) <= 1.0)}
 
 
 def summarize_latent(cfg, m):
@@ -413,7 +462,10 @@ def summarize(cfg, m, layers):
             'distinct_experts': m['distinct'] if layers > 1 else m['distinct'][0],
             'algorithmic_bytes': m['bytes'], 'hbm_GBps': round(gbps, 1),
             'hbm_frac': round(gbps/8000.0, 4), 'tflops': round(m['flops']/(ms_mean*1e-3)/1e12, 3),
-            'graph_matches_eager': m['graph_matches_eager'], **({'trace': m['trace']} if m['trace'] else {})}
+            'graph_matches_eager': m['graph_matches_eager'],
+            **({'host_us_per_call': round(statistics.median(m['host_us']), 2),
+                'host_us_per_call_loop': round(m['host_loop_us'], 2)} if m['host_us'] else {}),
+            **({'trace': m['trace']} if m['trace'] else {})}
 
 
 def cpu_baseline(cfg, host_inputs, reps=3):
@@ -614,13 +666,15 @@ def main():
         if not args.no_extra:
             runs += [(configs.TP8_B64_L8, 8, False, [0, 21, 42, 63]),
                      (configs.PREFILL, 1, False, [0, 1, 2047, 4095])]
+            # the latent block of the reference's own Kimi K3 TP8 rank (896 experts, top-16, I=384)
+            runs += [(configs.KIMI_K3_TP8.with_tokens(b), 1, False, LATENT_ROWS[b]) for b in (1, 8, 64)]
         workload = f'tp8-rank-b{batches[0]}'
     elif args.workload == 'tp8-l8':
         runs = [(configs.TP8_B64_L8, 8, False, [0, 21, 42, 63])]
         workload = 'tp8-rank-b64-8-stacked-layers'
     elif args.workload == 'kimi-latent':
         batches = [int(b) for b in args.batches.split(',')]
-        runs = [(configs.KIMI_K3_TP8.with_tokens(b), 1, False, None) for b in batches]
+        runs = [(configs.KIMI_K3_TP8.with_tokens(b), 1, False, LATENT_ROWS.get(b)) for b in batches]
         workload = f'kimi-k3-tp8-rank-latent-block-b{batches[0]}'
     else:
         runs = [(configs.PREFILL, 1, False, [0, 1, 2047, 4095])]
@@ -639,10 +693,14 @@ def main():
     results, host, timed, failures = {}, {}, {}, []
     for cfg, layers, host_gen, rows in runs:
         log(f'bench: {cfg.name} layers={layers} steps={args.steps} warmup={args.warmup} cold={cold}')
-        if args.workload == 'kimi-latent':
+        if cfg.latent:
             m = measure_latent(cfg, seed=args.seed, steps=args.steps, warmup=args.warmup, cold=cold, device=device)
             results[cfg.name] = summarize_latent(cfg, m)
             host[cfg.name] = m['host']
+            if not args.no_check:
+                log(f'bench: oracle check of the latent block {cfg.name}, rows {rows}')
+                results[cfg.name]['check'] = latent_check(cfg, m['timed'], m['host'], rows=rows)
+            del m
         else:
             m = measure(cfg, seed=args.seed, steps=args.steps, warmup=args.warmup, cold=cold, device=device,
                         layers=layers, host_gen=host_gen, launch=args.launch)
@@ -666,6 +724,9 @@ def main():
     head_cfg, head_layers, _, _ = runs[0]
     head = results[head_cfg.name]
     measured = measured_traffic()
+    for cfg, layers, _, _ in runs[1:]:
+        if cfg.name == configs.PREFILL.name:   # its MFMA roofline beside the decode batches' HBM one
+            results[cfg.name]['roofline'] = roofline_entry(results[cfg.name], cfg, layers, measured, 'prefill')
     for name, r in results.items():
         if name in measured and r['layers'] == 1:
             r['hbm_traffic_bytes'] = measured[name]['traffic_bytes']
@@ -674,7 +735,7 @@ def main():
         # the latent block's oracle decodes every routed expert (up to 896 at b64): head batch only;
         # the CPU baseline covers the configurations made on the host (the batches of one layer)
         for cfg, _, host_gen, _ in (runs[:1] if args.workload == 'kimi-latent' else runs):
-            if args.workload != 'kimi-latent' and not host_gen:
+            if args.workload != 'kimi-latent' and (not host_gen or cfg.latent):
                 results[cfg.name]['cpu_us_per_layer'] = None
                 continue
             log(f'cpu baseline: {cfg.name}')
@@ -693,7 +754,7 @@ def main():
                'cpu': cpu_model()}
     if args.workload != 'kimi-latent' and not args.no_check:
         for cfg, layers, host_gen, rows in runs:
-            if not host_gen:
+            if not host_gen or cfg.latent:
                 continue
             log(f'bench: oracle check of {cfg.name}')
             orc = per[cfg.name]['oracle'] if cfg.name in per else None

@@ -138,10 +138,15 @@ int k3moe_moe_step(const k3moe_dims *dims,
  * held until the process ends (every step of the persistent decode path fits:
  * tokens <= 64; a step that needs more, such as a prefill chunk, fails with
  * K3MOE_EWORKSPACE and a message). The first call on a device looks its
- * address up and zeroes its control block with a kernel on `stream`; no call
- * allocates or frees memory. All calls on one GPU share the array, so calls
- * that may overlap on one GPU (other streams, other threads) race. Arguments,
- * outputs, numerics and errors are those of k3moe_moe_step. */
+ * address up, zeroes its control block with a kernel on `stream` and waits
+ * for that kernel (once per device and process, so later calls on any stream
+ * find it initialised; that first call must not be under stream capture:
+ * call k3moe_workspace_init(NULL, 0, stream) before capturing); no call
+ * allocates or frees memory. Its status word is read with
+ * k3moe_workspace_status(NULL, ...) and reset, after a K3MOE_STATUS_TIMEOUT
+ * too, with k3moe_workspace_init(NULL, ...). All calls on one GPU share the
+ * array, so calls that may overlap on one GPU (other streams, other threads)
+ * race. Arguments, outputs, numerics and errors are those of k3moe_moe_step. */
 int k3moe_moe_step_noalloc(const k3moe_dims *dims,
                            const void *x, const void *latent,
                            const void *router, const float *router_bias,
@@ -196,8 +201,12 @@ int k3moe_workspace_layout(const k3moe_dims *dims, k3moe_layout *layout);
  * kernel on `stream`. A workspace must be
  * initialised once before its first step; each step leaves the counters at
  * zero, so one workspace serves any number of consecutive steps on one
- * stream (steps that overlap on one workspace race). No reference
- * counterpart: the reference allocates its temporaries per call. */
+ * stream (steps that overlap on one workspace race). workspace == NULL
+ * means the current device's allocation-free scratch (k3moe_moe_step_noalloc;
+ * workspace_bytes is then ignored): it zeroes the same bytes of it, or, if no
+ * call on this device has used the scratch yet, initialises it and waits for
+ * that. No reference counterpart: the reference allocates its temporaries per
+ * call. */
 int k3moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 
 /* Status bits of the workspace's sticky status word (an OR over every step
@@ -214,8 +223,10 @@ int k3moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 /* Copy the workspace's sticky status word to *status (0 = every step so far
  * completed normally, else K3MOE_STATUS_* bits). Synchronises `stream`.
  * k3moe_moe_step and the latent entry points never synchronise, so a caller
- * that needs the guarantee reads the status after its steps. No reference
- * counterpart. */
+ * that needs the guarantee reads the status after its steps. workspace ==
+ * NULL reads the current device's allocation-free scratch (the status of
+ * k3moe_moe_step_noalloc calls on this device since its initialisation or
+ * the last k3moe_workspace_init(NULL, ...)). No reference counterpart. */
 int k3moe_workspace_status(const void *workspace, int32_t *status, void *stream);
 
 /* Geometry of the latent MoE block around the routed experts of a Kimi K3

@@ -249,10 +249,20 @@ __global__ void k_zero_words(uint32_t *p, int n) {
 }
 
 // The device address of `scratch` on the current device, looked up once per
-// device; the first lookup also zeroes its control block, zero area and
-// counters with a kernel on `st` (stream-ordered before the step that follows).
+// device. The first lookup also zeroes its control block, zero area, counters
+// and tag area with a kernel on `st` and waits for it (once per device and
+// process), so that calls on any stream after it find the array initialised;
+// a first call inside a stream capture would record that kernel instead of
+// running it, so it is refused with a message.
 std::mutex g_scratch_mu;
 void *g_scratch[64];
+
+bool scratch_ready() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return g_scratch[dev] != nullptr;
+}
 
 int scratch_address(void **out, hipStream_t st) {
   int dev = 0;
@@ -261,14 +271,25 @@ int scratch_address(void **out, hipStream_t st) {
   if (dev < 0 || dev >= 64) return fail(K3MOE_EINVAL, "device ordinal %d out of range", dev);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch[dev]) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess)
+      return fail(K3MOE_EHIP, "hipStreamIsCapturing failed: %s", hipGetErrorString(hipGetLastError()));
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(K3MOE_EINVAL,
+                  "the allocation-free scratch of device %d is initialised by the first call on that device, "
+                  "which must not be captured: call k3moe_workspace_init(NULL, 0, stream) once before capturing",
+                  dev);
     void *ptr = nullptr;
     const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (err != hipSuccess || !ptr)
       return fail(K3MOE_EHIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev, hipGetErrorString(err));
     hipLaunchKernelGGL(k_zero_words, dim3(cdiv(kInitBytes / 4, 256)), dim3(256), 0, st, reinterpret_cast<uint32_t *>(ptr),
                        kInitBytes / 4);
-    const int rc = launch_check("scratch init");
+    int rc = launch_check("scratch init");
     if (rc) return rc;
+    if (hipStreamSynchronize(st) != hipSuccess)
+      return fail(K3MOE_EHIP, "waiting for the scratch init on device %d failed: %s", dev,
+                  hipGetErrorString(hipGetLastError()));
     g_scratch[dev] = ptr;
   }
   *out = g_scratch[dev];
@@ -320,18 +341,33 @@ int k3moe_workspace_layout(const k3moe_dims *dims, k3moe_layout *layout) {
 
 int k3moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {
   g_err[0] = 0;
-  if (!workspace || workspace_bytes < (size_t)kInitBytes)
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!workspace) {  // the current device's allocation-free scratch
+    void *ws = nullptr;
+    const bool fresh = !scratch_ready();
+    int rc = scratch_address(&ws, st);
+    if (rc || fresh) return rc;  // a first lookup has just zeroed it
+    workspace = ws;
+    workspace_bytes = kScratchBytes;
+  }
+  if (workspace_bytes < (size_t)kInitBytes)
     return fail(K3MOE_EWORKSPACE, "workspace must hold at least %d bytes", kInitBytes);
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(K3MOE_EWORKSPACE, "workspace must be 256-byte aligned");
-  hipLaunchKernelGGL(k_zero_words, dim3(cdiv(kInitBytes / 4, 256)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+  hipLaunchKernelGGL(k_zero_words, dim3(cdiv(kInitBytes / 4, 256)), dim3(256), 0, st,
                      reinterpret_cast<uint32_t *>(workspace), kInitBytes / 4);
   return launch_check("workspace_init");
 }
 
 int k3moe_workspace_status(const void *workspace, int32_t *status, void *stream) {
   g_err[0] = 0;
-  if (!workspace || !status) return fail(K3MOE_EINVAL, "a required pointer is NULL");
+  if (!status) return fail(K3MOE_EINVAL, "status is NULL");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!workspace) {  // the current device's allocation-free scratch
+    void *ws = nullptr;
+    int rc = scratch_address(&ws, st);
+    if (rc) return rc;
+    workspace = ws;
+  }
   uint32_t word = 0;
   const uint32_t *src = reinterpret_cast<const uint32_t *>(workspace) + kCtlErr;
   if (hipMemcpyAsync(&word, src, 4, hipMemcpyDeviceToHost, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)

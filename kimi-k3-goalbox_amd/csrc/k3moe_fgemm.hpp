@@ -8,8 +8,8 @@
 // eh = floor(log2 max|v|) - 7 and el the same for the remainders, each scale
 // one E8M0 byte per block. The MFMA runs once on hi and once on lo into the
 // same fp32 accumulator. A bf16 value has 8 significant bits and E4M3 4, so
-// hi + lo equals v for every element within 2^9 of its block's maximum
-// (smaller ones lose only bits below 2^-17 of it): the products, accumulated
+// hi + lo equals v for every element within 2^8 of its block's maximum
+// (smaller ones lose only bits below 2^-16 of it): the products, accumulated
 // in fp32, are those of the bf16 operands. A single E4M3 term would leave the
 // reference's band (kimi.py:413-429) by a factor of about 7.
 //

@@ -179,3 +179,35 @@ def test_fp4_grouped_gemms_only_for_whole_output_units(K, I, fp4):
     assert (lay['input_split'] >= 0) == fp4
     assert (lay['h_split'] >= 0) == fp4
     assert (lay['pair_h'] == -1) == fp4
+
+
+def test_device_code_has_no_packed_fp32():
+    from k3moe import build
+    assert build.check_no_packed_fp32(_native.LIB_PATH) > 100_000
+
+
+PACKED_PROBE = r'''
+#include <hip/hip_runtime.h>
+extern "C" __global__ void probe(float2* a, const float2* b, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) { float2 x = a[i], y = b[i]; x.x = x.x * y.x + 1.0f; x.y = x.y * y.y + 1.0f; a[i] = x; }
+}
+'''
+
+
+def test_packed_fp32_check_sees_what_the_option_removes(tmp_path):
+    """A float2 kernel built without the option holds packed FP32 and fails the
+    check; built with the library's options it passes."""
+    import subprocess
+    from k3moe import build
+    src = tmp_path / 'probe.hip'
+    src.write_text(PACKED_PROBE)
+    flags = build.command(str(tmp_path / 'with.so'))
+    cmd_with = [a if a != os.path.join(build.CSRC, 'k3moe.hip') else str(src) for a in flags]
+    cmd_without = [a for a in cmd_with if a not in ('-Xclang', '-target-feature', '-packed-fp32-ops')]
+    cmd_without[cmd_without.index(str(tmp_path / 'with.so'))] = str(tmp_path / 'without.so')
+    subprocess.run(cmd_with, check=True, capture_output=True)
+    subprocess.run(cmd_without, check=True, capture_output=True)
+    build.check_no_packed_fp32(str(tmp_path / 'with.so'))
+    with pytest.raises(RuntimeError, match='packed FP32'):
+        build.check_no_packed_fp32(str(tmp_path / 'without.so'))

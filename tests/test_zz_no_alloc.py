@@ -87,3 +87,50 @@ def test_noalloc_rejects_a_step_larger_than_its_scratch(gpu):
     assert rc == -2
     msg = lib.k3moe_last_error().decode()
     assert 'allocation-free' in msg and 'workspace' in msg, msg
+
+
+def scratch_status(dev):
+    st = ctypes.c_int32(-1)
+    rc = _native.load().k3moe_workspace_status(None, ctypes.byref(st),
+                                              ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    _native.check(rc, 'k3moe_workspace_status(NULL)')
+    return st.value
+
+
+def scratch_init(dev):
+    rc = _native.load().k3moe_workspace_init(None, 0, ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    _native.check(rc, 'k3moe_workspace_init(NULL)')
+
+
+def test_noalloc_status_is_readable_and_resettable(gpu):
+    """workspace == NULL reads and resets the scratch's status word: a forced-route row with a repeated
+    id sets K3MOE_STATUS_ROUTES (that row falls back to its own top-k, as the workspace entry point's
+    does), the word stays set over a clean call, and k3moe_workspace_init(NULL) clears it; the next
+    steps again equal the workspace entry point's bit for bit."""
+    scratch_init(gpu)
+    assert scratch_status(gpu) == 0
+    cfg = MoEConfig('forced-b6', 32, 4, 128, 64, 6)
+    say(f'case: {cfg.name} seed=13, a repeated forced id through the allocation-free entry point')
+    g = synthetic.moe_layer_inputs(cfg, 13, device=gpu)
+    own = workspace_step(cfg, g)['expert_ids']
+    routes = own.flip(-1).clone()
+    routes[2, 3] = routes[2, 1]                 # repeated: row 2 is invalid
+    got = noalloc_step(cfg, g, routes.contiguous())
+    torch.cuda.synchronize(gpu)
+    assert scratch_status(gpu) == 2
+    assert torch.equal(got['expert_ids'][2], own[2])
+    clean = noalloc_step(cfg, g)
+    torch.cuda.synchronize(gpu)
+    assert scratch_status(gpu) == 2             # sticky until reset
+    scratch_init(gpu)
+    assert scratch_status(gpu) == 0
+    for cfg2, seed in ((configs.TP8_B8, 14), (configs.TP8_B1, 15)):
+        say(f'case: {cfg2.name} seed={seed} after the reset')
+        g2 = synthetic.moe_layer_inputs(cfg2, seed, device=gpu)
+        want = workspace_step(cfg2, g2)
+        got2 = noalloc_step(cfg2, g2)
+        torch.cuda.synchronize(gpu)
+        for key in want:
+            assert torch.equal(got2[key], want[key]), (cfg2.name, key)
+    assert scratch_status(gpu) == 0
+    assert torch.equal(clean['expert_ids'], own)
