@@ -7,10 +7,10 @@
 //       all its loads in flight, the waves meet in LDS and one partial per
 //       (split, logit) reaches memory.                          (kimi.py:308)
 //   --- barrier 1
-//   T   gating and top-k, one wave per token: partials summed in split
-//       order, sigmoid + bias (or softmax), a register-sorted DPP tournament
-//       for the k largest, weights renormalised, ids sorted. For B <= 16
-//       every workgroup routes every token itself.             (kimi.py:308-316)
+//   T   gating and top-k: partials summed in split order, sigmoid + bias (or
+//       softmax), the k largest by the workgroup's threshold-and-rank
+//       selection (block_topk), weights renormalised, ids sorted; token t is
+//       routed by workgroup t, which publishes its pairs.     (kimi.py:308-316)
 //   --- barrier 2 (only when tokens are routed by different workgroups)
 //   G   every workgroup rebuilds the expert grouping in its own LDS (active
 //       experts ascending, token pairs ascending inside an expert, chunk
@@ -87,6 +87,12 @@ __device__ __forceinline__ uint64_t *lds_align8(int *p) {
   return reinterpret_cast<uint64_t *>(c + ((8 - (reinterpret_cast<uintptr_t>(c) & 7)) & 7));
 }
 
+// The first 16-byte aligned address at or after p (an LDS pointer; see lds_align8).
+__device__ __forceinline__ char *lds_align16(int *p) {
+  char *c = reinterpret_cast<char *>(p);
+  return c + ((16 - (reinterpret_cast<uintptr_t>(c) & 15)) & 15);
+}
+
 // Trace slots of workgroup blockIdx.x starting at `slot`, or null when not tracing.
 __device__ __forceinline__ uint64_t *trace_slots(const Plan &pl, char *ws, int slot) {
   return pl.o_trace ? reinterpret_cast<uint64_t *>(ws + pl.o_trace) + blockIdx.x * kTraceSlots + slot : nullptr;
@@ -116,6 +122,123 @@ __device__ __forceinline__ float red_sum(const float *red, int idx) {
 // Position of element (row, col) of a 16x16 MFMA result in a wave's 256-float tile.
 __device__ __forceinline__ int tile_index(int row, int col) { return (col + 16 * (row >> 2)) * 4 + (row & 3); }
 
+// ------------------------------------------------------- workgroup top-k --
+// LDS of block_topk: per wave the group maxima, the candidates, their count.
+struct BlockTopk {
+  uint64_t gmax[kDecWaves * 32];
+  uint64_t cand[kMaxExperts + 8];  // zeros past the candidates
+  int count;
+};
+
+// One DPP step of a 64-bit maximum or minimum with the lane the control selects.
+template <int Ctrl, bool Max>
+__device__ __forceinline__ uint64_t dpp_fold64(uint64_t v) {
+  const uint64_t o = ((uint64_t)dpp<Ctrl, 0xF>((uint32_t)(v >> 32)) << 32) | dpp<Ctrl, 0xF>((uint32_t)v);
+  return Max ? (o > v ? o : v) : (o < v ? o : v);
+}
+
+// Folds v over aligned runs of n consecutive lanes (n a power of two up to 64):
+// every lane of a run ends with the run's maximum (Max) or minimum. Runs of up
+// to 16 lanes use DPP (quad swaps, then the half-row and row mirrors, which
+// pair every lane with one of the other half once the halves are uniform);
+// longer runs add cross-row shuffles.
+template <bool Max>
+__device__ __forceinline__ uint64_t fold_runs(uint64_t v, int n) {
+  if (n >= 2) v = dpp_fold64<kDppQuadXor1, Max>(v);
+  if (n >= 4) v = dpp_fold64<kDppQuadXor2, Max>(v);
+  if (n >= 8) v = dpp_fold64<kDppHalfMirror, Max>(v);
+  if (n >= 16) v = dpp_fold64<kDppMirror, Max>(v);
+#pragma unroll
+  for (int d = 16; d < 64; d *= 2) {
+    if (n > d) {
+      const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), d, kWave) << 32) |
+                         (uint32_t)__shfl_xor((int)(uint32_t)v, d, kWave);
+      v = Max ? (o > v ? o : v) : (o < v ? o : v);
+    }
+  }
+  return v;
+}
+
+// Top-k (1 <= k <= 32) of the ordered keys kyl[0..E) (E <= 1024) by the whole
+// workgroup, with the order of wave_topk: larger keys first, equal keys in
+// ascending expert order, i.e. the k largest of the distinct 64-bit values
+// key << 32 | ~expert; sel[0..k) gets the experts in that rank order.
+//   1. Threshold: thread t holds experts t and t + 512; with G the power of
+//      two >= k, group g is the experts whose thread's lane lies in the g-th
+//      run of 64 / G lanes (so e mod 64 falls in [64 g / G, 64 (g + 1) / G)).
+//      T = the smallest of the G group maxima. Those maxima are G >= k distinct
+//      values >= T, so the k-th largest value is >= T, and every value above
+//      a top-k value is >= T too: the top k are the k best candidates (v >= T)
+//      and their ranks among the candidates are their ranks. (A group without
+//      experts has maximum 0: then every expert is a candidate.) For
+//      sigmoid-gated routing on 384 experts, top-8, about 21 experts are
+//      candidates.
+//   2. Candidates are appended to an LDS list (order free: a rank does not
+//      depend on it); thread c counts the candidates above candidate c,
+//      reading the list in batches of 8 (LDS broadcasts), and writes ranks
+//      below k to sel.
+// Every thread of the workgroup calls it; it ends with a barrier after sel is written.
+__device__ __forceinline__ void block_topk(const uint32_t *kyl, int E, int k, int *sel, BlockTopk &tk) {
+  const int tid = threadIdx.x, w = wave_id(), l = tid & 63;
+  int G = 1;
+  while (G < k) G <<= 1;
+  const int run = 64 / G;
+  const int e0 = tid, e1 = tid + kDecThreads;
+  const uint64_t v0 = e0 < E ? ((uint64_t)kyl[e0] << 32) | (uint32_t)~e0 : 0ull;
+  const uint64_t v1 = e1 < E ? ((uint64_t)kyl[e1] << 32) | (uint32_t)~e1 : 0ull;
+  const uint64_t m = fold_runs<true>(v0 > v1 ? v0 : v1, run);
+  if ((l & (run - 1)) == 0) tk.gmax[w * 32 + l / run] = m;
+  if (tid == 0) tk.count = 0;
+  // zeros past the candidates: the rank loop reads whole batches of 8, and a zero is above no candidate
+  tk.cand[tid] = 0ull;
+  tk.cand[tid + kDecThreads] = 0ull;
+  __syncthreads();
+  // every wave: lane g < G takes group g's maximum over the waves, then the minimum over lanes 0 .. G - 1
+  uint64_t g = ~0ull;
+  if (l < G) {
+    g = tk.gmax[l];
+#pragma unroll
+    for (int ww = 1; ww < kDecWaves; ++ww) {
+      const uint64_t o = tk.gmax[ww * 32 + l];
+      g = o > g ? o : g;
+    }
+  }
+  g = fold_runs<false>(g, G);
+  const uint64_t T = ((uint64_t)lane_u32((uint32_t)(g >> 32), 0) << 32) | lane_u32((uint32_t)g, 0);
+  const bool f0 = e0 < E && v0 >= T, f1 = e1 < E && v1 >= T;
+  const uint64_t b0 = __ballot(f0), b1 = __ballot(f1);
+  const int n0 = __popcll(b0), n = n0 + __popcll(b1);
+  int base = 0;
+  if (n > 0) {
+    if (l == 0) base = atomicAdd(&tk.count, n);
+    base = __builtin_amdgcn_readfirstlane(base);
+  }
+  const int below0 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b0, 0u));
+  const int below1 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0u));
+  if (f0) tk.cand[base + below0] = v0;
+  if (f1) tk.cand[base + n0 + below1] = v1;
+  __syncthreads();
+  // candidate c by thread c; the list is read in batches of 8 (LDS broadcasts: every lane reads the same words)
+  const int nc = __builtin_amdgcn_readfirstlane(tk.count);
+  for (int c0 = w * 64; c0 < nc; c0 += kDecThreads) {
+    const int c = c0 + l;
+    const uint64_t me = c < nc ? tk.cand[c] : 0ull;
+    int rank = 0;
+    for (int j = 0; j < nc; j += 8) {
+      const u32x4 *p = reinterpret_cast<const u32x4 *>(tk.cand + j);
+      u32x4 q4[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) q4[t] = p[t];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint64_t oa = ((uint64_t)q4[t][1] << 32) | q4[t][0], ob = ((uint64_t)q4[t][3] << 32) | q4[t][2];
+        rank += (oa > me ? 1 : 0) + (ob > me ? 1 : 0);
+      }
+    }
+    if (c < nc && rank < k) sel[rank] = (int)~(uint32_t)me;
+  }
+  __syncthreads();
+}
 
 // ---------------------------------------------------------------- gate/up --
 // A unit is 8 gate + 8 up rows of one (active expert, chunk of up to NX
@@ -1021,58 +1144,17 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       __syncthreads();
       if (s_fail) return give_up();
       trace_mark(pl, a.ws, 10);
-      // One token per pass: the 8 waves share its selection. With E <= 512
-      // and k <= 8, wave w selects the 8 best of experts 64 w .. 64 w + 63 as
-      // (key, ~expert) values with a bitonic network (8-lane sorts, three
-      // merge levels) and offers its k best; wave 0 merges the 8 sorted
-      // offers the same way and keeps the first k. With E <= 1024 and k <= 32, wave w
-      // sorts experts 64 w .. and 64 (w + 8) .. and merges them into its 32
-      // best; wave 0 merges the 8 offers in a tree of three levels. Otherwise
-      // one wave per token runs wave_topk.
-      const bool coop = nt == 1 && E <= kDecWaves * 64 && k <= 8;
-      const bool coop2 = nt == 1 && !coop && E <= 2 * kDecWaves * 64 && k <= 32;
+      // One token per pass: the workgroup's threshold-and-rank selection
+      // (block_topk, E <= 1024, k <= 32). Several tokens per pass: one wave
+      // per token runs wave_topk.
+      const bool coop = nt == 1;
       for (int tg = 0; tg < nt; tg += kDecWaves) {
-        if (coop2) {
-          uint64_t *cand = lds_align8(sel + kDecWaves * kMaxTopk);  // [8][32]
-          const int e0 = w * 64 + l, e1 = (w + kDecWaves) * 64 + l;
-          uint64_t v0 = e0 < E ? ((uint64_t)kyl[e0] << 32) | (uint32_t)~e0 : 0ull;
-          uint64_t v1 = e1 < E ? ((uint64_t)kyl[e1] << 32) | (uint32_t)~e1 : 0ull;
-          v0 = wave_sort_desc(v0);
-          v1 = wave_sort_desc(v1);
-          const uint64_t mine = merge_top32(v0, v1);
-          if (l < 32) cand[w * 32 + l] = mine;
-          __syncthreads();
-          if (w == 0) {
-            uint64_t c[kDecWaves];
-#pragma unroll
-            for (int j = 0; j < kDecWaves; ++j) c[j] = cand[j * 32 + (l & 31)];
-            const uint64_t c01 = merge_top32(c[0], c[1]), c23 = merge_top32(c[2], c[3]);
-            const uint64_t c45 = merge_top32(c[4], c[5]), c67 = merge_top32(c[6], c[7]);
-            const uint64_t top = merge_top32(merge_top32(c01, c23), merge_top32(c45, c67));
-            if (l < k) sel[l] = (int)~(uint32_t)top;
-            wave_lds_order();
-          }
-        }
-        if (coop) {
-          uint64_t *cand = lds_align8(sel + kDecWaves * kMaxTopk);  // [8 k]
-          const int e = w * 64 + l;
-          uint64_t v = e < E ? ((uint64_t)kyl[e] << 32) | (uint32_t)~e : 0ull;
-          v = wave_top8_desc(v);
-          if (l < k) cand[w * k + l] = v;
-          __syncthreads();
-          if (w == 0) {
-            // offer j in lanes 8 j .. 8 j + 7, descending, zeros past its k
-            uint64_t c = (l & 7) < k ? cand[(l >> 3) * k + (l & 7)] : 0ull;
-            c = wave_merge8_desc(c);
-            if (l < k) sel[l] = (int)~(uint32_t)c;
-            wave_lds_order();
-          }
-        }
+        if (coop) block_topk(kyl, E, k, sel, *reinterpret_cast<BlockTopk *>(lds_align16(sel + kDecWaves * kMaxTopk)));
         const int tl = tg + w;
         if (tl >= nt) continue;
         const int t = t0 + tl;
         int *mysel = sel + w * kMaxTopk;
-        if (!coop && !coop2) wave_topk(kyl + tl * E, E, k, mysel);
+        if (!coop) wave_topk(kyl + tl * E, E, k, mysel);
         wave_lds_order();
         trace_mark(pl, a.ws, 30);
         const bool writer = redundant ? blockIdx.x == 0 : true;

@@ -488,42 +488,6 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v) {
   return v;
 }
 
-// Levels 1-3 of a top-8 selection: 8-lane lists in lanes 8 g .. 8 g + 7,
-// descending for even g and ascending for odd g, are merged pairwise (lanes
-// l and l ^ 8, then l ^ 16, then l ^ 32): the larger of each pair stays in the
-// lower list, whose 8 values then form a bitonic sequence that three stages
-// sort, in the direction the next level needs. Lanes 0..7 end with the 8
-// largest values, descending.
-__device__ __forceinline__ uint64_t wave_top8_levels(uint64_t v, int l) {
-  v = bitonic_step<64, 8>(v, l);
-  v = bitonic_merge<16, 4>(v, l);
-  v = bitonic_step<64, 16>(v, l);
-  v = bitonic_merge<32, 4>(v, l);
-  v = bitonic_step<64, 32>(v, l);
-  return bitonic_merge<64, 4>(v, l);
-}
-
-// The 8 largest of one 64-bit value per lane, descending in lanes 0..7: the
-// 8-lane groups are sorted with alternating directions (the first six stages
-// of a bitonic sort), then merged in three levels (18 stages instead of 21).
-__device__ __forceinline__ uint64_t wave_top8_desc(uint64_t v) {
-  const int l = __lane_id();
-  v = bitonic_merge<2, 1>(v, l);
-  v = bitonic_merge<4, 2>(v, l);
-  v = bitonic_merge<8, 4>(v, l);
-  return wave_top8_levels(v, l);
-}
-
-// The 8 largest of eight lists sorted descending in lanes 8 g .. 8 g + 7,
-// descending in lanes 0..7: odd lists reversed (DPP half-row mirror), then the
-// three merge levels (13 stages).
-__device__ __forceinline__ uint64_t wave_merge8_desc(uint64_t v) {
-  const int l = __lane_id();
-  const uint64_t m = ((uint64_t)dpp<kDppHalfMirror, 0xF>((uint32_t)(v >> 32)) << 32) |
-                     dpp<kDppHalfMirror, 0xF>((uint32_t)v);
-  return wave_top8_levels((l & 8) ? m : v, l);
-}
-
 // Top 32 of two lists sorted descending in lanes 0..31 (a and b), sorted
 // descending in lanes 0..31: b reversed into lanes 32..63 makes a bitonic
 // sequence of 64, which one 6-stage merge sorts.

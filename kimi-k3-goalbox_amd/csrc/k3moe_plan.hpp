@@ -34,6 +34,9 @@ constexpr int kDecMaxLds = 160 * 1024;   // gfx950: 160 KiB of LDS per workgroup
 constexpr int kDecStaticLds = 1024;
 constexpr int kDnStage = 128;        // decode down: y rows staged per wave (32 B + a 4-byte tag each)  // decode kernel's static LDS (round table, counters), upper bound
 
+// LDS of the workgroup top-k (block_topk): per-wave group maxima, up to kMaxExperts candidates, a count
+constexpr int kBlockTopkBytes = 8 * (kDecWaves * 32 + kMaxExperts + 8) + 16;
+
 constexpr int kRedundantTokens = 1;    // decode: route every token in every workgroup up to this batch
 constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert) keys
 
@@ -129,7 +132,7 @@ inline int decode_lds(Plan &p) {
   p.redundant = p.B * p.E <= kRedundantKeys && p.B <= kRedundantTokens;
   const int nt = p.redundant ? p.B : 1;
   const int routed = 8 * p.P;                                       // ids + weights per pair
-  const int topk = routed + 4 * (3 * nt * p.E + kDecWaves * kMaxTopk) + 8 * kDecWaves * 32 + 8;  // keys, scores, picks, offers
+  const int topk = routed + 4 * (3 * nt * p.E + kDecWaves * kMaxTopk) + 16 + kBlockTopkBytes;  // keys, scores, picks, block_topk
   const int group = routed + 4 * (4 * p.E + 32);                    // counts, offsets, bitmaps, wave sums
   int down = (p.B <= 16 ? 2 : 1) * kDecWaves * p.B * 16 * 4;       // paired down: per-wave accumulators (2 row tiles)
   if (down < kDecWaves * kDnStage * 36) down = kDecWaves * kDnStage * 36;  // expert-major down: per-wave y stages
@@ -150,15 +153,14 @@ inline int decode_lds(Plan &p) {
 }
 
 // The single-token kernel (k3moe_single.hpp) takes the step when it fits:
-// one token, top-k <= 8 of at most 512 experts (its top-k is the 8-wave
-// cooperative selection), the expert width K a multiple of 512 (whole
+// one token, top-k <= 8 of at most 512 experts, the expert width K a multiple of 512 (whole
 // 512-column gate/up super-steps, at most kSingleMaxSS per wave) and at most
 // 8192 (its staged row), I <= 256 (the down projection's two k-steps), at most
 // two 16-row output tiles per workgroup, and its tagged partials and
 // intermediates fitting the tag area. Its dynamic LDS: the keys (3 E words),
-// the staged row (2 K bytes) and fixed scratch.
+// the staged row (2 K bytes), fixed scratch and the top-k's.
 constexpr int kSingleMaxSS = 2;  // gate/up super-steps of 512 columns per wave: ceil(K / 4096)
-inline int single_lds(const Plan &p) { return align16(3 * 4 * p.E) + 2 * p.K + 8192; }
+inline int single_lds(const Plan &p) { return align16(3 * 4 * p.E) + 2 * p.K + 8192 + kBlockTopkBytes; }
 inline void single_plan(const k3moe_dims &d, Plan &p) {
   const bool tags_fit = (long)kTagCopies * p.E * 8 * 8 + (long)p.k * (p.I / 2) * 8 <= kTagBytes;
   p.single = (d.path == K3MOE_PATH_AUTO || d.path == K3MOE_PATH_SINGLE) && p.B == 1 && p.k <= 8 && p.E <= 512 &&

@@ -13,7 +13,8 @@
 //   T   every workgroup polls the partials of the experts its threads hold
 //       (thread e: expert e), sums them in split order, gates them (sigmoid
 //       + bias, or the logits; kimi.py:308-315, tasks/distributed.py:174-176)
-//       and selects the top k (k <= 8) with the 8-wave cooperative network;
+//       and selects the top k (k <= 8) with the workgroup's threshold-and-rank
+//       selection (block_topk);
 //       valid forced routes replace the selection (kimi.py:311-313).
 //   GU  gate/up (kimi.py:321-322): the k x I/8 units (8 gate + 8 up rows of
 //       one chosen expert) go to the workgroups in turn (exactly one each at
@@ -47,7 +48,6 @@ constexpr uint32_t kTraceSingle = 0x5349u;  // trace slot 55 of the single-token
 // Fixed LDS scratch of the single-token kernel, after the keys and the staged row.
 struct SingleScratch {
   int sel[kDecWaves * kMaxTopk];         // selection output (sel[0..k) in rank order)
-  uint64_t cand[kDecWaves * 8];          // the waves' top-8 offers
   float rred[kDecWaves * 16];            // router: the waves' 16 partial logits
   float gred[kDecWaves * 16];            // gate/up: the waves' 16 partial rows
   uint16_t hs[8 * 256];                  // down: each chosen expert's h (bf16)
@@ -56,6 +56,7 @@ struct SingleScratch {
   float wts[8];                          // their gating weights
 };
 static_assert(sizeof(SingleScratch) <= 8192, "single_lds reserves 8 KiB of scratch");
+static_assert(sizeof(SingleScratch) % 16 == 0 && sizeof(BlockTopk) <= kBlockTopkBytes, "single_lds layout");
 
 // Polls tagged slots until every lane's `n` slots (n in 0..2, read as one
 // 16-byte device-coherent load at byte offset `off` of `r`) carry `tag`;
@@ -91,6 +92,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   float *scl = kyf + E;                               // [E] scores
   uint16_t *xs = reinterpret_cast<uint16_t *>(lds + align16(12 * E));  // [K] the token's expert-input row
   SingleScratch &sh = *reinterpret_cast<SingleScratch *>(lds + align16(12 * E) + 2 * K);
+  BlockTopk &tk = *reinterpret_cast<BlockTopk *>(lds + align16(12 * E) + 2 * K + sizeof(SingleScratch));
   __shared__ uint32_t s_tag, s_abort0;
   __shared__ int s_fail;
 
@@ -281,20 +283,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     __syncthreads();
     if (s_fail) return leave(true);
     trace_mark(pl, a.ws, 3);
-    // wave w offers the 8 best of experts 64 w .. 64 w + 63; wave 0 merges the offers
-    {
-      const int e = w * 64 + l;
-      uint64_t v = e < E ? ((uint64_t)kyl[e] << 32) | (uint32_t)~e : 0ull;
-      v = wave_top8_desc(v);
-      if (l < k) sh.cand[w * k + l] = v;
-      __syncthreads();
-      if (w == 0) {
-        uint64_t c = (l & 7) < k ? sh.cand[(l >> 3) * k + (l & 7)] : 0ull;
-        c = wave_merge8_desc(c);
-        if (l < k) sh.sel[l] = (int)~(uint32_t)c;
-        wave_lds_order();
-      }
-    }
+    // the workgroup's top-k: a threshold from group maxima, then exact ranks among the candidates
+    block_topk(kyl, E, k, sh.sel, tk);
     trace_mark(pl, a.ws, 4);
     if (w == 0) {
       // forced routes replace the selection when the row is valid (kimi.py:311-313)
