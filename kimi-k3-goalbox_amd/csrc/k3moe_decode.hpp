@@ -601,6 +601,134 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
   trace_mark(pl, a.ws, 15);
 }
 
+// ------------------------------------------------------ gate/up, pinned --
+// For batches whose token rows all fit in LDS (xs, row t at t * xpitch): the
+// gate/up units (8 gate + 8 up rows of one chunk of up to 16 of an active
+// expert's tokens; unit u = chunk u / U8, rows 8 (u mod U8) ..) are shared out
+// over all waves of the grid as contiguous ranges of whole units: global wave
+// gw = 8 b + w takes units [NU gw / 8G, NU (gw + 1) / 8G). First the rows of
+// the tokens in the workgroup's chunks go to LDS (direct-to-LDS loads, 1 KiB
+// of a row per instruction, spread over the waves), each wave issuing its share
+// before its first three super-steps of weights, so that waiting for its rows
+// (vmcnt) leaves the weights in flight; a barrier publishes the rows. Then a
+// wave streams its units' super-steps (16 MXFP4 blocks of 16 rows, 512 k) with
+// four in flight and finishes each unit itself (activation, bf16 h): it
+// shares nothing with the workgroup's other waves and moves on to the down
+// phase as soon as its units are done. Every wave of the workgroup calls it;
+// it returns after the wave's h stores have completed.
+template <bool AL>
+__device__ __forceinline__ void gu_pinned(const Plan &pl, const DecodeArgs &a, const int *g_act, const int *g_aoff,
+                                          const int *g_acnt, const int *g_coff, const int *g_cexp, const int *g_ptok,
+                                          uint16_t *xs, int *s_prog, uint16_t *hbuf, int ua, int ub, int wa, int wb) {
+  static_assert(AL, "pinned rows are loaded in whole 512-column chunks");
+  const int w = wave_id(), l = threadIdx.x & 63, i = l & 15;
+  const int KB = pl.K / kBlockK, NSS = KB / 16, U8 = pl.U8;
+  const int n = (ub - ua) * NSS;  // this wave's super-steps
+  const uint8_t *const lane_blk = i >= 8 ? a.ublk : a.gblk;
+  const uint8_t *const lane_scl = i >= 8 ? a.uscl : a.gscl;
+  // chunk c of active expert d = g_cexp[c]: pairs pbase .. pbase + nt - 1 of the expert
+  auto chunk = [&](int c, int &pbase, int &nt) {
+    const int d = g_cexp[c];
+    pbase = g_aoff[d] + (c - g_coff[d]) * 16;
+    nt = min(16, g_aoff[d] + g_acnt[d] - pbase);
+  };
+  trace_mark(pl, a.ws, 12);
+  // the workgroup's token rows: tokens of its chunks (units [wa, wb)), as a bit set (B <= 64)
+  uint64_t rows = 0;
+  if (wa < wb) {
+    for (int c = wa / U8; c <= (wb - 1) / U8; ++c) {
+      int pbase, nt;
+      chunk(c, pbase, nt);
+      const int t = l < nt ? g_ptok[pbase + l] : 0;
+      const uint64_t bit = l < nt ? 1ull << t : 0ull;  // each lane's token bit, OR-ed over the wave
+      rows |= ((uint64_t)wave_or_u32((uint32_t)(bit >> 32)) << 32) | wave_or_u32((uint32_t)bit);
+    }
+  }
+  {
+    const int per_row = pl.K / 512, nrows = __popcll(rows);
+    uint64_t left = rows;
+    int r = 0, rr = -1;
+    for (int c = w; c < nrows * per_row; c += kDecWaves) {
+      const int want = c / per_row;  // the want-th set bit of rows
+      while (rr < want) {
+        r = __builtin_ctzll(left);
+        left &= left - 1;
+        ++rr;
+      }
+      const int j = c - want * per_row;
+      load_lds<16>(a.xin + (size_t)r * pl.K + j * 512 + l * 8,
+                   reinterpret_cast<char *>(xs + (size_t)r * pl.xpitch + j * 512));
+    }
+  }
+  asm volatile("" ::: "memory");  // the row loads stay ahead of the weights
+  auto rows_of = [&](int u, const uint8_t *(&wr)[1], const uint8_t *(&sr)[1]) {
+    const int c = u / U8;
+    const size_t row = (size_t)g_act[g_cexp[c]] * pl.I + (u - c * U8) * 8 + (i & 7);
+    wr[0] = lane_blk + row * KB * 16;
+    sr[0] = lane_scl + row * KB;
+  };
+  auto xrow_of = [&](int u) {  // lane column i: token i of the unit's chunk (the last one again past its end)
+    int pbase, nt;
+    chunk(u / U8, pbase, nt);
+    return (const uint16_t *)(xs + (size_t)g_ptok[pbase + min(i, nt - 1)] * pl.xpitch);
+  };
+  // issue cursor: position ip (unit iu, super-step iss); past the last position it stays there
+  // (an unconditional issue of an L2-resident step keeps the compiler's waits exact)
+  const uint8_t *iwr[1], *isr[1];
+  int ip = 0, iu = ua, iss = 0;
+  auto issue = [&](GuSS<1> &buf) {
+    gu_issue<1, AL>(buf, iwr, isr, iss, KB);
+    if (ip + 1 < n) {
+      ++ip;
+      if (++iss == NSS) {
+        iss = 0;
+        rows_of(++iu, iwr, isr);
+      }
+    }
+  };
+  GuSS<1> R0, R1, R2, R3;
+  if (n > 0) {
+    rows_of(iu, iwr, isr);
+    issue(R0);
+    issue(R1);
+    issue(R2);
+    wait_vm<3 * 5>();  // this wave's row loads have landed; the 3 super-steps (5 loads each) stay in flight
+  } else {
+    wait_vm<0>();
+  }
+  trace_mark(pl, a.ws, 13);
+  ring_barrier();  // every wave's rows are in LDS
+  trace_mark(pl, a.ws, 33);
+  if (n <= 0) return;
+  int cu = ua, css = 0;
+  const uint16_t *xrow = xrow_of(cu);
+  f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
+  // step(pos): issue position pos + 3 into nxt, then compute position pos from cur
+  auto step = [&](GuSS<1> &cur, GuSS<1> &nxt, int pos) {
+    issue(nxt);
+    if (pos >= n) return;  // wave-uniform: the tail of the last group of four
+    gu_compute<1, AL>(cur, xrow, css, KB, acc);
+    balance_waves(s_prog, pos + 1, n);
+    if (++css == NSS) {
+      int pbase, nt;
+      chunk(cu / U8, pbase, nt);
+      gu_finish_wave(pl, hbuf, acc[0], pbase + i, i < nt, (cu % U8) * 8);
+      acc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      css = 0;
+      if (pos + 1 < n) xrow = xrow_of(++cu);
+    }
+  };
+  for (int pos = 0; pos < n; pos += 4) {
+    step(R0, R3, pos);
+    step(R1, R0, pos + 1);
+    step(R2, R1, pos + 2);
+    step(R3, R2, pos + 3);
+  }
+  __builtin_amdgcn_s_setprio(0);
+  trace_mark(pl, a.ws, 34);
+  wait_vmem();  // the h stores (device-coherent) have completed
+}
+
 // ---------------------------------------------------- down, expert-major --
 // For many active experts: a wave streams a contiguous run of (expert, 16-row
 // tile) items; the B operand (the expert's h rows, KSD = I / 128 k-steps) is
@@ -647,9 +775,10 @@ __device__ __forceinline__ void dnc_issue(DnTileBatch<KSD> &bt, const Plan &pl, 
 // weight stream would queue behind (and hold up) its loads. The buffer is
 // written out with 16-byte stores when full and at the end of the wave's range.
 struct DnStage {
-  uint16_t *rows;  // [kDnStage][16] bf16
-  int *tag;        // [kDnStage] pair << 16 | row tile
+  uint16_t *rows;  // [cap][16] bf16
+  int *tag;        // [cap] pair << 16 | row tile
   int fill;
+  int cap;         // rows the stage holds (kDnStage, or what the pinned rows leave)
 };
 
 __device__ __forceinline__ void dn_flush(DnStage &st, const Plan &pl, uint16_t *ybuf) {
@@ -684,7 +813,7 @@ __device__ __forceinline__ void dnc_compute(const DnTileBatch<KSD> &bt, const Pl
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) acc = mfma16(av[kk], as_bf16x8(hb[ks][kk]), acc);
     }
-    if (st.fill + ncol > kDnStage) dn_flush(st, pl, ybuf);
+    if (st.fill + ncol > st.cap) dn_flush(st, pl, ybuf);
     if (i < ncol) {
       const u32x2 packed = {(uint32_t)f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16),
                             (uint32_t)f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16)};
@@ -897,6 +1026,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   int *g_pof = reinterpret_cast<int *>(g_pw + pl.P);  // pair index of (token, slot)
   int *g_cexp = g_pof + pl.P;  // [P] active expert (index into g_act) of each gate/up chunk
   char *scr = lds + pl.lds_red + pl.lds_grp;
+  uint16_t *xpin = reinterpret_cast<uint16_t *>(scr + pl.lds_scr);  // pinned: every token's expert-input row
   __shared__ int s_nact;
   __shared__ GuChunk s_tab[16];
   __shared__ int s_round[2], s_rowtok[16];
@@ -979,6 +1109,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       code_probe = *reinterpret_cast<const __attribute__((address_space(1))) u32x4 *>(at);
     }
   };
+
+  if (l == 0) __hip_atomic_store(s_prog + w, 4096, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 
   // ------------------------------------------------------------ R: router --
   // Workgroup unit = (16 router rows, k-split s) for every token tile: the 8
@@ -1105,9 +1237,13 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
         const uint32_t pbase = (uint32_t)(kTagDecPart + (size_t)t0 * pl.Srw * pl.Epad * 8);
         const uint32_t sstride = (uint32_t)pl.Epad * 8;
         u32x2 v0[kDecMaxSplits], v1[kDecMaxSplits];
+#pragma unroll
+        for (int sp = 0; sp < kDecMaxSplits; ++sp) v0[sp] = v1[sp] = u32x2{0u, tag};
         bool ok = true;
         unsigned spins = 0;
-        for (;;) {
+        // a wave without experts to poll skips the loop (wave-uniform): its
+        // waits would also cover loads it issued earlier (the pinned rows)
+        for (; w * 64 < E;) {
 #pragma unroll
           for (int sp = 0; sp < kDecMaxSplits; ++sp) {
             v0[sp] = sp < n0 ? bload8_dev(tagr, pbase + sp * sstride + e0 * 8) : u32x2{0u, tag};
@@ -1212,10 +1348,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   trace_mark(pl, a.ws, 3);
   if (!redundant) {
     // every pair's slot (pairs tid and tid + 512), polled until both halves carry this launch's tag
-    u32x4 pv[2];
+    u32x4 pv[2] = {u32x4{0u, tag, 0u, tag}, u32x4{0u, tag, 0u, tag}};
     bool ok = true;
     unsigned spins = 0;
-    for (;;) {
+    for (; w * 64 < pl.P;) {  // waves without pairs to poll skip it (see the logit poll)
       bool ready = true;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -1355,7 +1491,22 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   trace_mark(pl, a.ws, 5);
 
   // ------------------------------------------------------------ GU: gate/up --
-  {
+  // pinned: this wave's range of whole units (global wave gw of 8 G)
+  const unsigned gw = blockIdx.x * kDecWaves + w;
+  const int pin_nu = g_coff[D] * pl.U8;
+  auto wave_unit = [&](unsigned v) {  // NU v / 8G for the persistent grid (a power of two)
+    return (int)(((uint64_t)(unsigned)pin_nu * v) >> (__builtin_ctz(gridDim.x) + 3));
+  };
+  const int pin_ua = wave_unit(gw), pin_ub = wave_unit(gw + 1);
+  bool pinned_done = false;  // (pinned plans have K a multiple of 512: AL)
+  if constexpr (AL) {
+    if (pl.pinned) {
+      gu_pinned<AL>(pl, a, g_act, g_aoff, g_acnt, g_coff, g_cexp, g_ptok, xpin, s_prog, hbuf, pin_ua, pin_ub,
+                    wave_unit(blockIdx.x * kDecWaves), wave_unit((blockIdx.x + 1) * kDecWaves));
+      pinned_done = true;
+    }
+  }
+  if (!pinned_done) {
     uint16_t *xs = reinterpret_cast<uint16_t *>(scr);  // staged activation rows (the scratch is free now)
     if (gu_pairs(g_coff[D] * pl.U8))
       gu_phase<2, AL>(pl, a, red, g_act, g_aoff, g_acnt, g_coff, g_cexp, g_ptok, xs, s_tab, s_round, s_rowtok, s_prog, D, hbuf, xpre, xpre_ok);
@@ -1387,16 +1538,25 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   const int ngu = g_coff[D] * (pl.U8 / gu_w);
   // the workgroup whose range holds group x: the largest b with NG b / G <= x
   auto wg_of = [&](unsigned x) { return (int)(((x + 1u) * gridDim.x - 1u) / (unsigned)ngu); };
+  // pinned: the wave whose range holds unit u: the largest gw with NU gw / 8G <= u
+  auto wave_of = [&](unsigned u) {
+    return (int)(((uint64_t)(u + 1u) * (gridDim.x * kDecWaves) - 1u) / (unsigned)pin_nu);
+  };
   auto wait_expert = [&](int d) {  // bounded: a timeout sets the status word; gives up with the launch
     const unsigned gpc = (unsigned)(pl.U8 / gu_w);
-    const int b0 = wg_of((unsigned)g_coff[d] * gpc), b1 = wg_of((unsigned)g_coff[d + 1] * gpc - 1u);
+    // the slots to poll: workgroups b0 .. b1 (slot d + b), or, pinned, waves b0 .. b1 (slot gw)
+    const int b0 = pl.pinned ? wave_of((unsigned)g_coff[d] * pl.U8) : wg_of((unsigned)g_coff[d] * gpc);
+    const int b1 = pl.pinned ? wave_of((unsigned)g_coff[d + 1] * pl.U8 - 1u)
+                             : wg_of((unsigned)g_coff[d + 1] * gpc - 1u);
     unsigned spins = 0;
     for (int bs = b0; bs <= b1; bs += 64) {
       const int b = bs + l;
-      // workgroups in [b0, b1] with an empty range (fewer groups than workgroups) write no slot
-      const bool need = b <= b1 && grid_share(ngu, b) < grid_share(ngu, b + 1);
+      // workgroups (waves) in [b0, b1] with an empty range (fewer groups than workgroups) write no slot
+      const bool need = b <= b1 && (pl.pinned ? wave_unit(b) < wave_unit(b + 1)
+                                              : grid_share(ngu, b) < grid_share(ngu, b + 1));
+      const uint32_t slot = (uint32_t)(kTagDecDone + (pl.pinned ? b : d + b) * 8);
       for (;;) {
-        const u32x2 v = need ? bload8_dev(tagr, (uint32_t)(kTagDecDone + (d + b) * 8)) : u32x2{0u, tag};
+        const u32x2 v = need ? bload8_dev(tagr, slot) : u32x2{0u, tag};
         if (__ballot(v[1] != tag) == 0) break;
         ++spins;
         if ((spins & 63u) == 0u && aborted(ctl, abort0)) return;
@@ -1411,7 +1571,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     // order; this keeps the compiler from hoisting them)
     asm volatile("" ::: "memory");
   };
-  if (expert_major || dn_pair) {
+  if ((expert_major || dn_pair) && pl.pinned) {
+    // this wave's units are done (gu_pinned waited for its h stores): its slot gw
+    if (pin_ua < pin_ub && l == 0) st_dev64(tagr, (uint32_t)(kTagDecDone + gw * 8), u32x2{0u, tag});
+  } else if (expert_major || dn_pair) {
     wait_vmem();
     __syncthreads();
     const int ga = grid_share(ngu, blockIdx.x), gb = grid_share(ngu, blockIdx.x + 1);
@@ -1439,9 +1602,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     const int NT = D * pl.RTd;  // (expert, 16-row tile) items, expert-major
     const int gw = blockIdx.x * kDecWaves + w;
     const int ta = grid_share(NT, gw) >> 3, tb = grid_share(NT, gw + 1) >> 3;  // NT * gw / (8 G)
-    DnStage st;  // this wave's y stage in the scratch area (free after gate/up)
-    st.rows = reinterpret_cast<uint16_t *>(scr) + w * kDnStage * 16;
-    st.tag = reinterpret_cast<int *>(scr + kDecWaves * kDnStage * 32) + w * kDnStage;
+    DnStage st;  // this wave's y stage in the scratch area (free after the grouping)
+    st.cap = pl.dn_cap;
+    st.rows = reinterpret_cast<uint16_t *>(scr) + w * st.cap * 16;
+    st.tag = reinterpret_cast<int *>(scr + kDecWaves * st.cap * 32) + w * st.cap;
     st.fill = 0;
     if constexpr (KSD > 0) dn_expert_major<KSD>(pl, a, g_act, g_aoff, g_acnt, zero, hrs, st, ybuf, ta, tb, wait_expert);
     if (pl.o_trace && l == 0)  // every wave's stream end (before its y flush)

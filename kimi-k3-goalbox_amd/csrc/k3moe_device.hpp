@@ -355,6 +355,16 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+  v |= dpp<kDppQuadXor1, 0xF>(v);
+  v |= dpp<kDppQuadXor2, 0xF>(v);
+  v |= dpp<kDppHalfMirror, 0xF>(v);
+  v |= dpp<kDppMirror, 0xF>(v);
+  v |= dpp<kDppBcast15, 0xA>(v);
+  v |= dpp<kDppBcast31, 0xC>(v);
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   v = min(v, dpp<kDppQuadXor1, 0xF>(v));
   v = min(v, dpp<kDppQuadXor2, 0xF>(v));

@@ -81,10 +81,11 @@ constexpr int kTagBytes = 2 * 1024 * 1024;
 constexpr int kTagCopies = 8;  // single-token router partials: one copy per XCD (workgroup b reads copy b mod 8)
 // The decode kernel's regions: the routed pairs (16-byte slots {id, tag,
 // weight, tag}), the gate/up completion slots (slot d + b: active expert d,
-// workgroup b), then the router partials ([B][Srw][Epad] slots).
+// workgroup b; or, pinned, slot gw: the workgroup's wave gw = 8 b + w), then
+// the router partials ([B][Srw][Epad] slots).
 constexpr int kTagDecPairs = 0;
 constexpr int kTagDecDone = kTagDecPairs + kDecMaxPairs * 16;
-constexpr int kTagDecPart = kTagDecDone + (kMaxExperts + 1024) * 8;
+constexpr int kTagDecPart = kTagDecDone + 8 * 1024 * 8;  // done slots: d + b (staged), or wave gw < 8 x 1024 (pinned)
 constexpr int kOffTag = kOffLatCnt + kLatCntBytes;
 constexpr int kInitBytes = kOffTag + kTagBytes;  // control block (page-padded), zero area, counters, tags
 constexpr int kTraceSlots = 56;    // phase timestamps per workgroup when tracing
@@ -110,6 +111,10 @@ struct Plan {
   int lds_red, lds_grp, lds_scr, lds_total;  // dynamic LDS layout, bytes
   int NX;      // gate/up: activation rows staged in LDS per round (also the chunk size in tokens)
   int xpitch;  // staged row pitch in elements (K + 8: rows start in different banks)
+  int pinned;  // 1: every token's expert-input row stays in LDS from the kernel's start (gate/up by whole units per wave)
+  int lds_pin;  // bytes of the pinned rows (the last LDS region)
+  int dn_cap;   // expert-major down: y rows staged per wave
+  int pad_;
   int trace;      // 1: the decode kernel records phase timestamps at o_trace
   int single;     // 1: the single-token kernel runs the step (k3moe_single.hpp)
   int redundant;  // 1: every workgroup routes every token (no barrier before grouping)
@@ -125,11 +130,47 @@ __host__ __device__ inline int cdiv(long a, long b) { return (int)((a + b - 1) /
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 __host__ __device__ inline int align16(int v) { return (v + 15) & ~15; }
 
-// Decode-path LDS layout for plan p; returns the total bytes.
+// Decode-path LDS layout for plan p; returns the total bytes. Regions: red
+// (the router's per-wave tiles; the staged gate/up's cut-group tiles), grp
+// (the grouping lists), scr (top-k, grouping and down scratch; the staged
+// gate/up's activation rows), then, when pinned, every token's row.
+// Pinned: from 2 tokens up to as many as fit, the token rows are loaded to LDS
+// at the kernel's start; gate/up then gives each wave whole units (no
+// staging rounds, no groups cut between waves) and chunks of up to 16 tokens.
 inline int decode_lds(Plan &p) {
-  p.lds_red = kDecWaves * 2 * 2 * 256 * 4;                          // per wave 2 x 2 16x16 fp32 tiles
+  const int room_all = kDecMaxLds - kDecStaticLds;
+  p.xpitch = p.K + 8;
   p.lds_grp = align16(4 * (4 * p.Dmax + 1 + 4 * p.P));              // active list + chunk offsets + pairs + chunk experts
   p.redundant = p.B * p.E <= kRedundantKeys && p.B <= kRedundantTokens;
+  {
+    const int nt = p.redundant ? p.B : 1;
+    const int topk = 8 * p.P + 4 * (3 * nt * p.E + kDecWaves * kMaxTopk) + 16 + kBlockTopkBytes;
+    const int group = 8 * p.P + 4 * (4 * p.E + 32);
+    int scr = topk > group ? topk : group;
+    int down = (p.B <= 16 ? 2 : 1) * kDecWaves * p.B * 16 * 4;
+    if (down < p.P * 16 * 4) down = p.P * 16 * 4;
+    if (down > scr) scr = down;
+    const int red = cdiv(p.B, 16) * kDecWaves * 256 * 4;
+    const int pin = p.B * p.xpitch * 2;
+    // the expert-major down's y stage takes what is left, up to kDnStage rows per wave
+    int cap = (room_all - red - p.lds_grp - pin - 16) / (kDecWaves * 36);
+    if (cap > kDnStage) cap = kDnStage;
+    cap &= ~15;
+    if (kDecWaves * cap * 36 > scr) scr = kDecWaves * cap * 36;
+    p.pinned = p.B >= 2 && p.K % 512 == 0 && cap >= 32 && red + p.lds_grp + align16(scr) + pin <= room_all;
+    if (p.pinned) {
+      p.lds_red = red;
+      p.lds_scr = align16(scr);
+      p.lds_pin = pin;
+      p.dn_cap = cap;
+      p.NX = 16;
+      p.lds_total = p.lds_red + p.lds_grp + p.lds_scr + p.lds_pin;
+      return p.lds_total;
+    }
+  }
+  p.lds_pin = 0;
+  p.dn_cap = kDnStage;
+  p.lds_red = kDecWaves * 2 * 2 * 256 * 4;                          // per wave 2 x 2 16x16 fp32 tiles
   const int nt = p.redundant ? p.B : 1;
   const int routed = 8 * p.P;                                       // ids + weights per pair
   const int topk = routed + 4 * (3 * nt * p.E + kDecWaves * kMaxTopk) + 16 + kBlockTopkBytes;  // keys, scores, picks, block_topk
@@ -141,7 +182,6 @@ inline int decode_lds(Plan &p) {
   if (group > scr) scr = group;
   if (down > scr) scr = down;
   // gate/up stages activation rows in the same scratch: as many rows as fit, at most 16
-  p.xpitch = p.K + 8;
   const int room = kDecMaxLds - kDecStaticLds - p.lds_red - p.lds_grp;
   p.NX = room > 0 ? room / (p.xpitch * 2) : 0;
   if (p.NX > 16) p.NX = 16;
