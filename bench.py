@@ -42,7 +42,9 @@ latent_up and shared_down; bf16 weights outside the experts), its three kernels
 timed separately with events between them; CPU baseline: the restatement of the
 block (oracle/latent_ref.py).
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--workload tp8|tp8-l8|prefill|kimi-latent]
+Workload kimi-moe: the MoE step alone on that rank (its latent as the experts' input).
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--workload tp8|tp8-l8|prefill|kimi-latent|kimi-moe]
                        [--no-extra] [--no-check] [--no-cpu-baseline]
 """
 
@@ -631,7 +633,7 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=2)
-    ap.add_argument('--workload', default='tp8', choices=['tp8', 'tp8-l8', 'prefill', 'kimi-latent'])
+    ap.add_argument('--workload', default='tp8', choices=['tp8', 'tp8-l8', 'prefill', 'kimi-latent', 'kimi-moe'])
     ap.add_argument('--batches', default='1,8,64', help='batches of the tp8 workload; the first is the headline')
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--warm-cache', action='store_true', help='skip the L2/MALL flush before each replay')
@@ -672,6 +674,10 @@ def main():
     elif args.workload == 'tp8-l8':
         runs = [(configs.TP8_B64_L8, 8, False, [0, 21, 42, 63])]
         workload = 'tp8-rank-b64-8-stacked-layers'
+    elif args.workload == 'kimi-moe':
+        batches = [int(b) for b in args.batches.split(',')]
+        runs = [(configs.KIMI_K3_TP8.with_tokens(b), 1, True, None) for b in batches]
+        workload = f'kimi-k3-tp8-rank-moe-step-b{batches[0]}'
     elif args.workload == 'kimi-latent':
         batches = [int(b) for b in args.batches.split(',')]
         runs = [(configs.KIMI_K3_TP8.with_tokens(b), 1, False, LATENT_ROWS.get(b)) for b in batches]
@@ -693,7 +699,7 @@ def main():
     results, host, timed, failures = {}, {}, {}, []
     for cfg, layers, host_gen, rows in runs:
         log(f'bench: {cfg.name} layers={layers} steps={args.steps} warmup={args.warmup} cold={cold}')
-        if cfg.latent:
+        if cfg.latent and args.workload != 'kimi-moe':
             m = measure_latent(cfg, seed=args.seed, steps=args.steps, warmup=args.warmup, cold=cold, device=device)
             results[cfg.name] = summarize_latent(cfg, m)
             host[cfg.name] = m['host']
@@ -731,11 +737,11 @@ def main():
         if name in measured and r['layers'] == 1:
             r['hbm_traffic_bytes'] = measured[name]['traffic_bytes']
     cpu, per = None, {}
-    if not args.no_cpu_baseline and args.workload in ('tp8', 'kimi-latent'):
+    if not args.no_cpu_baseline and args.workload in ('tp8', 'kimi-latent', 'kimi-moe'):
         # the latent block's oracle decodes every routed expert (up to 896 at b64): head batch only;
         # the CPU baseline covers the configurations made on the host (the batches of one layer)
         for cfg, _, host_gen, _ in (runs[:1] if args.workload == 'kimi-latent' else runs):
-            if args.workload != 'kimi-latent' and (not host_gen or cfg.latent):
+            if args.workload == 'tp8' and (not host_gen or cfg.latent):
                 results[cfg.name]['cpu_us_per_layer'] = None
                 continue
             log(f'cpu baseline: {cfg.name}')
@@ -754,7 +760,7 @@ def main():
                'cpu': cpu_model()}
     if args.workload != 'kimi-latent' and not args.no_check:
         for cfg, layers, host_gen, rows in runs:
-            if not host_gen or cfg.latent:
+            if not host_gen or (cfg.latent and args.workload != 'kimi-moe'):
                 continue
             log(f'bench: oracle check of {cfg.name}')
             orc = per[cfg.name]['oracle'] if cfg.name in per else None

@@ -141,6 +141,13 @@ DecodeKernel decode_kernel(const Plan &p, int &slot) {
   return table[al][v];
 }
 
+// The single-token kernel's instantiation `slot` may use more than 64 KiB of dynamic LDS.
+int allow_single_lds(const void *fn, int slot, int bytes) {
+  static int granted[4] = {0};
+  if (bytes <= 65536) return K3MOE_OK;
+  return grant_lds(fn, kDecMaxLds - kDecStaticLds, granted[slot], "single-token");
+}
+
 int allow_lds(DecodeKernel fn, int slot, int bytes) {
   static int granted[8] = {0};
   if (bytes <= 65536) return K3MOE_OK;
@@ -398,8 +405,8 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
                 kDecMaxPairs);
   if (dims->path == K3MOE_PATH_SINGLE && !p.single)
     return fail(K3MOE_EINVAL,
-                "the single-token kernel needs tokens == 1, topk <= 8, experts <= 512, latent a multiple of 512 "
-                "up to 8192, inter <= 256 (got tokens %d, topk %d, experts %d, latent %d, inter %d)",
+                "the single-token kernel needs tokens == 1, topk <= 16, experts <= 1024, latent a multiple of 512 "
+                "up to 8192, inter <= 512 (got tokens %d, topk %d, experts %d, latent %d, inter %d)",
                 dims->tokens, dims->topk, dims->experts, dims->latent, dims->inter);
   if (!workspace || workspace_bytes < p.total)
     return fail(K3MOE_EWORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
@@ -426,7 +433,18 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
     a.out_short = shortfall;
     a.ws = ws;
     if (p.single) {
-      hipLaunchKernelGGL(k_moe_single, dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
+      // instantiations: chosen experts per wave in the down phase (1: k <= 8, 2: k <= 16) and
+      // the down projection's k-steps (2: I <= 256, 4: I <= 512)
+      const bool je2 = p.k > kDecWaves, ks4 = p.I > 256;
+      const void *fn = je2 ? (ks4 ? reinterpret_cast<const void *>(&k_moe_single<2, 4>)
+                                  : reinterpret_cast<const void *>(&k_moe_single<2, 2>))
+                           : (ks4 ? reinterpret_cast<const void *>(&k_moe_single<1, 4>)
+                                  : reinterpret_cast<const void *>(&k_moe_single<1, 2>));
+      if ((rc = allow_single_lds(fn, je2 * 2 + ks4, p.lds_total))) return rc;
+      if (je2 && ks4) hipLaunchKernelGGL((k_moe_single<2, 4>), dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
+      else if (je2) hipLaunchKernelGGL((k_moe_single<2, 2>), dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
+      else if (ks4) hipLaunchKernelGGL((k_moe_single<1, 4>), dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
+      else hipLaunchKernelGGL((k_moe_single<1, 2>), dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
       return launch_check("single-token step");
     }
     int slot = 0;

@@ -355,6 +355,21 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
+// Wave-wide FP32 sum in a fixed order (pairs inside quads, half-rows, rows,
+// then the row broadcasts into lane 63), returned to every lane.
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  auto add = [](float a, uint32_t b) { return __fadd_rn(a, __uint_as_float(b)); };
+  v = add(v, dpp<kDppQuadXor1, 0xF>(__float_as_uint(v)));
+  v = add(v, dpp<kDppQuadXor2, 0xF>(__float_as_uint(v)));
+  v = add(v, dpp<kDppHalfMirror, 0xF>(__float_as_uint(v)));
+  v = add(v, dpp<kDppMirror, 0xF>(__float_as_uint(v)));
+  const float b15 = __uint_as_float(dpp<kDppBcast15, 0xA>(__float_as_uint(v)));
+  v = (__lane_id() & 16) ? __fadd_rn(v, b15) : v;
+  const float b31 = __uint_as_float(dpp<kDppBcast31, 0xC>(__float_as_uint(v)));
+  v = (__lane_id() & 32) ? __fadd_rn(v, b31) : v;
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
   v |= dpp<kDppQuadXor1, 0xF>(v);
   v |= dpp<kDppQuadXor2, 0xF>(v);

@@ -193,19 +193,31 @@ inline int decode_lds(Plan &p) {
 }
 
 // The single-token kernel (k3moe_single.hpp) takes the step when it fits:
-// one token, top-k <= 8 of at most 512 experts, the expert width K a multiple of 512 (whole
-// 512-column gate/up super-steps, at most kSingleMaxSS per wave) and at most
-// 8192 (its staged row), I <= 256 (the down projection's two k-steps), at most
-// two 16-row output tiles per workgroup, and its tagged partials and
-// intermediates fitting the tag area. Its dynamic LDS: the keys (3 E words),
-// the staged row (2 K bytes), fixed scratch and the top-k's.
+// one token, top-k <= 16 of at most 1024 experts, the expert width K a
+// multiple of 512 (whole 512-column gate/up super-steps, at most kSingleMaxSS
+// per wave) and at most 8192 (its staged row), I <= 512 (the down
+// projection's k-steps, at most 4), at most two 16-row output tiles per
+// workgroup, the workgroup's gate/up units times a wave's super-steps at most
+// kSingleSlots (all loaded at once), and its tagged partials
+// and intermediates fitting the tag area. Its dynamic LDS: the keys (3 E
+// words), the staged row (2 K bytes), fixed scratch, the top-k's, the chosen
+// experts' h (2 k I bytes) and the down products (2 row tiles x k x 16 fp32).
 constexpr int kSingleMaxSS = 2;  // gate/up super-steps of 512 columns per wave: ceil(K / 4096)
-inline int single_lds(const Plan &p) { return align16(3 * 4 * p.E) + 2 * p.K + 8192 + kBlockTopkBytes; }
+constexpr int kSingleMaxTopk = 16;
+constexpr int kSingleRouterRows = 4;  // router rows (experts) per workgroup: E <= 4 G
+constexpr int kSingleSlots = 4;  // gate/up register slots per wave: units of the workgroup x super-steps per wave
+constexpr int kSingleScratchBytes = 3840;
+inline int single_lds(const Plan &p) {
+  return align16(3 * 4 * p.E) + 2 * p.K + kSingleScratchBytes + kBlockTopkBytes + align16(2 * p.k * p.I) +
+         2 * p.k * 16 * 4;
+}
 inline void single_plan(const k3moe_dims &d, Plan &p) {
-  const bool tags_fit = (long)kTagCopies * p.E * 8 * 8 + (long)p.k * (p.I / 2) * 8 <= kTagBytes;
-  p.single = (d.path == K3MOE_PATH_AUTO || d.path == K3MOE_PATH_SINGLE) && p.B == 1 && p.k <= 8 && p.E <= 512 &&
-             p.K % 512 == 0 && p.K <= kSingleMaxSS * kDecWaves * 512 && p.I <= 256 && p.I % 32 == 0 && p.h % 128 == 0 &&
-             p.RTd <= 2 * p.G && p.k * (p.I / 8) <= 4 * p.G && tags_fit && p.Srw <= kDecMaxSplits;
+  const bool tags_fit = (long)kTagCopies * p.E * 8 + (long)p.k * (p.I / 2) * 8 <= kTagBytes;
+  p.single = (d.path == K3MOE_PATH_AUTO || d.path == K3MOE_PATH_SINGLE) && p.B == 1 && p.k <= kSingleMaxTopk &&
+             p.E <= kMaxExperts && p.K % 512 == 0 && p.K <= kSingleMaxSS * kDecWaves * 512 && p.I <= 512 &&
+             p.I % 32 == 0 && p.h % 128 == 0 && p.h <= 16 * kDecThreads && p.E <= kSingleRouterRows * p.G &&
+             p.RTd <= 2 * p.G &&
+             cdiv(p.k * (p.I / 8), p.G) * (p.K / 512 > kDecWaves ? 2 : 1) <= kSingleSlots && tags_fit;
 }
 
 // n_cus: compute units of the device (the persistent grid size); trace: reserve

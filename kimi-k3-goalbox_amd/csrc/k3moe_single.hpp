@@ -7,11 +7,10 @@
 // one memory round trip after the last write, where a grid barrier costs its
 // counter round trips and then a separate gather.
 //
-//   R   router logits (kimi.py:308): unit = (16 router rows, k-split s) as in
-//       the general persistent kernel; each (expert, split) partial goes to
-//       its tagged slot.
-//   T   every workgroup polls the partials of the experts its threads hold
-//       (thread e: expert e), sums them in split order, gates them (sigmoid
+//   R   router logits (kimi.py:308): workgroup b computes the whole logits
+//       of experts b, b + G, ..; each goes to its tagged slot.
+//   T   every workgroup polls the logits of the experts its threads hold
+//       (thread e: experts e, e + 512), gates them (sigmoid
 //       + bias, or the logits; kimi.py:308-315, tasks/distributed.py:174-176)
 //       and selects the top k (k <= 8) with the workgroup's threshold-and-rank
 //       selection (block_topk);
@@ -35,6 +34,8 @@
 // leaves NaN in its share of the output and leaves.
 #pragma once
 
+#include <type_traits>
+
 #include "k3moe_barrier.hpp"
 #include "k3moe_decode.hpp"
 #include "k3moe_device.hpp"
@@ -45,40 +46,30 @@ namespace k3moe {
 constexpr int kTagPartials = 0;  // tag area: router partials, [E][8 splits] slots
 constexpr uint32_t kTraceSingle = 0x5349u;  // trace slot 55 of the single-token kernel's rows
 
-// Fixed LDS scratch of the single-token kernel, after the keys and the staged row.
+// Fixed LDS scratch of the single-token kernel, after the keys and the staged
+// row; then the top-k's (BlockTopk), the chosen experts' h ([k][I] bf16) and
+// the down products ([2 row tiles][k][16] fp32).
 struct SingleScratch {
   int sel[kDecWaves * kMaxTopk];         // selection output (sel[0..k) in rank order)
-  float rred[kDecWaves * 16];            // router: the waves' 16 partial logits
-  float gred[kDecWaves * 16];            // gate/up: the waves' 16 partial rows
-  uint16_t hs[8 * 256];                  // down: each chosen expert's h (bf16)
-  float dacc[2 * kDecWaves * 16];        // down: w x bf16(y) per row tile, wave, row
-  int ids[8];                            // chosen experts, ascending
-  float wts[8];                          // their gating weights
+  float rred[kDecWaves * 16];            // router: the waves' partial logits
+  float gred[kSingleSlots * kDecWaves * 16];  // gate/up: per unit, the waves' 16 partial rows
+  int ids[kSingleMaxTopk];               // chosen experts, ascending
+  float wts[kSingleMaxTopk];             // their gating weights
 };
-static_assert(sizeof(SingleScratch) <= 8192, "single_lds reserves 8 KiB of scratch");
-static_assert(sizeof(SingleScratch) % 16 == 0 && sizeof(BlockTopk) <= kBlockTopkBytes, "single_lds layout");
+static_assert(sizeof(SingleScratch) % 16 == 0 && sizeof(SingleScratch) <= kSingleScratchBytes, "single_lds layout");
+static_assert(sizeof(BlockTopk) <= kBlockTopkBytes, "single_lds layout");
 
-// Polls tagged slots until every lane's `n` slots (n in 0..2, read as one
-// 16-byte device-coherent load at byte offset `off` of `r`) carry `tag`;
-// wave-uniform. Returns false when the wait gave up (a timeout, which it
-// records, or another wait of this launch that gave up).
-__device__ __forceinline__ bool poll_tagged(__amdgpu_buffer_rsrc_t r, uint32_t off, int n, uint32_t tag,
-                                            unsigned *ctl, unsigned abort0, u32x4 &v) {
-  unsigned spins = 0;
-  for (;;) {
-    v = n > 0 ? bload16_dev(r, off) : u32x4{0, 0, 0, 0};
-    const bool ok = (n < 1 || v[1] == tag) && (n < 2 || v[3] == tag);
-    if (__ballot(!ok) == 0) return true;
-    ++spins;
-    if ((spins & 63u) == 0u && aborted(ctl, abort0)) return false;
-    if (spins > kSpinLimit) {
-      if ((threadIdx.x & 63) == 0) raise_timeout(ctl);
-      return false;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
+// Down weights of one (expert, row tile) for KSD k-steps: a lane's 16 bytes
+// and the aligned dword holding its scale byte (taken apart at use, as DnLoad).
+template <int KSD>
+struct SgDn {
+  u32x4 w[KSD];
+  uint32_t s[KSD], sh[KSD];
+};
 
+// JE: chosen experts per wave in the down phase (k <= 8 JE); KSD: the down
+// projection's k-steps of 128 (I <= 128 KSD).
+template <int JE, int KSD>
 __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, DecodeArgs a_arg) {
   const uint64_t kargs = touch_kernargs<sizeof(Plan) + sizeof(DecodeArgs)>();
   const Plan pl = load_const<Plan>(kargs);
@@ -91,8 +82,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   float *kyf = reinterpret_cast<float *>(kyl + E);    // [E] keys
   float *scl = kyf + E;                               // [E] scores
   uint16_t *xs = reinterpret_cast<uint16_t *>(lds + align16(12 * E));  // [K] the token's expert-input row
-  SingleScratch &sh = *reinterpret_cast<SingleScratch *>(lds + align16(12 * E) + 2 * K);
-  BlockTopk &tk = *reinterpret_cast<BlockTopk *>(lds + align16(12 * E) + 2 * K + sizeof(SingleScratch));
+  char *fixed = lds + align16(12 * E) + 2 * K;
+  SingleScratch &sh = *reinterpret_cast<SingleScratch *>(fixed);
+  BlockTopk &tk = *reinterpret_cast<BlockTopk *>(fixed + kSingleScratchBytes);
+  uint16_t *hs = reinterpret_cast<uint16_t *>(fixed + kSingleScratchBytes + kBlockTopkBytes);  // [k][I]
+  float *dacc = reinterpret_cast<float *>(fixed + kSingleScratchBytes + kBlockTopkBytes + align16(2 * k * I));
   __shared__ uint32_t s_tag, s_abort0;
   __shared__ int s_fail;
 
@@ -100,11 +94,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   unsigned *ctl = reinterpret_cast<unsigned *>(a.ws + pl.o_ctl);
   char *tag_area = a.ws + kOffTag;
   const __amdgpu_buffer_rsrc_t tagr = make_rsrc(tag_area, kTagBytes);
-  // tag area: the router partials, kTagCopies copies of [8 splits][E] slots
-  // (split-major: one poll instruction reads 64 consecutive experts' slots of a
-  // split; workgroup b polls copy b mod 8, the copy of its XCD: fewer readers
-  // per line), then the h slots, [k][I/2]
-  const uint32_t copy_bytes = (uint32_t)E * kDecMaxSplits * 8;
+  // tag area: the logits, kTagCopies copies of [E] slots (workgroup b polls
+  // copy b mod 8, the copy of its XCD: fewer readers per line), then the h
+  // slots, [k][I/2]
+  const uint32_t copy_bytes = (uint32_t)E * 8;
   const uint32_t my_copy = (blockIdx.x % kTagCopies) * copy_bytes;
   const uint32_t h_base = kTagCopies * copy_bytes;
   const uint8_t *zero = reinterpret_cast<const uint8_t *>(a.ws + pl.o_zero);
@@ -171,47 +164,57 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   };
 
   // ------------------------------------------------------------ R: router --
+  // Workgroup b computes the whole logits (kimi.py:308) of experts b, b + G, ..
+  // (at most kSingleRouterRows): wave w takes the w-th eighth of the h / 8
+  // 16-byte chunks of x and of each row (at most two per lane), each lane sums
+  // its bf16 products in FP32, the wave sums its lanes (a fixed DPP tree) and
+  // the waves meet in LDS, summed in wave order; each logit goes to its tagged
+  // slot in every copy.
   {
-    const int NU = pl.RTr * pl.Srw, KB = pl.h / kBlockK;
-    for (int u = blockIdx.x; u < NU; u += gridDim.x) {
-      const int s = u % pl.Srw, rt = u / pl.Srw;
-      const int k0 = (int)((unsigned)(s * pl.KSr) / (unsigned)pl.Srw);
-      const int k1 = (int)((unsigned)((s + 1) * pl.KSr) / (unsigned)pl.Srw);
-      const int ka = k0 + (k1 - k0) * w / kDecWaves, kb1 = k0 + (k1 - k0) * (w + 1) / kDecWaves;
-      const int row = rt * 16 + i;
-      const bool row_ok = row < E;
-      const uint16_t *arow = a.router + (size_t)(row_ok ? row : 0) * pl.h;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int ks = ka; ks < kb1; ++ks) {
-        const int kb = ks * 4 + q;
-        const bool ok = kb < KB;
-        u32x4 va[4], vb[4];
+    const int KC = pl.h / 8, c0 = KC * w / kDecWaves, c1 = KC * (w + 1) / kDecWaves;
+    u32x4 rv[kSingleRouterRows][2], xv[2];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          va[kk] = (ok && row_ok) ? load16(arow + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
-          vb[kk] = (ok && i == 0) ? load16(a.x + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
+    for (int r = 0; r < kSingleRouterRows; ++r) {
+      const int e = (int)blockIdx.x + r * (int)gridDim.x;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int c = c0 + l + 64 * m;
+        rv[r][m] = (e < E && c < c1) ? load16(a.router + (size_t)e * pl.h + c * 8) : u32x4{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int c = c0 + l + 64 * m;
+      xv[m] = c < c1 ? load16(a.x + c * 8) : u32x4{0, 0, 0, 0};
+    }
+    warm_code();
+    make_tag();
+#pragma unroll
+    for (int r = 0; r < kSingleRouterRows; ++r) {
+      if ((int)blockIdx.x + r * (int)gridDim.x >= E) break;  // workgroup-uniform
+      float p = 0.f;
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t av = rv[r][m][d], bv = xv[m][d];
+          p = __fadd_rn(p, __fmul_rn(bf16_bits_to_f32(av & 0xFFFFu), bf16_bits_to_f32(bv & 0xFFFFu)));
+          p = __fadd_rn(p, __fmul_rn(bf16_bits_to_f32(av >> 16), bf16_bits_to_f32(bv >> 16)));
         }
-        warm_code();
-        make_tag();
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) acc = mfma16(as_bf16x8(va[kk]), as_bf16x8(vb[kk]), acc);
-      }
-      make_tag();
-      if (i == 0) {  // column 0 (the token): rows 4q .. 4q + 3
-#pragma unroll
-        for (int v = 0; v < 4; ++v) sh.rred[w * 16 + 4 * q + v] = acc[v];
-      }
-      __syncthreads();
-      if (tid < 16 * kTagCopies && rt * 16 + (tid & 15) < E) {
-        // the split's partial of expert rt * 16 + (tid & 15), waves in order, into copy tid / 16
-        const int r = tid & 15;
+      p = wave_sum_f32(p);
+      if (l == 0) sh.rred[w * kSingleRouterRows + r] = p;
+    }
+    make_tag();
+    __syncthreads();
+    if (tid < kSingleRouterRows * kTagCopies) {
+      const int r = tid % kSingleRouterRows, e = (int)blockIdx.x + r * (int)gridDim.x;
+      if (e < E) {
         float sum = sh.rred[r];
 #pragma unroll
-        for (int ww = 1; ww < kDecWaves; ++ww) sum += sh.rred[ww * 16 + r];
-        st_dev64(tagr, (uint32_t)(kTagPartials + (tid >> 4) * copy_bytes + (s * E + rt * 16 + r) * 8),
+        for (int ww = 1; ww < kDecWaves; ++ww) sum = __fadd_rn(sum, sh.rred[ww * kSingleRouterRows + r]);
+        st_dev64(tagr, (uint32_t)(kTagPartials + (tid / kSingleRouterRows) * copy_bytes + e * 8),
                  u32x2{__float_as_uint(sum), s_tag});
       }
-      __syncthreads();
     }
   }
   warm_code();
@@ -230,21 +233,22 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   // -------------------------------------------------------- T: top-k/gating --
   int w0_rank = 0, w0_e = -1;  // wave 0, lane l < k: the l-th chosen expert and its ascending rank
   {
-    // thread e polls expert e's partials (splits 0 .. Srw - 1, slot s E + e of
-    // its copy), every split's 8-byte load per round, then sums them in split order
-    float logit = 0.f;
+    // thread e polls the logits of experts e and e + 512 (slot e of its copy)
+    float logit0 = 0.f, logit1 = 0.f;
     bool ok = true;
-    {
-      const int ns = tid < E ? pl.Srw : 0;
-      u32x2 v[kDecMaxSplits];
+    // TWO: experts past 512 exist (a second expert per thread); a separate
+    // loop without them otherwise
+    auto poll = [&](auto two_) {
+      constexpr bool TWO = decltype(two_)::value;
+      const int e0 = tid, e1 = tid + kDecThreads;
+      const bool n0 = e0 < E, n1 = TWO && e1 < E;
+      u32x2 v0 = {0, 0}, v1 = {0, 0};
       unsigned spins = 0;
       for (;;) {
-        bool ready = true;
-#pragma unroll
-        for (int sp = 0; sp < kDecMaxSplits; ++sp)
-          v[sp] = sp < ns ? bload8_dev(tagr, (uint32_t)(kTagPartials + my_copy + (sp * E + tid) * 8)) : u32x2{0, 0};
-#pragma unroll
-        for (int sp = 0; sp < kDecMaxSplits; ++sp) ready = ready && (sp >= ns || v[sp][1] == tag);
+        v0 = n0 ? bload8_dev(tagr, (uint32_t)(kTagPartials + my_copy + e0 * 8)) : u32x2{0, tag};
+        if constexpr (TWO) v1 = n1 ? bload8_dev(tagr, (uint32_t)(kTagPartials + my_copy + e1 * 8)) : u32x2{0, tag};
+        bool ready = v0[1] == tag;
+        if constexpr (TWO) ready = ready && v1[1] == tag;
         if (spins == 0 && w == 0) trace_mark(pl, a.ws, 10);
         if (__ballot(!ready) == 0) break;
         ++spins;
@@ -259,27 +263,30 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
         }
         __builtin_amdgcn_s_sleep(1);
       }
-#pragma unroll
-      for (int sp = 0; sp < kDecMaxSplits; ++sp)
-        if (sp < ns) logit = sp == 0 ? __uint_as_float(v[0][0]) : logit + __uint_as_float(v[sp][0]);
+      logit0 = __uint_as_float(v0[0]);
+      if constexpr (TWO) logit1 = __uint_as_float(v1[0]);
       if (pl.o_trace && tid == 0)
         reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + 11] = spins + 1;
-    }
+    };
+    if (E > kDecThreads) poll(std::true_type{});
+    else poll(std::false_type{});
     if (!ok) s_fail = 1;
     trace_mark(pl, a.ws, 2);
-    if (tid < E) {  // gating (kimi.py:308-309; tasks/distributed.py:174)
+    auto gate = [&](int e, float logit, float bias) {  // gating (kimi.py:308-309; tasks/distributed.py:174)
       float score, key;
       if (pl.gating == K3MOE_GATING_SIGMOID_BIAS) {
         score = 1.0f / (1.0f + expf(-logit));
-        key = a.bias ? __fadd_rn(score, bias_pre[0]) : score;
+        key = a.bias ? __fadd_rn(score, bias) : score;
       } else {
         score = logit;
         key = logit;
       }
-      scl[tid] = score;
-      kyf[tid] = key;
-      kyl[tid] = ordered_key(key);
-    }
+      scl[e] = score;
+      kyf[e] = key;
+      kyl[e] = ordered_key(key);
+    };
+    if (tid < E) gate(tid, logit0, bias_pre[0]);
+    if (tid + kDecThreads < E) gate(tid + kDecThreads, logit1, bias_pre[1]);
     __syncthreads();
     if (s_fail) return leave(true);
     trace_mark(pl, a.ws, 3);
@@ -315,23 +322,25 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   const int ss0 = NSS * w / kDecWaves, ss1 = NSS * (w + 1) / kDecWaves;
   const uint8_t *const lane_blk = i >= 8 ? a.ublk : a.gblk;
   const uint8_t *const lane_scl = i >= 8 ? a.uscl : a.gscl;
-  u32x4 ga[kSingleMaxSS][4], gsc[kSingleMaxSS];
-  auto gu_issue1 = [&](int u) {
-    const int j = u / U8, rg = u % U8;
-    const size_t row = (size_t)sh.ids[j] * I + rg * 8 + (i & 7);
-    const uint8_t *wr = lane_blk + row * KB * 16, *sr = lane_scl + row * KB;
+  // This workgroup's units are b, b + G, .. (nu of them); their loads are all
+  // issued at once, in kSingleSlots register slots: slot sl holds unit
+  // b + (sl / ssw) G, super-step ss0 + sl mod ssw (ssw = 1 or 2 super-steps per
+  // wave), so one memory round trip brings every unit's rows.
+  const int ssw = NSS > kDecWaves ? 2 : 1, lg_ssw = ssw - 1;
+  const int nu = (NU - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  u32x4 ga[kSingleSlots][4], gsc[kSingleSlots];
 #pragma unroll
-    for (int m = 0; m < kSingleMaxSS; ++m) {
-      if (ss0 + m < ss1) {
-        const int ss = ss0 + m;
+  for (int sl = 0; sl < kSingleSlots; ++sl) {
+    const int mu = sl >> lg_ssw, ss = ss0 + (sl & lg_ssw);
+    if (mu < nu && ss < ss1) {  // wave-uniform
+      const int u = (int)blockIdx.x + mu * (int)gridDim.x, j = u / U8, rg = u - j * U8;
+      const size_t row = (size_t)sh.ids[j] * I + rg * 8 + (i & 7);
+      const uint8_t *wr = lane_blk + row * KB * 16, *sr = lane_scl + row * KB;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) ga[m][t] = load16(wr + (16 * ss + 4 * t + q) * 16);
-        gsc[m] = load16(sr + 16 * ss);
-      }
+      for (int t = 0; t < 4; ++t) ga[sl][t] = load16(wr + (16 * ss + 4 * t + q) * 16);
+      gsc[sl] = load16(sr + 16 * ss);
     }
-  };
-  int u0 = blockIdx.x;
-  if (u0 < NU) gu_issue1(u0);
+  }
   trace_mark(pl, a.ws, 9);
 
   if (w == 0) {
@@ -374,107 +383,176 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   // for wave w's expert are issued once the gate/up data has arrived, so that
   // the gate/up stream has the memory system to itself; they arrive while h is
   // exchanged. A tile past the last reads the zero area.
-  DnLoad pf[2];
+  SgDn<KSD> pf[JE][2];
   bool dn_issued = false;
+  const int KBd = I / kBlockK;
   auto dn_issue = [&]() {
     if (dn_issued) return;
     dn_issued = true;
-    if (w < k) {
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-        dn_issue_w(pl, a, zero, sh.ids, (int)blockIdx.x + tt * (int)gridDim.x, w, 0, I / kBlockK, pf[tt]);
+    for (int je = 0; je < JE; ++je) {
+      const int j = w + kDecWaves * je;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int rt = (int)blockIdx.x + tt * (int)gridDim.x;
+        const bool rt_ok = j < k && rt < pl.RTd;  // wave-uniform
+        const size_t row = (size_t)(rt_ok ? sh.ids[j] : 0) * K + (rt_ok ? rt : 0) * 16 + i;
+#pragma unroll
+        for (int ks = 0; ks < KSD; ++ks) {
+          const int kb = ks * 4 + q;
+          const bool okb = rt_ok && kb < KBd;
+          // unconditional loads: a skipped one is joined by a copy that waits for it at once
+          pf[je][tt].w[ks] = load16(okb ? a.dblk + (row * KBd + kb) * 16 : zero);
+          const uint8_t *sp = okb ? a.dscl + row * KBd + kb : zero;
+          const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(sp) & 3u;
+          pf[je][tt].s[ks] = *reinterpret_cast<const uint32_t *>(sp - mis);
+          pf[je][tt].sh[ks] = mis * 8u;
+        }
+      }
     }
   };
-  for (; u0 < NU; u0 += gridDim.x) {
+  // every unit's partial rows (this wave's super-steps), then one barrier; wave
+  // mu finishes unit mu
+#pragma unroll
+  for (int mu = 0; mu < kSingleSlots; ++mu) {
+    if (mu >= nu) break;  // wave-uniform
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int m = 0; m < kSingleMaxSS; ++m) {
-      if (ss0 + m < ss1) {
+    for (int sl = 0; sl < kSingleSlots; ++sl) {
+      const int ss = ss0 + (sl & lg_ssw);
+      if ((sl >> lg_ssw) == mu && ss < ss1) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const int kb = 16 * (ss0 + m) + 4 * t + q;
+          const int kb = 16 * ss + 4 * t + q;
           bf16x8 av[4];
-          convert_block_fast(ga[m][t], (gsc[m][t] >> (8 * q)) & 0xFFu, av);
+          convert_block_fast(ga[sl][t], (gsc[sl][t] >> (8 * q)) & 0xFFu, av);
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk)
             acc = mfma16(av[kk], as_bf16x8(*reinterpret_cast<const u32x4 *>(xs + kb * kBlockK + kk * 8)), acc);
         }
       }
     }
-    if (u0 == (int)blockIdx.x) trace_mark(pl, a.ws, 12);
     if (i == 0) {  // column 0: rows 4q .. 4q + 3 (0-7 gate, 8-15 up)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) sh.gred[w * 16 + 4 * q + v] = acc[v];
+      for (int v = 0; v < 4; ++v) sh.gred[(mu * kDecWaves + w) * 16 + 4 * q + v] = acc[v];
     }
-    ring_barrier();  // every wave's gate/up data has arrived
-    dn_issue();
-    if (u0 == (int)blockIdx.x) trace_mark(pl, a.ws, 13);
-    if (u0 + (int)gridDim.x < NU) gu_issue1(u0 + gridDim.x);  // the next unit's loads (grids smaller than k I / 8)
-    if (w == 0) {
-      // h = act(bf16(gate), bf16(up)) of the unit's 8 rows: lane r < 16 sums
-      // row r over the waves in order (gate rows 0-7, up rows 8-15); the
-      // activation's transcendental factors run in separate lanes (act_parts)
-      // and lane r < 8 combines them in the reference's order
-      const int r = l & 15;
-      float v = sh.gred[r];
+  }
+  trace_mark(pl, a.ws, 12);
+  ring_barrier();  // every wave's gate/up data has arrived
+  dn_issue();
+  trace_mark(pl, a.ws, 13);
+  if (w < nu) {
+    // h = act(bf16(gate), bf16(up)) of unit w's 8 rows: lane r < 16 sums row r
+    // over the waves in order (gate rows 0-7, up rows 8-15); the activation's
+    // transcendental factors run in separate lanes (act_parts) and lane r < 8
+    // combines them in the reference's order
+    const int u0 = (int)blockIdx.x + w * (int)gridDim.x;
+    const float *red = sh.gred + w * kDecWaves * 16;
+    const int r = l & 15;
+    float v = red[r];
 #pragma unroll
-      for (int ww = 1; ww < kDecWaves; ++ww) v += sh.gred[ww * 16 + r];
-      v = round_bf16(v);
-      const float g = __shfl(v, l & 7, kWave), up = __shfl(v, 8 + (l & 7), kWave);
-      const float hv = act_parts(pl.act, g, up);
-      const uint32_t hb = f32_to_bf16_bits(hv);
-      const uint32_t pair = hb | ((uint32_t)__shfl_down((int)hb, 1, kWave) << 16);
-      const int j = u0 / U8, rg = u0 % U8;
-      if (l < 8 && (l & 1) == 0)
-        st_dev64(tagr, h_base + (uint32_t)((j * (I / 2) + rg * 4 + (l >> 1)) * 8), u32x2{pair, tag});
-      if (u0 == (int)blockIdx.x) trace_mark(pl, a.ws, 14);
-    }
-    ring_barrier();  // gred is free again
+    for (int ww = 1; ww < kDecWaves; ++ww) v += red[ww * 16 + r];
+    v = round_bf16(v);
+    const float g = __shfl(v, l & 7, kWave), up = __shfl(v, 8 + (l & 7), kWave);
+    const float hv = act_parts(pl.act, g, up);
+    const uint32_t hb = f32_to_bf16_bits(hv);
+    const uint32_t pair = hb | ((uint32_t)__shfl_down((int)hb, 1, kWave) << 16);
+    const int j = u0 / U8, rg = u0 % U8;
+    if (l < 8 && (l & 1) == 0)
+      st_dev64(tagr, h_base + (uint32_t)((j * (I / 2) + rg * 4 + (l >> 1)) * 8), u32x2{pair, tag});
+    if (w == 0) trace_mark(pl, a.ws, 14);
   }
   dn_issue();    // a workgroup without a gate/up unit
   ring_barrier();  // wave 0's gating weights (sh.wts) are visible to the down phase
   trace_mark(pl, a.ws, 6);
 
   // ------------------------------------------------------- DN: down+combine --
-  const int KBd = I / kBlockK;
+  // wave w: chosen experts w, w + 8, .. (JE of them); each expert's h is polled
+  // (lane l: values 4 l .. 4 l + 3 and 256 + 4 l .., two 8-byte slots each),
+  // put in LDS and read back as the B operand
+  // all of a wave's h slots are polled together: every load of a round in flight at once
   bool ok = true;
-  if (w < k) {
-    // expert w's h: lane l holds h values 4 l .. 4 l + 3 (slots 2 l, 2 l + 1)
-    const int n = 4 * l < I ? 2 : 0;
-    u32x4 v;
-    ok = poll_tagged(tagr, h_base + (uint32_t)((w * (I / 2) + 2 * l) * 8), n, tag, ctl, abort0, v);
-    if (n > 0) *reinterpret_cast<u32x2 *>(sh.hs + w * 256 + 4 * l) = u32x2{v[0], v[2]};
-    wave_lds_order();
-    if (w == 0) trace_mark(pl, a.ws, 7);
-    // B operand: k-step jj covers blocks 4 jj + q of h (lane group q)
-    u32x4 hb[kDnDepth][4];
+  {
+    u32x4 hv[JE][2];
+    int hn[JE][2];
 #pragma unroll
-    for (int jj = 0; jj < kDnDepth; ++jj) {
-      const int kb = jj * 4 + q;
+    for (int je = 0; je < JE; ++je)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int j = w + kDecWaves * je, v0 = hh * 256 + 4 * l;
+        hn[je][hh] = (j < k && v0 < I) ? 2 : 0;
+        hv[je][hh] = u32x4{0, 0, 0, 0};
+      }
+    unsigned spins = 0;
+    for (;;) {
+      bool ready = true;
+#pragma unroll
+      for (int je = 0; je < JE; ++je)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int j = w + kDecWaves * je, v0 = hh * 256 + 4 * l;
+          hv[je][hh] = hn[je][hh] ? bload16_dev(tagr, h_base + (uint32_t)((j * (I / 2) + v0 / 2) * 8)) : u32x4{0, tag, 0, tag};
+        }
+#pragma unroll
+      for (int je = 0; je < JE; ++je)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) ready = ready && hv[je][hh][1] == tag && hv[je][hh][3] == tag;
+      if (__ballot(!ready) == 0) break;
+      ++spins;
+      if ((spins & 63u) == 0u && aborted(ctl, abort0)) {
+        ok = false;
+        break;
+      }
+      if (spins > kSpinLimit) {
+        if (l == 0) raise_timeout(ctl);
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int je = 0; je < JE; ++je)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int j = w + kDecWaves * je, v0 = hh * 256 + 4 * l;
+        if (hn[je][hh]) *reinterpret_cast<u32x2 *>(hs + j * I + v0) = u32x2{hv[je][hh][0], hv[je][hh][2]};
+      }
+  }
+  wave_lds_order();
+  if (w == 0) trace_mark(pl, a.ws, 7);
+#pragma unroll
+  for (int je = 0; je < JE; ++je) {
+    const int j = w + kDecWaves * je;
+    if (j >= k) break;  // wave-uniform
+    // B operand: k-step ks covers blocks 4 ks + q of h (lane group q)
+    u32x4 hb[KSD][4];
+#pragma unroll
+    for (int ks = 0; ks < KSD; ++ks) {
+      const int kb = ks * 4 + q;
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
-        hb[jj][kk] = kb < KBd ? *reinterpret_cast<const u32x4 *>(sh.hs + w * 256 + kb * kBlockK + kk * 8)
-                              : u32x4{0, 0, 0, 0};
+        hb[ks][kk] = kb < KBd ? *reinterpret_cast<const u32x4 *>(hs + j * I + kb * kBlockK + kk * 8) : u32x4{0, 0, 0, 0};
     }
-    const float wt = sh.wts[w];
+    const float wt = sh.wts[j];
     // The down scale bytes are taken apart only here, after the h poll
-    // (dn_scale): the compiler would otherwise convert them right where they
-    // are loaded and wait there for the loads, which are meant to arrive
+    // (as dn_scale): the compiler would otherwise convert them right where
+    // they are loaded and wait there for the loads, which are meant to arrive
     // while h is exchanged.
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int jj = 0; jj < kDnDepth; ++jj) {
-        if (jj >= pl.KSd) break;
+      for (int ks = 0; ks < KSD; ++ks) {
+        uint32_t sc = pf[je][tt].s[ks];
+        asm volatile("" : "+v"(sc));
         bf16x8 av[4];
-        convert_block_fast(pf[tt].w[jj], dn_scale(pf[tt], jj), av);
+        convert_block_fast(pf[je][tt].w[ks], (sc >> pf[je][tt].sh[ks]) & 0xffu, av);
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) acc = mfma16(av[kk], as_bf16x8(hb[jj][kk]), acc);
+        for (int kk = 0; kk < 4; ++kk) acc = mfma16(av[kk], as_bf16x8(hb[ks][kk]), acc);
       }
       if (i == 0) {  // column 0: rows 4q .. 4q + 3 of the tile
 #pragma unroll
-        for (int vv = 0; vv < 4; ++vv) sh.dacc[(tt * kDecWaves + w) * 16 + 4 * q + vv] = __fmul_rn(round_bf16(acc[vv]), wt);
+        for (int vv = 0; vv < 4; ++vv) dacc[(tt * k + j) * 16 + 4 * q + vv] = __fmul_rn(round_bf16(acc[vv]), wt);
       }
     }
   }
@@ -485,7 +563,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     const int tt = tid >> 4, r = tid & 15, rt = (int)blockIdx.x + tt * (int)gridDim.x;
     if (rt < pl.RTd) {
       float sum = 0.f;
-      for (int j = 0; j < k; ++j) sum = __fadd_rn(sum, sh.dacc[(tt * kDecWaves + j) * 16 + r]);
+      for (int j = 0; j < k; ++j) sum = __fadd_rn(sum, dacc[(tt * k + j) * 16 + r]);
       a.out[rt * 16 + r] = sum;
     }
   }

@@ -213,9 +213,12 @@ def test_moe_small_geometries(gpu, cfg, seed, path):
     run_and_check(cfg, synthetic.moe_layer_inputs(cfg, seed, scale_mode='kimi'), gpu, path=path)
 
 
-# one token on the single-token kernel: top-k <= 8 of <= 512 experts, K a multiple of 1024
+# one token on the single-token kernel: top-k <= 16 of <= 1024 experts, K a multiple of 512, I <= 512
 SINGLE = [
     MoEConfig('single-e64-k8', 64, 8, 1024, 256, 1),
+    MoEConfig('single-e896-k16-i384', 896, 16, 1024, 384, 1, latent=512),   # the Kimi rank's shape, narrower
+    MoEConfig('single-e600-k12-i512', 600, 12, 512, 512, 1),
+    MoEConfig('single-e1024-k9-i160', 1024, 9, 1536, 160, 1),
     MoEConfig('single-e40-k5-i96', 40, 5, 2048, 96, 1),
     MoEConfig('single-e512-softmax-silu', 512, 8, 1024, 128, 1, gating='softmax', activation='silu'),
     MoEConfig('single-k1', 16, 1, 1024, 64, 1),
@@ -232,9 +235,20 @@ def test_moe_single_token_geometries(gpu, cfg, seed, path):
     run_and_check(cfg, synthetic.moe_layer_inputs(cfg, seed, scale_mode='kimi'), gpu, path=path)
 
 
+def test_single_token_kimi_rank_geometry(gpu):
+    """The reference's own Kimi K3 TP8 rank at one token (E=896, top-16, I=384, latent 3584, h 7168;
+    megabench/cases.py:48-55) on the single-token kernel, against the oracle."""
+    cfg = configs.KIMI_K3_TP8.with_tokens(1)
+    say(f'case: {cfg.name} seed=5 path=single')
+    g = synthetic.moe_layer_inputs(cfg, 5, device=gpu)
+    run_and_check(cfg, g, gpu, path='single', host=host_view(g))
+
+
 def test_single_and_decode_kernels_agree_tp8_b1(gpu):
-    """The same router arithmetic (splits and wave order): identical expert ids and weights;
-    gate/up sums in another order, so expert_sum agrees to the oracle's rounding steps."""
+    """The two kernels sum the router logits in different orders (whole rows per workgroup
+    against k-splits on MFMA), both within FP32 rounding of the oracle: the same expert ids and
+    weights to a few ulps; gate/up sums in another order, so expert_sum agrees to the oracle's
+    rounding steps."""
     cfg = configs.TP8_B1
     say(f'case: {cfg.name} seed=11, single-token kernel vs general persistent kernel')
     g = to_dev(synthetic.moe_layer_inputs(cfg, 11), gpu)
@@ -244,7 +258,7 @@ def test_single_and_decode_kernels_agree_tp8_b1(gpu):
         torch.cuda.synchronize(gpu)
     a, b = outs['single'], outs['decode']
     assert torch.equal(a['expert_ids'], b['expert_ids'])
-    assert torch.equal(a['route_weights'], b['route_weights'])
+    assert float((a['route_weights'] - b['route_weights']).abs().max()) <= 4e-7
     assert moe_ref.rel_l2(a['expert_sum'].cpu(), b['expert_sum'].cpu()) < 2e-3
 
 
