@@ -124,4 +124,27 @@ __device__ __forceinline__ bool grid_barrier(unsigned *ctl, const BarrierBase &b
   return s_ok != 0;
 }
 
+// Launch tags of the single-token and decode kernels number their launches
+// modulo 2^32 / G (the launch counters' sum over the grid size G, plus one),
+// so a slot that no launch wrote for a whole cycle would carry a current tag.
+// The last launch of each cycle (tag 2^32 / G) therefore ends with a grid
+// barrier, after which each workgroup zeroes its share of the tag area: every
+// launch of the next cycle then finds slots written in that cycle or zeros
+// (which no tag matches).
+__device__ __forceinline__ uint32_t last_tag_of_cycle() {
+  return (uint32_t)(0x100000000ull >> __builtin_ctz(gridDim.x));
+}
+
+// Barrier `n` of the launch, then this workgroup's share of the tag area
+// cleared with device-coherent stores (the next launch polls it with
+// device-coherent loads). Returns false when the barrier's wait gave up.
+__device__ __forceinline__ bool clear_tag_area(unsigned *ctl, const BarrierBase &bb, unsigned n,
+                                               __amdgpu_buffer_rsrc_t tagr) {
+  if (!grid_barrier(ctl, bb, n, nullptr, false)) return false;
+  const uint32_t share = (uint32_t)kTagBytes / gridDim.x;  // a multiple of 16 (G <= 1024)
+  for (uint32_t off = blockIdx.x * share + threadIdx.x * 16; off < (blockIdx.x + 1) * share; off += blockDim.x * 16)
+    st_dev128(tagr, off, u32x4{0u, 0u, 0u, 0u});
+  return true;
+}
+
 }  // namespace k3moe

@@ -1776,6 +1776,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     crange[0] = pc0;
     crange[1] = program_counter();
   }
+  if (tag == last_tag_of_cycle() && !clear_tag_area(ctl, bb, ++nbar, tagr)) return give_up();
   leave();
 }
 

@@ -574,6 +574,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     crange[0] = pc0;
     crange[1] = program_counter();
   }
+  if (tag == last_tag_of_cycle()) {
+    // the barrier counters, read now: no barrier of this launch completes before this workgroup arrives
+    const BarrierBase bb = tid == 0 ? barrier_base(ctl) : BarrierBase{0u, 0u, 0u};
+    if (!clear_tag_area(ctl, bb, 1, tagr)) return leave(true);
+  }
   leave(false);
 }
 

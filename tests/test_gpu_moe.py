@@ -290,12 +290,16 @@ def test_single_token_tags_across_launches(gpu):
     assert k3moe.workspace_status(ws) == 0
 
 
+@pytest.mark.parametrize('stale', [False, True], ids=['zeroed', 'stale-slots'])
 @pytest.mark.parametrize('cfg,path', [(configs.TP8_B1, 'single'), (configs.TP8_B1, 'decode'),
                                       (configs.TP8_B8, 'decode')], ids=['b1-single', 'b1-decode', 'b8-decode'])
-def test_tags_from_a_large_launch_count(gpu, cfg, path):
+def test_tags_from_a_large_launch_count(gpu, cfg, path, stale):
     """The tag of the single-token and decode kernels comes from the launch counters' sum: preset
     them to a large, consistent count (as after 2**32 / G - 3 launches) and run across the tag's
-    wrap-around point."""
+    wrap-around point. With stale slots: the tag area first holds slots carrying tag 1, the first
+    tag after the wrap (as left by a launch a whole tag cycle earlier), with zero payloads (in-range
+    ids and finite values); the cycle's last launch must clear them, so every step still equals a
+    fresh workspace's."""
     from k3moe.moe import dims_for, workspace_bytes
     say(f'case: {cfg.name} seed=5 path={path}, launch counters preset near the 32-bit wrap')
     g = to_dev(synthetic.moe_layer_inputs(cfg, 5), gpu)
@@ -315,6 +319,10 @@ def test_tags_from_a_large_launch_count(gpu, cfg, path):
     for gi in range(16):
         v = (per[gi] * launches) & 0xFFFFFFFF
         ctl[640 + 16 * gi] = v - (1 << 32) if v >= 1 << 31 else v
+    if stale:   # the tag area is the last 2 MiB of the initialised prefix: 8-byte slots {payload, tag}
+        tags = ws[k3moe.moe.INIT_BYTES - (2 << 20): k3moe.moe.INIT_BYTES].view(torch.int32).view(-1, 2)
+        tags[:, 0] = 0
+        tags[:, 1] = 1
     torch.cuda.synchronize(gpu)
     for step in range(6):
         got = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, path=path, workspace=ws)
