@@ -296,12 +296,20 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, 
     host_us = host_us[-steps*layers:]
     # the host side of one moe_step call alone (Python checks, the C ABI call and its launch),
     # back to back with no flush between calls: it bounds a drop-in loop of consecutive layers
-    host_loop_us = None
+    host_loop_us = host_prepared_us = None
     if launch == 'stream':
         t = time.perf_counter()
         for _ in range(50):
             run()
         host_loop_us = (time.perf_counter() - t)*1e6/(50*layers)
+        torch.cuda.synchronize(device)
+        # the same launches through prepared steps (validated once, k3moe.prepare_step)
+        prepared = [k3moe.prepare_step(*a, **k_) for a, k_ in calls]
+        t = time.perf_counter()
+        for _ in range(50):
+            for p in prepared:
+                p()
+        host_prepared_us = (time.perf_counter() - t)*1e6/(50*layers)
         torch.cuda.synchronize(device)
     # the last timed run's outputs, for the oracle checks
     timed = [{k: v.cpu() for k, v in o.items()} for o in outs]
@@ -322,7 +330,7 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, 
     trace = read_trace(cfg, device) if os.environ.get('K3MOE_TRACE') == '1' and layers == 1 else None
     del graph, outs, flush
     return {'ms': ms, 'wall_s': wall, 'distinct': distinct, 'bytes': nbytes, 'flops': flops,
-            'host_us': host_us, 'host_loop_us': host_loop_us,
+            'host_us': host_us, 'host_loop_us': host_loop_us, 'host_prepared_us': host_prepared_us,
             'graph_matches_eager': same, 'host_inputs': [h for _, h in data], 'trace': trace,
             'timed': timed, 'status': status, 'device_inputs': [d for d, _ in data]}
 
@@ -466,7 +474,8 @@ def summarize(cfg, m, layers):
             'hbm_frac': round(gbps/8000.0, 4), 'tflops': round(m['flops']/(ms_mean*1e-3)/1e12, 3),
             'graph_matches_eager': m['graph_matches_eager'],
             **({'host_us_per_call': round(statistics.median(m['host_us']), 2),
-                'host_us_per_call_loop': round(m['host_loop_us'], 2)} if m['host_us'] else {}),
+                'host_us_per_call_loop': round(m['host_loop_us'], 2),
+                'host_us_per_call_prepared': round(m['host_prepared_us'], 2)} if m['host_us'] else {}),
             **({'trace': m['trace']} if m['trace'] else {})}
 
 

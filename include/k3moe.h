@@ -289,6 +289,15 @@ int k3moe_latent_out(const k3moe_latent_dims *dims, const float *expert_sum, con
 int k3moe_mxfp4_decode(const uint8_t *blocks, const uint8_t *scales, int64_t n_blocks,
                        int32_t out_dtype, void *out, void *stream);
 
+/* Debug: the expert GEMMs' activation act(g, u) (K3MOE_ACT_SITU, kimi.py:194-196,
+ * or K3MOE_ACT_SILU, tasks/distributed.py:184) on n fp32 pairs, written to out:
+ * fast = 0 is the library-function form the decode kernels use, fast = 1 the
+ * exponential-and-reciprocal form of the prefill GEMM's epilogue. For tests
+ * that pin both against a float64 reference. No reference counterpart beyond
+ * the formulas. */
+int k3moe_activation(int32_t act, int32_t fast, const float *g, const float *u, float *out, int64_t n,
+                     void *stream);
+
 /* MXFP4 encode, pack_mxfp4 (megabench/tasks/quantization.py:13-37): n_blocks
  * groups of 32 consecutive values of in_dtype (K3MOE_DTYPE_F32, _BF16 or
  * _F16; in 16-byte aligned) -> n_blocks blocks of 16 bytes (byte j: element

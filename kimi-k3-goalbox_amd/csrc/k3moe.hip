@@ -250,6 +250,12 @@ int latent_launch(const k3moe_latent_dims *dims, int out, const LatArgs &a, size
   return K3MOE_OK;
 }
 
+// The expert GEMMs' activation, elementwise (debug entry point k3moe_activation).
+__global__ void k_activation(int act, int fast, const float *g, const float *u, float *out, long n) {
+  for (long j = (long)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += (long)gridDim.x * blockDim.x)
+    out[j] = fast ? fast_act(act, g[j], u[j]) : apply_act(act, g[j], u[j]);
+}
+
 __global__ void k_zero_words(uint32_t *p, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0u;
@@ -568,6 +574,20 @@ int k3moe_mxfp4_decode(const uint8_t *blocks, const uint8_t *scales, int64_t n_b
   hipLaunchKernelGGL(k_decode, dim3((unsigned)grid), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), blocks,
                      scales, n_blocks, out_dtype, out);
   return launch_check("decode");
+}
+
+int k3moe_activation(int32_t act, int32_t fast, const float *g, const float *u, float *out, int64_t n, void *stream) {
+  g_err[0] = 0;
+  if (act != K3MOE_ACT_SITU && act != K3MOE_ACT_SILU) return fail(K3MOE_EINVAL, "act must be SITU or SILU, got %d", act);
+  if (fast != 0 && fast != 1) return fail(K3MOE_EINVAL, "fast must be 0 or 1, got %d", fast);
+  if (n < 0) return fail(K3MOE_EINVAL, "n must be >= 0");
+  if (n == 0) return K3MOE_OK;
+  if (!g || !u || !out) return fail(K3MOE_EINVAL, "a required pointer is NULL");
+  long grid = (long)((n + 255) / 256);
+  if (grid > 65536) grid = 65536;
+  hipLaunchKernelGGL(k_activation, dim3((unsigned)grid), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), act,
+                     fast, g, u, out, n);
+  return launch_check("activation");
 }
 
 int k3moe_mxfp4_encode(const void *in, int32_t in_dtype, int64_t n_blocks, uint8_t *blocks, uint8_t *scales,

@@ -307,6 +307,38 @@ __device__ __forceinline__ float apply_act(int act, float g, float u) {
   return act == 0 ? act_situ(g, u) : act_silu(g, u);
 }
 
+// The same activations from the hardware's base-2 exponential and reciprocal
+// (v_exp_f32, v_rcp_f32, about 1 ulp each) instead of the library's expf and
+// tanhf, for the prefill GEMM's epilogue, where they are most of its time:
+//   sigmoid(g) = 1 / (1 + e), or e / (1 + e) for g < 0, with e = 2^(-|g| log2 e),
+//   tanh(y) = sign(y) (1 - e) / (1 + e) with e = 2^(-2 |y| log2 e), and for
+//   |y| < 1/16, where 1 - e cancels, the Taylor series y - y^3/3 + 2 y^5/15
+//   (the next term is below 2^-27 of y there).
+// Relative error a few fp32 ulps (GPU test against a float64 reference), far
+// below the bf16 rounding of h that follows.
+constexpr float kLog2e = 1.44269504088896340736f;  // log2(e)
+__device__ __forceinline__ float fast_sigmoid(float g) {
+  // e = exp(-|g|) in (0, 1]: sigmoid(g) = 1 / (1 + e) for g >= 0, e / (1 + e) below (no overflow)
+  const float e = __builtin_amdgcn_exp2f(__fmul_rn(-fabsf(g), kLog2e));
+  const float r = __builtin_amdgcn_rcpf(__fadd_rn(1.0f, e));
+  return g >= 0.0f ? r : __fmul_rn(e, r);
+}
+__device__ __forceinline__ float fast_tanh(float y) {
+  const float a = fabsf(y), y2 = __fmul_rn(y, y);
+  const float poly = __fmul_rn(y, __fsub_rn(1.0f, __fmul_rn(y2, __fsub_rn(1.0f / 3.0f, __fmul_rn(y2, 2.0f / 15.0f)))));
+  const float e = __builtin_amdgcn_exp2f(__fmul_rn(-2.0f * kLog2e, a));
+  const float t = __fmul_rn(__fsub_rn(1.0f, e), __builtin_amdgcn_rcpf(__fadd_rn(1.0f, e)));
+  return a < 0.0625f ? poly : copysignf(t, y);
+}
+__device__ __forceinline__ float fast_act(int act, float g, float u) {
+  const float sig = fast_sigmoid(g);
+  if (act == 0) {
+    const float a = __fmul_rn(__fmul_rn(4.0f, fast_tanh(__fmul_rn(g, 0.25f))), sig);
+    return __fmul_rn(a, __fmul_rn(25.0f, fast_tanh(__fmul_rn(u, 0.04f))));
+  }
+  return __fmul_rn(__fmul_rn(g, sig), u);
+}
+
 // apply_act for row l & 7 of a wave, lanes 0-7 returning it, with its
 // transcendental factors spread over lanes: lane l computes factor l >> 3 of
 // row l & 7 (0: sigmoid(g), 1: tanh(g/4), 2: tanh(u/25)) and lanes 0-7 combine

@@ -44,7 +44,8 @@
 // weight rows is then read from memory in whole 64-byte pieces rather than 4
 // bytes per k-step, whose 128-byte lines were fetched about ten times each.
 //
-// Gate/up epilogue: h = act(bf16(gate), bf16(up)) in bf16 (kimi.py:322), split
+// Gate/up epilogue: h = act(bf16(gate), bf16(up)) in bf16 (kimi.py:322; the
+// activation from the hardware exponential and reciprocal, fast_act), split
 // into two E4M3 terms per 32 columns of I (two gate tiles are one block) and
 // stored for the down GEMM; down epilogue: bf16 y rows.
 #pragma once
@@ -460,7 +461,7 @@ __global__ __launch_bounds__(kFThreads, 1) void k_fgemm(Plan pl, MxAct a, const 
           for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
             for (int vv = 0; vv < 4; ++vv)
-              h[s2][vv] = round_bf16(apply_act(pl.act, round_bf16(acc[s2][t][vv]), round_bf16(acc[2 + s2][t][vv])));
+              h[s2][vv] = round_bf16(fast_act(pl.act, round_bf16(acc[s2][t][vv]), round_bf16(acc[2 + s2][t][vv])));
           float m8 = 0.f;
 #pragma unroll
           for (int s2 = 0; s2 < 2; ++s2)

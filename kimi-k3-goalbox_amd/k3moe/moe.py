@@ -136,32 +136,41 @@ def _validate_routes(routes: torch.Tensor, B: int, k: int, E: int, device) -> to
     return r
 
 
-def moe_step(x: torch.Tensor, router: torch.Tensor, router_bias: torch.Tensor | None,
-             gate_blocks: torch.Tensor, gate_scales: torch.Tensor,
-             up_blocks: torch.Tensor, up_scales: torch.Tensor,
-             down_blocks: torch.Tensor, down_scales: torch.Tensor, *,
-             topk: int, gating: str = 'sigmoid_bias', activation: str = 'situ',
-             fp32: bool = False, routes: torch.Tensor | None = None,
-             latent: torch.Tensor | None = None, out: dict | None = None,
-             workspace: torch.Tensor | None = None, path: str = 'auto') -> dict:
-    """One MXFP4 MoE step (kimi.py:307-324 without the TP all-reduce) on the GPU.
+class PreparedStep:
+    """One MoE step's validated launch: the tensors, outputs, workspace and the C-ABI argument
+    list are fixed when it is made (prepare_step), so a call only reads torch's current stream
+    and calls k3moe_moe_step (a few microseconds on the host, where moe_step's checks take
+    about 18). The tensors' contents may change between calls (new token rows in x, another
+    step's forced routes): the kernels read them at each launch. Calling it returns the same
+    output tensors each time, overwritten in stream order."""
 
-    x [B, h] bf16 (the router input, kimi.py:308); router [E, h] bf16;
-    router_bias [E] fp32 or None; gate/up blocks [E, I, K/32, 16] u8 and
-    scales [E, I, K/32] u8; down blocks [E, K, I/32, 16] u8 and scales
-    [E, K, I/32] u8 (kimi.py:114-119); latent [B, K] bf16 or None (the experts
-    then read x, K = h). routes [B, k] forces the expert sets
-    (kimi.py:311-313) and adds route_shortfall.
+    def __init__(self, device, args, result):
+        self.device = device
+        self.result = result
+        self._args = args
+        self._fn = _native.load().k3moe_moe_step
 
-    Returns {'expert_sum': fp32 [B, K], 'expert_ids': int64 [B, k] ascending,
-    'route_weights': fp32 [B, k] aligned with expert_ids,
-    ['route_shortfall': fp32 [B]]}, all on x's device. Inputs are never
-    written. `out` may supply preallocated output tensors by the same keys;
-    `workspace` an initialised workspace (new_workspace), else the device's
-    cached one is used. `path` forces an execution path ('auto', 'general',
-    'decode', or the general path with 'grouped' GEMM or 'streamed' expert
-    kernels); the default picks the persistent kernel for decode batches.
-    """
+    def __call__(self) -> dict:
+        dev = self.device
+        if torch.cuda.current_device() != dev.index:
+            with torch.cuda.device(dev):
+                return self()
+        rc = self._fn(*self._args, ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+        if rc:
+            check(rc, 'k3moe_moe_step')
+        return self.result
+
+
+def prepare_step(x: torch.Tensor, router: torch.Tensor, router_bias: torch.Tensor | None,
+                 gate_blocks: torch.Tensor, gate_scales: torch.Tensor,
+                 up_blocks: torch.Tensor, up_scales: torch.Tensor,
+                 down_blocks: torch.Tensor, down_scales: torch.Tensor, *,
+                 topk: int, gating: str = 'sigmoid_bias', activation: str = 'situ',
+                 fp32: bool = False, routes: torch.Tensor | None = None,
+                 latent: torch.Tensor | None = None, out: dict | None = None,
+                 workspace: torch.Tensor | None = None, path: str = 'auto') -> PreparedStep:
+    """Validate a step's arguments once (moe_step's checks and errors) and return a
+    PreparedStep that launches it; arguments as moe_step's."""
     if fp32:
         raise NotImplementedError('fp32=True is the FP32 truth mode of the CPU oracle; '
                                   'the GPU step computes the BF16 serving path (fp32=False)')
@@ -191,7 +200,6 @@ def moe_step(x: torch.Tensor, router: torch.Tensor, router_bias: torch.Tensor | 
     if routes is not None:
         routes = _validate_routes(routes, B, k, E, device)
 
-    lib = _native.load()
     ws_bytes = workspace_bytes(dims)
     with torch.cuda.device(device):
         out = dict(out or {})
@@ -216,18 +224,50 @@ def moe_step(x: torch.Tensor, router: torch.Tensor, router_bias: torch.Tensor | 
             workspace = get_workspace(dims, device)
         elif workspace.dtype != torch.uint8 or workspace.device != device or workspace.numel() < ws_bytes:
             raise ValueError(f'workspace must be a uint8 tensor of at least {ws_bytes} bytes on {device}')
-        stream = torch.cuda.current_stream(device).cuda_stream
-        rc = lib.k3moe_moe_step(ctypes.byref(dims), _dev_ptr(x), _dev_ptr(latent), _dev_ptr(router),
-                                _dev_ptr(router_bias), _dev_ptr(gate_blocks), _dev_ptr(gate_scales),
-                                _dev_ptr(up_blocks), _dev_ptr(up_scales), _dev_ptr(down_blocks),
-                                _dev_ptr(down_scales), _dev_ptr(routes), _dev_ptr(expert_sum), _dev_ptr(ids),
-                                _dev_ptr(weights), _dev_ptr(shortfall), _dev_ptr(workspace),
-                                ctypes.c_size_t(workspace.numel()), ctypes.c_void_p(stream))
-        check(rc, 'k3moe_moe_step')
+    args = (ctypes.byref(dims), _dev_ptr(x), _dev_ptr(latent), _dev_ptr(router), _dev_ptr(router_bias),
+            _dev_ptr(gate_blocks), _dev_ptr(gate_scales), _dev_ptr(up_blocks), _dev_ptr(up_scales),
+            _dev_ptr(down_blocks), _dev_ptr(down_scales), _dev_ptr(routes), _dev_ptr(expert_sum), _dev_ptr(ids),
+            _dev_ptr(weights), _dev_ptr(shortfall), _dev_ptr(workspace), ctypes.c_size_t(workspace.numel()))
     result = {'expert_sum': expert_sum, 'expert_ids': ids, 'route_weights': weights}
     if routes is not None:
         result['route_shortfall'] = shortfall
-    return result
+    step = PreparedStep(device, args, result)
+    # the tensors the argument list points at stay alive as long as the prepared step
+    step._keep = (dims, x, latent, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales, down_blocks,
+                  down_scales, routes, workspace)
+    return step
+
+
+def moe_step(x: torch.Tensor, router: torch.Tensor, router_bias: torch.Tensor | None,
+             gate_blocks: torch.Tensor, gate_scales: torch.Tensor,
+             up_blocks: torch.Tensor, up_scales: torch.Tensor,
+             down_blocks: torch.Tensor, down_scales: torch.Tensor, *,
+             topk: int, gating: str = 'sigmoid_bias', activation: str = 'situ',
+             fp32: bool = False, routes: torch.Tensor | None = None,
+             latent: torch.Tensor | None = None, out: dict | None = None,
+             workspace: torch.Tensor | None = None, path: str = 'auto') -> dict:
+    """One MXFP4 MoE step (kimi.py:307-324 without the TP all-reduce) on the GPU.
+
+    x [B, h] bf16 (the router input, kimi.py:308); router [E, h] bf16;
+    router_bias [E] fp32 or None; gate/up blocks [E, I, K/32, 16] u8 and
+    scales [E, I, K/32] u8; down blocks [E, K, I/32, 16] u8 and scales
+    [E, K, I/32] u8 (kimi.py:114-119); latent [B, K] bf16 or None (the experts
+    then read x, K = h). routes [B, k] forces the expert sets
+    (kimi.py:311-313) and adds route_shortfall.
+
+    Returns {'expert_sum': fp32 [B, K], 'expert_ids': int64 [B, k] ascending,
+    'route_weights': fp32 [B, k] aligned with expert_ids,
+    ['route_shortfall': fp32 [B]]}, all on x's device. Inputs are never
+    written. `out` may supply preallocated output tensors by the same keys;
+    `workspace` an initialised workspace (new_workspace), else the device's
+    cached one is used. `path` forces an execution path ('auto', 'general',
+    'decode', or the general path with 'grouped' GEMM or 'streamed' expert
+    kernels); the default picks the persistent kernel for decode batches.
+    prepare_step validates the same arguments once for repeated launches.
+    """
+    return prepare_step(x, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales, down_blocks,
+                        down_scales, topk=topk, gating=gating, activation=activation, fp32=fp32, routes=routes,
+                        latent=latent, out=out, workspace=workspace, path=path)()
 
 
 def moe_layer(values: dict, layer: int, x: torch.Tensor, *, topk: int, gating: str = 'sigmoid_bias',
@@ -247,6 +287,28 @@ def moe_layer(values: dict, layer: int, x: torch.Tensor, *, topk: int, gating: s
                     values[p + 'up_blocks'], values[p + 'up_scales'],
                     values[p + 'down_blocks'], values[p + 'down_scales'],
                     topk=topk, gating=gating, activation=activation, fp32=fp32, routes=routes, latent=latent)
+
+
+def activation(g: torch.Tensor, u: torch.Tensor, activation: str = 'situ', fast: bool = False) -> torch.Tensor:
+    """The expert GEMMs' activation act(g, u) on the GPU (debug entry point k3moe_activation):
+    fast=False is the decode kernels' library-function form, fast=True the prefill GEMM's
+    exponential-and-reciprocal form. g, u: fp32 tensors of one shape on one ROCm GPU."""
+    if activation not in ('situ', 'silu'):
+        raise ValueError(f"activation must be 'situ' or 'silu', got {activation!r}")
+    if not isinstance(g, torch.Tensor) or not isinstance(u, torch.Tensor) or g.shape != u.shape:
+        raise ValueError('g and u must be tensors of one shape')
+    if g.dtype != torch.float32 or u.dtype != torch.float32:
+        raise ValueError('g and u must be float32')
+    if g.device.type != 'cuda' or u.device != g.device:
+        raise ValueError('g and u must be on the same ROCm GPU')
+    g, u = g.contiguous(), u.contiguous()
+    out = torch.empty_like(g)
+    with torch.cuda.device(g.device):
+        stream = torch.cuda.current_stream(g.device).cuda_stream
+        rc = _native.load().k3moe_activation(0 if activation == 'situ' else 1, 1 if fast else 0, _dev_ptr(g),
+                                             _dev_ptr(u), _dev_ptr(out), g.numel(), ctypes.c_void_p(stream))
+        check(rc, 'k3moe_activation')
+    return out
 
 
 def mxfp4_decode(blocks: torch.Tensor, scales: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:

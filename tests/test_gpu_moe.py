@@ -747,3 +747,23 @@ def test_general_grouping_lists_match_oracle(gpu, cfg):
         p_of = torch.from_numpy(pof.reshape(B, k)[:, j].astype(np.int64))
         re = re + y[p_of]*wt[:, j, None]
     assert torch.equal(re, got['expert_sum'].cpu())
+
+
+def test_prepared_step_matches_moe_step(gpu):
+    """k3moe.prepare_step: validated once, then each call launches the step on the same tensors;
+    a new token row written into x in place is read by the next call."""
+    cfg = configs.TP8_B8
+    say(f'case: {cfg.name} seeds 21-22 through a prepared step')
+    g = to_dev(synthetic.moe_layer_inputs(cfg, 21), gpu)
+    g2 = to_dev(synthetic.moe_layer_inputs(cfg, 22), gpu)
+    rows = [g['x'].clone(), g2['x'].clone(), g['x'].clone()]
+    step = k3moe.prepare_step(*synthetic.step_args(g), topk=cfg.topk)
+    for xr in rows:
+        g['x'].copy_(xr)
+        got = {k: v.clone() for k, v in step().items()}
+        want = k3moe.moe_step(*synthetic.step_args(dict(g, x=xr)), topk=cfg.topk)
+        torch.cuda.synchronize(gpu)
+        for key in want:
+            assert torch.equal(got[key], want[key]), key
+    with pytest.raises(ValueError, match='shape'):
+        k3moe.prepare_step(g['x'][:, :64].contiguous(), *synthetic.step_args(g)[1:], topk=cfg.topk)
