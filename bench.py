@@ -231,7 +231,7 @@ def gpu_inputs(cfg, seed, layers, device, host_gen):
     return out
 
 
-def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, launch='stream'):
+def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, launch='stream', host_timing=True):
     """Time `steps` runs of `layers` MoE layers; returns per-run ms and the routing stats.
 
     launch 'stream': each run is the layers' kernel launches on the stream (outputs and
@@ -297,7 +297,7 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, 
     # the host side of one moe_step call alone (Python checks, the C ABI call and its launch),
     # back to back with no flush between calls: it bounds a drop-in loop of consecutive layers
     host_loop_us = host_prepared_us = None
-    if launch == 'stream':
+    if launch == 'stream' and host_timing:
         t = time.perf_counter()
         for _ in range(50):
             run()
@@ -473,9 +473,9 @@ def summarize(cfg, m, layers):
             'algorithmic_bytes': m['bytes'], 'hbm_GBps': round(gbps, 1),
             'hbm_frac': round(gbps/8000.0, 4), 'tflops': round(m['flops']/(ms_mean*1e-3)/1e12, 3),
             'graph_matches_eager': m['graph_matches_eager'],
-            **({'host_us_per_call': round(statistics.median(m['host_us']), 2),
-                'host_us_per_call_loop': round(m['host_loop_us'], 2),
-                'host_us_per_call_prepared': round(m['host_prepared_us'], 2)} if m['host_us'] else {}),
+            **({'host_us_per_call': round(statistics.median(m['host_us']), 2)} if m['host_us'] else {}),
+            **({'host_us_per_call_loop': round(m['host_loop_us'], 2),
+                'host_us_per_call_prepared': round(m['host_prepared_us'], 2)} if m['host_loop_us'] else {}),
             **({'trace': m['trace']} if m['trace'] else {})}
 
 
@@ -657,6 +657,8 @@ def main():
     ap.add_argument('--no-extra', action='store_true', help='tp8 workload: leave out the 8-stacked-layer and '
                     'prefill configurations (reported beside the batches by default)')
     ap.add_argument('--no-check', action='store_true', help='skip the oracle checks of the timed outputs')
+    ap.add_argument('--no-host-timing', action='store_true', help='leave out the host-cost loops (50 back-to-back '
+                    'moe_step calls and 50 prepared launches per workload, warm): for profiles of the timed launches')
     args = ap.parse_args()
     if args.trace:
         os.environ['K3MOE_TRACE'] = '1'
@@ -718,7 +720,7 @@ def main():
             del m
         else:
             m = measure(cfg, seed=args.seed, steps=args.steps, warmup=args.warmup, cold=cold, device=device,
-                        layers=layers, host_gen=host_gen, launch=args.launch)
+                        layers=layers, host_gen=host_gen, launch=args.launch, host_timing=not args.no_host_timing)
             results[cfg.name] = summarize(cfg, m, layers)
             results[cfg.name]['workspace_status'] = m['status']
             if m['status'] != 0:

@@ -29,10 +29,10 @@ constexpr int kDecWaves = 8;       // decode path: waves per workgroup
 constexpr int kDecThreads = kDecWaves * 64;
 constexpr int kDecMaxTokens = 64;
 constexpr int kDecMaxPairs = 1024;
-constexpr int kDecMaxSplits = 8;   // router k-splits across workgroups
+constexpr int kDecMaxSplits = 10;  // router k-splits across workgroups
 constexpr int kDecMaxLds = 160 * 1024;   // gfx950: 160 KiB of LDS per workgroup
-constexpr int kDecStaticLds = 1024;
-constexpr int kDnStage = 128;        // decode down: y rows staged per wave (32 B + a 4-byte tag each)  // decode kernel's static LDS (round table, counters), upper bound
+constexpr int kDecStaticLds = 1024;  // decode kernel's static LDS (round table, counters), upper bound
+constexpr int kDnStage = 128;        // decode down: y rows staged per wave (32 B + a 4-byte tag each)
 
 // LDS of the workgroup top-k (block_topk): per-wave group maxima, up to kMaxExperts candidates, a count
 constexpr int kBlockTopkBytes = 8 * (kDecWaves * 32 + kMaxExperts + 8) + 16;
@@ -249,8 +249,10 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   p.G = 1;
   while (p.G * 2 <= n_cus && p.G * 2 <= 1024) p.G *= 2;
   long base = (long)p.RTr * p.TTr;
-  int srw_cap = p.KSr / kDecWaves;
-  if (srw_cap > kDecMaxSplits) srw_cap = kDecMaxSplits;
+  // (a split of fewer k-steps than waves leaves waves idle, but spreads the
+  // router and x reads over more workgroups)
+  int srw_cap = kDecMaxSplits;
+  if (srw_cap > p.KSr) srw_cap = p.KSr;
   if (srw_cap < 1) srw_cap = 1;
   // the decode kernel's router partials, [B][Srw][Epad] tagged slots, fit the tag area
   const long part_room = kTagBytes - kTagDecPart;

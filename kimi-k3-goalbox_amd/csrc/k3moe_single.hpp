@@ -8,30 +8,35 @@
 // counter round trips and then a separate gather.
 //
 //   R   router logits (kimi.py:308): workgroup b computes the whole logits
-//       of experts b, b + G, ..; each goes to its tagged slot.
+//       of experts b, b + G, .. (at most 4 rows, FP32 sums of the bf16
+//       products); each goes to its tagged slot, one copy per XCD.
 //   T   every workgroup polls the logits of the experts its threads hold
 //       (thread e: experts e, e + 512), gates them (sigmoid
 //       + bias, or the logits; kimi.py:308-315, tasks/distributed.py:174-176)
-//       and selects the top k (k <= 8) with the workgroup's threshold-and-rank
+//       and selects the top k (k <= 16) with the workgroup's threshold-and-rank
 //       selection (block_topk);
 //       valid forced routes replace the selection (kimi.py:311-313).
 //   GU  gate/up (kimi.py:321-322): the k x I/8 units (8 gate + 8 up rows of
-//       one chosen expert) go to the workgroups in turn (exactly one each at
-//       top-8, I = 256 on a grid of 256); the 8 waves split the unit's K
-//       evenly and issue all their weight loads as soon as the ids are known;
-//       the waves' partial tiles meet in LDS in wave order, the activation is
-//       applied, and the unit's 8 bf16 h values go to tagged slots.
-//   DN  down and combine (kimi.py:322-323): wave j takes the j-th chosen
-//       expert (ascending ids) in the workgroup's one or two 16-row output
+//       one chosen expert) go to the workgroups in turn (unit u to workgroup
+//       u mod G: exactly one each at top-8, I = 256 on a grid of 256, at most
+//       4); the 8 waves split the K axis evenly and issue the weight loads of
+//       all the workgroup's units at once as soon as the ids are known; the
+//       waves' partial tiles meet in LDS, wave m sums unit m's in wave order,
+//       applies the activation, and writes the unit's 8 bf16 h values to
+//       tagged slots.
+//   DN  down and combine (kimi.py:322-323): wave w takes the chosen experts
+//       w, w + 8 (ascending ids) in the workgroup's one or two 16-row output
 //       tiles; its weights are loaded once the gate/up data has arrived (they
-//       then arrive while h is exchanged), it polls the expert's h,
-//       multiplies, and the waves' w x bf16(y) rows are summed in LDS from zero
-//       in ascending expert order.
+//       then arrive while h is exchanged), it polls all its experts' h slots
+//       together, multiplies, and the waves' w x bf16(y) rows are summed in
+//       LDS from zero in ascending expert order.
 // Each workgroup adds one to a launch counter when it leaves, on every path;
 // the counters' sum at a launch's start, over the grid size, numbers the
 // launch, and its tag is that number + 1 (a zeroed slot never matches).
 // Every wait is bounded: a workgroup that gives up sets the status word,
-// leaves NaN in its share of the output and leaves.
+// leaves NaN in its share of the output and leaves. The launch whose tag is
+// the last of the 32-bit cycle clears the tag area behind a grid barrier, so
+// that no slot written a whole cycle earlier carries a current tag.
 #pragma once
 
 #include <type_traits>
@@ -43,7 +48,7 @@
 
 namespace k3moe {
 
-constexpr int kTagPartials = 0;  // tag area: router partials, [E][8 splits] slots
+constexpr int kTagPartials = 0;  // tag area: router logits, kTagCopies copies of [E] slots
 constexpr uint32_t kTraceSingle = 0x5349u;  // trace slot 55 of the single-token kernel's rows
 
 // Fixed LDS scratch of the single-token kernel, after the keys and the staged

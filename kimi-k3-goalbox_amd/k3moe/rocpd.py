@@ -20,6 +20,8 @@ import sqlite3
 import statistics
 
 STEP_KERNELS = ('k_moe_single', 'k_moe_decode')  # the one-launch step kernels (one token; up to 64)
+# (kernel_table takes any kernels: python -m k3moe.rocpd --kt KT.db [--fetch .. --write .. --copy-bytes N]
+#  --table k_latent,k_moe)
 COPY_KERNEL = 'copyBuffer'
 
 
@@ -82,16 +84,74 @@ def step_counter(db: str, counter: str) -> list[dict]:
             for lds, vals in _runs(rows)]
 
 
+def _short(name: str) -> str:
+    """A kernel's name without its namespace and arguments (k3moe::k_latent<0>(...) -> k_latent<0>)."""
+    return name.split('(')[0].replace('void ', '').replace('k3moe::', '')
+
+
+def kernel_table(kt: str, fetch: str | None, write: str | None, names, copy_bytes: int | None) -> list[dict]:
+    """Per (kernel, LDS size) group of dispatches in launch order, for kernels whose name contains
+    one of `names`: median and mean duration and, with the counter runs, the median HBM read and
+    write bytes per dispatch (FETCH_SIZE and WRITE_SIZE calibrated on the copy probe)."""
+    con = sqlite3.connect(kt)
+    cond, args = _like(names)
+    groups: dict = {}
+    for name, lds, dur in con.execute(f'select name, lds_size, duration from kernels where {cond} order by start', args):
+        groups.setdefault((_short(name), lds), []).append(dur / 1e3)
+    counters = {}
+    for db, counter in ((fetch, 'FETCH_SIZE'), (write, 'WRITE_SIZE')):
+        if not db:
+            continue
+        f = calibration(db, counter, copy_bytes)
+        c = sqlite3.connect(db)
+        cn, ca = _like(names)
+        cn = cn.replace('name like', 'kernel_name like')
+        vals: dict = {}
+        for kn, lds, v in c.execute('select kernel_name, lds_block_size, sum(value) from counters_collection '
+                                    f'where counter_name = ? and {cn} group by dispatch_id order by start',
+                                    (counter,) + ca):
+            vals.setdefault((_short(kn), lds), []).append(v * f)
+        counters[counter] = vals
+    out = []
+    for (name, lds), us in groups.items():
+        row = {'kernel': name, 'lds_bytes': lds, 'dispatches': len(us), 'median_us': round(statistics.median(us), 2),
+               'avg_us': round(statistics.fmean(us), 2)}
+        for counter, key in (('FETCH_SIZE', 'read_bytes'), ('WRITE_SIZE', 'write_bytes')):
+            v = counters.get(counter, {}).get((name, lds))
+            if v:
+                row[key] = round(statistics.median(v))
+        out.append(row)
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
     ap.add_argument('--kt', required=True, help='rocpd database of the --kernel-trace --stats run')
-    ap.add_argument('--fetch', required=True, help='rocpd database of the --pmc FETCH_SIZE run')
-    ap.add_argument('--write', required=True, help='rocpd database of the --pmc WRITE_SIZE run')
-    ap.add_argument('--copy-bytes', type=int, required=True, help='bytes of the copy probe (bench.py --copy-probe)')
-    ap.add_argument('--labels', required=True, help='workload names, in launch order')
+    ap.add_argument('--fetch', help='rocpd database of the --pmc FETCH_SIZE run')
+    ap.add_argument('--write', help='rocpd database of the --pmc WRITE_SIZE run')
+    ap.add_argument('--copy-bytes', type=int, help='bytes of the copy probe (bench.py --copy-probe)')
+    ap.add_argument('--labels', help='workload names, in launch order (the step-kernel summary)')
     ap.add_argument('--algorithmic', default='', help='algorithmic bytes per workload, comma separated')
-    ap.add_argument('--json', help='write the per-workload traffic here')
+    ap.add_argument('--json', help='write the per-workload traffic here (merged into an existing file)')
+    ap.add_argument('--table', help='instead: a per (kernel, LDS size) table for kernels whose names contain '
+                    'one of these comma-separated strings')
     a = ap.parse_args(argv)
+    if a.table:
+        print('| kernel | LDS bytes | dispatches | median us | avg us | HBM read MB | HBM write MB |')
+        print('|---|---|---|---|---|---|---|')
+        for r in kernel_table(a.kt, a.fetch, a.write, a.table.split(','), a.copy_bytes):
+            rd = f"{r['read_bytes'] / 1e6:.1f}" if 'read_bytes' in r else '-'
+            wr = f"{r['write_bytes'] / 1e6:.2f}" if 'write_bytes' in r else '-'
+            print(f"| `{r['kernel']}` | {r['lds_bytes']} | {r['dispatches']} | {r['median_us']} | {r['avg_us']} | "
+                  f"{rd} | {wr} |")
+        print('\nKernels of the whole run by total time:\n')
+        print('| kernel | dispatches | avg us | total us |')
+        print('|---|---|---|---|')
+        for r in top_kernels(a.kt):
+            print(f"| `{r['kernel']}` | {r['dispatches']} | {r['avg_us']} | {r['total_us']} |")
+        return
+    if not (a.fetch and a.write and a.copy_bytes and a.labels):
+        raise SystemExit('--fetch, --write, --copy-bytes and --labels are needed for the step-kernel summary')
     labels = a.labels.split(',')
     algo = [int(x) for x in a.algorithmic.split(',')] if a.algorithmic else [None] * len(labels)
     durs = kernel_durations(a.kt)
@@ -121,9 +181,16 @@ def main(argv=None):
     print('|---|---|---|---|')
     for r in top_kernels(a.kt):
         print(f"| `{r['kernel']}` | {r['dispatches']} | {r['avg_us']} | {r['total_us']} |")
-    if a.json:
+    if a.json:   # merged into the file's workloads when it exists (one run per workload)
+        doc = {'fetch_bytes_per_kib': ff, 'write_bytes_per_kib': fw, 'workloads': {}}
+        try:
+            with open(a.json) as fh:
+                doc['workloads'] = json.load(fh).get('workloads', {})
+        except (OSError, ValueError):
+            pass
+        doc['workloads'].update(table)
         with open(a.json, 'w') as fh:
-            json.dump({'fetch_bytes_per_kib': ff, 'write_bytes_per_kib': fw, 'workloads': table}, fh, indent=1)
+            json.dump(doc, fh, indent=1)
             fh.write('\n')
 
 
