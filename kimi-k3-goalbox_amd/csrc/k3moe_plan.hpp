@@ -1,9 +1,13 @@
 // Launch plan and workspace layout of one MoE step (host and device).
 //
-// Two execution paths share the workspace conventions:
+// Three execution paths share the workspace conventions:
+//   single   B = 1 on shapes it fits: one persistent kernel, no grid barrier
+//            (k3moe_single.hpp)
 //   decode   B <= 64 tokens: one persistent kernel, one 512-thread workgroup
-//            per CU, phases separated by grid barriers (k3moe_decode.hpp)
-//   general  any B: a chain of six kernels (k3moe_general.hpp)
+//            per CU, phases handed over through tagged slots and at most two
+//            grid barriers (k3moe_decode.hpp)
+//   general  any B: a chain of eight to ten kernels (k3moe_general.hpp,
+//            k3moe_xgemm.hpp, k3moe_fgemm.hpp)
 // The workspace starts with a control block (kCtlBytes): the barrier counters
 // of the persistent kernel and a sticky error word. It must be zero before the
 // first step; the barrier counters only grow (32-bit, wrapping), and each
@@ -111,8 +115,8 @@ struct Plan {
   int lds_red, lds_grp, lds_scr, lds_total;  // dynamic LDS layout, bytes
   int NX;      // gate/up: activation rows staged in LDS per round (also the chunk size in tokens)
   int xpitch;  // staged row pitch in elements (K + 8: rows start in different banks)
-  int pinned;  // 1: every token's expert-input row stays in LDS from the kernel's start (gate/up by whole units per wave)
-  int lds_pin;  // bytes of the pinned rows (the last LDS region)
+  int pinned;  // 1: gate/up by whole units per wave, the rows of the workgroup's tokens in LDS (row t at t xpitch)
+  int lds_pin;  // bytes of the pinned rows' region, room for every token's row (the last LDS region)
   int dn_cap;   // expert-major down: y rows staged per wave
   int pad_;
   int trace;      // 1: the decode kernel records phase timestamps at o_trace
@@ -133,10 +137,11 @@ __host__ __device__ inline int align16(int v) { return (v + 15) & ~15; }
 // Decode-path LDS layout for plan p; returns the total bytes. Regions: red
 // (the router's per-wave tiles; the staged gate/up's cut-group tiles), grp
 // (the grouping lists), scr (top-k, grouping and down scratch; the staged
-// gate/up's activation rows), then, when pinned, every token's row.
-// Pinned: from 2 tokens up to as many as fit, the token rows are loaded to LDS
-// at the kernel's start; gate/up then gives each wave whole units (no
-// staging rounds, no groups cut between waves) and chunks of up to 16 tokens.
+// gate/up's activation rows), then, when pinned, room for every token's row.
+// Pinned: from 2 tokens up to as many as fit, gate/up gives each wave whole
+// units (no staging rounds, no groups cut between waves) of chunks of up to 16
+// tokens, and after the grouping each workgroup loads the rows of the tokens
+// its units need, under its first weight loads.
 inline int decode_lds(Plan &p) {
   const int room_all = kDecMaxLds - kDecStaticLds;
   p.xpitch = p.K + 8;
