@@ -123,12 +123,15 @@ __device__ __forceinline__ float red_sum(const float *red, int idx) {
 __device__ __forceinline__ int tile_index(int row, int col) { return (col + 16 * (row >> 2)) * 4 + (row & 3); }
 
 // ------------------------------------------------------- workgroup top-k --
-// LDS of block_topk: per wave the group maxima, the candidates, their count.
+// LDS of block_topk: the group maxima of the 32-bit keys and of the 64-bit
+// values ([group][wave] each), the candidates, their counts.
 struct BlockTopk {
-  uint64_t gmax[kDecWaves * 32];
-  uint64_t cand[kMaxExperts + 8];  // zeros past the candidates
-  int count;
+  uint32_t gmax[32 * kDecWaves];
+  uint64_t gmax64[32 * kDecWaves];
+  uint64_t cand[kMaxExperts];
+  int count, count64;
 };
+constexpr int kTopkCandCap = 64;  // more candidates than this after the 32-bit threshold: the 64-bit one
 
 // One DPP step of a 64-bit maximum or minimum with the lane the control selects.
 template <int Ctrl, bool Max>
@@ -158,84 +161,136 @@ __device__ __forceinline__ uint64_t fold_runs(uint64_t v, int n) {
   }
   return v;
 }
+// The same for 32-bit values.
+template <bool Max>
+__device__ __forceinline__ uint32_t fold_runs32(uint32_t v, int n) {
+  auto op = [](uint32_t x, uint32_t y) { return Max ? (x > y ? x : y) : (x < y ? x : y); };
+  if (n >= 2) v = op(v, dpp<kDppQuadXor1, 0xF>(v));
+  if (n >= 4) v = op(v, dpp<kDppQuadXor2, 0xF>(v));
+  if (n >= 8) v = op(v, dpp<kDppHalfMirror, 0xF>(v));
+  if (n >= 16) v = op(v, dpp<kDppMirror, 0xF>(v));
+#pragma unroll
+  for (int d = 16; d < 64; d *= 2)
+    if (n > d) v = op(v, (uint32_t)__shfl_xor((int)v, d, kWave));
+  return v;
+}
+__device__ __forceinline__ uint64_t lane0_u64(uint64_t v) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32)) << 32) |
+         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+}
 
-// Top-k (1 <= k <= 32) of the ordered keys kyl[0..E) (E <= 1024) by the whole
-// workgroup, with the order of wave_topk: larger keys first, equal keys in
-// ascending expert order, i.e. the k largest of the distinct 64-bit values
-// key << 32 | ~expert; sel[0..k) gets the experts in that rank order.
-//   1. Threshold: thread t holds experts t and t + 512; with G the power of
-//      two >= k, group g is the experts whose thread's lane lies in the g-th
-//      run of 64 / G lanes (so e mod 64 falls in [64 g / G, 64 (g + 1) / G)).
-//      T = the smallest of the G group maxima. Those maxima are G >= k distinct
-//      values >= T, so the k-th largest value is >= T, and every value above
-//      a top-k value is >= T too: the top k are the k best candidates (v >= T)
-//      and their ranks among the candidates are their ranks. (A group without
-//      experts has maximum 0: then every expert is a candidate.) For
-//      sigmoid-gated routing on 384 experts, top-8, about 21 experts are
-//      candidates.
+// Top-k (1 <= k <= 32) of the ordered keys key0 (expert tid) and key1 (expert
+// tid + 512) of every thread (E <= 1024 experts), with the order of wave_topk:
+// larger keys first, equal keys in ascending expert order, i.e. the k largest
+// of the distinct 64-bit values key << 32 | ~expert; sel[0..k) gets the
+// experts in that rank order.
+//   1. Threshold: with G the power of two >= k, group g is the experts whose
+//      thread's lane lies in the g-th run of 64 / G lanes; T = the smallest of
+//      the G group maxima of the keys. At least G >= k experts have a key >= T
+//      (each group's maximum is an expert's key; a group without experts has
+//      maximum 0, and then every key is >= T), so the k-th largest key is >= T
+//      and every top-k expert is a candidate (key >= T). Group maxima are taken
+//      in DPP runs and over the waves ([group][wave] in LDS, two 16-byte reads).
+//      When exact ties leave more than kTopkCandCap candidates, the threshold
+//      is taken again on the 64-bit values: their G group maxima are distinct,
+//      so at most ~G + 64 values reach it whatever the ties.
 //   2. Candidates are appended to an LDS list (order free: a rank does not
-//      depend on it); thread c counts the candidates above candidate c,
-//      reading the list in batches of 8 (LDS broadcasts), and writes ranks
-//      below k to sel.
+//      depend on it).
+//   3. Ranks: wave w takes candidates 8w + 64 c .. (8 lanes each, c = 0, 1, ..);
+//      lane part p of a candidate counts the candidates j = p mod 8 above it
+//      (four reads in flight), the 8 lanes add their counts (DPP), and ranks
+//      below k are written to sel.
 // Every thread of the workgroup calls it; it ends with a barrier after sel is written.
-__device__ __forceinline__ void block_topk(const uint32_t *kyl, int E, int k, int *sel, BlockTopk &tk) {
+__device__ __forceinline__ void block_topk(uint32_t key0, uint32_t key1, int E, int k, int *sel, BlockTopk &tk) {
   const int tid = threadIdx.x, w = wave_id(), l = tid & 63;
   int G = 1;
   while (G < k) G <<= 1;
   const int run = 64 / G;
   const int e0 = tid, e1 = tid + kDecThreads;
-  const uint64_t v0 = e0 < E ? ((uint64_t)kyl[e0] << 32) | (uint32_t)~e0 : 0ull;
-  const uint64_t v1 = e1 < E ? ((uint64_t)kyl[e1] << 32) | (uint32_t)~e1 : 0ull;
-  const uint64_t m = fold_runs<true>(v0 > v1 ? v0 : v1, run);
-  if ((l & (run - 1)) == 0) tk.gmax[w * 32 + l / run] = m;
-  if (tid == 0) tk.count = 0;
-  // zeros past the candidates: the rank loop reads whole batches of 8, and a zero is above no candidate
-  tk.cand[tid] = 0ull;
-  tk.cand[tid + kDecThreads] = 0ull;
+  const bool ok0 = e0 < E, ok1 = e1 < E;
+  {
+    const uint32_t a0 = ok0 ? key0 : 0u, a1 = ok1 ? key1 : 0u;
+    const uint32_t m = fold_runs32<true>(a0 > a1 ? a0 : a1, run);
+    if ((l & (run - 1)) == 0) tk.gmax[(l / run) * kDecWaves + w] = m;
+  }
+  if (tid == 0) {
+    tk.count = 0;
+    tk.count64 = 0;
+  }
   __syncthreads();
-  // every wave: lane g < G takes group g's maximum over the waves, then the minimum over lanes 0 .. G - 1
-  uint64_t g = ~0ull;
+  // lane g < G: group g's maximum over the waves; then the minimum over lanes 0 .. G - 1
+  uint32_t g = 0xFFFFFFFFu;
   if (l < G) {
-    g = tk.gmax[l];
+    const u32x4 p0 = *reinterpret_cast<const u32x4 *>(tk.gmax + l * kDecWaves);
+    const u32x4 p1 = *reinterpret_cast<const u32x4 *>(tk.gmax + l * kDecWaves + 4);
+    g = p0[0];
 #pragma unroll
-    for (int ww = 1; ww < kDecWaves; ++ww) {
-      const uint64_t o = tk.gmax[ww * 32 + l];
-      g = o > g ? o : g;
+    for (int t = 1; t < 4; ++t) g = p0[t] > g ? p0[t] : g;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) g = p1[t] > g ? p1[t] : g;
+  }
+  const uint32_t T = (uint32_t)__builtin_amdgcn_readfirstlane((int)fold_runs32<false>(g, G));
+  const uint64_t v0 = ok0 ? ((uint64_t)key0 << 32) | (uint32_t)~e0 : 0ull;
+  const uint64_t v1 = ok1 ? ((uint64_t)key1 << 32) | (uint32_t)~e1 : 0ull;
+  // appends the values with flag f0 / f1 to the candidate list, counted on cnt
+  auto append = [&](bool f0, bool f1, int &cnt) {
+    const uint64_t b0 = __ballot(f0), b1 = __ballot(f1);
+    const int n0 = __popcll(b0), n = n0 + __popcll(b1);
+    int base = 0;
+    if (n > 0) {
+      if (l == 0) base = atomicAdd(&cnt, n);
+      base = __builtin_amdgcn_readfirstlane(base);
     }
-  }
-  g = fold_runs<false>(g, G);
-  const uint64_t T = ((uint64_t)lane_u32((uint32_t)(g >> 32), 0) << 32) | lane_u32((uint32_t)g, 0);
-  const bool f0 = e0 < E && v0 >= T, f1 = e1 < E && v1 >= T;
-  const uint64_t b0 = __ballot(f0), b1 = __ballot(f1);
-  const int n0 = __popcll(b0), n = n0 + __popcll(b1);
-  int base = 0;
-  if (n > 0) {
-    if (l == 0) base = atomicAdd(&tk.count, n);
-    base = __builtin_amdgcn_readfirstlane(base);
-  }
-  const int below0 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b0, 0u));
-  const int below1 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0u));
-  if (f0) tk.cand[base + below0] = v0;
-  if (f1) tk.cand[base + n0 + below1] = v1;
+    const int below0 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b0, 0u));
+    const int below1 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0u));
+    if (f0) tk.cand[base + below0] = v0;
+    if (f1) tk.cand[base + n0 + below1] = v1;
+  };
+  append(ok0 && key0 >= T, ok1 && key1 >= T, tk.count);
   __syncthreads();
-  // candidate c by thread c; the list is read in batches of 8 (LDS broadcasts: every lane reads the same words)
-  const int nc = __builtin_amdgcn_readfirstlane(tk.count);
-  for (int c0 = w * 64; c0 < nc; c0 += kDecThreads) {
-    const int c = c0 + l;
-    const uint64_t me = c < nc ? tk.cand[c] : 0ull;
-    int rank = 0;
-    for (int j = 0; j < nc; j += 8) {
-      const u32x4 *p = reinterpret_cast<const u32x4 *>(tk.cand + j);
+  int nc = __builtin_amdgcn_readfirstlane(tk.count);
+  if (nc > kTopkCandCap) {  // workgroup-uniform: exact ties; the threshold on the distinct 64-bit values
+    const uint64_t m = fold_runs<true>(v0 > v1 ? v0 : v1, run);
+    if ((l & (run - 1)) == 0) tk.gmax64[(l / run) * kDecWaves + w] = m;
+    __syncthreads();  // also: every thread has read the first count, so the list is free
+    uint64_t g64 = ~0ull;
+    if (l < G) {
+      const u32x4 *p = reinterpret_cast<const u32x4 *>(tk.gmax64 + l * kDecWaves);
       u32x4 q4[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) q4[t] = p[t];
+      g64 = 0ull;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const uint64_t oa = ((uint64_t)q4[t][1] << 32) | q4[t][0], ob = ((uint64_t)q4[t][3] << 32) | q4[t][2];
-        rank += (oa > me ? 1 : 0) + (ob > me ? 1 : 0);
+        g64 = oa > g64 ? oa : g64;
+        g64 = ob > g64 ? ob : g64;
       }
     }
-    if (c < nc && rank < k) sel[rank] = (int)~(uint32_t)me;
+    const uint64_t T64 = lane0_u64(fold_runs<false>(g64, G));
+    append(ok0 && v0 >= T64, ok1 && v1 >= T64, tk.count64);
+    __syncthreads();
+    nc = __builtin_amdgcn_readfirstlane(tk.count64);
+  }
+  const int cc = l >> 3, part = l & 7;
+  for (int c0 = 8 * w; c0 < nc; c0 += 8 * kDecWaves) {  // wave-uniform
+    const int c = c0 + cc;
+    const uint64_t me = tk.cand[c < nc ? c : 0];
+    int rank = 0;
+    for (int j0 = 0; j0 < nc; j0 += 32) {
+      uint64_t o[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = j0 + 8 * u + part;
+        o[u] = tk.cand[j < nc ? j : 0];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) rank += (j0 + 8 * u + part < nc && o[u] > me) ? 1 : 0;
+    }
+    rank += (int)dpp<kDppQuadXor1, 0xF>((uint32_t)rank);
+    rank += (int)dpp<kDppQuadXor2, 0xF>((uint32_t)rank);
+    rank += (int)dpp<kDppHalfMirror, 0xF>((uint32_t)rank);
+    if (part == 0 && c < nc && rank < k) sel[rank] = (int)~(uint32_t)me;
   }
   __syncthreads();
 }
@@ -1226,8 +1281,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
         }
         scl[f] = score;
         kyf[f] = key;
-        kyl[f] = ordered_key(key);
+        const uint32_t o = ordered_key(key);
+        kyl[f] = o;
+        return o;
       };
+      uint32_t key0 = 0u, key1 = 0u;  // this thread's ordered keys (experts tid, tid + 512)
       // logits of token t0: thread e polls the partial slots of experts e and
       // e + 512 (every split's 8-byte load per round) until each carries this
       // launch's tag, then sums them in split order
@@ -1274,18 +1332,24 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
             lg0 += __uint_as_float(v0[sp][0]);
             lg1 += __uint_as_float(v1[sp][0]);
           }
-        if (n0) gate(e0, lg0, bias_pre[0]);
-        if (n1) gate(e1, lg1, bias_pre[1]);
+        if (n0) key0 = gate(e0, lg0, bias_pre[0]);
+        if (n1) key1 = gate(e1, lg1, bias_pre[1]);
       }
-      __syncthreads();
-      if (s_fail) return give_up();
-      trace_mark(pl, a.ws, 10);
       // One token per pass: the workgroup's threshold-and-rank selection
-      // (block_topk, E <= 1024, k <= 32). Several tokens per pass: one wave
-      // per token runs wave_topk.
+      // (block_topk, E <= 1024, k <= 32) on the keys in registers; its
+      // barriers publish s_fail, the scores and keys. Several tokens per
+      // pass: one wave per token runs wave_topk on the keys in LDS.
       const bool coop = nt == 1;
+      if (!coop) {
+        __syncthreads();
+        if (s_fail) return give_up();
+      }
+      trace_mark(pl, a.ws, 10);
       for (int tg = 0; tg < nt; tg += kDecWaves) {
-        if (coop) block_topk(kyl, E, k, sel, *reinterpret_cast<BlockTopk *>(lds_align16(sel + kDecWaves * kMaxTopk)));
+        if (coop) {
+          block_topk(key0, key1, E, k, sel, *reinterpret_cast<BlockTopk *>(lds_align16(sel + kDecWaves * kMaxTopk)));
+          if (s_fail) return give_up();
+        }
         const int tl = tg + w;
         if (tl >= nt) continue;
         const int t = t0 + tl;

@@ -38,8 +38,9 @@ constexpr int kDecMaxLds = 160 * 1024;   // gfx950: 160 KiB of LDS per workgroup
 constexpr int kDecStaticLds = 1024;  // decode kernel's static LDS (round table, counters), upper bound
 constexpr int kDnStage = 128;        // decode down: y rows staged per wave (32 B + a 4-byte tag each)
 
-// LDS of the workgroup top-k (block_topk): per-wave group maxima, up to kMaxExperts candidates, a count
-constexpr int kBlockTopkBytes = 8 * (kDecWaves * 32 + kMaxExperts + 8) + 16;
+// LDS of the workgroup top-k (block_topk): group maxima of the 32- and 64-bit keys per wave, up to
+// kMaxExperts candidates, two counts
+constexpr int kBlockTopkBytes = 12 * kDecWaves * 32 + 8 * kMaxExperts + 16;
 
 constexpr int kRedundantTokens = 1;    // decode: route every token in every workgroup up to this batch
 constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert) keys

@@ -23,9 +23,10 @@
 //       all the workgroup's units at once as soon as the ids are known; the
 //       waves' partial tiles meet in LDS, wave m sums unit m's in wave order,
 //       applies the activation, and writes the unit's 8 bf16 h values to
-//       tagged slots.
+//       tagged slots. Chosen expert j is the j-th of the selection (or of a
+//       forced route row), so the loads go out right after the selection.
 //   DN  down and combine (kimi.py:322-323): wave w takes the chosen experts
-//       w, w + 8 (ascending ids) in the workgroup's one or two 16-row output
+//       w, w + 8 (selection order) in the workgroup's one or two 16-row output
 //       tiles; its weights are loaded once the gate/up data has arrived (they
 //       then arrive while h is exchanged), it polls all its experts' h slots
 //       together, multiplies, and the waves' w x bf16(y) rows are summed in
@@ -58,8 +59,9 @@ struct SingleScratch {
   int sel[kDecWaves * kMaxTopk];         // selection output (sel[0..k) in rank order)
   float rred[kDecWaves * 16];            // router: the waves' partial logits
   float gred[kSingleSlots * kDecWaves * 16];  // gate/up: per unit, the waves' 16 partial rows
-  int ids[kSingleMaxTopk];               // chosen experts, ascending
-  float wts[kSingleMaxTopk];             // their gating weights
+  int ids[kSingleMaxTopk];               // forced routes: the chosen experts, in the row's order
+  float wts[kSingleMaxTopk];             // gating weight of chosen expert j (selection order)
+  int ord[kSingleMaxTopk];               // ord[r]: the chosen expert of ascending rank r (its j)
 };
 static_assert(sizeof(SingleScratch) % 16 == 0 && sizeof(SingleScratch) <= kSingleScratchBytes, "single_lds layout");
 static_assert(sizeof(BlockTopk) <= kBlockTopkBytes, "single_lds layout");
@@ -236,7 +238,6 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   const uint32_t tag = s_tag, abort0 = s_abort0;
 
   // -------------------------------------------------------- T: top-k/gating --
-  int w0_rank = 0, w0_e = -1;  // wave 0, lane l < k: the l-th chosen expert and its ascending rank
   {
     // thread e polls the logits of experts e and e + 512 (slot e of its copy)
     float logit0 = 0.f, logit1 = 0.f;
@@ -277,7 +278,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     else poll(std::false_type{});
     if (!ok) s_fail = 1;
     trace_mark(pl, a.ws, 2);
-    auto gate = [&](int e, float logit, float bias) {  // gating (kimi.py:308-309; tasks/distributed.py:174)
+    // gating (kimi.py:308-309; tasks/distributed.py:174); returns the ordered key
+    auto gate = [&](int e, float logit, float bias) {
       float score, key;
       if (pl.gating == K3MOE_GATING_SIGMOID_BIAS) {
         score = 1.0f / (1.0f + expf(-logit));
@@ -288,35 +290,37 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
       }
       scl[e] = score;
       kyf[e] = key;
-      kyl[e] = ordered_key(key);
+      return ordered_key(key);
     };
-    if (tid < E) gate(tid, logit0, bias_pre[0]);
-    if (tid + kDecThreads < E) gate(tid + kDecThreads, logit1, bias_pre[1]);
-    __syncthreads();
-    if (s_fail) return leave(true);
+    uint32_t key0 = 0u, key1 = 0u;
+    if (tid < E) key0 = gate(tid, logit0, bias_pre[0]);
+    if (tid + kDecThreads < E) key1 = gate(tid + kDecThreads, logit1, bias_pre[1]);
     trace_mark(pl, a.ws, 3);
-    // the workgroup's top-k: a threshold from group maxima, then exact ranks among the candidates
-    block_topk(kyl, E, k, sh.sel, tk);
+    // the workgroup's top-k: a threshold from group maxima, then exact ranks
+    // among the candidates (its barriers also publish s_fail, the scores and keys)
+    block_topk(key0, key1, E, k, sh.sel, tk);
+    if (s_fail) return leave(true);
     trace_mark(pl, a.ws, 4);
-    if (w == 0) {
+    if (a.routes) {  // kernel-uniform
       // forced routes replace the selection when the row is valid (kimi.py:311-313)
-      int fid = 0;
-      const bool forced = a.routes && forced_route(a.routes, 0, k, E, &fid);
-      if (a.routes && !forced && l == 0 && blockIdx.x == 0)
-        __hip_atomic_fetch_or(ctl + kCtlErr, (unsigned)kErrRoutes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int my_e = l < k ? (forced ? fid : sh.sel[l]) : -1;
-      int rank = 0;
-      for (int r = 0; r < k; ++r) rank += ((int)lane_u32((uint32_t)my_e, r) < my_e) ? 1 : 0;
-      if (l < k) sh.ids[rank] = my_e;
-      w0_rank = rank;  // kept in registers for the weights, after the loads are issued
-      w0_e = my_e;
+      if (w == 0) {
+        int fid = 0;
+        const bool forced = forced_route(a.routes, 0, k, E, &fid);
+        if (!forced && l == 0 && blockIdx.x == 0)
+          __hip_atomic_fetch_or(ctl + kCtlErr, (unsigned)kErrRoutes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (l < k) sh.ids[l] = forced ? fid : sh.sel[l];
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
+  // the chosen experts in selection order: chosen expert j of the gate/up
+  // units, the h slots and the down waves (the combine adds them in ascending
+  // expert order through sh.ord)
+  const int *const chosen = a.routes ? sh.ids : sh.sel;
   trace_mark(pl, a.ws, 5);
 
   // ------------------------------------------------------------- GU issue --
-  // gate/up unit u: chosen expert j = u / U8 (ascending ids), rows 8 rg .. 8 rg + 7
+  // gate/up unit u: chosen expert j = u / U8 (selection order), rows 8 rg .. 8 rg + 7
   // of gate (lanes i < 8) and of up (lanes i >= 8). The rows' K / 512
   // super-steps of 16 MXFP4 blocks are shared out over the 8 waves (at most
   // kSingleMaxSS each: the CU's bytes in flight, not one wave's, set the
@@ -339,7 +343,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     const int mu = sl >> lg_ssw, ss = ss0 + (sl & lg_ssw);
     if (mu < nu && ss < ss1) {  // wave-uniform
       const int u = (int)blockIdx.x + mu * (int)gridDim.x, j = u / U8, rg = u - j * U8;
-      const size_t row = (size_t)sh.ids[j] * I + rg * 8 + (i & 7);
+      const size_t row = (size_t)chosen[j] * I + rg * 8 + (i & 7);
       const uint8_t *wr = lane_blk + row * KB * 16, *sr = lane_scl + row * KB;
 #pragma unroll
       for (int t = 0; t < 4; ++t) ga[sl][t] = load16(wr + (16 * ss + 4 * t + q) * 16);
@@ -351,7 +355,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   if (w == 0) {
     // the gating weights, while the loads are in flight; the down phase reads
     // them after the gate/up phase's LDS barriers
-    const int rank = w0_rank, my_e = w0_e;
+    const int my_e = l < k ? chosen[l] : -1;
+    int rank = 0;  // ascending rank of my_e among the chosen
+    for (int r = 0; r < k; ++r) rank += ((int)lane_u32((uint32_t)my_e, r) < my_e) ? 1 : 0;
     const float my_score = l < k ? scl[my_e] : 0.f, my_key = l < k ? kyf[my_e] : 0.f;
     {
       // weights in selection order (kimi.py:314-315; tasks/distributed.py:176)
@@ -368,7 +374,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
         for (int r = 0; r < k; ++r) sum = __fadd_rn(sum, lane_f32(ex, r));
         wt = ex / sum;
       }
-      if (l < k) sh.wts[rank] = wt;
+      if (l < k) {
+        sh.wts[l] = wt;
+        sh.ord[rank] = l;
+      }
       if (blockIdx.x == 0) {
         if (l < k) {
           a.out_ids[rank] = my_e;
@@ -401,7 +410,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
       for (int tt = 0; tt < 2; ++tt) {
         const int rt = (int)blockIdx.x + tt * (int)gridDim.x;
         const bool rt_ok = j < k && rt < pl.RTd;  // wave-uniform
-        const size_t row = (size_t)(rt_ok ? sh.ids[j] : 0) * K + (rt_ok ? rt : 0) * 16 + i;
+        const size_t row = (size_t)(rt_ok ? chosen[j] : 0) * K + (rt_ok ? rt : 0) * 16 + i;
 #pragma unroll
         for (int ks = 0; ks < KSD; ++ks) {
           const int kb = ks * 4 + q;
@@ -568,7 +577,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     const int tt = tid >> 4, r = tid & 15, rt = (int)blockIdx.x + tt * (int)gridDim.x;
     if (rt < pl.RTd) {
       float sum = 0.f;
-      for (int j = 0; j < k; ++j) sum = __fadd_rn(sum, dacc[(tt * k + j) * 16 + r]);
+      for (int jj = 0; jj < k; ++jj) sum = __fadd_rn(sum, dacc[(tt * k + sh.ord[jj]) * 16 + r]);
       a.out[rt * 16 + r] = sum;
     }
   }
