@@ -110,6 +110,10 @@ def read_trace(cfg, device):
     while G*2 <= min(torch.cuda.get_device_properties(device).multi_processor_count, 1024):
         G *= 2
     full = full[:G]
+    dump = os.environ.get('K3MOE_TRACE_DUMP')
+    if dump:
+        import numpy as np
+        np.save(f'{dump}_{cfg.name}.npy', full.numpy())
     if int(full[0, 55].item()) == 0x5349:   # the single-token kernel's rows
         names = ('router', 'poll_partials', 'gating', 'select', 'weights_ids', 'gate_up', 'poll_h', 'down_combine')
         t0 = full[:, 0].min()
@@ -136,10 +140,6 @@ def read_trace(cfg, device):
         out['poll_rounds_median'] = float(full[:, 11].median())
         return out
     raw = full[:, :9]
-    dump = os.environ.get('K3MOE_TRACE_DUMP')
-    if dump:
-        import numpy as np
-        np.save(f'{dump}_{cfg.name}.npy', full.numpy())
     t0 = raw[:, 0].min()
     out = {'workgroups': G}
     for n, name in enumerate(PHASES):

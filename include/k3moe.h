@@ -298,6 +298,16 @@ int k3moe_mxfp4_decode(const uint8_t *blocks, const uint8_t *scales, int64_t n_b
 int k3moe_activation(int32_t act, int32_t fast, const float *g, const float *u, float *out, int64_t n,
                      void *stream);
 
+/* Test hook for the failure path of the persistent kernels (no reference
+ * counterpart): with polls > 0, the router-logit waits of every later
+ * k3moe_moe_step / k3moe_moe_step_noalloc on the single-token or decode kernel
+ * never see their data and give up after `polls` polls, as a wait that timed
+ * out does: the step leaves NaN in expert_sum, sets K3MOE_STATUS_TIMEOUT in the
+ * workspace status and every workgroup ends normally; k3moe_workspace_init then
+ * makes the workspace usable again. polls = 0 (the default) turns it off.
+ * Process-wide; returns K3MOE_EINVAL for polls < 0. */
+int k3moe_debug_stall(int32_t polls);
+
 /* MXFP4 encode, pack_mxfp4 (megabench/tasks/quantization.py:13-37): n_blocks
  * groups of 32 consecutive values of in_dtype (K3MOE_DTYPE_F32, _BF16 or
  * _F16; in 16-byte aligned) -> n_blocks blocks of 16 bytes (byte j: element

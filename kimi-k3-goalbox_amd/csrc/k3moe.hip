@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 
+#include <atomic>
 #include <mutex>
 #include <stdio.h>
 #include <stdlib.h>
@@ -103,6 +104,11 @@ int device_cus() {
 // K3MOE_TRACE=1 in the environment makes decode steps record per-workgroup
 // phase timestamps (32 x uint64 per workgroup, 100 MHz) in the last 256 KiB
 // of the workspace, a profiling aid; the workspace size includes that area.
+// Test hook (k3moe_debug_stall): > 0 makes every later step's router-logit
+// waits give up after this many polls; 0, the default, leaves them bounded by
+// kSpinLimit only.
+std::atomic<int> g_stall{0};
+
 int trace_enabled() {
   static int v = -1;
   if (v < 0) {
@@ -406,6 +412,7 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
                 dims->latent, dims->hidden);
   Plan p;
   make_plan(*dims, device_cus(), p, trace_enabled());
+  p.stall = g_stall.load(std::memory_order_relaxed);
   if (dims->path == K3MOE_PATH_DECODE && p.path != kPathDecode)
     return fail(K3MOE_EINVAL, "the persistent decode path needs tokens <= %d and tokens*topk <= %d", kDecMaxTokens,
                 kDecMaxPairs);
@@ -605,6 +612,13 @@ int k3moe_mxfp4_encode(const void *in, int32_t in_dtype, int64_t n_blocks, uint8
   hipLaunchKernelGGL(k_encode, dim3((unsigned)grid), dim3(kEncThreads), 0, reinterpret_cast<hipStream_t>(stream), in,
                      in_dtype, n_blocks, blocks, scales);
   return launch_check("encode");
+}
+
+int k3moe_debug_stall(int32_t polls) {
+  g_err[0] = 0;
+  if (polls < 0) return fail(K3MOE_EINVAL, "polls must be >= 0 (got %d)", polls);
+  g_stall.store(polls, std::memory_order_relaxed);
+  return K3MOE_OK;
 }
 
 int k3moe_moe_step_noalloc(const k3moe_dims *dims, const void *x, const void *latent, const void *router,

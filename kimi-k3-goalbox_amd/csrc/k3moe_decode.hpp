@@ -1307,7 +1307,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
             v0[sp] = sp < n0 ? bload8_dev(tagr, pbase + sp * sstride + e0 * 8) : u32x2{0u, tag};
             v1[sp] = sp < n1 ? bload8_dev(tagr, pbase + sp * sstride + e1 * 8) : u32x2{0u, tag};
           }
-          bool ready = true;
+          bool ready = pl.stall == 0;  // (a test hook: the wait never ends and gives up)
 #pragma unroll
           for (int sp = 0; sp < kDecMaxSplits; ++sp) ready = ready && v0[sp][1] == tag && v1[sp][1] == tag;
           if (spins == 0 && w == 0) trace_mark(pl, a.ws, 44);
@@ -1317,7 +1317,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
             ok = false;
             break;
           }
-          if (spins > kSpinLimit) {
+          if (spins > (pl.stall ? (unsigned)pl.stall : kSpinLimit)) {
             if (l == 0) raise_timeout(ctl);
             ok = false;
             break;

@@ -119,7 +119,7 @@ struct Plan {
   int pinned;  // 1: gate/up by whole units per wave, the rows of the workgroup's tokens in LDS (row t at t xpitch)
   int lds_pin;  // bytes of the pinned rows' region, room for every token's row (the last LDS region)
   int dn_cap;   // expert-major down: y rows staged per wave
-  int pad_;
+  int stall;     // test hook (k3moe_debug_stall): > 0 makes the router-logit waits give up after this many polls
   int trace;      // 1: the decode kernel records phase timestamps at o_trace
   int single;     // 1: the single-token kernel runs the step (k3moe_single.hpp)
   int redundant;  // 1: every workgroup routes every token (no barrier before grouping)
@@ -324,6 +324,7 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   // pair outputs: the general path, and the decode path's expert-major down (I = 256, 384, 512)
   p.o_y = take((general || p.I == 256 || p.I == 384 || p.I == 512) ? (size_t)p.P * p.K * 2 : 0);
   p.trace = trace && p.path == kPathDecode;
+  p.stall = 0;
   single_plan(d, p);
   if (p.single) {
     p.path = kPathDecode;

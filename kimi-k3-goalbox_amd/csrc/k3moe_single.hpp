@@ -253,7 +253,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
       for (;;) {
         v0 = n0 ? bload8_dev(tagr, (uint32_t)(kTagPartials + my_copy + e0 * 8)) : u32x2{0, tag};
         if constexpr (TWO) v1 = n1 ? bload8_dev(tagr, (uint32_t)(kTagPartials + my_copy + e1 * 8)) : u32x2{0, tag};
-        bool ready = v0[1] == tag;
+        bool ready = v0[1] == tag && pl.stall == 0;  // (a test hook: the wait never ends and gives up)
         if constexpr (TWO) ready = ready && v1[1] == tag;
         if (spins == 0 && w == 0) trace_mark(pl, a.ws, 10);
         if (__ballot(!ready) == 0) break;
@@ -262,7 +262,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
           ok = false;
           break;
         }
-        if (spins > kSpinLimit) {
+        if (spins > (pl.stall ? (unsigned)pl.stall : kSpinLimit)) {
           if (l == 0) raise_timeout(ctl);
           ok = false;
           break;

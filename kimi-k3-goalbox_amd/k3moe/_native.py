@@ -50,7 +50,7 @@ STATUS_TIMEOUT, STATUS_ROUTES = 1, 2
 EXPORTS = ('k3moe_workspace_bytes', 'k3moe_workspace_init', 'k3moe_workspace_status', 'k3moe_moe_step',
            'k3moe_mxfp4_decode', 'k3moe_last_error', 'k3moe_version', 'k3moe_latent_workspace_bytes',
            'k3moe_latent_in', 'k3moe_latent_out', 'k3moe_workspace_layout',
-           'k3moe_moe_step_noalloc', 'k3moe_mxfp4_encode', 'k3moe_activation')
+           'k3moe_moe_step_noalloc', 'k3moe_mxfp4_encode', 'k3moe_activation', 'k3moe_debug_stall')
 
 _lib = None
 
@@ -88,6 +88,8 @@ def load(path: str | None = None):
     lib.k3moe_mxfp4_encode.restype = ctypes.c_int
     lib.k3moe_activation.argtypes = [i32, i32, p, p, p, i64, p]
     lib.k3moe_activation.restype = ctypes.c_int
+    lib.k3moe_debug_stall.argtypes = [i32]
+    lib.k3moe_debug_stall.restype = ctypes.c_int
     lib.k3moe_latent_workspace_bytes.argtypes = [ctypes.POINTER(LatentDims), ctypes.POINTER(sz)]
     lib.k3moe_latent_workspace_bytes.restype = ctypes.c_int
     lib.k3moe_latent_in.argtypes = [ctypes.POINTER(LatentDims)] + [p]*6 + [p, sz, p]

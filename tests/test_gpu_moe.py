@@ -640,6 +640,55 @@ def test_old_status_does_not_shorten_waits(gpu, path):
     assert k3moe.workspace_status(clean) == 0
 
 
+def debug_stall(polls):
+    """k3moe_debug_stall: with polls > 0 the router-logit waits give up after that many polls."""
+    from k3moe import _native
+    _native.check(_native.load().k3moe_debug_stall(polls), 'k3moe_debug_stall')
+
+
+def reinit(ws):
+    """k3moe_workspace_init on an existing workspace (on the current stream)."""
+    import ctypes
+    from k3moe import _native
+    _native.check(_native.load().k3moe_workspace_init(
+        ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(ws.numel()),
+        ctypes.c_void_p(torch.cuda.current_stream(ws.device).cuda_stream)), 'k3moe_workspace_init')
+
+
+@pytest.mark.parametrize('path', ['decode', 'single'])
+def test_wait_that_gives_up_poisons_output_and_reinit_restores(gpu, path):
+    """The failure path of the bounded waits, forced from the host: with k3moe_debug_stall(256)
+    the router-logit waits never see their data and give up after 256 polls (a timeout). Every
+    workgroup still ends (the others leave their own waits when the abort counter moves),
+    expert_sum is NaN everywhere, the status word has the timeout bit; after
+    k3moe_workspace_init the same workspace gives a clean workspace's outputs bit for bit."""
+    cfg = configs.TP8_B1 if path == 'single' else configs.TP8_B8
+    say(f'case: {cfg.name} seed=9 path={path}, router-logit waits forced to give up after 256 polls')
+    g = to_dev(synthetic.moe_layer_inputs(cfg, 9), gpu)
+    from k3moe.moe import dims_for, workspace_bytes
+    need = workspace_bytes(dims_for(g['x'], g['router'], g['gate_blocks'], g['down_blocks'], cfg.topk, cfg.gating,
+                                    cfg.activation, None, path))
+    clean = k3moe.new_workspace(need, gpu)
+    ref = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, path=path, workspace=clean)
+    ws = k3moe.new_workspace(need, gpu)
+    debug_stall(256)
+    try:
+        bad = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, path=path, workspace=ws)
+        torch.cuda.synchronize(gpu)
+    finally:
+        debug_stall(0)
+    assert bool(torch.isnan(bad['expert_sum']).all())
+    assert k3moe.workspace_status(ws) & 1
+    reinit(ws)
+    assert k3moe.workspace_status(ws) == 0
+    for _ in range(2):
+        got = k3moe.moe_step(*synthetic.step_args(g), topk=cfg.topk, path=path, workspace=ws)
+        torch.cuda.synchronize(gpu)
+        for key in ('expert_sum', 'expert_ids', 'route_weights'):
+            assert torch.equal(got[key], ref[key]), key
+    assert k3moe.workspace_status(ws) == 0
+
+
 def raw_step(dims, g, routes, outs, ws):
     """k3moe_moe_step through the C ABI, without the Python layer's checks of `routes`."""
     import ctypes

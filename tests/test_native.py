@@ -27,6 +27,13 @@ def test_library_exports_every_declared_symbol():
     assert lib.k3moe_version().decode().startswith('k3moe')
 
 
+def test_debug_stall_takes_only_non_negative_polls():
+    lib = _native.load()
+    assert lib.k3moe_debug_stall(-1) == -1
+    assert 'polls' in lib.k3moe_last_error().decode()
+    assert lib.k3moe_debug_stall(0) == 0
+
+
 def test_dims_struct_matches_header():
     text = open(HEADER).read()
     body = re.search(r'typedef struct k3moe_dims \{(.*?)\} k3moe_dims;', text, flags=re.S).group(1)
