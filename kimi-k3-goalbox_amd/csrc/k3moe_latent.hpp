@@ -435,8 +435,10 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
     ring_barrier();
   }
 
-  // one unit: the split's k-steps of row tile rt0 + rstep j from `buf`, partials out
-  auto unit = [&](int j, const u32x4 (&buf)[kLatKW][4]) {
+  // one unit: the split's k-steps of row tile rt0 + rstep j from `buf`, partials
+  // out; `buf` takes unit j + 3 as soon as this wave's products are done (before
+  // the unit's barriers, which wait for the workgroup's slowest wave)
+  auto unit = [&](int j, u32x4 (&buf)[kLatKW][4]) {
     const int rt = rt0 + rstep * j;
     f32x4 acc0[4], acc1[4];
 #pragma unroll
@@ -464,6 +466,7 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
         }
       }
     }
+    if (j + 3 < J) issue(j + 3, buf);
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       if (tt >= TT) continue;
@@ -489,16 +492,13 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
   };
 
   mark(1);
-  // three units in flight: a buffer is refilled with unit j + 3 once unit j is multiplied
+  // three units in flight: a buffer is refilled with unit j + 3 once this wave has multiplied unit j
   for (int j = 0; j < J; j += 3) {
     unit(j, b0);
-    if (j + 3 < J) issue(j + 3, b0);
     if (j + 1 >= J) break;
     unit(j + 1, b1);
-    if (j + 4 < J) issue(j + 4, b1);
     if (j + 2 >= J) break;
     unit(j + 2, b2);
-    if (j + 5 < J) issue(j + 5, b2);
   }
   mark(45);
 
@@ -528,23 +528,28 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
     while (s0 < SP && (((s0 + 1) * pl.KS) >> lsp) <= pl.KS0) ++s0;
     last0 = ((s0 * pl.KS) >> lsp) < pl.KS0 ? s0 + 1 : s0;
   }
-  // member s finishes the group's tiles j = s, s + SP, ..: per output, every
-  // split's partial is loaded before the sum (in split order)
-  for (int j = s; j < J; j += SP) {
-    const int rt = rt0 + rstep * j;
-    const bool pair = !OUT && rt >= pl.ntile0;
+  // member s finishes the group's tiles j = s, s + SP, ..: output item it of
+  // the nj tiles' nj x B x 16 (tile jj = it / (16 B), token, row) goes to a
+  // thread, so the partial loads of all its tiles are in flight together; per
+  // output, every split's partial is loaded before the sum (in split order)
+  const int nj = J > s ? (J - s + SP - 1) >> lsp : 0;
+  const int per_tile = B * 16, items = nj * per_tile;
+  for (int it0 = 0; it0 < items; it0 += 2 * kLatThreads) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {  // B * 16 <= 2 * kLatThreads outputs
-      const int it = tid + c * kLatThreads;
-      const int t = it >> 4, r = it & 15;
-      const bool ok = t < B && (!pair || r < 8);
+    for (int c = 0; c < 2; ++c) {
+      const int it = it0 + tid + c * kLatThreads;
+      const int jj = it / per_tile, rem = it - jj * per_tile;
+      const int t = rem >> 4, r = rem & 15;
+      const int rt = rt0 + rstep * (s + SP * jj);
+      const bool pair = !OUT && rt >= pl.ntile0;
+      const bool ok = it < items && (!pair || r < 8);
       // (only the splits that wrote a part: <1>'s part 1 lives in the last few)
       float va[kLatMaxSplits], vb[kLatMaxSplits];
 #pragma unroll
       for (int ss = 0; ss < kLatMaxSplits; ++ss) {
         va[ss] = vb[ss] = 0.f;
         if (ss < SP) {
-          const uint32_t o = (uint32_t)((((long)ss * pl.RT + rt) * B + t) * 64 + r * 4);
+          const uint32_t o = ok ? (uint32_t)((((long)ss * pl.RT + rt) * B + t) * 64 + r * 4) : 0u;
           va[ss] = bload4_dev(rp0, ok && ss < last0 ? o : kOffNone);
           vb[ss] = bload4_dev(OUT ? rp1 : rp0, ok && (OUT ? ss >= s0 : pair) ? o + (OUT ? 0 : 32) : kOffNone);
         }
