@@ -131,6 +131,27 @@ __device__ __forceinline__ bool grid_barrier(unsigned *ctl, const BarrierBase &b
 // barrier, after which each workgroup zeroes its share of the tag area: every
 // launch of the next cycle then finds slots written in that cycle or zeros
 // (which no tag matches).
+// Code warm-up of a persistent kernel whose last launch recorded its code
+// range [range[0], range[1]) (the program counter at its start and near its
+// end): at a launch with the same start every workgroup loads a slice of the
+// range as data (wave w of workgroup b: 1 KiB chunk b / 8 + 32 w, so the 32
+// workgroups of an XCD cover up to 256 KiB of its L2), so that the kernel's
+// first instruction fetches of each stretch of code hit L2 instead of queueing
+// for HBM behind its own weight loads. Loads only inside the recorded range
+// (the kernel's own first bytes otherwise); the caller keeps the returned
+// value live until the loads may complete. Waits for the range words first.
+__device__ __forceinline__ u32x4 warm_code_range(const uint64_t *range, uint64_t pc0) {
+  const uint64_t c0 = range[0], c1 = range[1];
+  u32x4 v = {0, 0, 0, 0};
+  if (c0 == pc0 && c1 > pc0 && c1 - pc0 < (1u << 20)) {
+    const uint64_t lo = pc0 & ~(uint64_t)1023;
+    const uint64_t addr = lo + (uint64_t)((blockIdx.x >> 3) + 32 * (threadIdx.x >> 6)) * 1024 + (threadIdx.x & 63) * 16;
+    const uint64_t at = addr + 16 <= c1 ? addr : (pc0 & ~(uint64_t)15);
+    v = *reinterpret_cast<const __attribute__((address_space(1))) u32x4 *>(at);
+  }
+  return v;
+}
+
 __device__ __forceinline__ uint32_t last_tag_of_cycle() {
   return (uint32_t)(0x100000000ull >> __builtin_ctz(gridDim.x));
 }

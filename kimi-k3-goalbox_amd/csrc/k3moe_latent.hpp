@@ -267,6 +267,10 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
   const uint32_t part_bytes = (uint32_t)((long)SP * pl.RT * B * 64);
   const __amdgpu_buffer_rsrc_t rp0 = make_rsrc(a.ws + pl.o_part0, part_bytes);
   const __amdgpu_buffer_rsrc_t rp1 = make_rsrc(a.ws + (OUT ? pl.o_part1 : pl.o_part0), part_bytes);
+  // this kernel's code into L2 before the weight loads (the range its last launch recorded)
+  const uint64_t pc0 = program_counter();
+  uint64_t *const crange = reinterpret_cast<uint64_t *>(ctl + kCtlCodeLatent + 4 * OUT);
+  const u32x4 code_probe = warm_code_range(crange, pc0);
   BarrierBase bb{0u, 0u, 0u};
   if (OUT && !local && tid == 0) bb = barrier_base(ctl);
   // the group counter before this launch: no member can have added a whole kLatGrpTotal yet
@@ -332,19 +336,25 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
     // 16-byte chunks k = 4 (l + 64 m) of its expert-sum row:
     //   en = bf16(bf16(e r) w), e = bf16(expert_sum), r = 1/sqrt(mean(e^2) + eps),
     // and writes the chunks in this split's latent range to the slice. The
-    // expert sum, the norm weights of the range and the shared_h chunks are
-    // loaded before the first units' weights.
+    // shared_h chunks, the expert sum and the norm weights of the range are
+    // loaded before the first units' weights; the staging goes first (its
+    // number of loads varies), so that the expert sum's use waits for a fixed
+    // count of later loads and not for the weights.
     const int t = w;
     const int kr0 = k0 * kStepK, kr1 = (touch0 ? (k1 < pl.KS0 ? k1 : pl.KS0) : k0) * kStepK;
+    stage();
     f32x4 ec[kLatNormChunks];
 #pragma unroll
-    for (int m = 0; m < kLatNormChunks; ++m) {
-      const int k = 4 * (l + 64 * m);
-      ec[m] = *reinterpret_cast<const f32x4 *>(t < B && k < pl.lh ? a.esum + (long)t * pl.lh + k
-                                                                  : reinterpret_cast<const float *>(zlane));
+    for (int m = 0; m < kLatNormChunks; ++m) ec[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (t < B) {  // wave-uniform: the other waves load nothing here
+#pragma unroll
+      for (int m = 0; m < kLatNormChunks; ++m) {
+        const int k = 4 * (l + 64 * m);
+        ec[m] = *reinterpret_cast<const f32x4 *>(k < pl.lh ? a.esum + (long)t * pl.lh + k
+                                                           : reinterpret_cast<const float *>(zlane));
+      }
     }
     const u32x4 wnv = load16(tid * 8 < kr1 - kr0 ? a.norm + kr0 + tid * 8 : zlane);
-    stage();
     issue(0, b0);
     issue(1, b1);
     issue(2, b2);
@@ -492,6 +502,7 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
   };
 
   mark(1);
+  asm volatile("" ::"v"(code_probe));  // (issued first: complete with the staging)
   // three units in flight: a buffer is refilled with unit j + 3 once this wave has multiplied unit j
   for (int j = 0; j < J; j += 3) {
     unit(j, b0);
@@ -574,6 +585,10 @@ __global__ __launch_bounds__(kLatThreads, 1) void k_latent(LatPlan pl_arg, LatAr
     __syncthreads();
     poison_share<true>(a.ya, (long)B * (OUT ? pl.h : pl.lh));
     if (!OUT) poison_share<true>(a.yb, (long)B * pl.S);
+  }
+  if (blockIdx.x == 0 && tid == 0) {  // this kernel's code range, for the next launch's warm-up
+    crange[0] = pc0;
+    crange[1] = program_counter();
   }
   mark(47);
 }

@@ -57,6 +57,7 @@ constexpr int kRedundantKeys = 8192;   // ... and up to this many (token, expert
 constexpr int kCtlErr = 2;
 constexpr int kCtlAbort = 3;
 constexpr int kCtlCodeSingle = 8;  // 2 x uint64: the single-token kernel's code range of its last launch
+constexpr int kCtlCodeLatent = 12;  // 4 x (2 x uint64): the latent kernels' code ranges (k_latent<0>, <1>, k_latent_sk<0>, <1>)
 // Launch counters of the single-token and decode kernels (k3moe_single.hpp,
 // k3moe_decode.hpp): each of their workgroups adds one, on counter blockIdx %
 // kEpochCounters, when it leaves; the sum, divided by the grid size (the same
