@@ -445,8 +445,13 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
   // holds); otherwise they are issued again.
   GuSS<W> B0, B1;
   int s_pre = -1;
+  // Whole 512-column row chunks (K a multiple of 512, more than one token):
+  // each round's activation rows are loaded straight into LDS before its
+  // first weights, and only the rows are waited for; no weights go out before
+  // the round table (their issue would hold up the table's barrier).
+  const bool dma_rows = AL && !xpre_ok;
   trace_mark(pl, a.ws, 12);
-  if (ga < gb) {
+  if (!dma_rows && ga < gb) {
     const int work = (gb - ga) * NSS;
     const int s = wave_share(work, w), e = wave_share(work, w + 1);
     if (s < e) {
@@ -530,6 +535,16 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
     };
     const uint8_t *iwr[W], *isr[W];
     int ig = s / NSS, iss = s % NSS;  // issue cursor
+    if (dma_rows) {
+      // the round's rows (1 KiB of a row per instruction, spread over the waves), then the weights
+      const int per_row = pl.K / 512;
+      for (int c = w; c < rows * per_row; c += kDecWaves) {
+        const int r = c / per_row, j = c - r * per_row;
+        load_lds<16>(a.xin + (size_t)s_rowtok[r] * pl.K + j * 512 + l * 8,
+                     reinterpret_cast<char *>(xs + (size_t)r * pl.xpitch + j * 512));
+      }
+      asm volatile("" ::: "memory");  // the row loads stay ahead of the weights
+    }
     if (s < e) {
       rows_of(ig, iwr, isr);
       if (s != s_pre) gu_issue<W, AL>(B0, iwr, isr, iss, KB);  // else issued before the table, the same loads
@@ -548,7 +563,11 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
         if (c < K8) *reinterpret_cast<u32x4 *>(xs + (size_t)r * pl.xpitch + c * 8) = xpre[hh];
       }
     }
-    for (int r0 = 0; !xpre_ok && r0 < rows; r0 += 8) {
+    if (dma_rows) {  // wait for the rows only: after them each wave issued 5 W weight loads, or none
+      if (s < e) wait_vm<5 * W>();
+      else wait_vm<0>();
+    }
+    for (int r0 = 0; !xpre_ok && !dma_rows && r0 < rows; r0 += 8) {
       for (int c0 = 0; c0 < K8; c0 += 2 * kDecThreads) {
         u32x4 v[8][2];
 #pragma unroll
