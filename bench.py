@@ -319,6 +319,8 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, 
                                                     inp0['down_blocks'], cfg.topk, cfg.gating, cfg.activation,
                                                     inp0.get('latent')), device)
     status = k3moe.workspace_status(ws)
+    # the phase timestamps of the last timed (cold) step, before the eager step below overwrites them
+    trace = read_trace(cfg, device) if os.environ.get('K3MOE_TRACE') == '1' and layers == 1 else None
     # the graph's outputs equal an eager step on the same inputs (bitwise)
     eager = k3moe.moe_step(*synthetic.step_args(inp0), **kw, latent=inp0.get('latent'))
     torch.cuda.synchronize(device)
@@ -327,7 +329,6 @@ def measure(cfg, *, seed, steps, warmup, cold, device, layers=1, host_gen=True, 
                                     distinct=d, K=cfg.width) for d in distinct)
     flops = layers*traffic.step_flops(B=cfg.tokens, E=cfg.experts, k=cfg.topk, h=cfg.hidden, I=cfg.inter,
                                       K=cfg.width)
-    trace = read_trace(cfg, device) if os.environ.get('K3MOE_TRACE') == '1' and layers == 1 else None
     del graph, outs, flush
     return {'ms': ms, 'wall_s': wall, 'distinct': distinct, 'bytes': nbytes, 'flops': flops,
             'host_us': host_us, 'host_loop_us': host_loop_us, 'host_prepared_us': host_prepared_us,

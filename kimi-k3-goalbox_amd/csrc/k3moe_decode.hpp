@@ -693,7 +693,8 @@ __device__ __forceinline__ void gu_phase(const Plan &pl, const DecodeArgs &a, fl
 template <bool AL>
 __device__ __forceinline__ void gu_pinned(const Plan &pl, const DecodeArgs &a, const int *g_act, const int *g_aoff,
                                           const int *g_acnt, const int *g_coff, const int *g_cexp, const int *g_ptok,
-                                          uint16_t *xs, int *s_prog, uint16_t *hbuf, int ua, int ub, int wa, int wb) {
+                                          uint16_t *xs, int *s_prog, uint16_t *hbuf, int ua, int ub, int wa, int wb,
+                                          bool staged) {
   static_assert(AL, "pinned rows are loaded in whole 512-column chunks");
   const int w = wave_id(), l = threadIdx.x & 63, i = l & 15;
   const int KB = pl.K / kBlockK, NSS = KB / 16, U8 = pl.U8;
@@ -707,9 +708,10 @@ __device__ __forceinline__ void gu_pinned(const Plan &pl, const DecodeArgs &a, c
     nt = min(16, g_aoff[d] + g_acnt[d] - pbase);
   };
   trace_mark(pl, a.ws, 12);
-  // the workgroup's token rows: tokens of its chunks (units [wa, wb)), as a bit set (B <= 64)
+  // the workgroup's token rows: tokens of its chunks (units [wa, wb)), as a bit set (B <= 64);
+  // none when every token's row is in LDS already (staged)
   uint64_t rows = 0;
-  if (wa < wb) {
+  if (!staged && wa < wb) {
     for (int c = wa / U8; c <= (wb - 1) / U8; ++c) {
       int pbase, nt;
       chunk(c, pbase, nt);
@@ -766,12 +768,12 @@ __device__ __forceinline__ void gu_pinned(const Plan &pl, const DecodeArgs &a, c
     issue(R0);
     issue(R1);
     issue(R2);
-    wait_vm<3 * 5>();  // this wave's row loads have landed; the 3 super-steps (5 loads each) stay in flight
+    if (!staged) wait_vm<3 * 5>();  // this wave's row loads have landed; the 3 super-steps (5 loads each) stay in flight
   } else {
-    wait_vm<0>();
+    if (!staged) wait_vm<0>();
   }
   trace_mark(pl, a.ws, 13);
-  ring_barrier();  // every wave's rows are in LDS
+  if (!staged) ring_barrier();  // every wave's rows are in LDS (staged: published by earlier barriers)
   trace_mark(pl, a.ws, 33);
   if (n <= 0) return;
   int cu = ua, css = 0;
@@ -1429,6 +1431,25 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     }
   }
   trace_mark(pl, a.ws, 3);
+  // Pinned gate/up in a workgroup that routed no token: it would wait here
+  // for the routed pairs with nothing to load, so it loads every token's row
+  // into its pinned rows now (1 KiB of a row per instruction, spread over the
+  // waves) and gate/up starts on its weights without a row wait. The pair
+  // poll below waits for these loads too (vmcnt counts in order); they land
+  // long before the pairs are published.
+  bool rows_staged = false;
+  if constexpr (AL) {
+    if (pl.pinned && !redundant && (int)blockIdx.x >= B) {
+      rows_staged = true;
+      const int per_row = pl.K / 512;
+      for (int c = w; c < B * per_row; c += kDecWaves) {
+        const int r = c / per_row, j = c - r * per_row;
+        load_lds<16>(a.xin + (size_t)r * pl.K + j * 512 + l * 8,
+                     reinterpret_cast<char *>(xpin + (size_t)r * pl.xpitch + j * 512));
+      }
+      wait_vm<0>();  // before the barriers below publish them
+    }
+  }
   if (!redundant) {
     // every pair's slot (pairs tid and tid + 512), polled until both halves carry this launch's tag
     u32x4 pv[2] = {u32x4{0u, tag, 0u, tag}, u32x4{0u, tag, 0u, tag}};
@@ -1585,7 +1606,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   if constexpr (AL) {
     if (pl.pinned) {
       gu_pinned<AL>(pl, a, g_act, g_aoff, g_acnt, g_coff, g_cexp, g_ptok, xpin, s_prog, hbuf, pin_ua, pin_ub,
-                    wave_unit(blockIdx.x * kDecWaves), wave_unit((blockIdx.x + 1) * kDecWaves));
+                    wave_unit(blockIdx.x * kDecWaves), wave_unit((blockIdx.x + 1) * kDecWaves), rows_staged);
       pinned_done = true;
     }
   }
