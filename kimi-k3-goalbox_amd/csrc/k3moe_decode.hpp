@@ -1161,36 +1161,35 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   // Code warm-up: a step runs much of this kernel's code once, and after other
   // work has evicted it every new stretch stalls on instruction fetches from
   // HBM. The last workgroup to leave records the kernel's code range in the
-  // control block; at the next launch with the same code each workgroup loads
-  // a slice of that range as data, so that it sits in its XCD's L2 (the 32
-  // workgroups b, b + 8, .. of an XCD cover up to 256 KiB, one 1 KiB chunk per
-  // wave). The range is read only if its recorded start is this launch's and
-  // never past its recorded end.
-  // The warm-up loads are issued after the router's own loads, so that the
-  // router's waits do not include them.
+  // control block; at the next launch with the same code the last wave of
+  // each workgroup loads eight 1 KiB chunks of that range as data, so that it
+  // sits in its XCD's L2 (the 32 workgroups b, b + 8, .. of an XCD cover up to
+  // 256 KiB). The range is read only if its recorded start is this launch's
+  // and never past its recorded end. That wave takes no router k-steps, so the
+  // router's waits never include these loads (nor the range read they
+  // depend on).
   uint64_t *crange = reinterpret_cast<uint64_t *>(ctl + kCtlCode);
   const uint64_t pc0 = program_counter();
   u32x4 code_probe = {0, 0, 0, 0};
-  bool warm = false;
-  auto warm_code = [&]() {
-    if (warm) return;
-    warm = true;
+  if (w == kDecWaves - 1) {
     const uint64_t c0 = crange[0], c1 = crange[1];
     if (c0 == pc0 && c1 > pc0 && c1 - pc0 < (1u << 20)) {
       const uint64_t lo = pc0 & ~(uint64_t)1023;
-      const uint64_t addr = lo + (uint64_t)((blockIdx.x >> 3) + 32 * w) * 1024 + l * 16;
-      // one unconditional global load (a conditional one would be joined by a
-      // copy that waits for it at once); out of range, the kernel's own first bytes
-      const uint64_t at = addr + 16 <= c1 ? addr : (pc0 & ~(uint64_t)15);
-      code_probe = *reinterpret_cast<const __attribute__((address_space(1))) u32x4 *>(at);
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const uint64_t addr = lo + (uint64_t)((blockIdx.x >> 3) * 8 + m) * 1024 + l * 16;
+        // out of range: the kernel's own first bytes
+        const uint64_t at = addr + 16 <= c1 ? addr : (pc0 & ~(uint64_t)15);
+        code_probe ^= *reinterpret_cast<const __attribute__((address_space(1))) u32x4 *>(at);
+      }
     }
-  };
+  }
 
   if (l == 0) __hip_atomic_store(s_prog + w, 4096, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 
   // ------------------------------------------------------------ R: router --
-  // Workgroup unit = (16 router rows, k-split s) for every token tile: the 8
-  // waves take consecutive k-steps of the split, load the row tile once and
+  // Workgroup unit = (16 router rows, k-split s) for every token tile: the
+  // first 7 waves take consecutive k-steps of the split, load the row tile once and
   // every token tile with all loads in flight, and meet in LDS; the sum over
   // waves is written as partial s of each logit.
   {
@@ -1199,7 +1198,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     for (int u = blockIdx.x; u < NU; u += gridDim.x) {
       const int s = u % pl.Srw, rt = u / pl.Srw;
       const int k0 = (int)((unsigned)(s * pl.KSr) / (unsigned)pl.Srw), k1 = (int)((unsigned)((s + 1) * pl.KSr) / (unsigned)pl.Srw);
-      const int ka = k0 + (k1 - k0) * w / kDecWaves, kb1 = k0 + (k1 - k0) * (w + 1) / kDecWaves;
+      constexpr int RW = kDecWaves - 1;  // router waves (the last one warms the code)
+      const int ka = w < RW ? k0 + (k1 - k0) * w / RW : k1, kb1 = w < RW ? k0 + (k1 - k0) * (w + 1) / RW : k1;
       const int row = rt * 16 + i;
       const bool row_ok = row < E;
       const uint16_t *arow = a.router + (size_t)(row_ok ? row : 0) * pl.h;
@@ -1220,7 +1220,6 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) vb[tt][kk] = tok_ok ? load16(brow + kk * 8) : u32x4{0, 0, 0, 0};
         }
-        warm_code();
         make_tag();
 #pragma unroll
         for (int tt = 0; tt < kDecMaxTokens / 16; ++tt) {
@@ -1248,7 +1247,6 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       __syncthreads();
     }
   }
-  warm_code();  // workgroups without router work
   make_tag();
   trace_mark(pl, a.ws, 1);
   asm volatile("" ::"v"(code_probe));  // the warm-up loads complete here
