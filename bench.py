@@ -38,9 +38,10 @@ cores, warmup 1, median of 3.
 Workload kimi-latent: the whole latent MoE block of a Kimi K3 TP8 rank
 (kimi.py:317-328: latent_down and the shared experts' gate/up, the MoE step on
 the 3584-wide latent with 896 experts top-16 and I=384, then the RMS norm,
-latent_up and shared_down; bf16 weights outside the experts), its three kernels
-timed separately with events between them; CPU baseline: the restatement of the
-block (oracle/latent_ref.py).
+latent_up and shared_down; bf16 weights outside the experts), timed as two calls
+with events between them: latent_down, the shared gate/up and the MoE step in one
+call (k3moe.latent_moe_step: one launch at one token, two launches otherwise),
+then latent_out; CPU baseline: the restatement of the block (oracle/latent_ref.py).
 
 Workload kimi-moe: the MoE step alone on that rank (its latent as the experts' input).
 
@@ -342,8 +343,8 @@ LATENT_ROWS = {1: None, 8: None, 64: [0, 21, 42, 63]}
 
 
 def measure_latent(cfg, *, seed, steps, warmup, cold, device):
-    """Time the latent block (latent_in, moe_step on the latent, latent_out) with events between
-    its three launches; returns per-stage and whole-block ms per run."""
+    """Time the latent block (latent_in and moe_step on the latent in one call, then latent_out) with
+    events between the two calls; returns per-stage and whole-block ms per run."""
     import torch
     import k3moe
     from k3moe import synthetic, traffic
@@ -356,11 +357,10 @@ def measure_latent(cfg, *, seed, steps, warmup, cold, device):
     distinct = int(r['expert_ids'].unique().numel())
     lat, sh, out = r['latent'], r['shared_h'], r['output']
     moe_out = {k: r[k] for k in ('expert_sum', 'expert_ids', 'route_weights')}
-    step = synthetic.step_args(dict(w, x=x))
+    # latent_in and the MoE step in one call (one launch at one token), then latent_out
     stages = [
-        ('latent_in', lambda: k3moe.latent_in(x, w['latent_down'], w['shared_gate'], w['shared_up'],
-                                              out={'latent': lat, 'shared_h': sh})),
-        ('moe_step', lambda: k3moe.moe_step(*step, **kw, latent=lat, out=moe_out)),
+        ('latent_in+moe_step', lambda: k3moe.latent_moe_step(x, w, **kw, out={'latent': lat, 'shared_h': sh,
+                                                                            **moe_out})),
         ('latent_out', lambda: k3moe.latent_out(moe_out['expert_sum'], w['latent_norm'], w['latent_up'], sh,
                                                 w['shared_down'], out=out)),
     ]
@@ -387,9 +387,8 @@ def measure_latent(cfg, *, seed, steps, warmup, cold, device):
              **{k: v.cpu() for k, v in moe_out.items()}}
     same = torch.equal(out, k3moe.latent_block(x, w, **kw)['output'])
     B, h, lh, S = cfg.tokens, cfg.hidden, cfg.latent, KIMI_SHARED
-    nbytes = {'latent_in': traffic.latent_in_bytes(B=B, h=h, lh=lh, S=S),
-              'moe_step': traffic.step_bytes(B=B, E=cfg.experts, k=cfg.topk, h=h, I=cfg.inter, distinct=distinct,
-                                             K=lh),
+    nbytes = {'latent_in+moe_step': traffic.latent_in_bytes(B=B, h=h, lh=lh, S=S)
+              + traffic.step_bytes(B=B, E=cfg.experts, k=cfg.topk, h=h, I=cfg.inter, distinct=distinct, K=lh),
               'latent_out': traffic.latent_out_bytes(B=B, h=h, lh=lh, S=S)}
     host = host_view(w)
     del flush

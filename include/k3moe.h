@@ -282,6 +282,33 @@ int k3moe_latent_out(const k3moe_latent_dims *dims, const float *expert_sum, con
                      const void *latent_up, const void *shared_h, const void *shared_down, void *out,
                      void *workspace, size_t workspace_bytes, void *stream);
 
+/* The block's input projections and its routed MoE step in one call
+ * (kimi.py:317 and the inner part of 326-327, then 307-324 on the latent):
+ * k3moe_latent_in's outputs and k3moe_moe_step's, the step taking the latent
+ * it computes as its expert input (`latent`, written here). `dims` is the
+ * step's geometry (dims->latent = lh, dims->activation also the shared
+ * experts'); `shared` is S. With one token and the single-token kernel's
+ * geometry (and at most 48 latent and shared rows per workgroup: lh/2 + S
+ * <= 24 x the CU count) both run in one launch: every workgroup streams its
+ * share of the projections' weights while the routing goes on, and the
+ * gate/up products wait for the latent through tagged slots. Otherwise the
+ * two run as k3moe_latent_in and k3moe_moe_step launches. The workspace must
+ * hold both k3moe_workspace_bytes(dims) and k3moe_latent_workspace_bytes of
+ * the block's dims. Arguments, outputs, numerics and errors as those two
+ * entry points'. */
+int k3moe_latent_moe_step(const k3moe_dims *dims, int32_t shared,
+                          const void *x, const void *latent_down,
+                          const void *shared_gate, const void *shared_up,
+                          void *latent, void *shared_h,
+                          const void *router, const float *router_bias,
+                          const uint8_t *gate_blocks, const uint8_t *gate_scales,
+                          const uint8_t *up_blocks, const uint8_t *up_scales,
+                          const uint8_t *down_blocks, const uint8_t *down_scales,
+                          const int64_t *routes,
+                          float *expert_sum, int64_t *expert_ids, float *route_weights,
+                          float *shortfall,
+                          void *workspace, size_t workspace_bytes, void *stream);
+
 /* MXFP4 decode, unpack_mxfp4 (megabench/tasks/quantization.py:40-51) plus the
  * `.to(act)` cast of kimi.py:321: n_blocks blocks of 16 bytes and n_blocks
  * scales -> n_blocks*32 values of out_dtype (K3MOE_DTYPE_F32 or _BF16),

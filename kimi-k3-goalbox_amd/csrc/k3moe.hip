@@ -395,6 +395,22 @@ int k3moe_workspace_status(const void *workspace, int32_t *status, void *stream)
   return K3MOE_OK;
 }
 
+// The latent block's input projections for k3moe_latent_moe_step's one-launch
+// path: the single-token kernel computes latent (into `latent`) and shared_h.
+struct LatInArgs {
+  int S;
+  const void *latent_down, *shared_gate, *shared_up;
+  void *latent, *shared_h;
+};
+constexpr int kNotFused = -1000;  // moe_step_impl: the plan has no one-launch latent path
+
+static int moe_step_impl(const k3moe_dims *dims, const void *x, const void *latent, const void *router,
+                         const float *router_bias, const uint8_t *gate_blocks, const uint8_t *gate_scales,
+                         const uint8_t *up_blocks, const uint8_t *up_scales, const uint8_t *down_blocks,
+                         const uint8_t *down_scales, const int64_t *routes, float *expert_sum, int64_t *expert_ids,
+                         float *route_weights, float *shortfall, void *workspace, size_t workspace_bytes,
+                         void *stream, const LatInArgs *lat);
+
 int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, const void *router,
                    const float *router_bias, const uint8_t *gate_blocks, const uint8_t *gate_scales,
                    const uint8_t *up_blocks, const uint8_t *up_scales, const uint8_t *down_blocks,
@@ -402,6 +418,43 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
                    float *route_weights, float *shortfall, void *workspace, size_t workspace_bytes,
                    void *stream) {
   g_err[0] = 0;
+  return moe_step_impl(dims, x, latent, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales,
+                       down_blocks, down_scales, routes, expert_sum, expert_ids, route_weights, shortfall, workspace,
+                       workspace_bytes, stream, nullptr);
+}
+
+int k3moe_latent_moe_step(const k3moe_dims *dims, int32_t shared, const void *x, const void *latent_down,
+                          const void *shared_gate, const void *shared_up, void *latent, void *shared_h,
+                          const void *router, const float *router_bias, const uint8_t *gate_blocks,
+                          const uint8_t *gate_scales, const uint8_t *up_blocks, const uint8_t *up_scales,
+                          const uint8_t *down_blocks, const uint8_t *down_scales, const int64_t *routes,
+                          float *expert_sum, int64_t *expert_ids, float *route_weights, float *shortfall,
+                          void *workspace, size_t workspace_bytes, void *stream) {
+  g_err[0] = 0;
+  if (!latent_down || !shared_gate || !shared_up || !latent || !shared_h)
+    return fail(K3MOE_EINVAL, "a required pointer is NULL");
+  if (!dims) return fail(K3MOE_EINVAL, "dims is NULL");
+  const LatInArgs lat{shared, latent_down, shared_gate, shared_up, latent, shared_h};
+  int rc = moe_step_impl(dims, x, latent, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales,
+                         down_blocks, down_scales, routes, expert_sum, expert_ids, route_weights, shortfall,
+                         workspace, workspace_bytes, stream, &lat);
+  if (rc != kNotFused) return rc;
+  // two launches: the input projections, then the step on their latent
+  const k3moe_latent_dims ld{dims->tokens, dims->hidden, dims->latent, shared, dims->activation};
+  if ((rc = k3moe_latent_in(&ld, x, latent_down, shared_gate, shared_up, latent, shared_h, workspace,
+                            workspace_bytes, stream)))
+    return rc;
+  return k3moe_moe_step(dims, x, latent, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales,
+                        down_blocks, down_scales, routes, expert_sum, expert_ids, route_weights, shortfall,
+                        workspace, workspace_bytes, stream);
+}
+
+static int moe_step_impl(const k3moe_dims *dims, const void *x, const void *latent, const void *router,
+                         const float *router_bias, const uint8_t *gate_blocks, const uint8_t *gate_scales,
+                         const uint8_t *up_blocks, const uint8_t *up_scales, const uint8_t *down_blocks,
+                         const uint8_t *down_scales, const int64_t *routes, float *expert_sum, int64_t *expert_ids,
+                         float *route_weights, float *shortfall, void *workspace, size_t workspace_bytes,
+                         void *stream, const LatInArgs *lat) {
   int rc = check_dims(dims);
   if (rc) return rc;
   if (!x || !router || !gate_blocks || !gate_scales || !up_blocks || !up_scales || !down_blocks ||
@@ -413,6 +466,7 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
   Plan p;
   make_plan(*dims, device_cus(), p, trace_enabled());
   p.stall = g_stall.load(std::memory_order_relaxed);
+  if (lat && !lat_in_plan(p, lat->S)) return kNotFused;
   if (dims->path == K3MOE_PATH_DECODE && p.path != kPathDecode)
     return fail(K3MOE_EINVAL, "the persistent decode path needs tokens <= %d and tokens*topk <= %d", kDecMaxTokens,
                 kDecMaxPairs);
@@ -431,7 +485,7 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
   const uint16_t *xin = reinterpret_cast<const uint16_t *>(latent ? latent : x);
 
   if (p.path == kPathDecode) {
-    DecodeArgs a;
+    DecodeArgs a{};
     a.x = reinterpret_cast<const uint16_t *>(x);
     a.xin = xin;
     a.router = reinterpret_cast<const uint16_t *>(router);
@@ -445,6 +499,13 @@ int k3moe_moe_step(const k3moe_dims *dims, const void *x, const void *latent, co
     a.out_w = route_weights;
     a.out_short = shortfall;
     a.ws = ws;
+    if (p.lat_in) {  // the kernel computes the latent into `latent` (the expert input) and shared_h
+      a.lat_ld = reinterpret_cast<const uint16_t *>(lat->latent_down);
+      a.lat_sg = reinterpret_cast<const uint16_t *>(lat->shared_gate);
+      a.lat_su = reinterpret_cast<const uint16_t *>(lat->shared_up);
+      a.lat_sh = reinterpret_cast<uint16_t *>(lat->shared_h);
+      a.xin = reinterpret_cast<const uint16_t *>(lat->latent);
+    }
     if (p.single) {
       // instantiations: chosen experts per wave in the down phase (1: k <= 8, 2: k <= 16) and
       // the down projection's k-steps (2: I <= 256, 4: I <= 512)

@@ -57,6 +57,11 @@ struct DecodeArgs {
   float *out_w;
   float *out_short;
   char *ws;
+  // the single-token kernel's latent block inputs (Plan::lat_in): latent_down
+  // [K, h], shared_gate / shared_up [S, h] (bf16) and shared_h [S] (bf16 out);
+  // the latent itself goes to xin
+  const uint16_t *lat_ld, *lat_sg, *lat_su;
+  uint16_t *lat_sh;
 };
 
 // The memory pipeline serves older waves first, so in a stream split evenly
@@ -1074,8 +1079,12 @@ __device__ __forceinline__ DecodeArgs load_args(uint64_t at) {
   K3_FIELD(out_w);
   K3_FIELD(out_short);
   K3_FIELD(ws);
+  K3_FIELD(lat_ld);
+  K3_FIELD(lat_sg);
+  K3_FIELD(lat_su);
+  K3_FIELD(lat_sh);
 #undef K3_FIELD
-  static_assert(sizeof(DecodeArgs) == 16 * sizeof(void *), "every field read");
+  static_assert(sizeof(DecodeArgs) == 20 * sizeof(void *), "every field read");
   return a;
 }
 

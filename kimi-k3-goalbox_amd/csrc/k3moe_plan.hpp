@@ -126,6 +126,8 @@ struct Plan {
   int redundant;  // 1: every workgroup routes every token (no barrier before grouping)
   int xgemm;      // general path: 1 = grouped-GEMM expert kernels, 0 = per-16-token streams
   int fgemm;      // grouped GEMMs on the scaled FP4 MFMA with two-term E4M3 activations (k3moe_fgemm.hpp)
+  int lat_in;     // single-token kernel: 1 = it also computes the latent block's inputs (latent, shared_h)
+  int lat_S;      // ... the shared experts' width S
   // workspace byte offsets
   size_t o_ctl, o_zero, o_logit, o_ids, o_w, o_nact, o_active, o_aoff, o_acnt, o_ptok, o_pw, o_pof, o_gpart, o_gcnt,
       o_gchunk, o_h, o_y, o_xq, o_hq, o_trace, total;
@@ -210,6 +212,7 @@ inline int decode_lds(Plan &p) {
 // words), the staged row (2 K bytes), fixed scratch, the top-k's, the chosen
 // experts' h (2 k I bytes) and the down products (2 row tiles x k x 16 fp32).
 constexpr int kSingleMaxSS = 2;  // gate/up super-steps of 512 columns per wave: ceil(K / 4096)
+constexpr int kSingleMaxK = kSingleMaxSS * 8 * 512;  // 8192: the expert width K
 constexpr int kSingleMaxTopk = 16;
 constexpr int kSingleRouterRows = 4;  // router rows (experts) per workgroup: E <= 4 G
 constexpr int kSingleSlots = 4;  // gate/up register slots per wave: units of the workgroup x super-steps per wave
@@ -225,6 +228,24 @@ inline void single_plan(const k3moe_dims &d, Plan &p) {
              p.I % 32 == 0 && p.h % 128 == 0 && p.h <= 16 * kDecThreads && p.E <= kSingleRouterRows * p.G &&
              p.RTd <= 2 * p.G &&
              cdiv(p.k * (p.I / 8), p.G) * (p.K / 512 > kDecWaves ? 2 : 1) <= kSingleSlots && tags_fit;
+}
+
+// The single-token kernel with the latent block's inputs (latent and shared_h
+// of the token, the projections of kimi.py:317 and 326): workgroup b computes
+// latent row pairs b, b + G, .. and shared pairs (gate and up row) b, b + G, ..
+// of width h, at most kLatRowsMax rows in all, and publishes the latent in
+// tagged slots (one per row pair, after the logits and the h slots) that every
+// workgroup polls before its gate/up products. Returns whether it applies to a
+// single-token plan with shared width S.
+constexpr int kLatRowsMax = 48;  // rows (latent rows + shared gate and up rows) per workgroup
+inline int lat_rows_max(const Plan &p, int S) { return 2 * cdiv(p.K / 2, p.G) + 2 * cdiv(S, p.G); }
+__host__ __device__ inline uint32_t lat_slot_base(const Plan &p) { return (uint32_t)(kTagCopies * p.E * 8 + p.k * (p.I / 2) * 8); }
+inline bool lat_in_plan(Plan &p, int S) {
+  const bool ok = p.single && S > 0 && lat_rows_max(p, S) <= kLatRowsMax &&
+                  (long)lat_slot_base(p) + (long)(p.K / 2) * 8 <= kTagBytes;
+  p.lat_in = ok ? 1 : 0;
+  p.lat_S = ok ? S : 0;
+  return ok;
 }
 
 // n_cus: compute units of the device (the persistent grid size); trace: reserve
@@ -326,6 +347,8 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   p.o_y = take((general || p.I == 256 || p.I == 384 || p.I == 512) ? (size_t)p.P * p.K * 2 : 0);
   p.trace = trace && p.path == kPathDecode;
   p.stall = 0;
+  p.lat_in = 0;
+  p.lat_S = 0;
   single_plan(d, p);
   if (p.single) {
     p.path = kPathDecode;

@@ -127,10 +127,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   // the token's expert-input row (two 16-byte chunks per thread), the gating
   // bias of experts tid and tid + 512: both needed later, loaded now
   u32x4 xpre[2] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
+  if (!pl.lat_in) {  // (with the latent block's inputs, the kernel computes the row itself)
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const int c = hh * kDecThreads + tid;
-    if (c < K / 8) xpre[hh] = load16(a.xin + c * 8);
+    for (int hh = 0; hh < 2; ++hh) {
+      const int c = hh * kDecThreads + tid;
+      if (c < K / 8) xpre[hh] = load16(a.xin + c * 8);
+    }
   }
   float bias_pre[2] = {0.f, 0.f};
   if (a.bias) {
@@ -177,9 +179,54 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   // its bf16 products in FP32, the wave sums its lanes (a fixed DPP tree) and
   // the waves meet in LDS, summed in wave order; each logit goes to its tagged
   // slot in every copy.
+  // wave w's share of h (16-byte chunks hc0 .. hc1 - 1; lane l takes hc0 + l
+  // and hc0 + l + 64) and its chunks of x, kept for the latent block's inputs
+  const int hc0 = (pl.h / 8) * w / kDecWaves, hc1 = (pl.h / 8) * (w + 1) / kDecWaves;
+  u32x4 xv[2];
+  // The latent block's input rows (Plan::lat_in; used in phase L below): this
+  // workgroup's rows, their two first batches issued with the router's loads
+  constexpr int RB = 4;
+  const int G = (int)gridDim.x, b = (int)blockIdx.x, h = pl.h, S = pl.lat_S;
+  const int nlp = K / 2 > b ? (K / 2 - b + G - 1) / G : 0, ns = S > b ? (S - b + G - 1) / G : 0;
+  const int n = 2 * (nlp + ns), nb = (n + RB - 1) / RB;
+  float *lred = sh.gred;  // [8 waves][kLatRowsMax]: the waves' partial sums (gate/up's area, free until then)
+  auto row_ptr = [&](int r) -> const uint16_t * {
+    if (r < 2 * nlp) return a.lat_ld + ((size_t)2 * (b + G * (r >> 1)) + (r & 1)) * h;
+    const int rs = r - 2 * nlp;
+    return ((rs & 1) ? a.lat_su : a.lat_sg) + (size_t)(b + G * (rs >> 1)) * h;
+  };
+  auto issue = [&](int bi, u32x4 (&buf)[RB][2]) {
+#pragma unroll
+    for (int rr = 0; rr < RB; ++rr) {
+      const int r = bi * RB + rr;
+      const uint16_t *row = r < n ? row_ptr(r) : nullptr;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int c = hc0 + l + 64 * m;
+        buf[rr][m] = load16((row && c < hc1) ? reinterpret_cast<const uint8_t *>(row + c * 8) : zero);
+      }
+    }
+  };
+  auto compute = [&](int bi, const u32x4 (&buf)[RB][2]) {
+#pragma unroll
+    for (int rr = 0; rr < RB; ++rr) {
+      float p = 0.f;
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t av = buf[rr][m][d], bv = xv[m][d];
+          p = fmaf(bf16_bits_to_f32(av & 0xFFFFu), bf16_bits_to_f32(bv & 0xFFFFu), p);
+          p = fmaf(bf16_bits_to_f32(av >> 16), bf16_bits_to_f32(bv >> 16), p);
+        }
+      p = wave_sum_f32(p);
+      if (l == 0 && bi * RB + rr < n) lred[w * kLatRowsMax + bi * RB + rr] = p;
+    }
+  };
+  u32x4 ba[RB][2], bb[RB][2];
   {
-    const int KC = pl.h / 8, c0 = KC * w / kDecWaves, c1 = KC * (w + 1) / kDecWaves;
-    u32x4 rv[kSingleRouterRows][2], xv[2];
+    const int c0 = hc0, c1 = hc1;
+    u32x4 rv[kSingleRouterRows][2];
 #pragma unroll
     for (int r = 0; r < kSingleRouterRows; ++r) {
       const int e = (int)blockIdx.x + r * (int)gridDim.x;
@@ -193,6 +240,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     for (int m = 0; m < 2; ++m) {
       const int c = c0 + l + 64 * m;
       xv[m] = c < c1 ? load16(a.x + c * 8) : u32x4{0, 0, 0, 0};
+    }
+    if (pl.lat_in) {
+      issue(0, ba);
+      issue(1, bb);
     }
     warm_code();
     make_tag();
@@ -228,14 +279,63 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   make_tag();
   trace_mark(pl, a.ws, 1);
   // the staged row for gate/up (its loads have long arrived)
+  if (!pl.lat_in) {
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const int c = hh * kDecThreads + tid;
-    if (c < K / 8) *reinterpret_cast<u32x4 *>(xs + c * 8) = xpre[hh];
+    for (int hh = 0; hh < 2; ++hh) {
+      const int c = hh * kDecThreads + tid;
+      if (c < K / 8) *reinterpret_cast<u32x4 *>(xs + c * 8) = xpre[hh];
+    }
   }
   __syncthreads();  // s_tag, s_abort0, the staged row
   asm volatile("" ::"v"(code_probe));
   const uint32_t tag = s_tag, abort0 = s_abort0;
+  const uint32_t lat_base = lat_slot_base(pl);  // the latent's row-pair slots, [K / 2]
+
+  // ------------------------------------------------ L: latent block inputs --
+  // With Plan::lat_in (kimi.py:317, 326): latent = bf16(x @ latent_down.T)
+  // and shared_h = bf16(act(bf16(x @ shared_gate.T), bf16(x @ shared_up.T))).
+  // Workgroup b takes latent row pairs b, b + G, .. and shared pairs b, b + G,
+  // ..; its waves take the router's shares of h (x already in registers), in
+  // batches of 4 rows with two batches in flight (rows past the workgroup's
+  // read the zero area, so every batch is 8 loads a lane and the waits are
+  // exact); each lane's 16 products are summed in FP32 (exact products, fused
+  // adds), the wave's lanes by the DPP tree and the waves in order in LDS. The
+  // latent goes to xin and, as bf16 pairs, to tagged slots that every
+  // workgroup polls before its gate/up products; shared_h goes to lat_sh.
+  if (pl.lat_in) {
+    for (int bi = 0; bi < nb; bi += 2) {  // batches past nb read the zero area
+      wait_vm<2 * RB>();
+      compute(bi, ba);
+      issue(bi + 2, ba);
+      wait_vm<2 * RB>();
+      compute(bi + 1, bb);
+      issue(bi + 3, bb);
+    }
+    wait_vm<0>();
+    __syncthreads();
+    if (tid < nlp) {  // latent rows 2 jp, 2 jp + 1
+      const int jp = b + G * tid;
+      float v0 = lred[2 * tid], v1 = lred[2 * tid + 1];
+#pragma unroll
+      for (int ww = 1; ww < kDecWaves; ++ww) {
+        v0 = __fadd_rn(v0, lred[ww * kLatRowsMax + 2 * tid]);
+        v1 = __fadd_rn(v1, lred[ww * kLatRowsMax + 2 * tid + 1]);
+      }
+      const uint32_t pair = (uint32_t)f32_to_bf16_bits(v0) | ((uint32_t)f32_to_bf16_bits(v1) << 16);
+      *reinterpret_cast<uint32_t *>(const_cast<uint16_t *>(a.xin) + 2 * jp) = pair;
+      st_dev64(tagr, lat_base + (uint32_t)jp * 8, u32x2{pair, tag});
+    } else if (tid >= 64 && tid < 64 + ns) {  // shared gate and up rows of pair s
+      const int j = tid - 64, r = 2 * nlp + 2 * j, sj = b + G * j;
+      float g = lred[r], u = lred[r + 1];
+#pragma unroll
+      for (int ww = 1; ww < kDecWaves; ++ww) {
+        g = __fadd_rn(g, lred[ww * kLatRowsMax + r]);
+        u = __fadd_rn(u, lred[ww * kLatRowsMax + r + 1]);
+      }
+      a.lat_sh[sj] = (uint16_t)f32_to_bf16_bits(apply_act(pl.act, round_bf16(g), round_bf16(u)));
+    }
+    trace_mark(pl, a.ws, 16);
+  }
 
   // -------------------------------------------------------- T: top-k/gating --
   {
@@ -390,6 +490,46 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
         }
       }
     }
+  }
+
+  if (pl.lat_in) {
+    // the latent row (the experts' input) from every workgroup's tagged row-pair
+    // slots (thread tid: pairs tid + 512 m), polled until each carries this
+    // launch's tag; its first check waits for this wave's gate/up loads too
+    // (issued before it), which are needed next anyway
+    const int lp = K / 2;
+    u32x2 v[kSingleMaxK / 1024];
+    bool ok = true;
+    unsigned spins = 0;
+    for (;;) {
+      bool ready = true;
+#pragma unroll
+      for (int m = 0; m < kSingleMaxK / 1024; ++m) {
+        const int c = tid + kDecThreads * m;
+        v[m] = c < lp ? bload8_dev(tagr, lat_base + (uint32_t)c * 8) : u32x2{0u, tag};
+        ready = ready && v[m][1] == tag;
+      }
+      if (__ballot(!ready) == 0) break;
+      ++spins;
+      if ((spins & 63u) == 0u && aborted(ctl, abort0)) {
+        ok = false;
+        break;
+      }
+      if (spins > kSpinLimit) {
+        if (l == 0) raise_timeout(ctl);
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int m = 0; m < kSingleMaxK / 1024; ++m) {
+      const int c = tid + kDecThreads * m;
+      if (c < lp) *reinterpret_cast<uint32_t *>(xs + 2 * c) = v[m][0];
+    }
+    if (!ok) s_fail = 1;
+    __syncthreads();
+    if (s_fail) return leave(true);
   }
 
   // ----------------------------------------------------------- GU compute --

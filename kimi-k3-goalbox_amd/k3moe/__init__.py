@@ -18,7 +18,7 @@ include/k3moe.h). There is no CPU fallback.
 from .moe import (moe_layer, moe_step, mxfp4_decode, new_workspace, pack_mxfp4, prepare_step,  # noqa: F401
                   workspace_bytes, workspace_layout, workspace_status)
 from .configs import ALL as CONFIGS, MoEConfig  # noqa: F401
-from .latent import latent_block, latent_in, latent_moe_layer, latent_out  # noqa: F401
+from .latent import latent_block, latent_in, latent_moe_layer, latent_moe_step, latent_out  # noqa: F401
 
 __all__ = ['moe_step', 'prepare_step', 'moe_layer', 'mxfp4_decode', 'pack_mxfp4', 'workspace_bytes', 'latent_in', 'latent_out', 'latent_block',
-           'latent_moe_layer', 'CONFIGS', 'MoEConfig']
+           'latent_moe_layer', 'latent_moe_step', 'CONFIGS', 'MoEConfig']

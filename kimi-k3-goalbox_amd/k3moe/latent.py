@@ -21,7 +21,7 @@ import torch
 
 from . import _native
 from ._native import ACTIVATION, LatentDims, check
-from .moe import _dev_ptr, _expect, cached_workspace, moe_step
+from .moe import _dev_ptr, _expect, cached_workspace, dims_for, prepare_step, workspace_bytes
 
 
 def latent_dims(tokens: int, hidden: int, latent: int, shared: int, activation: str = 'situ') -> LatentDims:
@@ -121,6 +121,49 @@ def latent_out(expert_sum: torch.Tensor, latent_norm: torch.Tensor, latent_up: t
     return out
 
 
+def latent_moe_step(normalized: torch.Tensor, w: dict, *, topk: int, gating: str = 'sigmoid_bias',
+                    activation: str = 'situ', routes: torch.Tensor | None = None,
+                    path: str = 'auto', out: dict | None = None) -> tuple[torch.Tensor, torch.Tensor, dict]:
+    """latent_in and moe_step on its latent in one call (k3moe_latent_moe_step): one launch for a
+    single token on the single-token kernel's geometry, else the two launches. Returns
+    (latent, shared_h, moe_step's dict); `w` as latent_block's. `out` may hold preallocated
+    'latent', 'shared_h' and moe_step output tensors."""
+    out = dict(out or {})
+    device = _device_of(normalized)
+    B, h = normalized.shape
+    lh, S = w['latent_down'].shape[0], w['shared_gate'].shape[0]
+    _expect(normalized, 'normalized', torch.bfloat16, (B, h), device)
+    _expect(w['latent_down'], 'latent_down', torch.bfloat16, (lh, h), device)
+    _expect(w['shared_gate'], 'shared_gate', torch.bfloat16, (S, h), device)
+    _expect(w['shared_up'], 'shared_up', torch.bfloat16, (S, h), device)
+    with torch.cuda.device(device):
+        latent = out.get('latent')
+        if latent is None:
+            latent = torch.empty(B, lh, dtype=torch.bfloat16, device=device)
+        shared_h = out.get('shared_h')
+        if shared_h is None:
+            shared_h = torch.empty(B, S, dtype=torch.bfloat16, device=device)
+    _expect(latent, 'latent', torch.bfloat16, (B, lh), device)
+    _expect(shared_h, 'shared_h', torch.bfloat16, (B, S), device)
+    # one workspace for both halves (the two-launch fallback runs latent_in on it too)
+    mdims = dims_for(normalized, w['router'], w['gate_blocks'], w['down_blocks'], topk, gating, activation, latent,
+                     path)
+    ws = cached_workspace(max(workspace_bytes(mdims), latent_workspace_bytes(latent_dims(B, h, lh, S, activation))),
+                          device)
+    step = prepare_step(normalized, w['router'], w.get('router_bias'), w['gate_blocks'], w['gate_scales'],
+                        w['up_blocks'], w['up_scales'], w['down_blocks'], w['down_scales'], topk=topk,
+                        gating=gating, activation=activation, routes=routes, latent=latent, path=path, workspace=ws,
+                        out=out)
+    a = step._args  # (dims, x, latent, router .. shortfall, workspace, workspace bytes)
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        check(_native.load().k3moe_latent_moe_step(
+            a[0], ctypes.c_int32(S), a[1], _dev_ptr(w['latent_down']), _dev_ptr(w['shared_gate']),
+            _dev_ptr(w['shared_up']), _dev_ptr(latent), _dev_ptr(shared_h), *a[3:16], _dev_ptr(ws),
+            ctypes.c_size_t(ws.numel()), ctypes.c_void_p(stream)), 'k3moe_latent_moe_step')
+    return latent, shared_h, step.result
+
+
 def latent_block(normalized: torch.Tensor, w: dict, *, topk: int, gating: str = 'sigmoid_bias',
                  activation: str = 'situ', fp32: bool = False, routes: torch.Tensor | None = None,
                  path: str = 'auto') -> dict:
@@ -135,11 +178,8 @@ def latent_block(normalized: torch.Tensor, w: dict, *, topk: int, gating: str = 
     if fp32:
         raise NotImplementedError('fp32=True is the FP32 truth mode of the CPU oracle; '
                                   'the GPU block computes the BF16 serving path (fp32=False)')
-    latent, shared_h = latent_in(normalized, w['latent_down'], w['shared_gate'], w['shared_up'],
-                                 activation=activation)
-    moe = moe_step(normalized, w['router'], w.get('router_bias'), w['gate_blocks'], w['gate_scales'],
-                   w['up_blocks'], w['up_scales'], w['down_blocks'], w['down_scales'], topk=topk,
-                   gating=gating, activation=activation, routes=routes, latent=latent, path=path)
+    latent, shared_h, moe = latent_moe_step(normalized, w, topk=topk, gating=gating, activation=activation,
+                                            routes=routes, path=path)
     output = latent_out(moe['expert_sum'], w['latent_norm'], w['latent_up'], shared_h, w['shared_down'])
     return {'output': output, 'latent': latent, 'shared_h': shared_h, **moe}
 

@@ -222,6 +222,50 @@ def run_block(cfg, shared, seed, shared_fan=None, routes=None, w=None):
         say(f'  {name}: {detail}')
 
 
+@pytest.mark.parametrize('cfg,shared,forced', [
+    (MoEConfig('kimi-rank-e128-b1', 128, 16, 7168, 384, 1, latent=3584), 768, False),   # one launch
+    (MoEConfig('kimi-rank-e128-b1', 128, 16, 7168, 384, 1, latent=3584), 768, True),
+    (MoEConfig('latent-one', 64, 8, 1024, 256, 1, latent=512), 256, False),             # one launch, small
+    (MoEConfig('latent-wide-shared', 64, 8, 1024, 256, 1, latent=512), 6400, False),    # 52 rows: two launches
+    (MoEConfig('latent-b3', 64, 8, 1024, 256, 3, latent=512), 256, False),              # two launches
+])
+def test_latent_moe_step_matches_separate_launches(cfg, shared, forced):
+    """k3moe.latent_moe_step (one launch for one token on the single-token kernel, else latent_in then
+    moe_step) against latent_in and moe_step called separately: the same expert sets, latent and
+    shared_h within a rounding step (mostly equal: the one-launch sums run in another order), the
+    expert sums within the step's band of the oracle."""
+    say(f'latent_moe_step {cfg.name} shared={shared} forced={forced}')
+    dev = torch.device('cuda:0')
+    w = block_case(cfg, 5, shared)
+    g = {k: (v.to(dev) if v is not None else None) for k, v in w.items()}
+    routes = None
+    if forced:
+        gen = torch.Generator().manual_seed(3)
+        routes = torch.stack([torch.randperm(cfg.experts, generator=gen)[:cfg.topk] for _ in range(cfg.tokens)])
+    r_dev = None if routes is None else routes.to(dev)
+    before = grading.snapshot({k: v for k, v in g.items() if v is not None})
+    lat, sh, moe = k3moe.latent_moe_step(g['x'], g, topk=cfg.topk, routes=r_dev)
+    lat2, sh2 = k3moe.latent_in(g['x'], g['latent_down'], g['shared_gate'], g['shared_up'])
+    moe2 = k3moe.moe_step(g['x'], g['router'], g['router_bias'], g['gate_blocks'], g['gate_scales'], g['up_blocks'],
+                          g['up_scales'], g['down_blocks'], g['down_scales'], topk=cfg.topk, latent=lat2, routes=r_dev)
+    torch.cuda.synchronize(dev)
+    grading.check_unchanged({k: v for k, v in g.items() if v is not None}, before)
+    assert torch.equal(moe['expert_ids'].cpu(), moe2['expert_ids'].cpu())
+    assert torch.equal(moe['route_weights'].cpu(), moe2['route_weights'].cpu())
+    if forced:
+        assert torch.equal(moe['route_shortfall'].cpu(), moe2['route_shortfall'].cpu())
+    near_oracle(lat, lat2.cpu(), 1)
+    near_oracle(sh, sh2.cpu(), 2)
+    oracle = latent_ref.latent_block(w['x'], w, topk=cfg.topk, routes=routes)
+    truth = latent_ref.latent_block(w['x'], w, topk=cfg.topk, fp32=True, routes=oracle['expert_ids'])
+    for name, got in (('latent', lat), ('shared_h', sh), ('expert_sum', moe['expert_sum'])):
+        detail = grading.band_check(got.cpu(), oracle[name], truth[name], truth[name], name=name)
+        say(f'  {name}: {detail}')
+    ws = k3moe.moe.get_workspace(k3moe.moe.dims_for(g['x'], g['router'], g['gate_blocks'], g['down_blocks'],
+                                                    cfg.topk, 'sigmoid_bias', 'situ', lat), dev)
+    assert k3moe.workspace_status(ws) == 0
+
+
 def test_latent_moe_layer_reads_reference_keys():
     cfg = MoEConfig('latent-small', 64, 8, 1024, 256, 4, latent=512)
     say(f'latent_moe_layer {cfg.name}')
