@@ -699,7 +699,7 @@ template <bool AL>
 __device__ __forceinline__ void gu_pinned(const Plan &pl, const DecodeArgs &a, const int *g_act, const int *g_aoff,
                                           const int *g_acnt, const int *g_coff, const int *g_cexp, const int *g_ptok,
                                           uint16_t *xs, int *s_prog, uint16_t *hbuf, int ua, int ub, int wa, int wb,
-                                          bool staged) {
+                                          bool staged, bool coherent) {
   static_assert(AL, "pinned rows are loaded in whole 512-column chunks");
   const int w = wave_id(), l = threadIdx.x & 63, i = l & 15;
   const int KB = pl.K / kBlockK, NSS = KB / 16, U8 = pl.U8;
@@ -737,8 +737,10 @@ __device__ __forceinline__ void gu_pinned(const Plan &pl, const DecodeArgs &a, c
         ++rr;
       }
       const int j = c - want * per_row;
-      load_lds<16>(a.xin + (size_t)r * pl.K + j * 512 + l * 8,
-                   reinterpret_cast<char *>(xs + (size_t)r * pl.xpitch + j * 512));
+      const uint16_t *src = a.xin + (size_t)r * pl.K + j * 512 + l * 8;
+      char *dst = reinterpret_cast<char *>(xs + (size_t)r * pl.xpitch + j * 512);
+      if (coherent) load_lds<16, kCpolDevice>(src, dst);  // (written in this launch by other workgroups)
+      else load_lds<16>(src, dst);
     }
   }
   asm volatile("" ::: "memory");  // the row loads stay ahead of the weights
@@ -1055,6 +1057,113 @@ __device__ __forceinline__ void dn_issue(const Plan &pl, const DecodeArgs &a, co
                                          const int *g_acnt, int rt, int d, int c, int kc, int KB, DnLoad &L) {
   dn_issue_w(pl, a, zero, g_act, rt, d, kc, KB, L);
   dn_issue_h(pl, hbuf, zero, g_aoff, g_acnt, d, c, kc, KB, L);
+}
+
+// The latent block's input projections (kimi.py:317, 326) in the decode
+// kernel (Plan::lat_in, at most 8 tokens): latent = bf16(x @ latent_down.T)
+// into xin and shared_h = bf16(act(bf16(x @ shared_gate.T), bf16(x @ shared_up.T))).
+// The rows are latent_down's lh rows, then the shared pairs (gate s, up s) as
+// rows lh + 2 s, lh + 2 s + 1; the workgroups that route no token share them
+// out in whole pairs, workgroup j of the NW taking rows [2 U j / NW, 2 U (j + 1)
+// / NW) (U = (lh + 2 S) / 2; at most 32 rows, two 16-row MFMA tiles, rows past
+// the range reading the zero area). The tokens' rows of x go to LDS first
+// (after the reduction area, row pitch h + 8; direct-to-LDS loads); the 8
+// waves split h in 128-column steps (MFMA 16x16x32 bf16: the weights as the A
+// operand from global memory, four steps in flight, the tokens as the B
+// operand from LDS); the waves' tiles meet in LDS in wave order. The latent
+// goes out with device-coherent stores (read by every workgroup after the
+// latent barrier), shared_h with plain ones (read by the next kernel).
+__device__ __forceinline__ void dec_latent_rows(const Plan &pl, const DecodeArgs &a, char *lds, const uint8_t *zero,
+                                                int j, int NW) {
+  const int w = wave_id(), l = threadIdx.x & 63, i = l & 15, q = l >> 4, tid = threadIdx.x;
+  const int h = pl.h, lh = pl.K, B = pl.B, S = pl.lat_S, hp = h + 8;
+  float *red = reinterpret_cast<float *>(lds);
+  uint16_t *xs = reinterpret_cast<uint16_t *>(lds + pl.lds_red);  // [B][h + 8]
+  const int U = (lh + 2 * S) / 2;
+  const int r0 = 2 * (int)((long)U * j / NW), n = 2 * (int)((long)U * (j + 1) / NW) - r0;
+  auto row_ptr = [&](int r) -> const uint16_t * {  // row r of the projections (r < lh + 2 S)
+    if (r < lh) return a.lat_ld + (size_t)r * h;
+    const int s = (r - lh) >> 1;
+    return (((r - lh) & 1) ? a.lat_su : a.lat_sg) + (size_t)s * h;
+  };
+  const uint16_t *rowa = i < n ? row_ptr(r0 + i) : nullptr, *rowb = 16 + i < n ? row_ptr(r0 + 16 + i) : nullptr;
+  const int KS = h / 128, ka = KS * w / kDecWaves, kb = KS * (w + 1) / kDecWaves;
+  struct Step {
+    u32x4 wa[4], wb[4];
+  };
+  // step ks, MFMA kk: lane (i, q) holds columns 128 ks + 32 kk + 8 q .. + 7 of
+  // row i (weights) and of token i (x), so that one load instruction reads 64
+  // contiguous bytes of each of the 16 rows
+  auto issue = [&](int ks, Step &st) {  // steps past the wave's range read the zero area
+    const bool in = ks < kb;
+    const int off = ks * 128 + q * 8;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      st.wa[kk] = load16((in && rowa) ? reinterpret_cast<const uint8_t *>(rowa + off + kk * 32) : zero);
+      st.wb[kk] = load16((in && rowb) ? reinterpret_cast<const uint8_t *>(rowb + off + kk * 32) : zero);
+    }
+  };
+  Step s0, s1, s2, s3;
+  issue(ka, s0);
+  issue(ka + 1, s1);
+  issue(ka + 2, s2);
+  issue(ka + 3, s3);
+  // the tokens' rows of x into LDS (1 KiB of a row per instruction), after the first weight loads
+  const int per_row = h / 512;
+  for (int c = w; c < B * per_row; c += kDecWaves) {
+    const int t = c / per_row, jj = c - t * per_row;
+    load_lds<16>(a.x + (size_t)t * h + jj * 512 + l * 8, reinterpret_cast<char *>(xs + (size_t)t * hp + jj * 512));
+  }
+  wait_vm<0>();
+  __syncthreads();
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  auto compute = [&](int ks, const Step &st) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 xv = i < B ? *reinterpret_cast<const u32x4 *>(xs + (size_t)i * hp + ks * 128 + kk * 32 + q * 8)
+                             : u32x4{0u, 0u, 0u, 0u};
+      acc[0] = mfma16(as_bf16x8(st.wa[kk]), as_bf16x8(xv), acc[0]);
+      acc[1] = mfma16(as_bf16x8(st.wb[kk]), as_bf16x8(xv), acc[1]);
+    }
+  };
+  for (int ks = ka; ks < kb; ks += 4) {  // (the first four steps have landed with the rows of x)
+    wait_vm<24>();
+    compute(ks, s0);
+    issue(ks + 4, s0);
+    wait_vm<24>();
+    if (ks + 1 < kb) compute(ks + 1, s1);  // wave-uniform
+    issue(ks + 5, s1);
+    wait_vm<24>();
+    if (ks + 2 < kb) compute(ks + 2, s2);
+    issue(ks + 6, s2);
+    wait_vm<24>();
+    if (ks + 3 < kb) compute(ks + 3, s3);
+    issue(ks + 7, s3);
+  }
+  wait_vm<0>();
+#pragma unroll
+  for (int t = 0; t < 2; ++t) *reinterpret_cast<f32x4 *>(red + (t * kDecWaves + w) * 256 + l * 4) = acc[t];
+  __syncthreads();
+  if (tid < 256) {
+    // thread tid: tile tid >> 7, elements 2 p and 2 p + 1 of its 16x16 tile
+    // (p = tid & 127): rows 2 v, 2 v + 1 (a latent pair or a shared gate/up
+    // pair, the range being pair-aligned) of token column c
+    const int t = tid >> 7, idx = 2 * (tid & 127), ln = idx >> 2, v = idx & 3;
+    const int rr = t * 16 + 4 * (ln >> 4) + v, c = ln & 15;
+    if (rr < n && c < B) {
+      const float v0 = red_sum(red + t * kDecWaves * 256, idx), v1 = red_sum(red + t * kDecWaves * 256, idx + 1);
+      const int row = r0 + rr;
+      if (row < lh) {
+        const uint32_t pair = (uint32_t)f32_to_bf16_bits(v0) | ((uint32_t)f32_to_bf16_bits(v1) << 16);
+        st_dev32(make_rsrc(a.xin, (uint32_t)B * lh * 2), (uint32_t)((c * lh + row) * 2), pair);
+      } else {
+        a.lat_sh[(size_t)c * S + ((row - lh) >> 1)] =
+            (uint16_t)f32_to_bf16_bits(apply_act(pl.act, round_bf16(v0), round_bf16(v1)));
+      }
+    }
+  }
+  wait_vmem();  // the latent's stores have completed (the latent barrier publishes them)
+  __syncthreads();
 }
 
 static_assert(sizeof(Plan) % alignof(DecodeArgs) == 0, "DecodeArgs follows Plan in the argument segment");
@@ -1438,6 +1547,17 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     }
   }
   trace_mark(pl, a.ws, 3);
+  // The latent block's input projections (Plan::lat_in): the workgroups that
+  // routed no token compute them now (the routed pairs arrive meanwhile); every
+  // workgroup arrives at the latent barrier here and waits at it before its
+  // gate/up rows are loaded.
+  unsigned lat_bar = 0;
+  if (pl.lat_in) {
+    if ((int)blockIdx.x >= B) dec_latent_rows(pl, a, lds, zero, (int)blockIdx.x - B, (int)gridDim.x - B);
+    trace_mark(pl, a.ws, 16);
+    lat_bar = ++nbar;
+    if (tid == 0) barrier_arrive(ctl, bb, lat_bar, nullptr);
+  }
   // Pinned gate/up in a workgroup that routed no token: it would wait here
   // for the routed pairs with nothing to load, so it loads every token's row
   // into its pinned rows now (1 KiB of a row per instruction, spread over the
@@ -1446,7 +1566,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   // long before the pairs are published.
   bool rows_staged = false;
   if constexpr (AL) {
-    if (pl.pinned && !redundant && (int)blockIdx.x >= B) {
+    if (pl.pinned && !redundant && !pl.lat_in && (int)blockIdx.x >= B) {
       rows_staged = true;
       const int per_row = pl.K / 512;
       for (int c = w; c < B * per_row; c += kDecWaves) {
@@ -1601,6 +1721,13 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   const int D = s_nact;
   trace_mark(pl, a.ws, 5);
 
+  if (pl.lat_in) {  // every workgroup's latent rows are out (read with device-coherent loads)
+    if (tid == 0 && !barrier_wait(ctl, bb, lat_bar, nullptr, false)) s_fail = 1;
+    __syncthreads();
+    if (s_fail) return give_up();
+    trace_mark(pl, a.ws, 17);
+  }
+
   // ------------------------------------------------------------ GU: gate/up --
   // pinned: this wave's range of whole units (global wave gw of 8 G)
   const unsigned gw = blockIdx.x * kDecWaves + w;
@@ -1613,7 +1740,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   if constexpr (AL) {
     if (pl.pinned) {
       gu_pinned<AL>(pl, a, g_act, g_aoff, g_acnt, g_coff, g_cexp, g_ptok, xpin, s_prog, hbuf, pin_ua, pin_ub,
-                    wave_unit(blockIdx.x * kDecWaves), wave_unit((blockIdx.x + 1) * kDecWaves), rows_staged);
+                    wave_unit(blockIdx.x * kDecWaves), wave_unit((blockIdx.x + 1) * kDecWaves), rows_staged,
+                    pl.lat_in != 0);
       pinned_done = true;
     }
   }

@@ -230,21 +230,32 @@ inline void single_plan(const k3moe_dims &d, Plan &p) {
              cdiv(p.k * (p.I / 8), p.G) * (p.K / 512 > kDecWaves ? 2 : 1) <= kSingleSlots && tags_fit;
 }
 
-// The single-token kernel with the latent block's inputs (latent and shared_h
-// of the token, the projections of kimi.py:317 and 326): workgroup b computes
-// latent row pairs b, b + G, .. and shared pairs (gate and up row) b, b + G, ..
-// of width h, at most kLatRowsMax rows in all, and publishes the latent in
-// tagged slots (one per row pair, after the logits and the h slots) that every
-// workgroup polls before its gate/up products. Returns whether it applies to a
-// single-token plan with shared width S.
+// The persistent kernels with the latent block's inputs (latent and shared_h,
+// the projections of kimi.py:317 and 326). The single-token kernel: workgroup
+// b computes latent row pairs b, b + G, .. and shared pairs (gate and up row)
+// b, b + G, .. of width h, at most kLatRowsMax rows in all, and publishes the
+// latent in tagged slots (one per row pair, after the logits and the h slots)
+// that every workgroup polls before its gate/up products. Returns whether one
+// of the two kernels takes them for shared width S (setting lat_in, lat_S).
 constexpr int kLatRowsMax = 48;  // rows (latent rows + shared gate and up rows) per workgroup
 inline int lat_rows_max(const Plan &p, int S) { return 2 * cdiv(p.K / 2, p.G) + 2 * cdiv(S, p.G); }
 __host__ __device__ inline uint32_t lat_slot_base(const Plan &p) { return (uint32_t)(kTagCopies * p.E * 8 + p.k * (p.I / 2) * 8); }
+// The decode kernel takes them too with the pinned gate/up and at most 16
+// tokens (one MFMA token tile) whose rows of x fit in LDS after the reduction
+// area (row pitch h + 8; at most 8 tokens of h 7168): the G - B workgroups
+// that route no token share the rows out in whole pairs, at most 16 pairs
+// (two 16-row tiles) each.
 inline bool lat_in_plan(Plan &p, int S) {
-  const bool ok = p.single && S > 0 && lat_rows_max(p, S) <= kLatRowsMax &&
-                  (long)lat_slot_base(p) + (long)(p.K / 2) * 8 <= kTagBytes;
+  const bool single = p.single && S > 0 && lat_rows_max(p, S) <= kLatRowsMax &&
+                      (long)lat_slot_base(p) + (long)(p.K / 2) * 8 <= kTagBytes;
+  const long lds_x = (long)p.lds_red + (long)p.B * (p.h + 8) * 2;
+  const bool decode = !p.single && p.path == kPathDecode && p.pinned && !p.redundant && p.B <= 16 && S > 0 &&
+                      p.h % 512 == 0 && p.G > p.B && cdiv((p.K + 2 * S) / 2, p.G - p.B) <= 16 &&
+                      lds_x <= kDecMaxLds - kDecStaticLds;
+  const bool ok = single || decode;
   p.lat_in = ok ? 1 : 0;
   p.lat_S = ok ? S : 0;
+  if (ok && decode && lds_x > p.lds_total) p.lds_total = (int)lds_x;
   return ok;
 }
 

@@ -227,11 +227,15 @@ def run_block(cfg, shared, seed, shared_fan=None, routes=None, w=None):
     (MoEConfig('kimi-rank-e128-b1', 128, 16, 7168, 384, 1, latent=3584), 768, True),
     (MoEConfig('latent-one', 64, 8, 1024, 256, 1, latent=512), 256, False),             # one launch, small
     (MoEConfig('latent-wide-shared', 64, 8, 1024, 256, 1, latent=512), 6400, False),    # 52 rows: two launches
-    (MoEConfig('latent-b3', 64, 8, 1024, 256, 3, latent=512), 256, False),              # two launches
+    (MoEConfig('latent-b3', 64, 8, 1024, 256, 3, latent=512), 256, False),              # decode kernel
+    (MoEConfig('kimi-rank-e128-b8', 128, 16, 7168, 384, 8, latent=3584), 768, False),   # decode kernel
+    (MoEConfig('kimi-rank-e128-b8', 128, 16, 7168, 384, 8, latent=3584), 768, True),
+    (MoEConfig('latent-b40', 64, 8, 1024, 256, 40, latent=512), 256, False),            # two launches
 ])
 def test_latent_moe_step_matches_separate_launches(cfg, shared, forced):
-    """k3moe.latent_moe_step (one launch for one token on the single-token kernel, else latent_in then
-    moe_step) against latent_in and moe_step called separately: the same expert sets, latent and
+    """k3moe.latent_moe_step (one launch of the single-token or decode kernel where they take the
+    projections, else latent_in then moe_step) against latent_in and moe_step called separately:
+    the same expert sets, latent and
     shared_h within a rounding step (mostly equal: the one-launch sums run in another order), the
     expert sums within the step's band of the oracle."""
     say(f'latent_moe_step {cfg.name} shared={shared} forced={forced}')
