@@ -38,10 +38,10 @@ cores, warmup 1, median of 3.
 Workload kimi-latent: the whole latent MoE block of a Kimi K3 TP8 rank
 (kimi.py:317-328: latent_down and the shared experts' gate/up, the MoE step on
 the 3584-wide latent with 896 experts top-16 and I=384, then the RMS norm,
-latent_up and shared_down; bf16 weights outside the experts), timed as two calls
-with events between them: latent_down, the shared gate/up and the MoE step in one
-call (k3moe.latent_moe_step: one launch at one token, two launches otherwise),
-then latent_out; CPU baseline: the restatement of the block (oracle/latent_ref.py).
+latent_up and shared_down; bf16 weights outside the experts), timed as one
+k3moe.latent_block call (one launch at one token; the input projections with the
+MoE step and then latent_out at 8 tokens; three launches at 64); CPU baseline: the
+restatement of the block (oracle/latent_ref.py).
 
 Workload kimi-moe: the MoE step alone on that rank (its latent as the experts' input).
 
@@ -343,8 +343,8 @@ LATENT_ROWS = {1: None, 8: None, 64: [0, 21, 42, 63]}
 
 
 def measure_latent(cfg, *, seed, steps, warmup, cold, device):
-    """Time the latent block (latent_in and moe_step on the latent in one call, then latent_out) with
-    events between the two calls; returns per-stage and whole-block ms per run."""
+    """Time the latent block (one k3moe.latent_block call) with events around it; returns the
+    block's ms per run (as its one stage too)."""
     import torch
     import k3moe
     from k3moe import synthetic, traffic
@@ -357,13 +357,9 @@ def measure_latent(cfg, *, seed, steps, warmup, cold, device):
     distinct = int(r['expert_ids'].unique().numel())
     lat, sh, out = r['latent'], r['shared_h'], r['output']
     moe_out = {k: r[k] for k in ('expert_sum', 'expert_ids', 'route_weights')}
-    # latent_in and the MoE step in one call (one launch at one token), then latent_out
-    stages = [
-        ('latent_in+moe_step', lambda: k3moe.latent_moe_step(x, w, **kw, out={'latent': lat, 'shared_h': sh,
-                                                                            **moe_out})),
-        ('latent_out', lambda: k3moe.latent_out(moe_out['expert_sum'], w['latent_norm'], w['latent_up'], sh,
-                                                w['shared_down'], out=out)),
-    ]
+    # the whole block in one call (k3moe.latent_block: one launch at one token)
+    outs = {'latent': lat, 'shared_h': sh, 'output': out, **moe_out}
+    stages = [('latent_block', lambda: k3moe.latent_block(x, w, **kw, out=outs))]
     flush = torch.ones(1 << 28, dtype=torch.float32, device=device) if cold else None
     sink = torch.zeros((), dtype=torch.float32, device=device)
     for _ in range(warmup):
@@ -387,9 +383,9 @@ def measure_latent(cfg, *, seed, steps, warmup, cold, device):
              **{k: v.cpu() for k, v in moe_out.items()}}
     same = torch.equal(out, k3moe.latent_block(x, w, **kw)['output'])
     B, h, lh, S = cfg.tokens, cfg.hidden, cfg.latent, KIMI_SHARED
-    nbytes = {'latent_in+moe_step': traffic.latent_in_bytes(B=B, h=h, lh=lh, S=S)
-              + traffic.step_bytes(B=B, E=cfg.experts, k=cfg.topk, h=h, I=cfg.inter, distinct=distinct, K=lh),
-              'latent_out': traffic.latent_out_bytes(B=B, h=h, lh=lh, S=S)}
+    nbytes = {'latent_block': traffic.latent_in_bytes(B=B, h=h, lh=lh, S=S)
+              + traffic.step_bytes(B=B, E=cfg.experts, k=cfg.topk, h=h, I=cfg.inter, distinct=distinct, K=lh)
+              + traffic.latent_out_bytes(B=B, h=h, lh=lh, S=S)}
     host = host_view(w)
     del flush
     return {'ms': block_ms, 'stage_ms': stage_ms, 'distinct': distinct, 'bytes': sum(nbytes.values()),

@@ -309,6 +309,31 @@ int k3moe_latent_moe_step(const k3moe_dims *dims, int32_t shared,
                           float *shortfall,
                           void *workspace, size_t workspace_bytes, void *stream);
 
+/* The whole latent MoE block in one call (kimi.py:317-328, one rank, no
+ * all-reduce): k3moe_latent_moe_step's outputs and k3moe_latent_out's `out`
+ * from its expert sum. With one token and the single-token kernel's geometry
+ * (as for k3moe_latent_moe_step, and lh <= 4096, lh + S <= 4608, h <= 32 x
+ * the CU count) all of it runs in one launch: after the combine every
+ * workgroup polls the expert sum and shared_h from the others' tagged slots,
+ * normalises it and streams its share of the output rows (their weights
+ * issued before the poll). Otherwise it runs as k3moe_latent_moe_step and
+ * k3moe_latent_out. Arguments, outputs, numerics and errors as those entry
+ * points' (the one-launch path sums the output rows in another FP32 order:
+ * within a bf16 step of the other's, mostly equal). */
+int k3moe_latent_block(const k3moe_dims *dims, int32_t shared,
+                       const void *x, const void *latent_down,
+                       const void *shared_gate, const void *shared_up,
+                       const void *latent_norm, const void *latent_up, const void *shared_down,
+                       const void *router, const float *router_bias,
+                       const uint8_t *gate_blocks, const uint8_t *gate_scales,
+                       const uint8_t *up_blocks, const uint8_t *up_scales,
+                       const uint8_t *down_blocks, const uint8_t *down_scales,
+                       const int64_t *routes,
+                       void *latent, void *shared_h,
+                       float *expert_sum, int64_t *expert_ids, float *route_weights,
+                       float *shortfall, void *out,
+                       void *workspace, size_t workspace_bytes, void *stream);
+
 /* MXFP4 decode, unpack_mxfp4 (megabench/tasks/quantization.py:40-51) plus the
  * `.to(act)` cast of kimi.py:321: n_blocks blocks of 16 bytes and n_blocks
  * scales -> n_blocks*32 values of out_dtype (K3MOE_DTYPE_F32 or _BF16),

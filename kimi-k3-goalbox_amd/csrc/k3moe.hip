@@ -401,6 +401,10 @@ struct LatInArgs {
   int S;
   const void *latent_down, *shared_gate, *shared_up;
   void *latent, *shared_h;
+  // the block's output too when the single-token kernel takes it (out != NULL; *did_out reports it)
+  const void *latent_norm, *latent_up, *shared_down;
+  void *out;
+  bool *did_out;
 };
 constexpr int kNotFused = -1000;  // moe_step_impl: the plan has no one-launch latent path
 
@@ -434,7 +438,8 @@ int k3moe_latent_moe_step(const k3moe_dims *dims, int32_t shared, const void *x,
   if (!latent_down || !shared_gate || !shared_up || !latent || !shared_h)
     return fail(K3MOE_EINVAL, "a required pointer is NULL");
   if (!dims) return fail(K3MOE_EINVAL, "dims is NULL");
-  const LatInArgs lat{shared, latent_down, shared_gate, shared_up, latent, shared_h};
+  const LatInArgs lat{shared, latent_down, shared_gate, shared_up, latent, shared_h,
+                      nullptr, nullptr, nullptr, nullptr, nullptr};
   int rc = moe_step_impl(dims, x, latent, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales,
                          down_blocks, down_scales, routes, expert_sum, expert_ids, route_weights, shortfall,
                          workspace, workspace_bytes, stream, &lat);
@@ -447,6 +452,39 @@ int k3moe_latent_moe_step(const k3moe_dims *dims, int32_t shared, const void *x,
   return k3moe_moe_step(dims, x, latent, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales,
                         down_blocks, down_scales, routes, expert_sum, expert_ids, route_weights, shortfall,
                         workspace, workspace_bytes, stream);
+}
+
+int k3moe_latent_block(const k3moe_dims *dims, int32_t shared, const void *x, const void *latent_down,
+                       const void *shared_gate, const void *shared_up, const void *latent_norm,
+                       const void *latent_up, const void *shared_down, const void *router,
+                       const float *router_bias, const uint8_t *gate_blocks, const uint8_t *gate_scales,
+                       const uint8_t *up_blocks, const uint8_t *up_scales, const uint8_t *down_blocks,
+                       const uint8_t *down_scales, const int64_t *routes, void *latent, void *shared_h,
+                       float *expert_sum, int64_t *expert_ids, float *route_weights, float *shortfall, void *out,
+                       void *workspace, size_t workspace_bytes, void *stream) {
+  g_err[0] = 0;
+  if (!latent_down || !shared_gate || !shared_up || !latent_norm || !latent_up || !shared_down || !latent ||
+      !shared_h || !out)
+    return fail(K3MOE_EINVAL, "a required pointer is NULL");
+  if (!dims) return fail(K3MOE_EINVAL, "dims is NULL");
+  bool did_out = false;
+  const LatInArgs lat{shared, latent_down, shared_gate, shared_up, latent, shared_h,
+                      latent_norm, latent_up, shared_down, out, &did_out};
+  int rc = moe_step_impl(dims, x, latent, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales,
+                         down_blocks, down_scales, routes, expert_sum, expert_ids, route_weights, shortfall,
+                         workspace, workspace_bytes, stream, &lat);
+  const k3moe_latent_dims ld{dims->tokens, dims->hidden, dims->latent, shared, dims->activation};
+  if (rc == kNotFused) {  // the input projections, then the step on their latent
+    if ((rc = k3moe_latent_in(&ld, x, latent_down, shared_gate, shared_up, latent, shared_h, workspace,
+                              workspace_bytes, stream)))
+      return rc;
+    rc = k3moe_moe_step(dims, x, latent, router, router_bias, gate_blocks, gate_scales, up_blocks, up_scales,
+                        down_blocks, down_scales, routes, expert_sum, expert_ids, route_weights, shortfall,
+                        workspace, workspace_bytes, stream);
+  }
+  if (rc || did_out) return rc;
+  return k3moe_latent_out(&ld, expert_sum, latent_norm, latent_up, shared_h, shared_down, out, workspace,
+                          workspace_bytes, stream);
 }
 
 static int moe_step_impl(const k3moe_dims *dims, const void *x, const void *latent, const void *router,
@@ -467,6 +505,7 @@ static int moe_step_impl(const k3moe_dims *dims, const void *x, const void *late
   make_plan(*dims, device_cus(), p, trace_enabled());
   p.stall = g_stall.load(std::memory_order_relaxed);
   if (lat && !lat_in_plan(p, lat->S)) return kNotFused;
+  if (lat && lat->out) *lat->did_out = lat_out_plan(p);
   if (dims->path == K3MOE_PATH_DECODE && p.path != kPathDecode)
     return fail(K3MOE_EINVAL, "the persistent decode path needs tokens <= %d and tokens*topk <= %d", kDecMaxTokens,
                 kDecMaxPairs);
@@ -505,6 +544,12 @@ static int moe_step_impl(const k3moe_dims *dims, const void *x, const void *late
       a.lat_su = reinterpret_cast<const uint16_t *>(lat->shared_up);
       a.lat_sh = reinterpret_cast<uint16_t *>(lat->shared_h);
       a.xin = reinterpret_cast<const uint16_t *>(lat->latent);
+    }
+    if (p.lat_out) {  // ... and the block's output
+      a.lat_norm = reinterpret_cast<const uint16_t *>(lat->latent_norm);
+      a.lat_up = reinterpret_cast<const uint16_t *>(lat->latent_up);
+      a.lat_sd = reinterpret_cast<const uint16_t *>(lat->shared_down);
+      a.lat_y = reinterpret_cast<uint16_t *>(lat->out);
     }
     if (p.single) {
       // instantiations: chosen experts per wave in the down phase (1: k <= 8, 2: k <= 16) and

@@ -57,11 +57,15 @@ struct DecodeArgs {
   float *out_w;
   float *out_short;
   char *ws;
-  // the single-token kernel's latent block inputs (Plan::lat_in): latent_down
-  // [K, h], shared_gate / shared_up [S, h] (bf16) and shared_h [S] (bf16 out);
-  // the latent itself goes to xin
+  // the latent block's input projections (Plan::lat_in): latent_down [K, h],
+  // shared_gate / shared_up [S, h] (bf16) and shared_h [B, S] (bf16 out); the
+  // latent itself goes to xin
   const uint16_t *lat_ld, *lat_sg, *lat_su;
   uint16_t *lat_sh;
+  // the single-token kernel's latent block output (Plan::lat_out): latent_norm
+  // [K], latent_up [h, K], shared_down [h, S] (bf16) and the block's output [h] (bf16)
+  const uint16_t *lat_norm, *lat_up, *lat_sd;
+  uint16_t *lat_y;
 };
 
 // The memory pipeline serves older waves first, so in a stream split evenly
@@ -1192,8 +1196,12 @@ __device__ __forceinline__ DecodeArgs load_args(uint64_t at) {
   K3_FIELD(lat_sg);
   K3_FIELD(lat_su);
   K3_FIELD(lat_sh);
+  K3_FIELD(lat_norm);
+  K3_FIELD(lat_up);
+  K3_FIELD(lat_sd);
+  K3_FIELD(lat_y);
 #undef K3_FIELD
-  static_assert(sizeof(DecodeArgs) == 20 * sizeof(void *), "every field read");
+  static_assert(sizeof(DecodeArgs) == 24 * sizeof(void *), "every field read");
   return a;
 }
 

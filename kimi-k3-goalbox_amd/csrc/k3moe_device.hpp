@@ -172,7 +172,7 @@ __device__ __forceinline__ void st_dev128(__amdgpu_buffer_rsrc_t r, uint32_t off
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCpolDevice);
 }
 
-// Reads the first Bytes of the kernel-argument segment with nine independent
+// Reads the first Bytes of the kernel-argument segment with ten independent
 // scalar loads (every 64-byte line, whatever the segment's alignment, and its
 // last dword) and one wait, and returns the segment's address. A kernel whose
 // arguments do not fit its scalar registers reads them in a chain of load /
@@ -181,26 +181,27 @@ __device__ __forceinline__ void st_dev128(__amdgpu_buffer_rsrc_t r, uint32_t off
 // step of that chain hit the scalar cache instead of missing to memory.
 template <int Bytes>
 __device__ __forceinline__ uint64_t touch_kernargs() {
-  static_assert(Bytes >= 8 && Bytes <= 516 && Bytes % 4 == 0, "nine loads cover at most 516 bytes");
+  static_assert(Bytes >= 8 && Bytes <= 580 && Bytes % 4 == 0, "ten loads cover at most 580 bytes");
   constexpr int last = Bytes - 4;
   uint64_t base = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
-  uint32_t t0, t1, t2, t3, t4, t5, t6, t7, t8;
+  uint32_t t0, t1, t2, t3, t4, t5, t6, t7, t8, t9;
   asm volatile(
-      "s_load_dword %0, %9, %10\n\t"
-      "s_load_dword %1, %9, %11\n\t"
-      "s_load_dword %2, %9, %12\n\t"
-      "s_load_dword %3, %9, %13\n\t"
-      "s_load_dword %4, %9, %14\n\t"
-      "s_load_dword %5, %9, %15\n\t"
-      "s_load_dword %6, %9, %16\n\t"
-      "s_load_dword %7, %9, %17\n\t"
-      "s_load_dword %8, %9, %18\n\t"
+      "s_load_dword %0, %10, %11\n\t"
+      "s_load_dword %1, %10, %12\n\t"
+      "s_load_dword %2, %10, %13\n\t"
+      "s_load_dword %3, %10, %14\n\t"
+      "s_load_dword %4, %10, %15\n\t"
+      "s_load_dword %5, %10, %16\n\t"
+      "s_load_dword %6, %10, %17\n\t"
+      "s_load_dword %7, %10, %18\n\t"
+      "s_load_dword %8, %10, %19\n\t"
+      "s_load_dword %9, %10, %20\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&s"(t0), "=&s"(t1), "=&s"(t2), "=&s"(t3), "=&s"(t4), "=&s"(t5), "=&s"(t6), "=&s"(t7), "=&s"(t8),
-        "+s"(base)
+        "=&s"(t9), "+s"(base)
       : "n"(0), "n"(64 < last ? 64 : last), "n"(128 < last ? 128 : last), "n"(192 < last ? 192 : last),
         "n"(256 < last ? 256 : last), "n"(320 < last ? 320 : last), "n"(384 < last ? 384 : last),
-        "n"(448 < last ? 448 : last), "n"(last));
+        "n"(448 < last ? 448 : last), "n"(512 < last ? 512 : last), "n"(last));
   return base;
 }
 

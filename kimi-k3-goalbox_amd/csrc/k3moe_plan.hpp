@@ -128,6 +128,7 @@ struct Plan {
   int fgemm;      // grouped GEMMs on the scaled FP4 MFMA with two-term E4M3 activations (k3moe_fgemm.hpp)
   int lat_in;     // single-token kernel: 1 = it also computes the latent block's inputs (latent, shared_h)
   int lat_S;      // ... the shared experts' width S
+  int lat_out;    // single-token kernel: 1 = it also computes the latent block's output (lat_in too)
   // workspace byte offsets
   size_t o_ctl, o_zero, o_logit, o_ids, o_w, o_nact, o_active, o_aoff, o_acnt, o_ptok, o_pw, o_pof, o_gpart, o_gcnt,
       o_gchunk, o_h, o_y, o_xq, o_hq, o_trace, total;
@@ -217,10 +218,13 @@ constexpr int kSingleMaxTopk = 16;
 constexpr int kSingleRouterRows = 4;  // router rows (experts) per workgroup: E <= 4 G
 constexpr int kSingleSlots = 4;  // gate/up register slots per wave: units of the workgroup x super-steps per wave
 constexpr int kSingleScratchBytes = 3840;
-inline int single_lds(const Plan &p) {
+__host__ __device__ inline int single_lds(const Plan &p) {
   return align16(3 * 4 * p.E) + 2 * p.K + kSingleScratchBytes + kBlockTopkBytes + align16(2 * p.k * p.I) +
          2 * p.k * 16 * 4;
 }
+// With the latent block's output (Plan::lat_out) the expert sum [K] fp32 and
+// [en | shared_h] [K + S] bf16 follow, from this (16-byte aligned) offset.
+__host__ __device__ inline int single_lds_base(const Plan &p) { return align16(single_lds(p)); }
 inline void single_plan(const k3moe_dims &d, Plan &p) {
   const bool tags_fit = (long)kTagCopies * p.E * 8 + (long)p.k * (p.I / 2) * 8 <= kTagBytes;
   p.single = (d.path == K3MOE_PATH_AUTO || d.path == K3MOE_PATH_SINGLE) && p.B == 1 && p.k <= kSingleMaxTopk &&
@@ -232,12 +236,19 @@ inline void single_plan(const k3moe_dims &d, Plan &p) {
 
 // The persistent kernels with the latent block's inputs (latent and shared_h,
 // the projections of kimi.py:317 and 326). The single-token kernel: workgroup
-// b computes latent row pairs b, b + G, .. and shared pairs (gate and up row)
-// b, b + G, .. of width h, at most kLatRowsMax rows in all, and publishes the
+// b computes a contiguous share of the latent row pairs and of the shared pairs (gate and up row)
+// of width h, at most kLatRowsMax rows in all, and publishes the
 // latent in tagged slots (one per row pair, after the logits and the h slots)
 // that every workgroup polls before its gate/up products. Returns whether one
 // of the two kernels takes them for shared width S (setting lat_in, lat_S).
 constexpr int kLatRowsMax = 48;  // rows (latent rows + shared gate and up rows) per workgroup
+// The single-token kernel's latent block output (Plan::lat_out): a lane's
+// 16-byte chunks of a row of [latent_up | shared_down] (K + S <= 64 x 8 x
+// kLatOutChunks), output rows per wave, the expert sum's width, its RMS epsilon
+// (kimi.py:325) and the slots a thread polls for [expert sum | shared_h].
+constexpr int kLatOutChunks = 9, kLatOutRowsPerWave = 4, kLatOutMaxK = 4096;
+constexpr int kLatOutPoll = (kLatOutMaxK + 512 + 511) / 512;  // K + S <= 64 x 8 x 9 = 4608 < 9 x 512 + 1
+constexpr float kLatOutRmsEps = 1e-5f;
 inline int lat_rows_max(const Plan &p, int S) { return 2 * cdiv(p.K / 2, p.G) + 2 * cdiv(S, p.G); }
 __host__ __device__ inline uint32_t lat_slot_base(const Plan &p) { return (uint32_t)(kTagCopies * p.E * 8 + p.k * (p.I / 2) * 8); }
 // The decode kernel takes them too with the pinned gate/up and at most 16
@@ -256,6 +267,21 @@ inline bool lat_in_plan(Plan &p, int S) {
   p.lat_in = ok ? 1 : 0;
   p.lat_S = ok ? S : 0;
   if (ok && decode && lds_x > p.lds_total) p.lds_total = (int)lds_x;
+  return ok;
+}
+
+// The single-token kernel also takes the block's output (after lat_in_plan):
+// K <= kLatOutMaxK, K + S within a lane's chunks, at most kLatOutRowsPerWave
+// output rows per wave (h <= 32 G), the expert sum and [en | shared_h] in LDS.
+inline bool lat_out_plan(Plan &p) {
+  const int S = p.lat_S;
+  const long lds = (long)single_lds_base(p) + align16(4 * p.K) + align16(2 * (p.K + S));
+  const bool ok = p.lat_in && p.single && p.K <= kLatOutMaxK && p.K % 8 == 0 && S % 8 == 0 &&
+                  p.K + S <= 64 * 8 * kLatOutChunks && cdiv(p.h, p.G) <= kDecWaves * kLatOutRowsPerWave &&
+                  (long)lat_slot_base(p) + (long)(p.K / 2 + S + p.K) * 8 <= kTagBytes &&
+                  lds <= kDecMaxLds - kDecStaticLds;
+  p.lat_out = ok ? 1 : 0;
+  if (ok) p.lds_total = (int)lds;
   return ok;
 }
 
@@ -360,6 +386,7 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   p.stall = 0;
   p.lat_in = 0;
   p.lat_S = 0;
+  p.lat_out = 0;
   single_plan(d, p);
   if (p.single) {
     p.path = kPathDecode;

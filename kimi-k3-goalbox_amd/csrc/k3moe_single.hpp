@@ -114,6 +114,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   // gave up, and this workgroup's count on its launch counter (every path).
   auto leave = [&](bool gave_up) {
     if (gave_up) poison_share<false>(a.out, (long)K);
+    if (gave_up && pl.lat_out) poison_share<true>(a.lat_y, (long)pl.h);
     if (tid == 0)
       __hip_atomic_fetch_add(ctl + kCtlEpoch + (blockIdx.x % kEpochCounters) * kCtlEpochStride, 1u, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
@@ -332,7 +333,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
         g = __fadd_rn(g, lred[ww * kLatRowsMax + r]);
         u = __fadd_rn(u, lred[ww * kLatRowsMax + r + 1]);
       }
-      a.lat_sh[sj] = (uint16_t)f32_to_bf16_bits(apply_act(pl.act, round_bf16(g), round_bf16(u)));
+      const uint16_t hv = f32_to_bf16_bits(apply_act(pl.act, round_bf16(g), round_bf16(u)));
+      a.lat_sh[sj] = hv;
+      if (pl.lat_out) st_dev64(tagr, lat_base + (uint32_t)(K / 2 + sj) * 8, u32x2{hv, tag});
     }
     trace_mark(pl, a.ws, 16);
   }
@@ -719,9 +722,159 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
       float sum = 0.f;
       for (int jj = 0; jj < k; ++jj) sum = __fadd_rn(sum, dacc[(tt * k + sh.ord[jj]) * 16 + r]);
       a.out[rt * 16 + r] = sum;
+      if (pl.lat_out)
+        st_dev64(tagr, lat_base + (uint32_t)(K / 2 + pl.lat_S + rt * 16 + r) * 8, u32x2{__float_as_uint(sum), tag});
     }
   }
   trace_mark(pl, a.ws, 8);
+
+  // ------------------------------------------------ O: latent block output --
+  // With Plan::lat_out (kimi.py:325-328): out = bf16(bf16(en @ latent_up.T) +
+  // bf16(shared_h @ shared_down.T)), en = bf16(bf16(e r) w) the RMS-normalised
+  // bf16(expert_sum) (r = 1 / sqrt(mean(e^2) + 1e-5), w = latent_norm).
+  // Workgroup b takes output rows b, b + G, .. (wave w: its rows w, w + 8, ..);
+  // a lane takes 16-byte chunks l + 64 j of the row's [latent_up | shared_down]
+  // (K + S columns) against the same chunks of [en | shared_h] in LDS. The
+  // first two rows' weights go out before the expert sum and shared_h are
+  // polled from every workgroup's tagged slots; wave 0 sums e^2 (lane l:
+  // chunks of 4 at 4 (l + 64 m), then the wave's butterfly); each lane sums its
+  // two parts separately in FP32, the wave's DPP tree sums them, and lane 0
+  // rounds each part and their sum.
+  if (pl.lat_out) {
+    const int G = (int)gridDim.x, b = (int)blockIdx.x, h = pl.h, S = pl.lat_S, KC = K / 8, NC = (K + S) / 8;
+    const int nro = h > b ? (h - b + G - 1) / G : 0;
+    float *es = reinterpret_cast<float *>(lds + single_lds_base(pl));       // [K] the expert sum
+    uint16_t *xo = reinterpret_cast<uint16_t *>(es + K);                    // [K + S] en, then shared_h
+    const uint32_t sh_base = lat_base + (uint32_t)(K / 2) * 8, es_base = sh_base + (uint32_t)S * 8;
+    struct Row {
+      u32x4 v[kLatOutChunks];
+    };
+    auto issue = [&](int m, Row &rw) {  // wave w's m-th row (row b + G (w + 8 m)); past its rows: the zero area
+      const int ri = w + kDecWaves * m, ro = b + G * ri;
+#pragma unroll
+      for (int jc = 0; jc < kLatOutChunks; ++jc) {
+        const int c = l + 64 * jc;
+        const uint16_t *src = c < KC ? a.lat_up + (size_t)ro * K + c * 8 : a.lat_sd + (size_t)ro * S + (c - KC) * 8;
+        rw.v[jc] = load16((ri < nro && c < NC) ? reinterpret_cast<const uint8_t *>(src) : zero);
+      }
+    };
+    Row r0w, r1w;
+    issue(0, r0w);
+    issue(1, r1w);
+    // this thread's norm weights (k = tid + 512 m), the expert sum and shared_h from their slots
+    uint16_t wn[kLatOutMaxK / kDecThreads];
+#pragma unroll
+    for (int m = 0; m < kLatOutMaxK / kDecThreads; ++m) {
+      const int kk = tid + kDecThreads * m;
+      wn[m] = kk < K ? a.lat_norm[kk] : (uint16_t)0;
+    }
+    {
+      // element c = tid + 512 m of [expert sum | shared_h], every load of a round in flight at once
+      bool ok = true;
+      unsigned spins = 0;
+      for (;;) {
+        u32x2 v[kLatOutPoll];
+#pragma unroll
+        for (int m = 0; m < kLatOutPoll; ++m) {
+          const int c = tid + kDecThreads * m;
+          const uint32_t off = c < K ? es_base + (uint32_t)c * 8 : sh_base + (uint32_t)(c - K) * 8;
+          v[m] = c < K + S ? bload8_dev(tagr, off) : u32x2{0u, tag};
+        }
+        bool ready = true;
+#pragma unroll
+        for (int m = 0; m < kLatOutPoll; ++m) {
+          const int c = tid + kDecThreads * m;
+          ready = ready && v[m][1] == tag;
+          if (c < K) es[c] = __uint_as_float(v[m][0]);
+          else if (c < K + S) xo[c] = (uint16_t)v[m][0];
+        }
+        if (__syncthreads_or(!ready) == 0) break;
+        ++spins;  // (the same in every thread: each exit below is taken by the whole workgroup)
+        if ((spins & 63u) == 0u && __syncthreads_or(aborted(ctl, abort0)) != 0) {
+          ok = false;
+          break;
+        }
+        if (spins > kSpinLimit) {
+          if (tid == 0) raise_timeout(ctl);
+          ok = false;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (!ok) return leave(true);
+    }
+    if (w == 0) {  // r = 1 / sqrt(mean(bf16(e)^2) + eps)
+      float ss = 0.f;
+      f32x4 ec[kLatOutMaxK / 256];  // every chunk read at once
+#pragma unroll
+      for (int m = 0; m < kLatOutMaxK / 256; ++m)
+        ec[m] = 4 * (l + 64 * m) < K ? *reinterpret_cast<const f32x4 *>(es + 4 * (l + 64 * m))
+                                      : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < kLatOutMaxK / 256; ++m) {
+        if (4 * (l + 64 * m) < K) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float e = round_bf16(ec[m][v]);
+            ss += e * e;
+          }
+        }
+      }
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
+      if (l == 0) sh.rred[0] = 1.0f / __fsqrt_rn(ss / (float)K + kLatOutRmsEps);
+    }
+    __syncthreads();
+    const float rn = sh.rred[0];
+#pragma unroll
+    for (int m = 0; m < kLatOutMaxK / kDecThreads; ++m) {
+      const int kk = tid + kDecThreads * m;
+      if (kk < K) xo[kk] = f32_to_bf16_bits(round_bf16(round_bf16(es[kk]) * rn) * bf16_bits_to_f32(wn[m]));
+    }
+    __syncthreads();
+    // the rows' values are stored after the loop: a store inside it would be
+    // counted by the next row's wait (vmcnt counts stores too)
+    uint16_t yv[kLatOutRowsPerWave];
+    auto row_out = [&](int m, const Row &rw) {
+      const int ri = w + kDecWaves * m;
+      if (ri >= nro) return;  // wave-uniform
+      float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+      for (int jc = 0; jc < kLatOutChunks; ++jc) {
+        const int c = l + 64 * jc;
+        if (c < NC) {
+          const u32x4 xv = *reinterpret_cast<const u32x4 *>(xo + c * 8);
+          float p = 0.f;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            p = fmaf(bf16_bits_to_f32(rw.v[jc][d] & 0xFFFFu), bf16_bits_to_f32(xv[d] & 0xFFFFu), p);
+            p = fmaf(bf16_bits_to_f32(rw.v[jc][d] >> 16), bf16_bits_to_f32(xv[d] >> 16), p);
+          }
+          if (c < KC) s1 += p;
+          else s2 += p;
+        }
+      }
+      s1 = wave_sum_f32(s1);
+      s2 = wave_sum_f32(s2);
+      yv[m] = f32_to_bf16_bits(round_bf16(s1) + round_bf16(s2));
+    };
+#pragma unroll
+    for (int m = 0; m < kLatOutRowsPerWave; m += 2) {
+      wait_vm<kLatOutChunks>();
+      row_out(m, r0w);
+      issue(m + 2, r0w);
+      wait_vm<kLatOutChunks>();
+      row_out(m + 1, r1w);
+      issue(m + 3, r1w);
+    }
+    wait_vm<0>();
+    if (l == 0) {
+#pragma unroll
+      for (int m = 0; m < kLatOutRowsPerWave; ++m)
+        if (w + kDecWaves * m < nro) a.lat_y[b + G * (w + kDecWaves * m)] = yv[m];
+    }
+    trace_mark(pl, a.ws, 19);
+  }
   if (pl.o_trace && tid == 0)
     reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + 55] = kTraceSingle;
   if (blockIdx.x == 0 && tid == 0) {  // this kernel's code range, for the next launch's warm-up

@@ -49,7 +49,7 @@ STATUS_TIMEOUT, STATUS_ROUTES = 1, 2
 
 EXPORTS = ('k3moe_workspace_bytes', 'k3moe_workspace_init', 'k3moe_workspace_status', 'k3moe_moe_step',
            'k3moe_mxfp4_decode', 'k3moe_last_error', 'k3moe_version', 'k3moe_latent_workspace_bytes',
-           'k3moe_latent_in', 'k3moe_latent_out', 'k3moe_latent_moe_step', 'k3moe_workspace_layout',
+           'k3moe_latent_in', 'k3moe_latent_out', 'k3moe_latent_moe_step', 'k3moe_latent_block', 'k3moe_workspace_layout',
            'k3moe_moe_step_noalloc', 'k3moe_mxfp4_encode', 'k3moe_activation', 'k3moe_debug_stall')
 
 _lib = None
@@ -98,6 +98,8 @@ def load(path: str | None = None):
     lib.k3moe_latent_out.restype = ctypes.c_int
     lib.k3moe_latent_moe_step.argtypes = [ctypes.POINTER(Dims), i32] + [p]*6 + [p]*13 + [p, sz, p]
     lib.k3moe_latent_moe_step.restype = ctypes.c_int
+    lib.k3moe_latent_block.argtypes = [ctypes.POINTER(Dims), i32] + [p]*23 + [p, sz, p]
+    lib.k3moe_latent_block.restype = ctypes.c_int
     lib.k3moe_last_error.argtypes = []
     lib.k3moe_last_error.restype = ctypes.c_char_p
     lib.k3moe_version.argtypes = []

@@ -166,22 +166,53 @@ def latent_moe_step(normalized: torch.Tensor, w: dict, *, topk: int, gating: str
 
 def latent_block(normalized: torch.Tensor, w: dict, *, topk: int, gating: str = 'sigmoid_bias',
                  activation: str = 'situ', fp32: bool = False, routes: torch.Tensor | None = None,
-                 path: str = 'auto') -> dict:
-    """The whole block: latent_in, the routed experts on the latent (moe_step), latent_out.
+                 path: str = 'auto', out: dict | None = None) -> dict:
+    """The whole block: latent_in, the routed experts on the latent (moe_step), latent_out, in one
+    call (k3moe_latent_block: one launch for one token on the single-token kernel's geometry, else
+    latent_moe_step's one or two launches and latent_out's).
 
     `w` holds latent_down, latent_up, latent_norm, shared_gate, shared_up, shared_down, router,
     router_bias and {gate,up,down}_{blocks,scales} (kimi.py:112-121 names without the layer
     prefix). Returns {'output' bf16 [B, h], 'latent', 'shared_h', 'expert_sum', 'expert_ids',
     'route_weights', ['route_shortfall']}. `activation` is the routed and shared experts'
-    (SiTU in kimi.py:322, 326).
+    (SiTU in kimi.py:322, 326). `out` may hold preallocated output tensors by those keys.
     """
     if fp32:
         raise NotImplementedError('fp32=True is the FP32 truth mode of the CPU oracle; '
                                   'the GPU block computes the BF16 serving path (fp32=False)')
-    latent, shared_h, moe = latent_moe_step(normalized, w, topk=topk, gating=gating, activation=activation,
-                                            routes=routes, path=path)
-    output = latent_out(moe['expert_sum'], w['latent_norm'], w['latent_up'], shared_h, w['shared_down'])
-    return {'output': output, 'latent': latent, 'shared_h': shared_h, **moe}
+    out = dict(out or {})
+    device = _device_of(normalized)
+    B, h = normalized.shape
+    lh, S = w['latent_down'].shape[0], w['shared_gate'].shape[0]
+    _expect(normalized, 'normalized', torch.bfloat16, (B, h), device)
+    for name, shape in (('latent_down', (lh, h)), ('shared_gate', (S, h)), ('shared_up', (S, h)),
+                        ('latent_norm', (lh,)), ('latent_up', (h, lh)), ('shared_down', (h, S))):
+        _expect(w[name], name, torch.bfloat16, shape, device)
+    with torch.cuda.device(device):
+        for name, shape in (('latent', (B, lh)), ('shared_h', (B, S)), ('output', (B, h))):
+            if out.get(name) is None:
+                out[name] = torch.empty(*shape, dtype=torch.bfloat16, device=device)
+            _expect(out[name], name, torch.bfloat16, shape, device)
+    latent, shared_h, output = out['latent'], out['shared_h'], out['output']
+    # one workspace for every launch of the block
+    mdims = dims_for(normalized, w['router'], w['gate_blocks'], w['down_blocks'], topk, gating, activation, latent,
+                     path)
+    ws = cached_workspace(max(workspace_bytes(mdims), latent_workspace_bytes(latent_dims(B, h, lh, S, activation))),
+                          device)
+    step = prepare_step(normalized, w['router'], w.get('router_bias'), w['gate_blocks'], w['gate_scales'],
+                        w['up_blocks'], w['up_scales'], w['down_blocks'], w['down_scales'], topk=topk,
+                        gating=gating, activation=activation, routes=routes, latent=latent, path=path, workspace=ws,
+                        out=out)
+    a = step._args  # (dims, x, latent, router .. routes, expert_sum .. shortfall, workspace, workspace bytes)
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        check(_native.load().k3moe_latent_block(
+            a[0], ctypes.c_int32(S), a[1], _dev_ptr(w['latent_down']), _dev_ptr(w['shared_gate']),
+            _dev_ptr(w['shared_up']), _dev_ptr(w['latent_norm']), _dev_ptr(w['latent_up']),
+            _dev_ptr(w['shared_down']), *a[3:12], _dev_ptr(latent), _dev_ptr(shared_h), *a[12:16],
+            _dev_ptr(output), _dev_ptr(ws), ctypes.c_size_t(ws.numel()), ctypes.c_void_p(stream)),
+            'k3moe_latent_block')
+    return {'output': output, 'latent': latent, 'shared_h': shared_h, **step.result}
 
 
 BLOCK_KEYS = ('latent_down', 'latent_up', 'latent_norm', 'router', 'router_bias', 'gate_blocks', 'gate_scales',

@@ -270,6 +270,47 @@ def test_latent_moe_step_matches_separate_launches(cfg, shared, forced):
     assert k3moe.workspace_status(ws) == 0
 
 
+@pytest.mark.parametrize('cfg,shared,forced', [
+    (MoEConfig('kimi-rank-e128-b1', 128, 16, 7168, 384, 1, latent=3584), 768, False),   # one launch
+    (MoEConfig('kimi-rank-e128-b1', 128, 16, 7168, 384, 1, latent=3584), 768, True),
+    (MoEConfig('latent-one', 64, 8, 1024, 256, 1, latent=512), 256, False),             # one launch, small
+    (MoEConfig('kimi-rank-e128-b8', 128, 16, 7168, 384, 8, latent=3584), 768, False),   # latent_out apart
+])
+def test_latent_block_one_call_matches_separate_calls(cfg, shared, forced):
+    """k3moe.latent_block (k3moe_latent_block: one launch for one token on the single-token
+    kernel, the block's output computed after the combine) against latent_moe_step and
+    latent_out called apart on the same workspace: the same expert sets and weights, the output
+    within a rounding step of theirs (mostly equal: its rows are summed in another FP32 order)
+    and in the oracle's band."""
+    say(f'latent_block one call {cfg.name} shared={shared} forced={forced}')
+    dev = torch.device('cuda:0')
+    w = block_case(cfg, 6, shared)
+    g = {k: (v.to(dev) if v is not None else None) for k, v in w.items()}
+    routes = None
+    if forced:
+        gen = torch.Generator().manual_seed(4)
+        routes = torch.stack([torch.randperm(cfg.experts, generator=gen)[:cfg.topk] for _ in range(cfg.tokens)])
+    r_dev = None if routes is None else routes.to(dev)
+    before = grading.snapshot({k: v for k, v in g.items() if v is not None})
+    got = k3moe.latent_block(g['x'], g, topk=cfg.topk, routes=r_dev)
+    lat, sh, moe = k3moe.latent_moe_step(g['x'], g, topk=cfg.topk, routes=r_dev)
+    out2 = k3moe.latent_out(moe['expert_sum'], g['latent_norm'], g['latent_up'], sh, g['shared_down'])
+    torch.cuda.synchronize(dev)
+    grading.check_unchanged({k: v for k, v in g.items() if v is not None}, before)
+    for key in ('expert_ids', 'route_weights', 'latent', 'shared_h', 'expert_sum'):
+        ref = {'latent': lat, 'shared_h': sh}.get(key, moe.get(key))
+        assert torch.equal(got[key].cpu(), ref.cpu()), key
+    near_oracle(got['output'], out2.cpu(), 1)
+    oracle = latent_ref.latent_block(w['x'], w, topk=cfg.topk, routes=routes)
+    truth = latent_ref.latent_block(w['x'], w, topk=cfg.topk, fp32=True, routes=oracle['expert_ids'])
+    detail = grading.band_check(got['output'].cpu(), oracle['output'], truth['output'], truth['output'],
+                                name='output')
+    say(f'  output: {detail}')
+    ws = k3moe.moe.get_workspace(k3moe.moe.dims_for(g['x'], g['router'], g['gate_blocks'], g['down_blocks'],
+                                                    cfg.topk, 'sigmoid_bias', 'situ', got['latent']), dev)
+    assert k3moe.workspace_status(ws) == 0
+
+
 def test_latent_moe_layer_reads_reference_keys():
     cfg = MoEConfig('latent-small', 64, 8, 1024, 256, 4, latent=512)
     say(f'latent_moe_layer {cfg.name}')
