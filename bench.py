@@ -614,8 +614,10 @@ def roofline_entry(head, cfg, layers, measured, workload):
     """The roofline object of the JSON line: HBM for the decode-sized steps (one persistent kernel),
     MFMA for the prefill step (grouped GEMMs on the scaled FP4 MFMA; its HBM rate is given beside it)."""
     if workload == 'kimi-latent':
-        return {'bound': 'hbm', 'kernel': 'k3moe::k_latent<0> + k3moe::k_moe_decode + k3moe::k_latent<1> '
-                                          '(the whole block; per-kernel rates in per_batch stages)',
+        return {'bound': 'hbm', 'kernel': 'k3moe::k_moe_single with the latent projections and output (the '
+                                          'whole block, one launch at 1 token); 8 tokens: k_moe_decode with the '
+                                          'projections + k_latent<1>; 64: k_latent_sk<0> + k_moe_decode + '
+                                          'k_latent_sk<1>',
                 'achieved': head['hbm_GBps'], 'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac'],
                 'traffic': None}
     if workload == 'prefill':
