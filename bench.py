@@ -39,9 +39,8 @@ Workload kimi-latent: the whole latent MoE block of a Kimi K3 TP8 rank
 (kimi.py:317-328: latent_down and the shared experts' gate/up, the MoE step on
 the 3584-wide latent with 896 experts top-16 and I=384, then the RMS norm,
 latent_up and shared_down; bf16 weights outside the experts), timed as one
-k3moe.latent_block call (one launch at one token; the input projections with the
-MoE step and then latent_out at 8 tokens; three launches at 64); CPU baseline: the
-restatement of the block (oracle/latent_ref.py).
+k3moe.latent_block call (one launch at one and at 8 tokens; three launches at
+64); CPU baseline: the restatement of the block (oracle/latent_ref.py).
 
 Workload kimi-moe: the MoE step alone on that rank (its latent as the experts' input).
 
@@ -357,7 +356,7 @@ def measure_latent(cfg, *, seed, steps, warmup, cold, device):
     distinct = int(r['expert_ids'].unique().numel())
     lat, sh, out = r['latent'], r['shared_h'], r['output']
     moe_out = {k: r[k] for k in ('expert_sum', 'expert_ids', 'route_weights')}
-    # the whole block in one call (k3moe.latent_block: one launch at one token)
+    # the whole block in one call (k3moe.latent_block: one launch at 1 and 8 tokens)
     outs = {'latent': lat, 'shared_h': sh, 'output': out, **moe_out}
     stages = [('latent_block', lambda: k3moe.latent_block(x, w, **kw, out=outs))]
     flush = torch.ones(1 << 28, dtype=torch.float32, device=device) if cold else None
@@ -616,8 +615,8 @@ def roofline_entry(head, cfg, layers, measured, workload):
     if workload == 'kimi-latent':
         return {'bound': 'hbm', 'kernel': 'k3moe::k_moe_single with the latent projections and output (the '
                                           'whole block, one launch at 1 token); 8 tokens: k_moe_decode with the '
-                                          'projections + k_latent<1>; 64: k_latent_sk<0> + k_moe_decode + '
-                                          'k_latent_sk<1>',
+                                          'projections and output (one launch); 64: k_latent_sk<0> + '
+                                          'k_moe_decode + k_latent_sk<1>',
                 'achieved': head['hbm_GBps'], 'peak': 8000.0, 'unit': 'GB/s', 'frac': head['hbm_frac'],
                 'traffic': None}
     if workload == 'prefill':

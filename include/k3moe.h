@@ -291,8 +291,12 @@ int k3moe_latent_out(const k3moe_latent_dims *dims, const float *expert_sum, con
  * geometry (and at most 48 latent and shared rows per workgroup: lh/2 + S
  * <= 24 x the CU count) both run in one launch: every workgroup streams its
  * share of the projections' weights while the routing goes on, and the
- * gate/up products wait for the latent through tagged slots. Otherwise the
- * two run as k3moe_latent_in and k3moe_moe_step launches. The workspace must
+ * gate/up products wait for the latent through tagged slots. With 2 to 16
+ * tokens on the decode kernel's pinned plans (and (lh + 2S)/2 rows at most 16
+ * per non-routing workgroup) they also run in one launch: the workgroups that
+ * route no token stream the projections while the routing runs and a grid
+ * barrier publishes the latent. Otherwise the two run as k3moe_latent_in and
+ * k3moe_moe_step launches. The workspace must
  * hold both k3moe_workspace_bytes(dims) and k3moe_latent_workspace_bytes of
  * the block's dims. Arguments, outputs, numerics and errors as those two
  * entry points'. */
@@ -316,8 +320,11 @@ int k3moe_latent_moe_step(const k3moe_dims *dims, int32_t shared,
  * the CU count) all of it runs in one launch: after the combine every
  * workgroup polls the expert sum and shared_h from the others' tagged slots,
  * normalises it and streams its share of the output rows (their weights
- * issued before the poll). Otherwise it runs as k3moe_latent_moe_step and
- * k3moe_latent_out. Arguments, outputs, numerics and errors as those entry
+ * issued before the poll). With 2 to 8 tokens where k3moe_latent_moe_step
+ * runs in one launch (and lh, S multiples of 128, lh <= 4096, h <= 32 x the
+ * CU count) the decode kernel does the same after a grid barrier over the
+ * expert sum (the combine also writes its bf16 rounding to the workspace for
+ * the norm). Otherwise it runs as k3moe_latent_moe_step and k3moe_latent_out. Arguments, outputs, numerics and errors as those entry
  * points' (the one-launch path sums the output rows in another FP32 order:
  * within a bf16 step of the other's, mostly equal). */
 int k3moe_latent_block(const k3moe_dims *dims, int32_t shared,

@@ -1071,7 +1071,8 @@ __device__ __forceinline__ void dn_issue(const Plan &pl, const DecodeArgs &a, co
 // out in whole pairs, workgroup j of the NW taking rows [2 U j / NW, 2 U (j + 1)
 // / NW) (U = (lh + 2 S) / 2; at most 32 rows, two 16-row MFMA tiles, rows past
 // the range reading the zero area). The tokens' rows of x go to LDS first
-// (after the reduction area, row pitch h + 8; direct-to-LDS loads); the 8
+// (after kLatRedBytes, clear of the reduction area; row pitch h + 8;
+// direct-to-LDS loads: the workgroup's LDS holds nothing else yet); the 8
 // waves split h in 128-column steps (MFMA 16x16x32 bf16: the weights as the A
 // operand from global memory, four steps in flight, the tokens as the B
 // operand from LDS); the waves' tiles meet in LDS in wave order. The latent
@@ -1081,8 +1082,8 @@ __device__ __forceinline__ void dec_latent_rows(const Plan &pl, const DecodeArgs
                                                 int j, int NW) {
   const int w = wave_id(), l = threadIdx.x & 63, i = l & 15, q = l >> 4, tid = threadIdx.x;
   const int h = pl.h, lh = pl.K, B = pl.B, S = pl.lat_S, hp = h + 8;
-  float *red = reinterpret_cast<float *>(lds);
-  uint16_t *xs = reinterpret_cast<uint16_t *>(lds + pl.lds_red);  // [B][h + 8]
+  float *red = reinterpret_cast<float *>(lds);                    // [2 tiles][8 waves][256]
+  uint16_t *xs = reinterpret_cast<uint16_t *>(lds + kLatRedBytes);  // [B][h + 8], clear of the reduction area
   const int U = (lh + 2 * S) / 2;
   const int r0 = 2 * (int)((long)U * j / NW), n = 2 * (int)((long)U * (j + 1) / NW) - r0;
   auto row_ptr = [&](int r) -> const uint16_t * {  // row r of the projections (r < lh + 2 S)
@@ -1161,13 +1162,192 @@ __device__ __forceinline__ void dec_latent_rows(const Plan &pl, const DecodeArgs
         const uint32_t pair = (uint32_t)f32_to_bf16_bits(v0) | ((uint32_t)f32_to_bf16_bits(v1) << 16);
         st_dev32(make_rsrc(a.xin, (uint32_t)B * lh * 2), (uint32_t)((c * lh + row) * 2), pair);
       } else {
-        a.lat_sh[(size_t)c * S + ((row - lh) >> 1)] =
-            (uint16_t)f32_to_bf16_bits(apply_act(pl.act, round_bf16(v0), round_bf16(v1)));
+        const uint16_t hv = f32_to_bf16_bits(apply_act(pl.act, round_bf16(v0), round_bf16(v1)));
+        const size_t at = (size_t)c * S + ((row - lh) >> 1);
+        if (pl.lat_out) {  // (read in this launch by dec_latent_out: device-coherent, a 16-bit store)
+          __builtin_amdgcn_raw_buffer_store_b16(hv, make_rsrc(a.lat_sh, (uint32_t)B * S * 2), (uint32_t)(at * 2), 0,
+                                                kCpolDevice);
+        } else {
+          a.lat_sh[at] = hv;
+        }
       }
     }
   }
   wait_vmem();  // the latent's stores have completed (the latent barrier publishes them)
   __syncthreads();
+}
+
+// The latent block's output (kimi.py:325-328) in the decode kernel
+// (Plan::lat_out, at most 8 tokens, after the step's expert sum): out =
+// bf16(bf16(en @ latent_up.T) + bf16(shared_h @ shared_down.T)), en =
+// bf16(bf16(e r) w) with e = bf16(expert_sum), r = 1 / sqrt(mean(e^2) + 1e-5),
+// w = latent_norm. Workgroup b takes a contiguous share of the h output rows
+// (at most 32: two 16-row MFMA tiles), the 8 waves split the K + S columns of
+// [latent_up | shared_down] in 128-column steps (K and S multiples of 128, so a
+// step lies in one part; one accumulator per part and tile); the workgroup
+// arrives at the grid barrier over the expert sum (`arrive`), issues the first
+// two steps' weights and then waits at it (`wait`), latent_norm and shared_h
+// (published at the latent barrier) going straight to LDS before the weights;
+// then the expert-sum loads and the next two steps' weights go out;
+// wave t < B normalises token t (the bf16 copy of its expert sum, written by
+// the combine at o_ebf, read with device-coherent loads; the sum of squares in
+// k_latent<1>'s order) and writes en beside
+// shared_h in LDS after kLatRedBytes (the step is over: nothing else lives in
+// LDS any more); the waves' tiles meet in
+// LDS in wave order and the two parts are rounded apart. Returns false when
+// the barrier gave up.
+template <class Arrive, class Wait>
+__device__ __forceinline__ bool dec_latent_out(const Plan &pl, const DecodeArgs &a, char *lds, const uint8_t *zero,
+                                               Arrive &&arrive, Wait &&wait) {
+  const int w = wave_id(), l = threadIdx.x & 63, i = l & 15, q = l >> 4, tid = threadIdx.x;
+  const int h = pl.h, K = pl.K, B = pl.B, S = pl.lat_S, KT = K + S, xp = KT + 8;
+  float *red = reinterpret_cast<float *>(lds);                    // [2 parts][2 tiles][8 waves][256]
+  uint16_t *xs = reinterpret_cast<uint16_t *>(lds + kLatRedBytes);  // [B][K + S + 8]: en, then shared_h
+  char *nw = lds + kLatRedBytes + align16((size_t)B * (K + S + 8) * 2);  // latent_norm, kLatOutMaxK bf16
+  const int G = (int)gridDim.x, rpw = (h + G - 1) / G, row0 = (int)blockIdx.x * rpw;
+  const int n = h > row0 ? min(rpw, h - row0) : 0;
+  const int KS = KT / 128, KS0 = K / 128, ka = KS * w / kDecWaves, kb = KS * (w + 1) / kDecWaves;
+  const bool ra = i < n, rb = 16 + i < n;
+  struct Step {
+    u32x4 wa[4], wb[4];
+  };
+  // step ks, MFMA kk: lane (i, q) holds columns 128 ks + 32 kk + 8 q .. + 7 of
+  // output row row0 + i (tile a) / row0 + 16 + i (tile b) and of token i
+  auto issue = [&](int ks, Step &st) {  // steps past the wave's range read the zero area
+    const bool in = ks < kb;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int c = ks * 128 + kk * 32 + q * 8;
+      const uint16_t *pa = c < K ? a.lat_up + (size_t)(row0 + i) * K + c : a.lat_sd + (size_t)(row0 + i) * S + (c - K);
+      const uint16_t *pb = c < K ? a.lat_up + (size_t)(row0 + 16 + i) * K + c
+                                 : a.lat_sd + (size_t)(row0 + 16 + i) * S + (c - K);
+      st.wa[kk] = load16((in && ra) ? reinterpret_cast<const uint8_t *>(pa) : zero);
+      st.wb[kk] = load16((in && rb) ? reinterpret_cast<const uint8_t *>(pb) : zero);
+    }
+  };
+  // arrive first (the expert-sum stores have completed); before waiting, stage
+  // what does not depend on the barrier (latent_norm; shared_h, published at
+  // the latent barrier, read device-coherent) straight into LDS and issue the
+  // first two steps' weights
+  arrive();
+  if (w < B)
+    for (int c = 0; c < S; c += 128)  // 64 lanes x 2 values
+      load_lds<4, kCpolDevice>(a.lat_sh + (size_t)w * S + c + 2 * l, reinterpret_cast<char *>(xs + (size_t)w * xp + K + c));
+  {
+    const int o = w * 1024 + l * 16;  // 8 waves x 64 lanes x 16 bytes = kLatOutMaxK bf16
+    load_lds<16>(o < 2 * K ? reinterpret_cast<const uint8_t *>(a.lat_norm) + o : zero, nw + w * 1024);
+  }
+  Step s0, s1, s2, s3;
+  issue(ka, s0);
+  issue(ka + 1, s1);
+  wait_vm<16>();  // the LDS loads, issued before the 16 weight loads, have landed (the barrier's sync publishes them)
+  if (!wait()) return false;
+  trace_mark(pl, a.ws, 36);  // the output barrier passed
+  // the expert-sum loads go out before the other two steps' weights, so that
+  // they queue behind half of the weight stream only
+  const __amdgpu_buffer_rsrc_t er = make_rsrc(a.ws + pl.o_ebf, (uint32_t)((size_t)B * K * 2));
+  u32x2 ec[kLatOutMaxK / 256];  // bf16 expert sum, 4 values a load
+#pragma unroll
+  for (int m = 0; m < kLatOutMaxK / 256; ++m)  // (no loads for waves w >= B: the offsets are past the end)
+    ec[m] = bload8_dev(er, w < B && 4 * (l + 64 * m) < K ? (uint32_t)(((size_t)w * K + 4 * (l + 64 * m)) * 2) : kOffNone);
+  issue(ka + 2, s2);
+  issue(ka + 3, s3);
+  if (w < B) {  // token w: en into LDS
+    float ss = 0.f;
+#pragma unroll
+    for (int m = 0; m < kLatOutMaxK / 256; ++m) {
+      if (4 * (l + 64 * m) < K) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float e = bf16_bits_to_f32(v & 1 ? ec[m][v >> 1] >> 16 : ec[m][v >> 1] & 0xFFFFu);
+          ss += e * e;
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
+    const float r = 1.0f / __fsqrt_rn(ss / (float)K + kLatOutRmsEps);
+#pragma unroll
+    for (int m = 0; m < kLatOutMaxK / 256; ++m) {
+      const int k = 4 * (l + 64 * m);
+      if (k < K) {
+        const u32x2 wp = *reinterpret_cast<const u32x2 *>(nw + 2 * k);
+        uint32_t o[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const uint32_t wb = v & 1 ? wp[v >> 1] >> 16 : wp[v >> 1] & 0xFFFFu;
+          const uint32_t eb = v & 1 ? ec[m][v >> 1] >> 16 : ec[m][v >> 1] & 0xFFFFu;
+          o[v] = f32_to_bf16_bits(round_bf16(bf16_bits_to_f32(eb) * r) * bf16_bits_to_f32(wb));
+        }
+        *reinterpret_cast<u32x2 *>(xs + (size_t)w * xp + k) = u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+      }
+    }
+  }
+  __syncthreads();
+  trace_mark(pl, a.ws, 37);  // en in LDS
+  f32x4 acc[2][2] = {{f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}},
+                     {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}}};
+  auto compute = [&](int ks, const Step &st) {
+    const int part = ks < KS0 ? 0 : 1;  // wave-uniform
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 xv = i < B ? *reinterpret_cast<const u32x4 *>(xs + (size_t)i * xp + ks * 128 + kk * 32 + q * 8)
+                             : u32x4{0u, 0u, 0u, 0u};
+      if (part == 0) {
+        acc[0][0] = mfma16(as_bf16x8(st.wa[kk]), as_bf16x8(xv), acc[0][0]);
+        acc[0][1] = mfma16(as_bf16x8(st.wb[kk]), as_bf16x8(xv), acc[0][1]);
+      } else {
+        acc[1][0] = mfma16(as_bf16x8(st.wa[kk]), as_bf16x8(xv), acc[1][0]);
+        acc[1][1] = mfma16(as_bf16x8(st.wb[kk]), as_bf16x8(xv), acc[1][1]);
+      }
+    }
+  };
+  // Steps past the wave's last one are not issued in the loop (their zero-area
+  // loads would only add latency at the end); before computing step ks, the
+  // wave's real steps after it, up to three, are the loads allowed in flight
+  // (any other load issued after them only makes the wait stricter).
+  auto wait_after = [](int later) {
+    if (later >= 3) wait_vm<24>();
+    else if (later == 2) wait_vm<16>();
+    else if (later == 1) wait_vm<8>();
+    else wait_vm<0>();
+  };
+  for (int ks = ka; ks < kb; ks += 4) {  // (wave-uniform conditions)
+    wait_after(kb - 1 - ks);
+    compute(ks, s0);
+    if (ks + 4 < kb) issue(ks + 4, s0);
+    if (ks + 1 >= kb) break;
+    wait_after(kb - 2 - ks);
+    compute(ks + 1, s1);
+    if (ks + 5 < kb) issue(ks + 5, s1);
+    if (ks + 2 >= kb) break;
+    wait_after(kb - 3 - ks);
+    compute(ks + 2, s2);
+    if (ks + 6 < kb) issue(ks + 6, s2);
+    if (ks + 3 >= kb) break;
+    wait_after(kb - 4 - ks);
+    compute(ks + 3, s3);
+    if (ks + 7 < kb) issue(ks + 7, s3);
+  }
+  if (kb - ka < 4) wait_vm<0>();  // the first four's zero-area loads past kb
+  trace_mark(pl, a.ws, 38);  // this wave-0 k-range done
+  __syncthreads();  // (the reduction area held nothing of this phase before: its LDS was only read)
+#pragma unroll
+  for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      *reinterpret_cast<f32x4 *>(red + ((pt * 2 + t) * kDecWaves + w) * 256 + l * 4) = acc[pt][t];
+  __syncthreads();
+  {
+    const int t = tid >> 8, idx = tid & 255, ln = idx >> 2, v = idx & 3;
+    const int rr = t * 16 + 4 * (ln >> 4) + v, c = ln & 15;
+    if (rr < n && c < B) {
+      const float s0 = red_sum(red + (0 * 2 + t) * kDecWaves * 256, idx);
+      const float s1 = red_sum(red + (1 * 2 + t) * kDecWaves * 256, idx);
+      a.lat_y[(size_t)c * h + row0 + rr] = f32_to_bf16_bits(round_bf16(s0) + round_bf16(s1));
+    }
+  }
+  return true;
 }
 
 static_assert(sizeof(Plan) % alignof(DecodeArgs) == 0, "DecodeArgs follows Plan in the argument segment");
@@ -1383,6 +1563,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   // a wait of this launch gave up: NaN in this workgroup's share of the output, and leave
   auto give_up = [&]() {
     poison_share<false>(a.out, (long)B * pl.K);
+    if (pl.lat_out) poison_share<true>(a.lat_y, (long)B * pl.h);
     leave();
   };
   trace_mark(pl, a.ws, 2);
@@ -1841,6 +2022,20 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     if (!grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 20), !dn_h_dev(pl))) return give_up();
   }
   trace_mark(pl, a.ws, 7);
+  // expert_sum stores; when the latent block's output follows in this launch,
+  // also its bf16 rounding (what the output's norm reads) at o_ebf, written
+  // device-coherent (other workgroups read it after a grid barrier)
+  const __amdgpu_buffer_rsrc_t ebr = make_rsrc(a.ws + pl.o_ebf, (uint32_t)((size_t)B * pl.K * 2));
+  auto put_out = [&](size_t at, f32x4 v) {
+    *reinterpret_cast<f32x4 *>(a.out + at) = v;
+    if (pl.lat_out)
+      st_dev64(ebr, (uint32_t)(at * 2), u32x2{f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16),
+                                              f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16)});
+  };
+  auto put_out1 = [&](size_t at, float v) {
+    a.out[at] = v;
+    if (pl.lat_out) __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v), ebr, (int)(at * 2), 0, kCpolDevice);
+  };
 
   // ------------------------------------------------------- DN: down+combine --
   if (expert_major) {
@@ -1878,7 +2073,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
         acc[2] = __fadd_rn(acc[2], __fmul_rn(bf16_bits_to_f32(yv[1] & 0xFFFFu), wt));
         acc[3] = __fadd_rn(acc[3], __fmul_rn(bf16_bits_to_f32(yv[1] >> 16), wt));
       }
-      *reinterpret_cast<f32x4 *>(a.out + (size_t)t * pl.K + c4) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+      put_out((size_t)t * pl.K + c4, f32x4{acc[0], acc[1], acc[2], acc[3]});
     }
   } else if (dn_pair) {
     // wave w: its expert's item in both row tiles, h loaded once after the barrier
@@ -1926,7 +2121,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
         float sum = acc_lds[tt * kDecWaves * BS + j];
 #pragma unroll
         for (int ww = 1; ww < kDecWaves; ++ww) sum = __fadd_rn(sum, acc_lds[(tt * kDecWaves + ww) * BS + j]);
-        a.out[(size_t)(j >> 4) * pl.K + rt * 16 + (j & 15)] = sum;
+        put_out1((size_t)(j >> 4) * pl.K + rt * 16 + (j & 15), sum);
       }
     }
   } else
@@ -2006,7 +2201,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
         const int t = j >> 4;
         float sum = 0.f;
         for (int sl = 0; sl < k; ++sl) sum = __fadd_rn(sum, pv[g_pof[t * k + sl] * 16 + (j & 15)]);
-        a.out[(size_t)t * pl.K + rt * 16 + (j & 15)] = sum;
+        put_out1((size_t)t * pl.K + rt * 16 + (j & 15), sum);
       }
       __syncthreads();
     }
@@ -2019,6 +2214,21 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     return;
   }
   trace_mark(pl, a.ws, 8);
+  if (pl.lat_out) {  // the latent block's output, after a grid barrier over the expert sum
+    const unsigned nb_out = ++nbar;
+    auto arrive = [&]() {
+      wait_vmem();  // this wave's expert-sum stores have completed
+      __syncthreads();
+      if (tid == 0) barrier_arrive(ctl, bb, nb_out, nullptr);
+    };
+    auto wait = [&]() {
+      if (tid == 0 && !barrier_wait(ctl, bb, nb_out, nullptr, false)) s_fail = 1;
+      __syncthreads();
+      return s_fail == 0;
+    };
+    if (!dec_latent_out(pl, a, lds, zero, arrive, wait)) return give_up();
+    trace_mark(pl, a.ws, 18);
+  }
   if (blockIdx.x == 0 && tid == 0) {  // this kernel's code range, for the next launch's warm-up
     crange[0] = pc0;
     crange[1] = program_counter();

@@ -126,12 +126,13 @@ struct Plan {
   int redundant;  // 1: every workgroup routes every token (no barrier before grouping)
   int xgemm;      // general path: 1 = grouped-GEMM expert kernels, 0 = per-16-token streams
   int fgemm;      // grouped GEMMs on the scaled FP4 MFMA with two-term E4M3 activations (k3moe_fgemm.hpp)
-  int lat_in;     // single-token kernel: 1 = it also computes the latent block's inputs (latent, shared_h)
+  int lat_in;     // single-token or decode kernel: 1 = it also computes the latent block's inputs (latent, shared_h)
   int lat_S;      // ... the shared experts' width S
-  int lat_out;    // single-token kernel: 1 = it also computes the latent block's output (lat_in too)
-  // workspace byte offsets
+  int lat_out;    // single-token or decode kernel: 1 = it also computes the latent block's output (lat_in too)
+  // workspace byte offsets (o_ebf: the decode kernel's bf16 copy of the expert
+  // sum, B x K, which the latent block's output phase reads)
   size_t o_ctl, o_zero, o_logit, o_ids, o_w, o_nact, o_active, o_aoff, o_acnt, o_ptok, o_pw, o_pof, o_gpart, o_gcnt,
-      o_gchunk, o_h, o_y, o_xq, o_hq, o_trace, total;
+      o_gchunk, o_h, o_y, o_xq, o_hq, o_ebf, o_trace, total;
 };
 
 __host__ __device__ inline int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
@@ -242,6 +243,10 @@ inline void single_plan(const k3moe_dims &d, Plan &p) {
 // that every workgroup polls before its gate/up products. Returns whether one
 // of the two kernels takes them for shared width S (setting lat_in, lat_S).
 constexpr int kLatRowsMax = 48;  // rows (latent rows + shared gate and up rows) per workgroup
+// The decode kernel's latent phases: their reduction area (the first 32 KiB of
+// the dynamic LDS: 2 parts x 2 tiles x 8 waves x 256 fp32), then their staged
+// token rows. The workgroup's LDS holds nothing else while they run.
+constexpr int kLatRedBytes = 32768;
 // The single-token kernel's latent block output (Plan::lat_out): a lane's
 // 16-byte chunks of a row of [latent_up | shared_down] (K + S <= 64 x 8 x
 // kLatOutChunks), output rows per wave, the expert sum's width, its RMS epsilon
@@ -252,14 +257,14 @@ constexpr float kLatOutRmsEps = 1e-5f;
 inline int lat_rows_max(const Plan &p, int S) { return 2 * cdiv(p.K / 2, p.G) + 2 * cdiv(S, p.G); }
 __host__ __device__ inline uint32_t lat_slot_base(const Plan &p) { return (uint32_t)(kTagCopies * p.E * 8 + p.k * (p.I / 2) * 8); }
 // The decode kernel takes them too with the pinned gate/up and at most 16
-// tokens (one MFMA token tile) whose rows of x fit in LDS after the reduction
-// area (row pitch h + 8; at most 8 tokens of h 7168): the G - B workgroups
+// tokens (one MFMA token tile) whose rows of x fit in LDS after kLatRedBytes
+// (row pitch h + 8; at most 8 tokens of h 7168): the G - B workgroups
 // that route no token share the rows out in whole pairs, at most 16 pairs
 // (two 16-row tiles) each.
 inline bool lat_in_plan(Plan &p, int S) {
   const bool single = p.single && S > 0 && lat_rows_max(p, S) <= kLatRowsMax &&
                       (long)lat_slot_base(p) + (long)(p.K / 2) * 8 <= kTagBytes;
-  const long lds_x = (long)p.lds_red + (long)p.B * (p.h + 8) * 2;
+  const long lds_x = (long)kLatRedBytes + (long)p.B * (p.h + 8) * 2;
   const bool decode = !p.single && p.path == kPathDecode && p.pinned && !p.redundant && p.B <= 16 && S > 0 &&
                       p.h % 512 == 0 && p.G > p.B && cdiv((p.K + 2 * S) / 2, p.G - p.B) <= 16 &&
                       lds_x <= kDecMaxLds - kDecStaticLds;
@@ -273,15 +278,27 @@ inline bool lat_in_plan(Plan &p, int S) {
 // The single-token kernel also takes the block's output (after lat_in_plan):
 // K <= kLatOutMaxK, K + S within a lane's chunks, at most kLatOutRowsPerWave
 // output rows per wave (h <= 32 G), the expert sum and [en | shared_h] in LDS.
+// The decode kernel takes it too with its latent projections and at most 8
+// tokens (wave t normalises token t): K and S multiples of 128, K <= 4096, at
+// most 32 output rows per workgroup, [en | shared_h] of every token and then
+// latent_norm in LDS after kLatRedBytes, the expert sum's bf16 copy at o_ebf.
 inline bool lat_out_plan(Plan &p) {
   const int S = p.lat_S;
-  const long lds = (long)single_lds_base(p) + align16(4 * p.K) + align16(2 * (p.K + S));
-  const bool ok = p.lat_in && p.single && p.K <= kLatOutMaxK && p.K % 8 == 0 && S % 8 == 0 &&
-                  p.K + S <= 64 * 8 * kLatOutChunks && cdiv(p.h, p.G) <= kDecWaves * kLatOutRowsPerWave &&
-                  (long)lat_slot_base(p) + (long)(p.K / 2 + S + p.K) * 8 <= kTagBytes &&
-                  lds <= kDecMaxLds - kDecStaticLds;
+  if (p.single) {
+    const long lds = (long)single_lds_base(p) + align16(4 * p.K) + align16(2 * (p.K + S));
+    const bool ok = p.lat_in && p.K <= kLatOutMaxK && p.K % 8 == 0 && S % 8 == 0 &&
+                    p.K + S <= 64 * 8 * kLatOutChunks && cdiv(p.h, p.G) <= kDecWaves * kLatOutRowsPerWave &&
+                    (long)lat_slot_base(p) + (long)(p.K / 2 + S + p.K) * 8 <= kTagBytes &&
+                    lds <= kDecMaxLds - kDecStaticLds;
+    p.lat_out = ok ? 1 : 0;
+    if (ok) p.lds_total = (int)lds;
+    return ok;
+  }
+  const long lds = (long)kLatRedBytes + align16((long)p.B * (p.K + S + 8) * 2) + 2 * kLatOutMaxK;
+  const bool ok = p.lat_in && p.path == kPathDecode && p.B <= kDecWaves && p.o_ebf && p.K % 128 == 0 && S % 128 == 0 &&
+                  p.K <= kLatOutMaxK && cdiv(p.h, p.G) <= 32 && lds <= kDecMaxLds - kDecStaticLds;
   p.lat_out = ok ? 1 : 0;
-  if (ok) p.lds_total = (int)lds;
+  if (ok && lds > p.lds_total) p.lds_total = (int)lds;
   return ok;
 }
 
@@ -387,6 +404,7 @@ inline void make_plan(const k3moe_dims &d, int n_cus, Plan &p, int trace = 0) {
   p.lat_in = 0;
   p.lat_S = 0;
   p.lat_out = 0;
+  p.o_ebf = take(p.path == kPathDecode && p.B <= kDecWaves ? (size_t)p.B * p.K * 2 : 0);
   single_plan(d, p);
   if (p.single) {
     p.path = kPathDecode;

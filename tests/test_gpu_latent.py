@@ -274,14 +274,16 @@ def test_latent_moe_step_matches_separate_launches(cfg, shared, forced):
     (MoEConfig('kimi-rank-e128-b1', 128, 16, 7168, 384, 1, latent=3584), 768, False),   # one launch
     (MoEConfig('kimi-rank-e128-b1', 128, 16, 7168, 384, 1, latent=3584), 768, True),
     (MoEConfig('latent-one', 64, 8, 1024, 256, 1, latent=512), 256, False),             # one launch, small
-    (MoEConfig('kimi-rank-e128-b8', 128, 16, 7168, 384, 8, latent=3584), 768, False),   # latent_out apart
+    (MoEConfig('kimi-rank-e128-b8', 128, 16, 7168, 384, 8, latent=3584), 768, False),   # decode kernel
+    (MoEConfig('latent-b3', 64, 8, 1024, 256, 3, latent=512), 256, True),
+    (MoEConfig('latent-b40', 64, 8, 1024, 256, 40, latent=512), 256, False),            # three launches
 ])
 def test_latent_block_one_call_matches_separate_calls(cfg, shared, forced):
     """k3moe.latent_block (k3moe_latent_block: one launch for one token on the single-token
-    kernel, the block's output computed after the combine) against latent_moe_step and
-    latent_out called apart on the same workspace: the same expert sets and weights, the output
-    within a rounding step of theirs (mostly equal: its rows are summed in another FP32 order)
-    and in the oracle's band."""
+    kernel, the decode kernel with the projections and the output at 8 tokens) against
+    latent_moe_step and latent_out called apart on the same workspace: the same expert sets and
+    weights, the output within a rounding step of theirs (mostly equal: its rows are summed in
+    another FP32 order) and in the oracle's band."""
     say(f'latent_block one call {cfg.name} shared={shared} forced={forced}')
     dev = torch.device('cuda:0')
     w = block_case(cfg, 6, shared)
@@ -300,7 +302,10 @@ def test_latent_block_one_call_matches_separate_calls(cfg, shared, forced):
     for key in ('expert_ids', 'route_weights', 'latent', 'shared_h', 'expert_sum'):
         ref = {'latent': lat, 'shared_h': sh}.get(key, moe.get(key))
         assert torch.equal(got[key].cpu(), ref.cpu()), key
-    near_oracle(got['output'], out2.cpu(), 1)
+    # out = bf16(bf16(routed) + bf16(shared)): where the two parts nearly cancel, one part's rounding
+    # step (another summation order moves a part by one) is many of the result's own steps, so the
+    # absolute floor is a part's step at a few times the output's RMS
+    near_oracle(got['output'], out2.cpu(), 1, floor=0.03)
     oracle = latent_ref.latent_block(w['x'], w, topk=cfg.topk, routes=routes)
     truth = latent_ref.latent_block(w['x'], w, topk=cfg.topk, fp32=True, routes=oracle['expert_ids'])
     detail = grading.band_check(got['output'].cpu(), oracle['output'], truth['output'], truth['output'],
