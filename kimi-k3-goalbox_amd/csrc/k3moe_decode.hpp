@@ -1242,6 +1242,7 @@ __device__ __forceinline__ bool dec_latent_out(const Plan &pl, const DecodeArgs 
   issue(ka + 1, s1);
   wait_vm<16>();  // the LDS loads, issued before the 16 weight loads, have landed (the barrier's sync publishes them)
   if (!wait()) return false;
+  // (trace slots 36-38 also hold the stream-K gate/up's per-wave ends: never in one launch with these)
   trace_mark(pl, a.ws, 36);  // the output barrier passed
   // the expert-sum loads go out before the other two steps' weights, so that
   // they queue behind half of the weight stream only
