@@ -1184,27 +1184,27 @@ __device__ __forceinline__ void dec_latent_rows(const Plan &pl, const DecodeArgs
 // w = latent_norm. Workgroup b takes a contiguous share of the h output rows
 // (at most 32: two 16-row MFMA tiles), the 8 waves split the K + S columns of
 // [latent_up | shared_down] in 128-column steps (K and S multiples of 128, so a
-// step lies in one part; one accumulator per part and tile); the workgroup
-// arrives at the grid barrier over the expert sum (`arrive`), issues the first
-// two steps' weights and then waits at it (`wait`), latent_norm and shared_h
-// (published at the latent barrier) going straight to LDS before the weights;
-// then the expert-sum loads and the next two steps' weights go out;
-// wave t < B normalises token t (the bf16 copy of its expert sum, written by
-// the combine at o_ebf, read with device-coherent loads; the sum of squares in
-// k_latent<1>'s order) and writes en beside
-// shared_h in LDS after kLatRedBytes (the step is over: nothing else lives in
-// LDS any more); the waves' tiles meet in
-// LDS in wave order and the two parts are rounded apart. Returns false when
-// the barrier gave up.
+// step lies in one part; one accumulator per part and tile; workgroups below
+// wg0, which write the expert sum after a grid barrier, take no rows); the
+// workgroup publishes its expert-sum stores (`arrive`), issues the first four
+// steps' weights and then waits until every workgroup has published (`wait`),
+// latent_norm and shared_h (published at the latent barrier) going straight to
+// LDS before the weights; then the expert-sum loads go out; wave t < B
+// normalises token t (the bf16 copy of its expert
+// sum, written by the combine at o_ebf, read with device-coherent loads; the
+// sum of squares in k_latent<1>'s order) and writes en beside shared_h in LDS
+// after kLatRedBytes (the step is over: nothing else lives in LDS any more);
+// the waves' tiles meet in LDS in wave order and the two parts are rounded
+// apart. Returns false when the wait gave up.
 template <class Arrive, class Wait>
 __device__ __forceinline__ bool dec_latent_out(const Plan &pl, const DecodeArgs &a, char *lds, const uint8_t *zero,
-                                               Arrive &&arrive, Wait &&wait) {
+                                               int wg0, Arrive &&arrive, Wait &&wait) {
   const int w = wave_id(), l = threadIdx.x & 63, i = l & 15, q = l >> 4, tid = threadIdx.x;
   const int h = pl.h, K = pl.K, B = pl.B, S = pl.lat_S, KT = K + S, xp = KT + 8;
   float *red = reinterpret_cast<float *>(lds);                    // [2 parts][2 tiles][8 waves][256]
   uint16_t *xs = reinterpret_cast<uint16_t *>(lds + kLatRedBytes);  // [B][K + S + 8]: en, then shared_h
   char *nw = lds + kLatRedBytes + align16((size_t)B * (K + S + 8) * 2);  // latent_norm, kLatOutMaxK bf16
-  const int G = (int)gridDim.x, rpw = (h + G - 1) / G, row0 = (int)blockIdx.x * rpw;
+  const int G = (int)gridDim.x - wg0, rpw = (h + G - 1) / G, row0 = ((int)blockIdx.x - wg0) * rpw;
   const int n = h > row0 ? min(rpw, h - row0) : 0;
   const int KS = KT / 128, KS0 = K / 128, ka = KS * w / kDecWaves, kb = KS * (w + 1) / kDecWaves;
   const bool ra = i < n, rb = 16 + i < n;
@@ -1240,19 +1240,17 @@ __device__ __forceinline__ bool dec_latent_out(const Plan &pl, const DecodeArgs 
   Step s0, s1, s2, s3;
   issue(ka, s0);
   issue(ka + 1, s1);
-  wait_vm<16>();  // the LDS loads, issued before the 16 weight loads, have landed (the barrier's sync publishes them)
+  issue(ka + 2, s2);
+  issue(ka + 3, s3);
+  wait_vm<32>();  // the LDS loads, issued before the 32 weight loads, have landed (the wait's sync publishes them)
   if (!wait()) return false;
   // (trace slots 36-38 also hold the stream-K gate/up's per-wave ends: never in one launch with these)
-  trace_mark(pl, a.ws, 36);  // the output barrier passed
-  // the expert-sum loads go out before the other two steps' weights, so that
-  // they queue behind half of the weight stream only
+  trace_mark(pl, a.ws, 36);  // every expert-sum share published
   const __amdgpu_buffer_rsrc_t er = make_rsrc(a.ws + pl.o_ebf, (uint32_t)((size_t)B * K * 2));
   u32x2 ec[kLatOutMaxK / 256];  // bf16 expert sum, 4 values a load
 #pragma unroll
   for (int m = 0; m < kLatOutMaxK / 256; ++m)  // (no loads for waves w >= B: the offsets are past the end)
     ec[m] = bload8_dev(er, w < B && 4 * (l + 64 * m) < K ? (uint32_t)(((size_t)w * K + 4 * (l + 64 * m)) * 2) : kOffNone);
-  issue(ka + 2, s2);
-  issue(ka + 3, s3);
   if (w < B) {  // token w: en into LDS
     float ss = 0.f;
 #pragma unroll
@@ -1561,6 +1559,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   const uint32_t tag = s_tag;
   const unsigned abort0 = s_abort0;
   unsigned nbar = 0;  // grid barriers of this launch passed so far
+  unsigned nb_late = 0;  // a barrier this workgroup arrived at without waiting (0: none)
   // a wait of this launch gave up: NaN in this workgroup's share of the output, and leave
   auto give_up = [&]() {
     poison_share<false>(a.out, (long)B * pl.K);
@@ -2056,8 +2055,19 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     dn_flush(st, pl, ybuf);
     trace_mark(pl, a.ws, 9);
     // (no acquire: the combine reads y only, with device-coherent loads; an
-    // agent-scope acquire would invalidate the XCD's L2 first)
-    if (!grid_barrier(ctl, bb, ++nbar, trace_slots(pl, a.ws, 24), false)) return give_up();
+    // agent-scope acquire would invalidate the XCD's L2 first). With the latent
+    // block's output following, a workgroup with no combine share only arrives
+    // and goes on to stream its output weights; it waits for the barrier later,
+    // before any other barrier (the group counters count arrivals in order).
+    const unsigned nb4 = ++nbar;
+    if (pl.lat_out && blockIdx.x * kDecThreads >= (unsigned)(B * (pl.K / 4))) {
+      wait_vmem();  // this wave's y stores have completed
+      __syncthreads();
+      if (tid == 0) barrier_arrive(ctl, bb, nb4, trace_slots(pl, a.ws, 24));
+      nb_late = nb4;
+    } else if (!grid_barrier(ctl, bb, nb4, trace_slots(pl, a.ws, 24), false)) {
+      return give_up();
+    }
     // combine (kimi.py:318,323): expert_sum[t][col] = sum over the token's
     // experts in ascending id order of w * bf16(y), from zero, FP32 adds
     const int K4 = pl.K / 4;
@@ -2210,31 +2220,79 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
 
   // ------------------------------------------------------------------ exit --
   __syncthreads();
-  if (aborted(ctl, abort0)) {  // a wait of this launch gave up (the down-phase waits have no barrier after them)
+  // a wait of this launch gave up (the down-phase waits have no barrier after
+  // them); with the latent block's output, checked after it
+  if (!pl.lat_out && aborted(ctl, abort0)) {
     give_up();
     return;
   }
   trace_mark(pl, a.ws, 8);
-  if (pl.lat_out) {  // the latent block's output, after a grid barrier over the expert sum
-    const unsigned nb_out = ++nbar;
+  if (pl.lat_out) {
+    // the latent block's output once every workgroup has published its
+    // expert-sum stores: workgroup b's slot kTagDecFlags + 8 b carries this
+    // launch's tag after its stores completed (workgroups without a share
+    // publish at once)
     auto arrive = [&]() {
       wait_vmem();  // this wave's expert-sum stores have completed
       __syncthreads();
-      if (tid == 0) barrier_arrive(ctl, bb, nb_out, nullptr);
+      if (tid == 0) st_dev64(tagr, (uint32_t)(kTagDecFlags + blockIdx.x * 8), u32x2{0u, tag});
     };
-    auto wait = [&]() {
-      if (tid == 0 && !barrier_wait(ctl, bb, nb_out, nullptr, false)) s_fail = 1;
+    auto wait = [&]() {  // wave 0 polls every workgroup's slot (bounded)
+      if (w == 0) {
+        unsigned spins = 0;
+        for (;;) {
+          bool ready = true;
+#pragma unroll
+          for (int m = 0; m < kLatFlagsMax / 64; ++m) {
+            const unsigned f = (unsigned)(l + 64 * m);
+            const u32x2 v = bload8_dev(tagr, f < gridDim.x ? (uint32_t)(kTagDecFlags + f * 8) : kOffNone);
+            ready = ready && (f >= gridDim.x || v[1] == tag);
+          }
+          if (__ballot(!ready) == 0) break;
+          ++spins;
+          if ((spins & 63u) == 0u && aborted(ctl, abort0)) {
+            if (l == 0) s_fail = 1;
+            break;
+          }
+          if (spins > kSpinLimit) {
+            if (l == 0) {
+              raise_timeout(ctl);
+              s_fail = 1;
+            }
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+      }
       __syncthreads();
       return s_fail == 0;
     };
-    if (!dec_latent_out(pl, a, lds, zero, arrive, wait)) return give_up();
+    // expert-major: the workgroups with a combine share (below ncomb) write
+    // their expert sum only after barrier 4; the output rows go to the others
+    // when at most 32 rows each
+    const int ncomb = (B * (pl.K / 4) + kDecThreads - 1) / kDecThreads;
+    const int wg0 = expert_major && ncomb < (int)gridDim.x && cdiv(pl.h, (int)gridDim.x - ncomb) <= 32 ? ncomb : 0;
+    if ((int)blockIdx.x < wg0) arrive();
+    else if (!dec_latent_out(pl, a, lds, zero, wg0, arrive, wait)) return give_up();
+    __syncthreads();
+    if (aborted(ctl, abort0)) {
+      give_up();
+      return;
+    }
     trace_mark(pl, a.ws, 18);
   }
   if (blockIdx.x == 0 && tid == 0) {  // this kernel's code range, for the next launch's warm-up
     crange[0] = pc0;
     crange[1] = program_counter();
   }
-  if (tag == last_tag_of_cycle() && !clear_tag_area(ctl, bb, ++nbar, tagr)) return give_up();
+  if (tag == last_tag_of_cycle()) {
+    if (nb_late) {  // the barrier this workgroup only arrived at, before its next arrival
+      if (tid == 0 && !barrier_wait(ctl, bb, nb_late, nullptr, false)) s_fail = 1;
+      __syncthreads();
+      if (s_fail) return give_up();
+    }
+    if (!clear_tag_area(ctl, bb, ++nbar, tagr)) return give_up();
+  }
   leave();
 }
 

@@ -92,6 +92,11 @@ constexpr int kTagCopies = 8;  // single-token router partials: one copy per XCD
 constexpr int kTagDecPairs = 0;
 constexpr int kTagDecDone = kTagDecPairs + kDecMaxPairs * 16;
 constexpr int kTagDecPart = kTagDecDone + 8 * 1024 * 8;  // done slots: d + b (staged), or wave gw < 8 x 1024 (pinned)
+// With the latent block's output (Plan::lat_out, pinned, at most 512
+// workgroups): workgroup b's "expert sum written" slot, the last 512 of the
+// done slots (pinned plans of at most 512 workgroups use the first 4096).
+constexpr int kLatFlagsMax = 512;
+constexpr int kTagDecFlags = kTagDecDone + (8 * 1024 - kLatFlagsMax) * 8;
 constexpr int kOffTag = kOffLatCnt + kLatCntBytes;
 constexpr int kInitBytes = kOffTag + kTagBytes;  // control block (page-padded), zero area, counters, tags
 constexpr int kTraceSlots = 56;    // phase timestamps per workgroup when tracing
@@ -295,7 +300,8 @@ inline bool lat_out_plan(Plan &p) {
     return ok;
   }
   const long lds = (long)kLatRedBytes + align16((long)p.B * (p.K + S + 8) * 2) + 2 * kLatOutMaxK;
-  const bool ok = p.lat_in && p.path == kPathDecode && p.B <= kDecWaves && p.o_ebf && p.K % 128 == 0 && S % 128 == 0 &&
+  const bool ok = p.lat_in && p.path == kPathDecode && p.B <= kDecWaves && p.G <= kLatFlagsMax && p.o_ebf &&
+                  p.K % 128 == 0 && S % 128 == 0 &&
                   p.K <= kLatOutMaxK && cdiv(p.h, p.G) <= 32 && lds <= kDecMaxLds - kDecStaticLds;
   p.lat_out = ok ? 1 : 0;
   if (ok && lds > p.lds_total) p.lds_total = (int)lds;
