@@ -316,6 +316,56 @@ def test_latent_block_one_call_matches_separate_calls(cfg, shared, forced):
     assert k3moe.workspace_status(ws) == 0
 
 
+@pytest.mark.parametrize('cfg,shared', [
+    (MoEConfig('kimi-rank-e128-b1', 128, 16, 7168, 384, 1, latent=3584), 768),   # single-token kernel
+    (MoEConfig('kimi-rank-e128-b8', 128, 16, 7168, 384, 8, latent=3584), 768),   # decode kernel
+], ids=['b1-single', 'b8-decode'])
+def test_latent_block_across_the_tag_wrap(cfg, shared):
+    """The one-launch latent block across the launch tag's wrap-around point: the launch counters
+    preset as after 2**32 / G - 3 launches and the tag area holding slots with the first tag after
+    the wrap (zero payloads), every call equals the first call on a fresh workspace. The cycle's
+    last launch clears the tag area (at 8 tokens, after the workgroups that only arrived at the
+    down phase's last barrier have waited for it)."""
+    say(f'latent_block across the tag wrap {cfg.name} shared={shared}')
+    dev = torch.device('cuda:0')
+    w = block_case(cfg, 8, shared)
+    g = {k: (v.to(dev) if v is not None else None) for k, v in w.items()}
+    key = (dev.type, dev.index)
+    saved = k3moe.moe._WORKSPACES.get(key)
+    try:
+        k3moe.moe._WORKSPACES.pop(key, None)      # a fresh workspace for this test alone
+        ref = {k: v.clone() for k, v in k3moe.latent_block(g['x'], g, topk=cfg.topk).items()}
+        torch.cuda.synchronize(dev)
+        ws = k3moe.moe._WORKSPACES[key]
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        G = 1
+        while G * 2 <= min(cus, 1024):
+            G *= 2
+        launches = (1 << 32) // G - 3
+        ctl = ws[:4096].view(torch.int32)
+        per = [0] * 16                           # launch counter c counts the workgroups b with b % 16 == c
+        for b in range(G):
+            per[b % 16] += 1
+        for c in range(16):
+            v = (per[c] * launches) & 0xFFFFFFFF
+            ctl[640 + 16 * c] = v - (1 << 32) if v >= 1 << 31 else v
+        tags = ws[k3moe.moe.INIT_BYTES - (2 << 20): k3moe.moe.INIT_BYTES].view(torch.int32).view(-1, 2)
+        tags[:, 0] = 0
+        tags[:, 1] = 1
+        torch.cuda.synchronize(dev)
+        for step in range(6):
+            got = k3moe.latent_block(g['x'], g, topk=cfg.topk)
+            torch.cuda.synchronize(dev)
+            for k in ('output', 'latent', 'shared_h', 'expert_sum', 'expert_ids', 'route_weights'):
+                assert torch.equal(got[k], ref[k]), (step, k)
+        assert k3moe.workspace_status(ws) == 0
+    finally:
+        if saved is not None:
+            k3moe.moe._WORKSPACES[key] = saved
+        else:
+            k3moe.moe._WORKSPACES.pop(key, None)
+
+
 def test_latent_moe_layer_reads_reference_keys():
     cfg = MoEConfig('latent-small', 64, 8, 1024, 256, 4, latent=512)
     say(f'latent_moe_layer {cfg.name}')
