@@ -103,7 +103,7 @@ def read_trace(cfg, device):
     r = torch.empty(cfg.experts, cfg.hidden, dtype=torch.bfloat16, device=device)
     lat = torch.empty(cfg.tokens, cfg.width, dtype=torch.bfloat16, device=device) if cfg.latent else None
     total = k3moe.workspace_bytes(moe.dims_for(x, r, g, d, cfg.topk, cfg.gating, cfg.activation, lat))
-    full = ws[total - 1024*56*8: total].cpu().view(torch.int64).view(1024, 56).double()
+    full = ws[total - 1024*64*8: total].cpu().view(torch.int64).view(1024, 64).double()
     # rows of the persistent grid: the largest power of two <= the CU count
     # (rows past it hold other launches' stamps or never-written memory)
     G = 1
@@ -114,6 +114,14 @@ def read_trace(cfg, device):
     if dump:
         import numpy as np
         np.save(f'{dump}_{cfg.name}.npy', full.numpy())
+    def bounds(out, t0, last):   # the workgroups' first instruction (slot 56) and end (slot 57)
+        ent, ext = full[:, 56], full[:, 57]
+        ok = (ent > 0) & (ext >= ent)
+        if bool(ok.any()):
+            out['workgroup_span_us'] = round(float((ext[ok].max() - ent[ok].min())*0.01), 2)
+            out['entry_to_first_mark_med_us'] = round(float(((full[ok, 0] - ent[ok])*0.01).median()), 2)
+            out['last_phase_to_end_us'] = round(float((ext[ok].max() - full[ok, last].max())*0.01), 2)
+            out['first_entry_before_t0_us'] = round(float((t0 - ent[ok].min())*0.01), 2)
     if int(full[0, 55].item()) == 0x5349:   # the single-token kernel's rows
         names = ('router', 'poll_partials', 'gating', 'select', 'weights_ids', 'gate_up', 'poll_h', 'down_combine')
         t0 = full[:, 0].min()
@@ -138,6 +146,7 @@ def read_trace(cfg, device):
                                     'gu_data_and_mfma_wave0': span(9, 12), 'gu_reduce': span(12, 13),
                                     'gu_epilogue_store': span(13, 14), 'gu_tail': span(14, 6)}
         out['poll_rounds_median'] = float(full[:, 11].median())
+        bounds(out, t0, 8)
         return out
     raw = full[:, :9]
     t0 = raw[:, 0].min()
@@ -152,6 +161,7 @@ def read_trace(cfg, device):
     out['gate_up_pct'] = [round(float(gu.quantile(q)), 1) for q in (0.0, 0.1, 0.5, 0.9, 1.0)]
     out['gate_up_slowest_wgs'] = [int(x) for x in gu.argsort(descending=True)[:8]]
     out['start_spread_us'] = round(float((raw[:, 0].max() - t0)*0.01), 2)
+    bounds(out, t0, 8)
     if float(full[:, 9].max()) > 0:   # expert-major down: stream end, then barrier 4 and the combine
         out['down_stream_done_at_us'] = round(float((full[:, 9].max() - t0)*0.01), 2)
     sub = full[:, 10:12]   # inside top-k: logits gathered, selection done (workgroups that routed a token)

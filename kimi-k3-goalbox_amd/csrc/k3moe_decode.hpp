@@ -1390,6 +1390,7 @@ __device__ __forceinline__ DecodeArgs load_args(uint64_t at) {
 // keeps the kernel's code (and its instruction-cache footprint) small.
 template <bool AL, int KSD>
 __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, DecodeArgs a_arg) {
+  const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();  // (stored when tracing)
   // The arguments, read through the touched segment (pl_arg at offset 0, a_arg after it).
   const uint64_t kargs = touch_kernargs<sizeof(Plan) + sizeof(DecodeArgs)>();
   const Plan pl = load_const<Plan>(kargs);
@@ -1450,6 +1451,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   const uint8_t *zero = reinterpret_cast<const uint8_t *>(a.ws + pl.o_zero);  // kZeroBytes of zeros
   const int B = pl.B, E = pl.E, k = pl.k;
   trace_mark(pl, a.ws, 0);
+  if (pl.o_trace && tid == 0)
+    reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + kTraceEntry] = t_entry;
   // The gating bias of experts tid and tid + 512: a token's one-logit-per-thread
   // gather uses exactly these, and loading them now keeps a cold HBM round trip
   // out of the top-k phase.
@@ -2294,6 +2297,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     if (!clear_tag_area(ctl, bb, ++nbar, tagr)) return give_up();
   }
   leave();
+  trace_mark(pl, a.ws, kTraceExit);
 }
 
 }  // namespace k3moe

@@ -99,7 +99,8 @@ constexpr int kLatFlagsMax = 512;
 constexpr int kTagDecFlags = kTagDecDone + (8 * 1024 - kLatFlagsMax) * 8;
 constexpr int kOffTag = kOffLatCnt + kLatCntBytes;
 constexpr int kInitBytes = kOffTag + kTagBytes;  // control block (page-padded), zero area, counters, tags
-constexpr int kTraceSlots = 56;    // phase timestamps per workgroup when tracing
+constexpr int kTraceSlots = 64;    // phase timestamps per workgroup when tracing
+constexpr int kTraceEntry = 56, kTraceExit = 57;  // the workgroup's first instruction and its end
 constexpr int kErrBarrierTimeout = 1;  // a wait timed out: that step's outputs are invalid
 constexpr int kErrRoutes = 2;          // forced routes out of range or repeated in a row: those rows used their own top-k
 

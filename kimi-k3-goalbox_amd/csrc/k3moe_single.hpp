@@ -78,6 +78,7 @@ struct SgDn {
 // projection's k-steps of 128 (I <= 128 KSD).
 template <int JE, int KSD>
 __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, DecodeArgs a_arg) {
+  const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();  // (stored when tracing)
   const uint64_t kargs = touch_kernargs<sizeof(Plan) + sizeof(DecodeArgs)>();
   const Plan pl = load_const<Plan>(kargs);
   const DecodeArgs a = load_args(kargs + sizeof(Plan));
@@ -109,6 +110,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   const uint32_t h_base = kTagCopies * copy_bytes;
   const uint8_t *zero = reinterpret_cast<const uint8_t *>(a.ws + pl.o_zero);
   trace_mark(pl, a.ws, 0);
+  if (pl.o_trace && threadIdx.x == 0)
+    reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + kTraceEntry] = t_entry;
 
   // Leaves the kernel: NaN in this workgroup's share of the output when a wait
   // gave up, and this workgroup's count on its launch counter (every path).
@@ -887,6 +890,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     if (!clear_tag_area(ctl, bb, 1, tagr)) return leave(true);
   }
   leave(false);
+  trace_mark(pl, a.ws, kTraceExit);
 }
 
 }  // namespace k3moe
