@@ -366,6 +366,54 @@ def test_latent_block_across_the_tag_wrap(cfg, shared):
             k3moe.moe._WORKSPACES.pop(key, None)
 
 
+@pytest.mark.parametrize('cfg,shared', [
+    (MoEConfig('kimi-rank-e128-b1', 128, 16, 7168, 384, 1, latent=3584), 768),   # single-token kernel
+    (MoEConfig('kimi-rank-e128-b8', 128, 16, 7168, 384, 8, latent=3584), 768),   # decode kernel
+], ids=['b1-single', 'b8-decode'])
+def test_latent_block_wait_that_gives_up(cfg, shared):
+    """The one-launch latent block's failure path, forced from the host (k3moe_debug_stall: the
+    router-logit waits give up after 256 polls): every workgroup still ends, the block's output
+    and the expert sum are NaN everywhere, the status word has the timeout bit, and after
+    k3moe_workspace_init the workspace gives the first call's outputs again."""
+    from k3moe import _native
+    import ctypes
+    say(f'latent_block failure path {cfg.name} shared={shared}')
+    dev = torch.device('cuda:0')
+    w = block_case(cfg, 10, shared)
+    g = {k: (v.to(dev) if v is not None else None) for k, v in w.items()}
+    key = (dev.type, dev.index)
+    saved = k3moe.moe._WORKSPACES.get(key)
+    try:
+        k3moe.moe._WORKSPACES.pop(key, None)      # a fresh workspace for this test alone
+        ref = {k: v.clone() for k, v in k3moe.latent_block(g['x'], g, topk=cfg.topk).items()}
+        torch.cuda.synchronize(dev)
+        ws = k3moe.moe._WORKSPACES[key]
+        _native.check(_native.load().k3moe_debug_stall(256), 'k3moe_debug_stall')
+        try:
+            bad = k3moe.latent_block(g['x'], g, topk=cfg.topk)
+            torch.cuda.synchronize(dev)
+        finally:
+            _native.check(_native.load().k3moe_debug_stall(0), 'k3moe_debug_stall')
+        assert bool(torch.isnan(bad['output'].float()).all())
+        assert bool(torch.isnan(bad['expert_sum']).all())
+        assert k3moe.workspace_status(ws) & 1
+        _native.check(_native.load().k3moe_workspace_init(
+            ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(ws.numel()),
+            ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)), 'k3moe_workspace_init')
+        assert k3moe.workspace_status(ws) == 0
+        for _ in range(2):
+            got = k3moe.latent_block(g['x'], g, topk=cfg.topk)
+            torch.cuda.synchronize(dev)
+            for k in ('output', 'latent', 'shared_h', 'expert_sum', 'expert_ids', 'route_weights'):
+                assert torch.equal(got[k], ref[k]), k
+        assert k3moe.workspace_status(ws) == 0
+    finally:
+        if saved is not None:
+            k3moe.moe._WORKSPACES[key] = saved
+        else:
+            k3moe.moe._WORKSPACES.pop(key, None)
+
+
 def test_latent_moe_layer_reads_reference_keys():
     cfg = MoEConfig('latent-small', 64, 8, 1024, 256, 4, latent=512)
     say(f'latent_moe_layer {cfg.name}')
