@@ -276,6 +276,8 @@ def test_latent_moe_step_matches_separate_launches(cfg, shared, forced):
     (MoEConfig('latent-one', 64, 8, 1024, 256, 1, latent=512), 256, False),             # one launch, small
     (MoEConfig('kimi-rank-e128-b8', 128, 16, 7168, 384, 8, latent=3584), 768, False),   # decode kernel
     (MoEConfig('latent-b3', 64, 8, 1024, 256, 3, latent=512), 256, True),
+    (MoEConfig('latent-b6', 64, 8, 1024, 256, 6, latent=512), 256, False),
+    (MoEConfig('latent-e8-b4', 8, 2, 1024, 256, 4, latent=512), 256, False),            # few active experts
     (MoEConfig('latent-b40', 64, 8, 1024, 256, 40, latent=512), 256, False),            # three launches
 ])
 def test_latent_block_one_call_matches_separate_calls(cfg, shared, forced):
