@@ -1225,10 +1225,10 @@ __device__ __forceinline__ bool dec_latent_out(const Plan &pl, const DecodeArgs 
       st.wb[kk] = load16((in && rb) ? reinterpret_cast<const uint8_t *>(pb) : zero);
     }
   };
-  // arrive first (the expert-sum stores have completed); before waiting, stage
-  // what does not depend on the barrier (latent_norm; shared_h, published at
-  // the latent barrier, read device-coherent) straight into LDS and issue the
-  // first two steps' weights
+  // publish first (the expert-sum stores have completed); before waiting,
+  // stage what does not depend on the other workgroups' expert sums
+  // (latent_norm; shared_h, published at the latent barrier, read
+  // device-coherent) straight into LDS and issue the first four steps' weights
   arrive();
   if (w < B)
     for (int c = 0; c < S; c += 128)  // 64 lanes x 2 values
@@ -2240,6 +2240,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
       __syncthreads();
       if (tid == 0) st_dev64(tagr, (uint32_t)(kTagDecFlags + blockIdx.x * 8), u32x2{0u, tag});
     };
+    // the abort counter, read by wave 0 once every slot is seen (every
+    // workgroup is past its down phase then, whose waits have no barrier
+    // after them) and used at the end, so that the read overlaps the output
+    unsigned abort_end = abort0;
     auto wait = [&]() {  // wave 0 polls every workgroup's slot (bounded)
       if (w == 0) {
         unsigned spins = 0;
@@ -2266,6 +2270,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
           }
           __builtin_amdgcn_s_sleep(1);
         }
+        abort_end = __hip_atomic_load(ctl + kCtlAbort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       __syncthreads();
       return s_fail == 0;
@@ -2275,12 +2280,17 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     // when at most 32 rows each
     const int ncomb = (B * (pl.K / 4) + kDecThreads - 1) / kDecThreads;
     const int wg0 = expert_major && ncomb < (int)gridDim.x && cdiv(pl.h, (int)gridDim.x - ncomb) <= 32 ? ncomb : 0;
-    if ((int)blockIdx.x < wg0) arrive();
-    else if (!dec_latent_out(pl, a, lds, zero, wg0, arrive, wait)) return give_up();
-    __syncthreads();
-    if (aborted(ctl, abort0)) {
-      give_up();
-      return;
+    if ((int)blockIdx.x < wg0) {
+      arrive();
+      // (its own down phase and combine are done; another workgroup's wait
+      // that gives up later poisons its own share and this workgroup's output
+      // is the expert sum only, which that workgroup's readers then poison)
+      if (aborted(ctl, abort0)) return give_up();
+    } else {
+      if (!dec_latent_out(pl, a, lds, zero, wg0, arrive, wait)) return give_up();
+      if (tid == 0 && abort_end != abort0) s_fail = 1;
+      __syncthreads();
+      if (s_fail) return give_up();
     }
     trace_mark(pl, a.ws, 18);
   }
