@@ -258,6 +258,7 @@ constexpr int kLatRedBytes = 32768;
 // kLatOutChunks), output rows per wave, the expert sum's width, its RMS epsilon
 // (kimi.py:325) and the slots a thread polls for [expert sum | shared_h].
 constexpr int kLatOutChunks = 9, kLatOutRowsPerWave = 4, kLatOutMaxK = 4096;
+constexpr int kLatOutRow1Bytes = 8 * kLatOutChunks * 1024;  // the single-token kernel: each wave's second output row
 constexpr int kLatOutPoll = (kLatOutMaxK + 512 + 511) / 512;  // K + S <= 64 x 8 x 9 = 4608 < 9 x 512 + 1
 constexpr float kLatOutRmsEps = 1e-5f;
 inline int lat_rows_max(const Plan &p, int S) { return 2 * cdiv(p.K / 2, p.G) + 2 * cdiv(S, p.G); }
@@ -291,7 +292,7 @@ inline bool lat_in_plan(Plan &p, int S) {
 inline bool lat_out_plan(Plan &p) {
   const int S = p.lat_S;
   if (p.single) {
-    const long lds = (long)single_lds_base(p) + align16(4 * p.K) + align16(2 * (p.K + S));
+    const long lds = (long)single_lds_base(p) + align16(4 * p.K) + align16(2 * (p.K + S)) + kLatOutRow1Bytes;
     const bool ok = p.lat_in && p.K <= kLatOutMaxK && p.K % 8 == 0 && S % 8 == 0 &&
                     p.K + S <= 64 * 8 * kLatOutChunks && cdiv(p.h, p.G) <= kDecWaves * kLatOutRowsPerWave &&
                     (long)lat_slot_base(p) + (long)(p.K / 2 + S + p.K) * 8 <= kTagBytes &&

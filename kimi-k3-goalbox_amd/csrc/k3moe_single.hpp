@@ -538,6 +538,30 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     if (s_fail) return leave(true);
   }
 
+  // The latent block's output rows (phase O below): wave w's first two rows'
+  // weights go out once the gate/up data has arrived, with the down weights,
+  // so that they stream while h is exchanged and the down products run; the
+  // first into registers, the second straight into LDS (kLatOutRow1Bytes
+  // after the expert sum and [en | shared_h]), which the down phase leaves
+  // free of registers.
+  struct OutRow {
+    u32x4 v[kLatOutChunks];
+  };
+  const int o_nro = pl.h > (int)blockIdx.x ? (pl.h - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+  auto out_issue = [&](int m, OutRow &rw) {  // wave w's m-th row (row b + G (w + 8 m)); past its rows: the zero area
+    const int KC = K / 8, NC = (K + pl.lat_S) / 8;
+    const int ri = w + kDecWaves * m, ro = (int)blockIdx.x + (int)gridDim.x * ri;
+#pragma unroll
+    for (int jc = 0; jc < kLatOutChunks; ++jc) {
+      const int c = l + 64 * jc;
+      const uint16_t *src = c < KC ? a.lat_up + (size_t)ro * K + c * 8 : a.lat_sd + (size_t)ro * pl.lat_S + (c - KC) * 8;
+      rw.v[jc] = load16((ri < o_nro && c < NC) ? reinterpret_cast<const uint8_t *>(src) : zero);
+    }
+  };
+  OutRow r0w, r1w;
+  char *const o_row1 = lds + single_lds_base(pl) + align16(4 * K) + align16(2 * (K + pl.lat_S)) +
+                       w * kLatOutChunks * 1024;  // wave w's second row (chunk jc at jc KiB, lane l at 16 l)
+
   // ----------------------------------------------------------- GU compute --
   // The down weights of this workgroup's row tiles (blockIdx.x, blockIdx.x + G)
   // for wave w's expert are issued once the gate/up data has arrived, so that
@@ -623,6 +647,16 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     if (w == 0) trace_mark(pl, a.ws, 14);
   }
   dn_issue();    // a workgroup without a gate/up unit
+  if (pl.lat_out) {
+    out_issue(0, r0w);
+    const int KC = K / 8, NC = (K + pl.lat_S) / 8, ri = w + kDecWaves, ro = (int)blockIdx.x + (int)gridDim.x * ri;
+#pragma unroll
+    for (int jc = 0; jc < kLatOutChunks; ++jc) {
+      const int c = l + 64 * jc;
+      const uint16_t *src = c < KC ? a.lat_up + (size_t)ro * K + c * 8 : a.lat_sd + (size_t)ro * pl.lat_S + (c - KC) * 8;
+      load_lds<16>((ri < o_nro && c < NC) ? reinterpret_cast<const uint8_t *>(src) : zero, o_row1 + jc * 1024);
+    }
+  }
   ring_barrier();  // wave 0's gating weights (sh.wts) are visible to the down phase
   trace_mark(pl, a.ws, 6);
 
@@ -738,8 +772,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   // Workgroup b takes output rows b, b + G, .. (wave w: its rows w, w + 8, ..);
   // a lane takes 16-byte chunks l + 64 j of the row's [latent_up | shared_down]
   // (K + S columns) against the same chunks of [en | shared_h] in LDS. The
-  // first two rows' weights go out before the expert sum and shared_h are
-  // polled from every workgroup's tagged slots; wave 0 sums e^2 (lane l:
+  // first two rows' weights go out after the gate/up data (the second of them
+  // straight into LDS), before the expert sum and shared_h are polled from
+  // every workgroup's tagged slots; wave 0 sums e^2 (lane l:
   // chunks of 4 at 4 (l + 64 m), then the wave's butterfly); each lane sums its
   // two parts separately in FP32, the wave's DPP tree sums them, and lane 0
   // rounds each part and their sum.
@@ -749,21 +784,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     float *es = reinterpret_cast<float *>(lds + single_lds_base(pl));       // [K] the expert sum
     uint16_t *xo = reinterpret_cast<uint16_t *>(es + K);                    // [K + S] en, then shared_h
     const uint32_t sh_base = lat_base + (uint32_t)(K / 2) * 8, es_base = sh_base + (uint32_t)S * 8;
-    struct Row {
-      u32x4 v[kLatOutChunks];
-    };
-    auto issue = [&](int m, Row &rw) {  // wave w's m-th row (row b + G (w + 8 m)); past its rows: the zero area
-      const int ri = w + kDecWaves * m, ro = b + G * ri;
-#pragma unroll
-      for (int jc = 0; jc < kLatOutChunks; ++jc) {
-        const int c = l + 64 * jc;
-        const uint16_t *src = c < KC ? a.lat_up + (size_t)ro * K + c * 8 : a.lat_sd + (size_t)ro * S + (c - KC) * 8;
-        rw.v[jc] = load16((ri < nro && c < NC) ? reinterpret_cast<const uint8_t *>(src) : zero);
-      }
-    };
-    Row r0w, r1w;
-    issue(0, r0w);
-    issue(1, r1w);
+    using Row = OutRow;
+    auto issue = out_issue;  // (rows 0 and 1 went out after the gate/up data)
     // this thread's norm weights (k = tid + 512 m), the expert sum and shared_h from their slots
     uint16_t wn[kLatOutMaxK / kDecThreads];
 #pragma unroll
@@ -838,6 +860,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     // the rows' values are stored after the loop: a store inside it would be
     // counted by the next row's wait (vmcnt counts stores too)
     uint16_t yv[kLatOutRowsPerWave];
+    // row 1 from LDS (its loads, older than the poll's, have landed)
+#pragma unroll
+    for (int jc = 0; jc < kLatOutChunks; ++jc) r1w.v[jc] = *reinterpret_cast<const u32x4 *>(o_row1 + jc * 1024 + 16 * l);
     auto row_out = [&](int m, const Row &rw) {
       const int ri = w + kDecWaves * m;
       if (ri >= nro) return;  // wave-uniform
