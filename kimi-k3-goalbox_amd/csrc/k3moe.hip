@@ -149,7 +149,7 @@ DecodeKernel decode_kernel(const Plan &p, int &slot) {
 
 // The single-token kernel's instantiation `slot` may use more than 64 KiB of dynamic LDS.
 int allow_single_lds(const void *fn, int slot, int bytes) {
-  static int granted[4] = {0};
+  static int granted[8] = {0};
   if (bytes <= 65536) return K3MOE_OK;
   return grant_lds(fn, kDecMaxLds - kDecStaticLds, granted[slot], "single-token");
 }
@@ -554,17 +554,24 @@ static int moe_step_impl(const k3moe_dims *dims, const void *x, const void *late
     if (p.single) {
       // instantiations: chosen experts per wave in the down phase (1: k <= 8, 2: k <= 16) and
       // the down projection's k-steps (2: I <= 256, 4: I <= 512)
-      const bool je2 = p.k > kDecWaves, ks4 = p.I > 256;
-      const void *fn = je2 ? (ks4 ? reinterpret_cast<const void *>(&k_moe_single<2, 4>)
-                                  : reinterpret_cast<const void *>(&k_moe_single<2, 2>))
-                           : (ks4 ? reinterpret_cast<const void *>(&k_moe_single<1, 4>)
-                                  : reinterpret_cast<const void *>(&k_moe_single<1, 2>));
-      if ((rc = allow_single_lds(fn, je2 * 2 + ks4, p.lds_total))) return rc;
-      if (je2 && ks4) hipLaunchKernelGGL((k_moe_single<2, 4>), dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
-      else if (je2) hipLaunchKernelGGL((k_moe_single<2, 2>), dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
-      else if (ks4) hipLaunchKernelGGL((k_moe_single<1, 4>), dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
-      else hipLaunchKernelGGL((k_moe_single<1, 2>), dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
-      return launch_check("single-token step");
+      // (and the latent block's phases: a separate instantiation)
+      const bool je2 = p.k > kDecWaves, ks4 = p.I > 256, lat = p.lat_in != 0;
+      auto launch = [&](auto kernel) -> int {
+        int r = allow_single_lds(reinterpret_cast<const void *>(kernel), lat * 4 + je2 * 2 + ks4, p.lds_total);
+        if (r) return r;
+        hipLaunchKernelGGL(kernel, dim3(p.G), dim3(kDecThreads), p.lds_total, st, p, a);
+        return launch_check("single-token step");
+      };
+      if (lat) {
+        if (je2 && ks4) return launch(k_moe_single<2, 4, true>);
+        if (je2) return launch(k_moe_single<2, 2, true>);
+        if (ks4) return launch(k_moe_single<1, 4, true>);
+        return launch(k_moe_single<1, 2, true>);
+      }
+      if (je2 && ks4) return launch(k_moe_single<2, 4, false>);
+      if (je2) return launch(k_moe_single<2, 2, false>);
+      if (ks4) return launch(k_moe_single<1, 4, false>);
+      return launch(k_moe_single<1, 2, false>);
     }
     int slot = 0;
     const DecodeKernel fn = decode_kernel(p, slot);

@@ -76,11 +76,14 @@ struct SgDn {
 
 // JE: chosen experts per wave in the down phase (k <= 8 JE); KSD: the down
 // projection's k-steps of 128 (I <= 128 KSD).
-template <int JE, int KSD>
+template <int JE, int KSD, bool LAT>
 __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, DecodeArgs a_arg) {
   const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();  // (stored when tracing)
   const uint64_t kargs = touch_kernargs<sizeof(Plan) + sizeof(DecodeArgs)>();
   const Plan pl = load_const<Plan>(kargs);
+  // the latent block's phases only in the LAT instantiations (the plain step's
+  // code then carries none of them)
+  const bool lat_in = LAT && pl.lat_in != 0, lat_out = LAT && pl.lat_out != 0;
   const DecodeArgs a = load_args(kargs + sizeof(Plan));
   (void)pl_arg;
   (void)a_arg;
@@ -117,7 +120,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   // gave up, and this workgroup's count on its launch counter (every path).
   auto leave = [&](bool gave_up) {
     if (gave_up) poison_share<false>(a.out, (long)K);
-    if (gave_up && pl.lat_out) poison_share<true>(a.lat_y, (long)pl.h);
+    if (gave_up && lat_out) poison_share<true>(a.lat_y, (long)pl.h);
     if (tid == 0)
       __hip_atomic_fetch_add(ctl + kCtlEpoch + (blockIdx.x % kEpochCounters) * kCtlEpochStride, 1u, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
@@ -131,7 +134,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   // the token's expert-input row (two 16-byte chunks per thread), the gating
   // bias of experts tid and tid + 512: both needed later, loaded now
   u32x4 xpre[2] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
-  if (!pl.lat_in) {  // (with the latent block's inputs, the kernel computes the row itself)
+  if (!lat_in) {  // (with the latent block's inputs, the kernel computes the row itself)
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const int c = hh * kDecThreads + tid;
@@ -245,7 +248,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
       const int c = c0 + l + 64 * m;
       xv[m] = c < c1 ? load16(a.x + c * 8) : u32x4{0, 0, 0, 0};
     }
-    if (pl.lat_in) {
+    if (lat_in) {
       issue(0, ba);
       issue(1, bb);
     }
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   make_tag();
   trace_mark(pl, a.ws, 1);
   // the staged row for gate/up (its loads have long arrived)
-  if (!pl.lat_in) {
+  if (!lat_in) {
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const int c = hh * kDecThreads + tid;
@@ -306,7 +309,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   // adds), the wave's lanes by the DPP tree and the waves in order in LDS. The
   // latent goes to xin and, as bf16 pairs, to tagged slots that every
   // workgroup polls before its gate/up products; shared_h goes to lat_sh.
-  if (pl.lat_in) {
+  if (lat_in) {
     for (int bi = 0; bi < nb; bi += 2) {  // batches past nb read the zero area
       wait_vm<2 * RB>();
       compute(bi, ba);
@@ -338,7 +341,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
       }
       const uint16_t hv = f32_to_bf16_bits(apply_act(pl.act, round_bf16(g), round_bf16(u)));
       a.lat_sh[sj] = hv;
-      if (pl.lat_out) st_dev64(tagr, lat_base + (uint32_t)(K / 2 + sj) * 8, u32x2{hv, tag});
+      if (lat_out) st_dev64(tagr, lat_base + (uint32_t)(K / 2 + sj) * 8, u32x2{hv, tag});
     }
     trace_mark(pl, a.ws, 16);
   }
@@ -498,7 +501,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     }
   }
 
-  if (pl.lat_in) {
+  if (lat_in) {
     // the latent row (the experts' input) from every workgroup's tagged row-pair
     // slots (thread tid: pairs tid + 512 m), polled until each carries this
     // launch's tag; its first check waits for this wave's gate/up loads too
@@ -647,7 +650,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
     if (w == 0) trace_mark(pl, a.ws, 14);
   }
   dn_issue();    // a workgroup without a gate/up unit
-  if (pl.lat_out) {
+  if (lat_out) {
     out_issue(0, r0w);
     const int KC = K / 8, NC = (K + pl.lat_S) / 8, ri = w + kDecWaves, ro = (int)blockIdx.x + (int)gridDim.x * ri;
 #pragma unroll
@@ -759,7 +762,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
       float sum = 0.f;
       for (int jj = 0; jj < k; ++jj) sum = __fadd_rn(sum, dacc[(tt * k + sh.ord[jj]) * 16 + r]);
       a.out[rt * 16 + r] = sum;
-      if (pl.lat_out)
+      if (lat_out)
         st_dev64(tagr, lat_base + (uint32_t)(K / 2 + pl.lat_S + rt * 16 + r) * 8, u32x2{__float_as_uint(sum), tag});
     }
   }
@@ -778,7 +781,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_single(Plan pl_arg, Deco
   // chunks of 4 at 4 (l + 64 m), then the wave's butterfly); each lane sums its
   // two parts separately in FP32, the wave's DPP tree sums them, and lane 0
   // rounds each part and their sum.
-  if (pl.lat_out) {
+  if (lat_out) {
     const int G = (int)gridDim.x, b = (int)blockIdx.x, h = pl.h, S = pl.lat_S, KC = K / 8, NC = (K + S) / 8;
     const int nro = h > b ? (h - b + G - 1) / G : 0;
     float *es = reinterpret_cast<float *>(lds + single_lds_base(pl));       // [K] the expert sum
