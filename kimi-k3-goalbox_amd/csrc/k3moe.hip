@@ -138,13 +138,20 @@ int grant_lds(const void *fn, int limit, int &granted, const char *what) {
 // multiple of 512) and the expert-major down variant of its I.
 typedef void (*DecodeKernel)(Plan, DecodeArgs);
 DecodeKernel decode_kernel(const Plan &p, int &slot) {
-  static const DecodeKernel table[2][4] = {
-      {k_moe_decode<false, 0>, k_moe_decode<false, 2>, k_moe_decode<false, 3>, k_moe_decode<false, 4>},
-      {k_moe_decode<true, 0>, k_moe_decode<true, 2>, k_moe_decode<true, 3>, k_moe_decode<true, 4>}};
+  // the latent block's phases (which need whole 512-column gate/up chunks, AL)
+  // in their own instantiations: row 2
+  static const DecodeKernel table[3][4] = {
+      {k_moe_decode<false, 0, false>, k_moe_decode<false, 2, false>, k_moe_decode<false, 3, false>,
+       k_moe_decode<false, 4, false>},
+      {k_moe_decode<true, 0, false>, k_moe_decode<true, 2, false>, k_moe_decode<true, 3, false>,
+       k_moe_decode<true, 4, false>},
+      {k_moe_decode<true, 0, true>, k_moe_decode<true, 2, true>, k_moe_decode<true, 3, true>,
+       k_moe_decode<true, 4, true>}};
   const int al = (p.K / kBlockK) % 16 == 0 ? 1 : 0;
+  const int row = p.lat_in ? 2 : al;  // (lat_in plans are pinned: AL)
   const int v = p.I == 256 ? 1 : p.I == 384 ? 2 : p.I == 512 ? 3 : 0;
-  slot = al * 4 + v;
-  return table[al][v];
+  slot = row * 4 + v;
+  return table[row][v];
 }
 
 // The single-token kernel's instantiation `slot` may use more than 64 KiB of dynamic LDS.
@@ -155,7 +162,7 @@ int allow_single_lds(const void *fn, int slot, int bytes) {
 }
 
 int allow_lds(DecodeKernel fn, int slot, int bytes) {
-  static int granted[8] = {0};
+  static int granted[12] = {0};
   if (bytes <= 65536) return K3MOE_OK;
   // dynamic + static LDS must fit the 160 KiB of a workgroup
   return grant_lds(reinterpret_cast<const void *>(fn), kDecMaxLds - kDecStaticLds, granted[slot], "decode");

@@ -1388,13 +1388,16 @@ __device__ __forceinline__ DecodeArgs load_args(uint64_t at) {
 // expert-major down path's k-steps per row (I / 128 for I = 256, 384, 512; 0:
 // that path is not used). Each instantiation holds one variant of each, which
 // keeps the kernel's code (and its instruction-cache footprint) small.
-template <bool AL, int KSD>
+template <bool AL, int KSD, bool LAT>
 __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, DecodeArgs a_arg) {
   const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();  // (stored when tracing)
   // The arguments, read through the touched segment (pl_arg at offset 0, a_arg after it).
   const uint64_t kargs = touch_kernargs<sizeof(Plan) + sizeof(DecodeArgs)>();
   const Plan pl = load_const<Plan>(kargs);
   const DecodeArgs a = load_args(kargs + sizeof(Plan));
+  // the latent block's phases only in the LAT instantiations (the plain step's
+  // code then carries none of them)
+  const bool lat_in = LAT && pl.lat_in != 0, lat_out = LAT && pl.lat_out != 0;
   (void)pl_arg;
   (void)a_arg;
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -1566,7 +1569,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   // a wait of this launch gave up: NaN in this workgroup's share of the output, and leave
   auto give_up = [&]() {
     poison_share<false>(a.out, (long)B * pl.K);
-    if (pl.lat_out) poison_share<true>(a.lat_y, (long)B * pl.h);
+    if (lat_out) poison_share<true>(a.lat_y, (long)B * pl.h);
     leave();
   };
   trace_mark(pl, a.ws, 2);
@@ -1744,7 +1747,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   // workgroup arrives at the latent barrier here and waits at it before its
   // gate/up rows are loaded.
   unsigned lat_bar = 0;
-  if (pl.lat_in) {
+  if (lat_in) {
     if ((int)blockIdx.x >= B) dec_latent_rows(pl, a, lds, zero, (int)blockIdx.x - B, (int)gridDim.x - B);
     trace_mark(pl, a.ws, 16);
     lat_bar = ++nbar;
@@ -1758,7 +1761,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   // long before the pairs are published.
   bool rows_staged = false;
   if constexpr (AL) {
-    if (pl.pinned && !redundant && !pl.lat_in && (int)blockIdx.x >= B) {
+    if (pl.pinned && !redundant && !lat_in && (int)blockIdx.x >= B) {
       rows_staged = true;
       const int per_row = pl.K / 512;
       for (int c = w; c < B * per_row; c += kDecWaves) {
@@ -1913,7 +1916,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   const int D = s_nact;
   trace_mark(pl, a.ws, 5);
 
-  if (pl.lat_in) {  // every workgroup's latent rows are out (read with device-coherent loads)
+  if (lat_in) {  // every workgroup's latent rows are out (read with device-coherent loads)
     if (tid == 0 && !barrier_wait(ctl, bb, lat_bar, nullptr, false)) s_fail = 1;
     __syncthreads();
     if (s_fail) return give_up();
@@ -1933,7 +1936,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     if (pl.pinned) {
       gu_pinned<AL>(pl, a, g_act, g_aoff, g_acnt, g_coff, g_cexp, g_ptok, xpin, s_prog, hbuf, pin_ua, pin_ub,
                     wave_unit(blockIdx.x * kDecWaves), wave_unit((blockIdx.x + 1) * kDecWaves), rows_staged,
-                    pl.lat_in != 0);
+                    lat_in != 0);
       pinned_done = true;
     }
   }
@@ -2031,13 +2034,13 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   const __amdgpu_buffer_rsrc_t ebr = make_rsrc(a.ws + pl.o_ebf, (uint32_t)((size_t)B * pl.K * 2));
   auto put_out = [&](size_t at, f32x4 v) {
     *reinterpret_cast<f32x4 *>(a.out + at) = v;
-    if (pl.lat_out)
+    if (lat_out)
       st_dev64(ebr, (uint32_t)(at * 2), u32x2{f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16),
                                               f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16)});
   };
   auto put_out1 = [&](size_t at, float v) {
     a.out[at] = v;
-    if (pl.lat_out) __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v), ebr, (int)(at * 2), 0, kCpolDevice);
+    if (lat_out) __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v), ebr, (int)(at * 2), 0, kCpolDevice);
   };
 
   // ------------------------------------------------------- DN: down+combine --
@@ -2063,7 +2066,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     // and goes on to stream its output weights; it waits for the barrier later,
     // before any other barrier (the group counters count arrivals in order).
     const unsigned nb4 = ++nbar;
-    if (pl.lat_out && blockIdx.x * kDecThreads >= (unsigned)(B * (pl.K / 4))) {
+    if (lat_out && blockIdx.x * kDecThreads >= (unsigned)(B * (pl.K / 4))) {
       wait_vmem();  // this wave's y stores have completed
       __syncthreads();
       if (tid == 0) barrier_arrive(ctl, bb, nb4, trace_slots(pl, a.ws, 24));
@@ -2225,12 +2228,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   __syncthreads();
   // a wait of this launch gave up (the down-phase waits have no barrier after
   // them); with the latent block's output, checked after it
-  if (!pl.lat_out && aborted(ctl, abort0)) {
+  if (!lat_out && aborted(ctl, abort0)) {
     give_up();
     return;
   }
   trace_mark(pl, a.ws, 8);
-  if (pl.lat_out) {
+  if (lat_out) {
     // the latent block's output once every workgroup has published its
     // expert-sum stores: workgroup b's slot kTagDecFlags + 8 b carries this
     // launch's tag after its stores completed (workgroups without a share
