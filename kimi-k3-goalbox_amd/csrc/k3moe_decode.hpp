@@ -913,14 +913,18 @@ __device__ __forceinline__ void dnc_compute(const DnTileBatch<KSD> &bt, const Pl
 
 // One wave's expert-major down range: items t in [ta, tb) of (active expert,
 // 16-row tile), expert-major; for each expert and 16-token chunk the h rows
-// (B operand) are loaded once, and the weight tiles stream in batches.
+// (B operand) are loaded once, and the weight tiles stream in batches. The
+// waves balance their progress in prog[8] (balance_waves; a wave with no items
+// counts as done, one not yet here as not started, so a wave still in gate/up
+// never loses its priority to the down waves).
 template <int KSD, class WaitExpert>
 __device__ __forceinline__ void dn_expert_major(const Plan &pl, const DecodeArgs &a, const int *g_act,
                                                 const int *g_aoff, const int *g_acnt, const uint8_t *zero,
                                                 __amdgpu_buffer_rsrc_t hrs, DnStage &st, uint16_t *ybuf, int ta,
-                                                int tb, const WaitExpert &wait_expert) {
+                                                int tb, const WaitExpert &wait_expert, int *prog) {
   constexpr int T = dn_tiles(KSD), KB = 4 * KSD;
   const int l = threadIdx.x & 63, i = l & 15, q = l >> 4;
+  if (ta >= tb && l == 0) __hip_atomic_store(prog + wave_id(), 4096, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   for (int t = ta; t < tb;) {
     const int d = t / pl.RTd;
     const int rt0 = t % pl.RTd, rt1 = min(pl.RTd, rt0 + (tb - t));
@@ -949,6 +953,7 @@ __device__ __forceinline__ void dn_expert_major(const Plan &pl, const DecodeArgs
       // batch cover it (vmcnt(0) at the join)
       for (int rt = rt0; rt < rt1; rt += 2 * T) {
         const int o1 = rt + T - rt0, o2 = rt + 2 * T - rt0;
+        balance_waves(prog, t - ta + (rt - rt0), tb - ta);
         dnc_issue<KSD>(b1, pl, wrow + o1 * tstride, srow + o1 * sstride, zero, rt + T, rt1);
         dnc_compute<KSD>(b0, pl, hb, st, ybuf, rt, rt1, p0 + c * 16, ncol);
         dnc_issue<KSD>(b0, pl, wrow + o2 * tstride, srow + o2 * sstride, zero, rt + 2 * T, rt1);
@@ -957,6 +962,7 @@ __device__ __forceinline__ void dn_expert_major(const Plan &pl, const DecodeArgs
     }
     t += rt1 - rt0;
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // Loads of one down-projection item: up to kDnDepth k-steps of A (weights and
@@ -1416,6 +1422,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   __shared__ GuChunk s_tab[16];
   __shared__ int s_round[2], s_rowtok[16];
   __shared__ __attribute__((aligned(16))) int s_prog[kDecWaves];
+  __shared__ __attribute__((aligned(16))) int s_dprog[kDecWaves];  // expert-major down progress
   __shared__ uint32_t s_tag;
   __shared__ int s_fail;
 
@@ -1497,6 +1504,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
   }
 
   if (l == 0) __hip_atomic_store(s_prog + w, 4096, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (l == 0) __hip_atomic_store(s_dprog + w, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 
   // ------------------------------------------------------------ R: router --
   // Workgroup unit = (16 router rows, k-split s) for every token tile: the
@@ -2055,7 +2063,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_moe_decode(Plan pl_arg, Deco
     st.rows = reinterpret_cast<uint16_t *>(scr) + w * st.cap * 16;
     st.tag = reinterpret_cast<int *>(scr + kDecWaves * st.cap * 32) + w * st.cap;
     st.fill = 0;
-    if constexpr (KSD > 0) dn_expert_major<KSD>(pl, a, g_act, g_aoff, g_acnt, zero, hrs, st, ybuf, ta, tb, wait_expert);
+    if constexpr (KSD > 0) dn_expert_major<KSD>(pl, a, g_act, g_aoff, g_acnt, zero, hrs, st, ybuf, ta, tb, wait_expert, s_dprog);
     if (pl.o_trace && l == 0)  // every wave's stream end (before its y flush)
       reinterpret_cast<uint64_t *>(a.ws + pl.o_trace)[blockIdx.x * kTraceSlots + 48 + w] = __builtin_amdgcn_s_memrealtime();
     dn_flush(st, pl, ybuf);
